@@ -1,0 +1,194 @@
+"""Benchmark of the MI355X backend on the GWP-0.5-shaped MoT hot path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Workloads (synthetic, seeded, random-init weights; inputs resident in HBM
+before the timed region):
+  ffn    one dense FFN block at 2048 tokens: LayerNorm+adaLN modulation ->
+         W_up [14336x3072] + bias + GELU-tanh -> W_down [3072x14336] + bias +
+         gated residual (bf16 hidden state, fp32 accumulation).
+  gemm   one MUL_MAT: W bf16 [3072x3072], X f32 [256x3072] -> Y f32.
+
+Prints one JSON line (rank 0) with roofline and cpu_baseline objects.  The
+dominant kernel's duration is measured with HIP events on the backend's
+stream; rocprofv3 summaries of the same command are kept under profiles/.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+for sub in ("wam.cpp_amd", "oracle"):
+    sys.path.insert(0, str(REPO / sub))
+
+import wamx  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def cpu_info():
+    cores = os.cpu_count() or 1
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return cores, model
+
+
+def time_op(be, fn, reps: int) -> float:
+    """Average ms of fn() over reps launches, HIP events on the backend stream."""
+    t = wamx.Timer(be)
+    fn()
+    be.sync()
+    t.start()
+    for _ in range(reps):
+        fn()
+    return t.stop_ms() / reps
+
+
+# ---------------------------------------------------------------------------
+def workload_gemm(be, args):
+    import oracle
+    M, K, N = 3072, 3072, 256
+    w = oracle.fill_normal(M * K, 0x5EED0000 + 1, 0.0, 0.02, oracle.BF16)
+    x = oracle.fill_normal(N * K, 0x5EED0000 + 2)
+    dw, dx, dy = be.array(w), be.array(x), be.empty(N * M * 4)
+
+    def step():
+        wamx.check(be.lib.wamx_op_mul_mat(be.ptr, dw.ptr, K, dx.ptr, wamx.TYPE_F32, K, dy.ptr, wamx.TYPE_F32, M,
+                                          M, N, K), "mul_mat")
+
+    flops = 2.0 * M * N * K
+    bytes_ = M * K * 2 + N * K * 4 + N * M * 4
+    for _ in range(args.warmup):
+        step()
+    be.sync()
+    t = wamx.Timer(be)
+    t.start()
+    for _ in range(args.steps):
+        step()
+    ms = t.stop_ms() / args.steps
+    roof = {"bound": "hbm", "achieved": bytes_ / (ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": bytes_ / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "traffic": None,
+            "kernel": "gemm_tile", "tflops": flops / (ms * 1e-3) / 1e12}
+    # CPU baseline: the oracle's MUL_MAT on the full problem.
+    t0 = time.perf_counter()
+    oracle.mul_mat(w.reshape(M, K), x.reshape(N, K))
+    cpu_ms = (time.perf_counter() - t0) * 1e3
+    cores, model = cpu_info()
+    cpu = {"value": cpu_ms, "unit": "ms per MUL_MAT", "cores": oracle.num_threads(), "kind": "port",
+           "sample": f"full 3072x3072x256 MUL_MAT on {model} ({cores} logical CPUs)"}
+    return {"metric": "ms per MUL_MAT (3072x3072 bf16 weight, 256 f32 tokens)", "unit": "ms", "value": ms,
+            "ms_per_step": ms, "higher_is_better": False, "dtype": "bf16",
+            "config": {"workload": "single MUL_MAT W[3072x3072] bf16 x X[256x3072] f32", "tokens": N},
+            "roofline": roof, "cpu_baseline": cpu}
+
+
+def workload_ffn(be, args):
+    import oracle
+    T, D, F = 2048, 3072, 14336
+    seed = 0x5EED0000 + 2
+    x = oracle.fill_normal(T * D, seed + 1, 0.0, 1.0, oracle.BF16)
+    shift = oracle.fill_normal(D, seed + 2, 0.0, 0.1)
+    scale = oracle.fill_normal(D, seed + 3, 0.0, 0.1)
+    gate = oracle.fill_normal(D, seed + 4, 0.0, 0.1)
+    w_up = oracle.fill_normal(F * D, seed + 5, 0.0, 0.02, oracle.BF16)
+    b_up = oracle.fill_normal(F, seed + 6, 0.0, 0.02, oracle.BF16)
+    w_dn = oracle.fill_normal(D * F, seed + 7, 0.0, 0.02, oracle.BF16)
+    b_dn = oracle.fill_normal(D, seed + 8, 0.0, 0.02, oracle.BF16)
+    dx, dsh, dsc, dg = be.array(x), be.array(shift), be.array(scale), be.array(gate)
+    dwu, dbu, dwd, dbd = be.array(w_up), be.array(b_up), be.array(w_dn), be.array(b_dn)
+    dn, dh, dout = be.empty(T * D * 2), be.empty(T * F * 2), be.empty(T * D * 2)
+    lib = be.lib
+
+    def norm():
+        wamx.check(lib.wamx_op_norm_modulation_bf16(be.ptr, dx.ptr, D, dsc.ptr, dsh.ptr, 0, dn.ptr, T, D, 1e-6))
+
+    def up():
+        wamx.check(lib.wamx_op_linear(be.ptr, dwu.ptr, dn.ptr, wamx.TYPE_BF16, dbu.ptr, wamx.EPI_BIAS_GELU, None,
+                                      None, dh.ptr, F, T, D))
+
+    def down():
+        wamx.check(lib.wamx_op_linear(be.ptr, dwd.ptr, dh.ptr, wamx.TYPE_BF16, dbd.ptr, wamx.EPI_BIAS_GATED, dx.ptr,
+                                      dg.ptr, dout.ptr, D, T, F))
+
+    def step():
+        norm()
+        up()
+        down()
+
+    for _ in range(args.warmup):
+        step()
+    be.sync()
+    t = wamx.Timer(be)
+    t.start()
+    for _ in range(args.steps):
+        step()
+    ms = t.stop_ms() / args.steps
+    gemm_flops = 2.0 * T * D * F
+    up_ms = time_op(be, up, 10)
+    down_ms = time_op(be, down, 10)
+    norm_ms = time_op(be, norm, 20)
+    dom_ms, dom = (up_ms, "gemm_tile (FFN up + bias + GELU)") if up_ms >= down_ms else \
+        (down_ms, "gemm_tile (FFN down + bias + gated residual)")
+    roof = {"bound": "mfma", "achieved": gemm_flops / (dom_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": gemm_flops / (dom_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "traffic": None,
+            "kernel": dom, "kernel_ms": dom_ms,
+            "kernels_ms": {"norm_mod_bf16": norm_ms, "ffn_up": up_ms, "ffn_down": down_ms},
+            "norm_gbs": (2 * T * D * 2) / (norm_ms * 1e-3) / 1e9}
+    # CPU baseline: the oracle's FFN block on 256 of the 2048 tokens, scaled x8.
+    ts = 256
+    xs = x.reshape(T, D)[:ts]
+    t0 = time.perf_counter()
+    n = oracle.norm_mod_bf16(xs, scale, shift, 1e-6)
+    h = oracle.linear(w_up.reshape(F, D), n, b_up, oracle.EPI_BIAS_GELU)
+    oracle.linear(w_dn.reshape(D, F), h, b_dn, oracle.EPI_BIAS_GATED, xs, gate)
+    cpu_ms = (time.perf_counter() - t0) * 1e3 * (T / ts)
+    cores, model = cpu_info()
+    cpu = {"value": cpu_ms, "unit": "ms per FFN block", "cores": oracle.num_threads(), "kind": "port",
+           "sample": f"{ts} of {T} tokens, scaled x{T // ts}, on {model} ({cores} logical CPUs)"}
+    return {"metric": "ms per dense FFN block (2048 tokens, 3072->14336->3072, bf16)", "unit": "ms", "value": ms,
+            "ms_per_step": ms, "higher_is_better": False, "dtype": "bf16",
+            "config": {"workload": "dense FFN block: LN+adaLN, W_up[14336x3072]+GELU, W_down[3072x14336]+gated "
+                                   "residual, 2048 tokens", "tokens": T, "gemm_tflops": gemm_flops * 2 / (ms * 1e-3) / 1e12},
+            "roofline": roof, "cpu_baseline": cpu}
+
+
+WORKLOADS = {"ffn": workload_ffn, "gemm": workload_gemm}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="ffn", choices=sorted(WORKLOADS))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path would shard by heads / independent chunks, see the design notes)", file=sys.stderr)
+        sys.exit(2)
+    be = wamx.Backend(0)
+    res = WORKLOADS[args.workload](be, args)
+    line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": res["higher_is_better"],
+            "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"], "data": "synthetic",
+            "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"]}
+    print(json.dumps(line), flush=True)
+    be.close()
+
+
+if __name__ == "__main__":
+    main()

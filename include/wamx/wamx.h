@@ -1,0 +1,526 @@
+/*
+ * wamx — MI355X (gfx950) compute backend for the GWP-0.5 Mixture-of-Transformers
+ * action path of wam.cpp.
+ *
+ * This header is the whole C ABI of libwamx.so.  It has four parts:
+ *
+ *   1. A tensor/graph IR shaped like ggml's (ne[]/nb[] strides, op + op_params,
+ *      src[] slots, views).  The engine in wam.cpp builds ggml graphs through
+ *      src/models/gwp05/engine/{mot,cache,weights}.cpp and submits them with
+ *      ggml_backend_graph_compute; the constructors below mirror the ggml entry
+ *      points those files call, including the ones added by
+ *      patches/llama-b9866-native-bf16.patch:7-51.
+ *   2. A backend plugin interface mirroring ggml-backend-impl.h of llama.cpp b9866
+ *      (ggml_backend_i / ggml_backend_device_i / buffer types / buffers).  ggml is
+ *      not vendored in the reference (cmake/Dependencies.cmake:73-89), so the
+ *      struct layouts and enum values are restated, not copied: numeric enum
+ *      values that must line up with ggml are listed in wamx_ggml_op_map (see
+ *      the end of this file) and are unverified against b9866 headers.
+ *   3. Single-op entry points on device pointers (wamx_op_*), used by the parity
+ *      tests and by callers that do not build graphs.
+ *   4. A synthetic GWP-0.5-shaped model driver (wamx_gwp_*) that builds the
+ *      prompt-projection, prefix and unrolled-denoise graphs the way
+ *      src/models/gwp05/engine/cache.cpp:53-485 and mot.cpp:358-594 do, and runs
+ *      them through the backend above.
+ *
+ * Conventions: every call returns a status or NULL, never aborts.  The last
+ * error message of the calling thread is available from wamx_last_error().
+ * One backend instance is not re-entrant: callers serialise, as wam.cpp does
+ * (src/models/gwp05/model.cpp:61).
+ */
+#ifndef WAMX_WAMX_H
+#define WAMX_WAMX_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <stdbool.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WAMX_API __attribute__((visibility("default")))
+
+#define WAMX_MAX_DIMS      4
+#define WAMX_MAX_SRC       10
+#define WAMX_MAX_OP_PARAMS 16   /* int32 slots, 64 bytes like ggml's GGML_MAX_OP_PARAMS */
+#define WAMX_MAX_NAME      64
+
+/* ---------------------------------------------------------------------------
+ * Enums.  Values of wamx_type follow enum ggml_type (F32=0, F16=1, I32=26,
+ * BF16=30).  wamx_status follows enum ggml_status.
+ * ------------------------------------------------------------------------- */
+typedef enum wamx_type {
+    WAMX_TYPE_F32  = 0,
+    WAMX_TYPE_F16  = 1,
+    WAMX_TYPE_I32  = 26,
+    WAMX_TYPE_BF16 = 30,
+} wamx_type;
+
+typedef enum wamx_status {
+    WAMX_STATUS_ALLOC_FAILED = -2,
+    WAMX_STATUS_FAILED       = -1,
+    WAMX_STATUS_SUCCESS      = 0,
+    WAMX_STATUS_ABORTED      = 1,
+} wamx_status;
+
+typedef enum wamx_op {
+    WAMX_OP_NONE = 0,
+    WAMX_OP_DUP,
+    WAMX_OP_ADD,        /* src[2] set: gated residual bf16 (native-bf16.patch:594-612) */
+    WAMX_OP_MUL,
+    WAMX_OP_SCALE,
+    WAMX_OP_CPY,        /* also ggml_cast */
+    WAMX_OP_CONT,
+    WAMX_OP_RESHAPE,
+    WAMX_OP_VIEW,
+    WAMX_OP_PERMUTE,
+    WAMX_OP_TRANSPOSE,
+    WAMX_OP_CONCAT,
+    WAMX_OP_REPEAT,
+    WAMX_OP_NORM,       /* src[1..2] set: bf16 norm + modulation / affine LN (patch:630-663) */
+    WAMX_OP_RMS_NORM,   /* src[1] set: bf16 in, bf16 weight, f32 out (patch:665-678) */
+    WAMX_OP_MUL_MAT,
+    WAMX_OP_SOFT_MAX,
+    WAMX_OP_ROPE,
+    WAMX_OP_UNARY,      /* GELU with src[1]: bias + GELU-tanh bf16 (patch:614-628) */
+    WAMX_OP_GET_ROWS,
+    WAMX_OP_IM2COL,
+    /* Fused ops with no single ggml counterpart.  They are what the engine's
+     * attention hook native_attention_context (mot.cpp:269-282) and a fused
+     * linear would emit.  Each one documents the unfused ggml subgraph it
+     * replaces, with identical rounding points. */
+    WAMX_OP_LINEAR,           /* MUL_MAT(bf16 out) [+ bf16 bias ADD] [+ GELU] [+ residual] */
+    WAMX_OP_QK_NORM_ROPE,     /* RMS_NORM(bf16->f32) + ROPE + CAST(bf16) + PERMUTE/CONT */
+    WAMX_OP_JOINT_ATTN,       /* CONCAT(K,V) + MUL_MAT(K,Q) + SOFT_MAX + MUL_MAT(V,P) + PERMUTE */
+    WAMX_OP_MODULATION,       /* CAST(f32) + ADD of the adaLN modulation and table */
+    WAMX_OP_COUNT
+} wamx_op;
+
+typedef enum wamx_unary_op {
+    WAMX_UNARY_GELU     = 0,  /* tanh approximation, ggml_gelu */
+    WAMX_UNARY_GELU_ERF = 1,
+    WAMX_UNARY_SILU     = 2,
+} wamx_unary_op;
+
+typedef enum wamx_prec {
+    WAMX_PREC_DEFAULT = 0,
+    WAMX_PREC_F32     = 10,   /* ggml_prec: GGML_PREC_F32 = 10 */
+} wamx_prec;
+
+/* Epilogue selector for WAMX_OP_LINEAR (op_params[0]). */
+typedef enum wamx_linear_epilogue {
+    WAMX_EPI_NONE          = 0, /* y = bf16(acc)                                        */
+    WAMX_EPI_BIAS          = 1, /* y = bf16(bf16(acc) + b)                              */
+    WAMX_EPI_BIAS_GELU     = 2, /* y = bf16(gelu_tanh(bf16(acc) + b))                   */
+    WAMX_EPI_BIAS_GATED    = 3, /* y = bf16(h + bf16(bf16(acc) + b) * g)   g f32 [M]    */
+    WAMX_EPI_BIAS_RESIDUAL = 4, /* y = bf16(h + bf16(bf16(acc) + b))                    */
+} wamx_linear_epilogue;
+
+/* Tensor flags (ggml_tensor_flag). */
+#define WAMX_TENSOR_FLAG_INPUT  1
+#define WAMX_TENSOR_FLAG_OUTPUT 2
+#define WAMX_TENSOR_FLAG_PARAM  4
+
+/* ---------------------------------------------------------------------------
+ * IR: tensors, contexts, graphs.
+ * ------------------------------------------------------------------------- */
+typedef struct wamx_buffer wamx_buffer;
+
+typedef struct wamx_tensor {
+    int32_t  type;                         /* wamx_type */
+    wamx_buffer * buffer;                  /* owning buffer, NULL until allocated */
+    int64_t  ne[WAMX_MAX_DIMS];            /* elements per dim, ne[0] innermost */
+    size_t   nb[WAMX_MAX_DIMS];            /* byte strides */
+    int32_t  op;                           /* wamx_op */
+    int32_t  op_params[WAMX_MAX_OP_PARAMS];
+    int32_t  flags;
+    struct wamx_tensor * src[WAMX_MAX_SRC];
+    struct wamx_tensor * view_src;
+    size_t   view_offs;
+    void *   data;                         /* device address once allocated */
+    char     name[WAMX_MAX_NAME];
+    void *   extra;
+} wamx_tensor;
+
+typedef struct wamx_context wamx_context;
+typedef struct wamx_cgraph  wamx_cgraph;
+
+/* A context owns tensor metadata only (ggml no_alloc=true contexts). */
+WAMX_API wamx_context * wamx_init(size_t max_tensors);
+WAMX_API void           wamx_free(wamx_context * ctx);
+
+WAMX_API size_t  wamx_type_size(int32_t type);
+WAMX_API const char * wamx_type_name(int32_t type);
+WAMX_API const char * wamx_op_name(int32_t op);
+WAMX_API int64_t wamx_nelements(const wamx_tensor * t);
+WAMX_API int64_t wamx_nrows(const wamx_tensor * t);
+WAMX_API size_t  wamx_nbytes(const wamx_tensor * t);
+WAMX_API bool    wamx_is_contiguous(const wamx_tensor * t);
+WAMX_API bool    wamx_are_same_shape(const wamx_tensor * a, const wamx_tensor * b);
+WAMX_API void    wamx_set_name(wamx_tensor * t, const char * name);
+WAMX_API void    wamx_set_input(wamx_tensor * t);
+WAMX_API void    wamx_set_output(wamx_tensor * t);
+
+WAMX_API wamx_tensor * wamx_new_tensor(wamx_context * ctx, int32_t type, int n_dims, const int64_t * ne);
+WAMX_API wamx_tensor * wamx_new_tensor_1d(wamx_context * ctx, int32_t type, int64_t ne0);
+WAMX_API wamx_tensor * wamx_new_tensor_2d(wamx_context * ctx, int32_t type, int64_t ne0, int64_t ne1);
+WAMX_API wamx_tensor * wamx_new_tensor_3d(wamx_context * ctx, int32_t type, int64_t ne0, int64_t ne1, int64_t ne2);
+WAMX_API wamx_tensor * wamx_new_tensor_4d(wamx_context * ctx, int32_t type, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3);
+
+/* Views (no compute; data aliases the source). */
+WAMX_API wamx_tensor * wamx_view_1d(wamx_context * ctx, wamx_tensor * a, int64_t ne0, size_t offset);
+WAMX_API wamx_tensor * wamx_view_2d(wamx_context * ctx, wamx_tensor * a, int64_t ne0, int64_t ne1, size_t nb1, size_t offset);
+WAMX_API wamx_tensor * wamx_view_3d(wamx_context * ctx, wamx_tensor * a, int64_t ne0, int64_t ne1, int64_t ne2, size_t nb1, size_t nb2, size_t offset);
+WAMX_API wamx_tensor * wamx_view_4d(wamx_context * ctx, wamx_tensor * a, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, size_t nb1, size_t nb2, size_t nb3, size_t offset);
+WAMX_API wamx_tensor * wamx_reshape_2d(wamx_context * ctx, wamx_tensor * a, int64_t ne0, int64_t ne1);
+WAMX_API wamx_tensor * wamx_reshape_3d(wamx_context * ctx, wamx_tensor * a, int64_t ne0, int64_t ne1, int64_t ne2);
+WAMX_API wamx_tensor * wamx_reshape_4d(wamx_context * ctx, wamx_tensor * a, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3);
+WAMX_API wamx_tensor * wamx_permute(wamx_context * ctx, wamx_tensor * a, int axis0, int axis1, int axis2, int axis3);
+WAMX_API wamx_tensor * wamx_transpose(wamx_context * ctx, wamx_tensor * a);
+
+/* Compute ops mirroring ggml constructors. */
+WAMX_API wamx_tensor * wamx_dup(wamx_context * ctx, wamx_tensor * a);
+WAMX_API wamx_tensor * wamx_cont(wamx_context * ctx, wamx_tensor * a);
+WAMX_API wamx_tensor * wamx_cast(wamx_context * ctx, wamx_tensor * a, int32_t type);
+WAMX_API wamx_tensor * wamx_cpy(wamx_context * ctx, wamx_tensor * a, wamx_tensor * b);
+WAMX_API wamx_tensor * wamx_concat(wamx_context * ctx, wamx_tensor * a, wamx_tensor * b, int dim);
+WAMX_API wamx_tensor * wamx_repeat(wamx_context * ctx, wamx_tensor * a, wamx_tensor * shape);
+WAMX_API wamx_tensor * wamx_add(wamx_context * ctx, wamx_tensor * a, wamx_tensor * b);
+WAMX_API wamx_tensor * wamx_mul(wamx_context * ctx, wamx_tensor * a, wamx_tensor * b);
+WAMX_API wamx_tensor * wamx_scale(wamx_context * ctx, wamx_tensor * a, float s);
+WAMX_API wamx_tensor * wamx_gelu(wamx_context * ctx, wamx_tensor * a);
+WAMX_API wamx_tensor * wamx_gelu_erf(wamx_context * ctx, wamx_tensor * a);
+WAMX_API wamx_tensor * wamx_silu(wamx_context * ctx, wamx_tensor * a);
+WAMX_API wamx_tensor * wamx_norm(wamx_context * ctx, wamx_tensor * a, float eps);
+WAMX_API wamx_tensor * wamx_rms_norm(wamx_context * ctx, wamx_tensor * a, float eps);
+WAMX_API wamx_tensor * wamx_mul_mat(wamx_context * ctx, wamx_tensor * a, wamx_tensor * b);
+WAMX_API wamx_tensor * wamx_mul_mat_out_type(wamx_context * ctx, wamx_tensor * a, wamx_tensor * b, int32_t type);
+WAMX_API void          wamx_mul_mat_set_prec(wamx_tensor * a, int32_t prec);
+WAMX_API wamx_tensor * wamx_soft_max_ext(wamx_context * ctx, wamx_tensor * a, wamx_tensor * mask, float scale, float max_bias);
+WAMX_API wamx_tensor * wamx_rope_ext(wamx_context * ctx, wamx_tensor * a, wamx_tensor * positions, wamx_tensor * freq_factors,
+                                     int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale,
+                                     float ext_factor, float attn_factor, float beta_fast, float beta_slow);
+WAMX_API wamx_tensor * wamx_get_rows(wamx_context * ctx, wamx_tensor * a, wamx_tensor * rows);
+/* ggml_im2col, 2-D: kernel ne={KW,KH,IC,OC} (shape only), input f32 ne={IW,IH,IC,N};
+ * result ne={IC*KH*KW, OW, OH, N} of dst_type (F32 or BF16), inner index
+ * ic*KH*KW + kh*KW + kw (the patch embedding of cache.cpp:203-218). */
+WAMX_API wamx_tensor * wamx_im2col(wamx_context * ctx, wamx_tensor * kernel, wamx_tensor * input, int s0, int s1,
+                                   int p0, int p1, int d0, int d1, int32_t dst_type);
+
+/* The fused ops of patches/llama-b9866-native-bf16.patch:566-678. */
+WAMX_API wamx_tensor * wamx_gated_residual_bf16(wamx_context * ctx, wamx_tensor * hidden, wamx_tensor * branch, wamx_tensor * gate);
+WAMX_API wamx_tensor * wamx_bias_gelu_bf16(wamx_context * ctx, wamx_tensor * input, wamx_tensor * bias);
+WAMX_API wamx_tensor * wamx_norm_modulation_bf16(wamx_context * ctx, wamx_tensor * input, wamx_tensor * scale, wamx_tensor * shift, float eps);
+WAMX_API wamx_tensor * wamx_layer_norm_bf16(wamx_context * ctx, wamx_tensor * input, wamx_tensor * weight, wamx_tensor * bias, float eps);
+WAMX_API wamx_tensor * wamx_rms_norm_bf16_f32(wamx_context * ctx, wamx_tensor * input, wamx_tensor * weight, float eps);
+
+/* Fused ops of this backend (see wamx_op).
+ *
+ * wamx_linear: y[N][M] bf16 from weight w bf16 [ne={K,M}], x bf16|f32 [ne={K,N}],
+ *   bias bf16 [M] (may be NULL for WAMX_EPI_NONE), residual bf16 [ne={M,N}] and
+ *   gate f32 [M] (row broadcast) as the epilogue needs.  Replaces
+ *   linear_with_activation / linear_gelu_with_activation (weights.cpp:819-849)
+ *   followed by gated_residual (mot.cpp:161-173) or the plain add of mot.cpp:338.
+ *
+ * wamx_qk_norm_rope: from a packed projection x bf16 [ne={d, T}] (row stride
+ *   nb[1]) computes RMSNorm over the full d (weights.cpp:904-917), rotates it
+ *   with NORMAL RoPE and writes bf16 into dst laid out [ne={head_dim, T_total, H}]
+ *   starting at token offset tok0 (the head-major layout mot.cpp:395-396 builds
+ *   with permute+cont).  rope_mode 0: 1-D rope over head_dim with pos0[T];
+ *   rope_mode 1: 3-section {44,42,42} rope with pos0/pos1/pos2 (mot.cpp:182-202);
+ *   rope_mode 2: no rope (cross-attention queries, mot.cpp:301-306).
+ *   Writes into an existing tensor (dst), returned as a node that depends on it.
+ *
+ * wamx_joint_attn: softmax(scale * Q K^T) V per head over the key set
+ *   [kv_a rows 0..na_split), kv_b, kv_a rows [na_split..)] i.e. the complete-MoT
+ *   order [state, action, reference] of mot.cpp:402-431 without the CONCAT copies.
+ *   Q bf16 [ne={dh, Tq, H}], K tensors bf16 [ne={dh, n, H}], V tensors bf16
+ *   transposed [ne={n, dh, H}] (cache.cpp:22-25).  kv_b may be NULL.  Output bf16
+ *   [ne={dh*H, Tq}], the layout the output projection consumes (mot.cpp:437-445).
+ *
+ * wamx_modulation: f32 [ne={d, 6, L}] = f32(mod [ne={d,6}]) + f32(table_l) for the
+ *   L per-layer tables packed in `tables` [ne={d, 6, L}] (mot.cpp:137-145, 380-393).
+ */
+WAMX_API wamx_tensor * wamx_linear(wamx_context * ctx, wamx_tensor * w, wamx_tensor * x, wamx_tensor * bias,
+                                   int32_t epilogue, wamx_tensor * residual, wamx_tensor * gate);
+WAMX_API wamx_tensor * wamx_qk_norm_rope(wamx_context * ctx, wamx_tensor * x, wamx_tensor * weight, wamx_tensor * dst,
+                                         int64_t tok0, int rope_mode, wamx_tensor * pos0, wamx_tensor * pos1,
+                                         wamx_tensor * pos2, float eps, float freq_base);
+WAMX_API wamx_tensor * wamx_joint_attn(wamx_context * ctx, wamx_tensor * q, wamx_tensor * k_a, wamx_tensor * v_a,
+                                       wamx_tensor * k_b, wamx_tensor * v_b, int64_t na_split, float scale);
+WAMX_API wamx_tensor * wamx_modulation(wamx_context * ctx, wamx_tensor * mod, wamx_tensor * tables);
+
+/* Graphs. */
+WAMX_API wamx_cgraph * wamx_new_graph(wamx_context * ctx, size_t max_nodes);
+WAMX_API void          wamx_build_forward_expand(wamx_cgraph * g, wamx_tensor * t);
+WAMX_API int           wamx_graph_n_nodes(const wamx_cgraph * g);
+WAMX_API wamx_tensor * wamx_graph_node(wamx_cgraph * g, int i);
+WAMX_API void          wamx_graph_assign_uid(wamx_cgraph * g);   /* native-bf16.patch:700-703 */
+WAMX_API uint64_t      wamx_graph_uid(const wamx_cgraph * g);
+
+/* ---------------------------------------------------------------------------
+ * Backend plugin interface (restating ggml-backend-impl.h, b9866).
+ * ------------------------------------------------------------------------- */
+typedef struct wamx_backend        * wamx_backend_t;
+typedef struct wamx_buffer_type    * wamx_buffer_type_t;
+typedef struct wamx_buffer         * wamx_buffer_t;
+typedef struct wamx_device         * wamx_device_t;
+typedef struct wamx_backend_reg    * wamx_backend_reg_t;
+
+typedef struct wamx_buffer_type_i {
+    const char *  (*get_name)      (wamx_buffer_type_t buft);
+    wamx_buffer_t (*alloc_buffer)  (wamx_buffer_type_t buft, size_t size);
+    size_t        (*get_alignment) (wamx_buffer_type_t buft);
+    size_t        (*get_max_size)  (wamx_buffer_type_t buft);
+    size_t        (*get_alloc_size)(wamx_buffer_type_t buft, const wamx_tensor * t);
+    bool          (*is_host)       (wamx_buffer_type_t buft);
+} wamx_buffer_type_i;
+
+typedef struct wamx_buffer_i {
+    void          (*free_buffer)  (wamx_buffer_t buf);
+    void *        (*get_base)     (wamx_buffer_t buf);
+    wamx_status   (*init_tensor)  (wamx_buffer_t buf, wamx_tensor * t);
+    void          (*memset_tensor)(wamx_buffer_t buf, wamx_tensor * t, uint8_t value, size_t offset, size_t size);
+    void          (*set_tensor)   (wamx_buffer_t buf, wamx_tensor * t, const void * data, size_t offset, size_t size);
+    void          (*get_tensor)   (wamx_buffer_t buf, const wamx_tensor * t, void * data, size_t offset, size_t size);
+    bool          (*cpy_tensor)   (wamx_buffer_t buf, const wamx_tensor * src, wamx_tensor * dst);
+    void          (*clear)        (wamx_buffer_t buf, uint8_t value);
+    void          (*reset)        (wamx_buffer_t buf);
+} wamx_buffer_i;
+
+typedef struct wamx_backend_i {
+    const char * (*get_name)        (wamx_backend_t backend);
+    void         (*free)            (wamx_backend_t backend);
+    void         (*set_tensor_async)(wamx_backend_t backend, wamx_tensor * t, const void * data, size_t offset, size_t size);
+    void         (*get_tensor_async)(wamx_backend_t backend, const wamx_tensor * t, void * data, size_t offset, size_t size);
+    bool         (*cpy_tensor_async)(wamx_backend_t src, wamx_backend_t dst, const wamx_tensor * a, wamx_tensor * b);
+    void         (*synchronize)     (wamx_backend_t backend);
+    wamx_status  (*graph_compute)   (wamx_backend_t backend, wamx_cgraph * g);
+} wamx_backend_i;
+
+typedef struct wamx_device_i {
+    const char *        (*get_name)       (wamx_device_t dev);
+    const char *        (*get_description)(wamx_device_t dev);
+    void                (*get_memory)     (wamx_device_t dev, size_t * free, size_t * total);
+    wamx_backend_t      (*init_backend)   (wamx_device_t dev, const char * params);
+    wamx_buffer_type_t  (*get_buffer_type)(wamx_device_t dev);
+    bool                (*supports_op)    (wamx_device_t dev, const wamx_tensor * op);
+    bool                (*supports_buft)  (wamx_device_t dev, wamx_buffer_type_t buft);
+    bool                (*offload_op)     (wamx_device_t dev, const wamx_tensor * op);
+} wamx_device_i;
+
+typedef struct wamx_backend_reg_i {
+    const char *  (*get_name)        (wamx_backend_reg_t reg);
+    size_t        (*get_device_count)(wamx_backend_reg_t reg);
+    wamx_device_t (*get_device)      (wamx_backend_reg_t reg, size_t index);
+    void *        (*get_proc_address)(wamx_backend_reg_t reg, const char * name);
+} wamx_backend_reg_i;
+
+/* Registry / device / backend lifetime (ggml_backend_cuda_init, weights.cpp:582-596). */
+WAMX_API wamx_backend_reg_t  wamx_backend_reg(void);
+WAMX_API const wamx_backend_reg_i * wamx_backend_reg_iface(void);
+WAMX_API const wamx_device_i      * wamx_device_iface(void);
+WAMX_API const wamx_backend_i     * wamx_backend_iface(void);
+WAMX_API const wamx_buffer_type_i * wamx_buffer_type_iface(void);
+WAMX_API const wamx_buffer_i      * wamx_buffer_iface(void);
+
+WAMX_API int             wamx_get_device_count(void);
+WAMX_API wamx_backend_t  wamx_backend_init(int device);
+WAMX_API void            wamx_backend_free(wamx_backend_t backend);
+WAMX_API const char *    wamx_backend_name(wamx_backend_t backend);
+WAMX_API void *          wamx_backend_stream(wamx_backend_t backend);   /* hipStream_t */
+WAMX_API wamx_buffer_type_t wamx_backend_get_default_buffer_type(wamx_backend_t backend);
+WAMX_API wamx_buffer_type_t wamx_backend_buffer_type(int device);
+
+/* Buffers (ggml_backend_buft_alloc_buffer, ggml_backend_alloc_ctx_tensors). */
+WAMX_API wamx_buffer_t wamx_buft_alloc_buffer(wamx_buffer_type_t buft, size_t size);
+WAMX_API size_t        wamx_buft_get_alignment(wamx_buffer_type_t buft);
+WAMX_API size_t        wamx_buft_get_alloc_size(wamx_buffer_type_t buft, const wamx_tensor * t);
+WAMX_API wamx_buffer_t wamx_backend_alloc_buffer(wamx_backend_t backend, size_t size);
+WAMX_API void          wamx_buffer_free(wamx_buffer_t buf);
+WAMX_API void *        wamx_buffer_get_base(wamx_buffer_t buf);
+WAMX_API size_t        wamx_buffer_get_size(wamx_buffer_t buf);
+WAMX_API wamx_status   wamx_tensor_alloc(wamx_buffer_t buf, wamx_tensor * t, void * addr);
+WAMX_API wamx_buffer_t wamx_backend_alloc_ctx_tensors(wamx_context * ctx, wamx_backend_t backend);
+
+/* Tensor data movement (ggml_backend_tensor_set/get/copy). */
+WAMX_API wamx_status wamx_backend_tensor_set(wamx_tensor * t, const void * data, size_t offset, size_t size);
+WAMX_API wamx_status wamx_backend_tensor_get(const wamx_tensor * t, void * data, size_t offset, size_t size);
+WAMX_API wamx_status wamx_backend_tensor_copy(const wamx_tensor * src, wamx_tensor * dst);
+WAMX_API wamx_status wamx_backend_tensor_memset(wamx_tensor * t, uint8_t value, size_t offset, size_t size);
+WAMX_API void        wamx_backend_synchronize(wamx_backend_t backend);
+
+/* Graph allocation (ggml_gallocr): allocates every unallocated tensor of the
+ * graph in one device buffer with liveness-based reuse. */
+typedef struct wamx_gallocr * wamx_gallocr_t;
+WAMX_API wamx_gallocr_t wamx_gallocr_new(wamx_backend_t backend);
+WAMX_API bool           wamx_gallocr_alloc_graph(wamx_gallocr_t galloc, wamx_cgraph * g);
+WAMX_API size_t         wamx_gallocr_get_buffer_size(wamx_gallocr_t galloc);
+WAMX_API void           wamx_gallocr_free(wamx_gallocr_t galloc);
+
+/* Compute.  graph_compute replays a captured HIP graph when the same graph
+ * (uid, node count and tensor addresses) was computed before; set
+ * WAMX_DISABLE_HIP_GRAPHS=1 to launch eagerly every time. */
+WAMX_API wamx_status wamx_backend_graph_compute(wamx_backend_t backend, wamx_cgraph * g);
+WAMX_API bool        wamx_backend_supports_op(wamx_backend_t backend, const wamx_tensor * op);
+
+/* ---------------------------------------------------------------------------
+ * Single-op entry points on device pointers (no graph).  All run on the
+ * backend's stream and return immediately (asynchronous).  Sizes are in
+ * elements; leading dimensions are row strides in elements.
+ * ------------------------------------------------------------------------- */
+
+/* GGML_OP_MUL_MAT semantics (native-bf16.patch:566-592): y[n][m] = sum_k w[m][k]*x[n][k]
+ * with x rounded to bf16 (round-to-nearest-even) when x_type is F32, fp32
+ * accumulation, output F32 or rounded BF16. */
+WAMX_API wamx_status wamx_op_mul_mat(wamx_backend_t be, const void * w, int64_t ldw,
+                                     const void * x, int32_t x_type, int64_t ldx,
+                                     void * y, int32_t y_type, int64_t ldy,
+                                     int64_t M, int64_t N, int64_t K);
+/* WAMX_OP_LINEAR on device pointers. */
+WAMX_API wamx_status wamx_op_linear(wamx_backend_t be, const void * w, const void * x, int32_t x_type,
+                                    const void * bias, int32_t epilogue, const void * residual,
+                                    const float * gate, void * y, int64_t M, int64_t N, int64_t K);
+/* norm_bf16_fused<bs,false> (native-bf16.patch:368-409): y = bf16(n*(1+scale)+shift).
+ * scale/shift f32, row stride ss (0 = broadcast). */
+WAMX_API wamx_status wamx_op_norm_modulation_bf16(wamx_backend_t be, const void * x, int64_t ldx,
+                                                  const float * scale, const float * shift, int64_t ss,
+                                                  void * y, int64_t rows, int64_t cols, float eps);
+/* norm_bf16_fused<bs,true>: y = bf16(n*w+b), w/b bf16 [cols]. */
+WAMX_API wamx_status wamx_op_layer_norm_bf16(wamx_backend_t be, const void * x, int64_t ldx,
+                                             const void * w, const void * b, void * y,
+                                             int64_t rows, int64_t cols, float eps);
+/* rms_norm_bf16_f32 (native-bf16.patch:411-430): y f32 = x*rsqrt(mean(x^2)+eps)*w. */
+WAMX_API wamx_status wamx_op_rms_norm_bf16_f32(wamx_backend_t be, const void * x, int64_t ldx,
+                                               const void * w, float * y, int64_t rows, int64_t cols, float eps);
+/* norm_modulation_f32 (p7-fusions.patch:19-51): one-pass variance, no FMA. */
+WAMX_API wamx_status wamx_op_norm_modulation_f32(wamx_backend_t be, const float * x, int64_t ldx,
+                                                 const float * scale, const float * shift, int64_t ss,
+                                                 float * y, int64_t rows, int64_t cols, float eps);
+/* gated_residual_bf16<gate_t> (native-bf16.patch:79-91): y = bf16(h + b*g). gate_type F32|BF16,
+ * gs row stride of gate (0 = broadcast). */
+WAMX_API wamx_status wamx_op_gated_residual_bf16(wamx_backend_t be, const void * h, const void * b,
+                                                 const void * g, int32_t gate_type, int64_t gs,
+                                                 void * y, int64_t rows, int64_t cols);
+/* gated_residual_f32 (p7-fusions.patch:122-134): y = r + b*g, no FMA. */
+WAMX_API wamx_status wamx_op_gated_residual_f32(wamx_backend_t be, const float * r, const float * b,
+                                                const float * g, int64_t gs, float * y,
+                                                int64_t rows, int64_t cols);
+/* bias_gelu_bf16_kernel (native-bf16.patch:507-514): y = bf16(gelu_tanh(x + bias[i % width])). */
+WAMX_API wamx_status wamx_op_bias_gelu_bf16(wamx_backend_t be, const void * x, const void * bias,
+                                            void * y, int64_t n, int64_t width);
+/* ROPE NORMAL on f32 [ne={head_dim, heads, tokens}] contiguous, rotating the first n_dims. */
+WAMX_API wamx_status wamx_op_rope_f32(wamx_backend_t be, const float * x, const int32_t * pos,
+                                      float * y, int64_t head_dim, int64_t heads, int64_t tokens,
+                                      int n_dims, float freq_base);
+/* Fused QK RMSNorm + RoPE + bf16 + head-major write (WAMX_OP_QK_NORM_ROPE). */
+WAMX_API wamx_status wamx_op_qk_norm_rope(wamx_backend_t be, const void * x, int64_t ldx,
+                                          const void * w, void * dst, int64_t heads, int64_t head_dim,
+                                          int64_t tokens, int64_t dst_tokens, int64_t tok0,
+                                          int rope_mode, const int32_t * pos0, const int32_t * pos1,
+                                          const int32_t * pos2, float eps, float freq_base);
+/* Joint attention (WAMX_OP_JOINT_ATTN) on device pointers.  q [H][Tq][dh], k_a [H][na][dh],
+ * vt_a [H][dh][na], k_b [H][nb][dh], vt_b [H][dh][nb], out bf16 [Tq][H*dh]. */
+WAMX_API wamx_status wamx_op_joint_attn(wamx_backend_t be, const void * q, const void * k_a,
+                                        const void * vt_a, int64_t na, const void * k_b,
+                                        const void * vt_b, int64_t nb, int64_t na_split,
+                                        void * out, int64_t heads, int64_t head_dim, int64_t tq,
+                                        float scale);
+/* SOFT_MAX_EXT without mask: y[r][:] = softmax(scale * x[r][:]) over ne0=cols, f32. */
+WAMX_API wamx_status wamx_op_soft_max_f32(wamx_backend_t be, const float * x, float * y,
+                                          int64_t rows, int64_t cols, float scale);
+
+/* Fill a device array with a seeded synthetic normal sample: splitmix64 on
+ * (seed, index) -> Box-Muller -> mean + std*z, stored as type (F32 or BF16, RNE). */
+WAMX_API wamx_status wamx_fill_normal(wamx_backend_t be, void * dst, int32_t type, int64_t n,
+                                      uint64_t seed, float mean, float std);
+
+/* Device memory helpers for callers without another allocator. */
+WAMX_API void *      wamx_device_malloc(wamx_backend_t be, size_t size);
+WAMX_API void        wamx_device_free(wamx_backend_t be, void * p);
+WAMX_API wamx_status wamx_memcpy_h2d(wamx_backend_t be, void * dst, const void * src, size_t size);
+WAMX_API wamx_status wamx_memcpy_d2h(wamx_backend_t be, void * dst, const void * src, size_t size);
+
+/* HIP event timing on the backend's stream. */
+typedef struct wamx_timer * wamx_timer_t;
+WAMX_API wamx_timer_t wamx_timer_new(wamx_backend_t be);
+WAMX_API void         wamx_timer_start(wamx_timer_t t);
+WAMX_API float        wamx_timer_stop_ms(wamx_timer_t t);   /* synchronises */
+WAMX_API void         wamx_timer_free(wamx_timer_t t);
+
+/* ---------------------------------------------------------------------------
+ * Synthetic GWP-0.5-shaped MoT driver.
+ * ------------------------------------------------------------------------- */
+typedef struct wamx_gwp_config {
+    int32_t n_layers;        /* gwp05.n_layers */
+    int32_t hidden;          /* visual expert width d = n_heads * head_dim */
+    int32_t n_heads;
+    int32_t head_dim;
+    int32_t ffn_dim;         /* visual expert FFN */
+    int32_t action_hidden;   /* action expert width */
+    int32_t action_ffn_dim;
+    int32_t action_chunk;    /* T */
+    int32_t action_dim;      /* max_action_dim == max_state_dim */
+    int32_t grid_h;          /* visual token grid (n_img = grid_h * grid_w) */
+    int32_t grid_w;
+    int32_t n_lang;          /* prompt tokens */
+    int32_t t5_hidden;       /* prompt embedding width */
+    int32_t z_dim;           /* latent channels (patch embedding input) */
+    int32_t num_steps;       /* flow-matching steps */
+    int32_t enc_hidden;      /* action/state encoder and decoder MLP width (128) */
+    float   shift;           /* flow-matching shift */
+    float   eps;             /* norm eps */
+} wamx_gwp_config;
+
+typedef struct wamx_gwp_model * wamx_gwp_t;
+
+/* Phase timings of the last predict, milliseconds (hipEvent on the stream). */
+typedef struct wamx_gwp_timing {
+    float prompt_ms;
+    float prefix_ms;
+    float denoise_ms;
+    float total_ms;
+} wamx_gwp_timing;
+
+WAMX_API wamx_gwp_config wamx_gwp_default_config(void);
+WAMX_API wamx_gwp_t  wamx_gwp_create(wamx_backend_t be, const wamx_gwp_config * cfg);
+WAMX_API void        wamx_gwp_free(wamx_gwp_t m);
+WAMX_API int         wamx_gwp_n_weights(wamx_gwp_t m);
+WAMX_API const char * wamx_gwp_weight_name(wamx_gwp_t m, int i);
+WAMX_API wamx_tensor * wamx_gwp_weight(wamx_gwp_t m, const char * name);
+WAMX_API uint64_t    wamx_gwp_param_count(wamx_gwp_t m);
+/* Random-init every weight on the device: bf16 matrices ~N(0, wstd), biases
+ * ~N(0, 0.02), norm weights 1 + N(0, 0.02), scale/shift tables ~N(0, 0.1). */
+WAMX_API wamx_status wamx_gwp_init_synthetic(wamx_gwp_t m, uint64_t seed, float wstd);
+/* Inputs: state f32 [action_dim], latent f32 [z_dim][2*grid_h][2*grid_w] (CHW),
+ * prompt f32 [n_lang][t5_hidden], noise f32 [action_chunk][action_dim]. */
+WAMX_API wamx_status wamx_gwp_set_inputs(wamx_gwp_t m, const float * state, const float * latent,
+                                         const float * prompt, const float * noise);
+/* Run the three graphs (prompt projection, prefix, unrolled denoise). */
+WAMX_API wamx_status wamx_gwp_predict(wamx_gwp_t m, wamx_gwp_timing * timing);
+WAMX_API wamx_status wamx_gwp_run_prompt(wamx_gwp_t m);
+WAMX_API wamx_status wamx_gwp_run_prefix(wamx_gwp_t m);
+WAMX_API wamx_status wamx_gwp_run_denoise(wamx_gwp_t m);
+/* Final action chunk (bf16 state widened to f32) [action_chunk][action_dim]. */
+WAMX_API wamx_status wamx_gwp_get_action(wamx_gwp_t m, float * out);
+/* Prefix K/V cache of one layer as stored: K bf16 [H][P][dh], V bf16 [H][dh][P]. */
+WAMX_API wamx_tensor * wamx_gwp_prefix_key(wamx_gwp_t m, int layer);
+WAMX_API wamx_tensor * wamx_gwp_prefix_value(wamx_gwp_t m, int layer);
+WAMX_API int         wamx_gwp_graph_nodes(wamx_gwp_t m, int which);  /* 0 prompt, 1 prefix, 2 denoise */
+
+/* Last error message of the calling thread ("" when none). */
+WAMX_API const char * wamx_last_error(void);
+
+/* ggml_op numbering correspondence: wamx_ggml_op_map[i] is the wamx_op for the
+ * i-th name in wamx_ggml_op_names (ggml's GGML_OP_* names).  Numeric ggml
+ * values are not reproduced because b9866 headers are not available. */
+WAMX_API int          wamx_ggml_op_count(void);
+WAMX_API const char * wamx_ggml_op_name(int i);
+WAMX_API int32_t      wamx_ggml_op_to_wamx(int i);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WAMX_WAMX_H */

@@ -1,0 +1,252 @@
+"""ctypes wrapper of oracle/liboracle.so — the CPU restatement of the
+reference arithmetic (test infrastructure: imported only by tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg).
+
+Arrays are numpy; bf16 arrays are uint16 bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+F32, BF16 = 0, 30
+EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_GATED, EPI_BIAS_RESIDUAL = 0, 1, 2, 3, 4
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+    lib = C.CDLL(str(LIB_PATH))
+    vp, i64, f32 = C.c_void_p, C.c_int64, C.c_float
+    sig = {
+        "orc_f32_to_bf16": (C.c_uint16, [f32]),
+        "orc_bf16_to_f32": (f32, [C.c_uint16]),
+        "orc_num_threads": (C.c_int, []),
+        "orc_gelu_tanh": (f32, [f32]),
+        "orc_gelu_erf": (f32, [f32]),
+        "orc_mul_mat": (None, [vp, i64, vp, C.c_int, i64, vp, C.c_int, i64, i64, i64, i64]),
+        "orc_linear": (None, [vp, vp, C.c_int, vp, C.c_int, vp, vp, vp, i64, i64, i64]),
+        "orc_norm_mod_bf16": (None, [vp, i64, vp, vp, i64, vp, i64, i64, f32]),
+        "orc_layer_norm_bf16": (None, [vp, i64, vp, vp, vp, i64, i64, f32]),
+        "orc_rms_norm_bf16_f32": (None, [vp, i64, vp, vp, i64, i64, f32]),
+        "orc_norm_mod_f32": (None, [vp, i64, vp, vp, i64, vp, i64, i64, f32]),
+        "orc_gated_residual_bf16": (None, [vp, vp, vp, C.c_int, i64, vp, i64, i64]),
+        "orc_gated_residual_f32": (None, [vp, vp, vp, i64, vp, i64, i64]),
+        "orc_bias_gelu_bf16": (None, [vp, vp, vp, i64, i64]),
+        "orc_rope_f32": (None, [vp, vp, vp, i64, i64, i64, C.c_int, f32]),
+        "orc_qk_norm_rope": (None, [vp, i64, vp, vp, i64, i64, i64, i64, i64, C.c_int, vp, vp, vp, f32, f32]),
+        "orc_softmax_f32": (None, [vp, vp, i64, i64, f32]),
+        "orc_attention": (None, [vp, vp, vp, i64, i64, vp, vp, i64, i64, i64, vp, i64, i64, i64, f32]),
+        "orc_modulation": (None, [vp, vp, vp, i64, i64]),
+        "orc_flow_schedule": (None, [C.c_int, f32, vp, vp]),
+        "orc_timestep_embedding": (None, [f32, i64, vp]),
+        "orc_fill_normal": (None, [vp, C.c_int, i64, C.c_uint64, f32, f32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def num_threads() -> int:
+    return int(load().orc_num_threads())
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    f = load().orc_f32_to_bf16
+    flat, of = x.reshape(-1), out.reshape(-1)
+    for i in range(flat.size):
+        of[i] = f(float(flat[i]))
+    return out
+
+
+def gelu_tanh(x: float) -> float:
+    return float(load().orc_gelu_tanh(x))
+
+
+def gelu_erf(x: float) -> float:
+    return float(load().orc_gelu_erf(x))
+
+
+def mul_mat(w_bf16, x, y_type=F32) -> np.ndarray:
+    """w bf16 [M][K], x f32|bf16(uint16) [N][K] -> y [N][M] (f32 or bf16 bits)."""
+    w = _c(w_bf16, np.uint16)
+    M, K = w.shape
+    x_type = BF16 if x.dtype == np.uint16 else F32
+    x = _c(x, np.uint16 if x_type == BF16 else np.float32)
+    N = x.shape[0]
+    y = np.empty((N, M), np.float32 if y_type == F32 else np.uint16)
+    load().orc_mul_mat(_p(w), K, _p(x), x_type, K, _p(y), y_type, M, M, N, K)
+    return y
+
+
+def linear(w, x, bias=None, epi=EPI_NONE, residual=None, gate=None) -> np.ndarray:
+    w = _c(w, np.uint16)
+    M, K = w.shape
+    x_type = BF16 if x.dtype == np.uint16 else F32
+    x = _c(x, np.uint16 if x_type == BF16 else np.float32)
+    N = x.shape[0]
+    b = None if bias is None else _c(bias, np.uint16)
+    r = None if residual is None else _c(residual, np.uint16)
+    g = None if gate is None else _c(gate, np.float32)
+    y = np.empty((N, M), np.uint16)
+    load().orc_linear(_p(w), _p(x), x_type, _p(b), epi, _p(r), _p(g), _p(y), M, N, K)
+    return y
+
+
+def norm_mod_bf16(x, scale, shift, eps) -> np.ndarray:
+    x = _c(x, np.uint16)
+    rows, cols = x.shape
+    scale, shift = _c(scale, np.float32), _c(shift, np.float32)
+    ss = 0 if scale.ndim == 1 else cols
+    y = np.empty_like(x)
+    load().orc_norm_mod_bf16(_p(x), cols, _p(scale), _p(shift), ss, _p(y), rows, cols, eps)
+    return y
+
+
+def layer_norm_bf16(x, w, b, eps) -> np.ndarray:
+    x = _c(x, np.uint16)
+    rows, cols = x.shape
+    y = np.empty_like(x)
+    load().orc_layer_norm_bf16(_p(x), cols, _p(_c(w, np.uint16)), _p(_c(b, np.uint16)), _p(y), rows, cols, eps)
+    return y
+
+
+def rms_norm_bf16_f32(x, w, eps) -> np.ndarray:
+    x = _c(x, np.uint16)
+    rows, cols = x.shape
+    y = np.empty((rows, cols), np.float32)
+    load().orc_rms_norm_bf16_f32(_p(x), cols, _p(_c(w, np.uint16)), _p(y), rows, cols, eps)
+    return y
+
+
+def norm_mod_f32(x, scale, shift, eps) -> np.ndarray:
+    x = _c(x, np.float32)
+    rows, cols = x.shape
+    scale, shift = _c(scale, np.float32), _c(shift, np.float32)
+    ss = 0 if scale.ndim == 1 else cols
+    y = np.empty_like(x)
+    load().orc_norm_mod_f32(_p(x), cols, _p(scale), _p(shift), ss, _p(y), rows, cols, eps)
+    return y
+
+
+def gated_residual_bf16(h, b, g) -> np.ndarray:
+    h, b = _c(h, np.uint16), _c(b, np.uint16)
+    rows, cols = h.shape
+    g_type = BF16 if g.dtype == np.uint16 else F32
+    g = _c(g, np.uint16 if g_type == BF16 else np.float32)
+    gs = 0 if g.ndim == 1 else cols
+    y = np.empty_like(h)
+    load().orc_gated_residual_bf16(_p(h), _p(b), _p(g), g_type, gs, _p(y), rows, cols)
+    return y
+
+
+def gated_residual_f32(r, b, g) -> np.ndarray:
+    r, b, g = _c(r, np.float32), _c(b, np.float32), _c(g, np.float32)
+    rows, cols = r.shape
+    gs = 0 if g.ndim == 1 else cols
+    y = np.empty_like(r)
+    load().orc_gated_residual_f32(_p(r), _p(b), _p(g), gs, _p(y), rows, cols)
+    return y
+
+
+def bias_gelu_bf16(x, bias) -> np.ndarray:
+    x, bias = _c(x, np.uint16), _c(bias, np.uint16)
+    y = np.empty_like(x)
+    load().orc_bias_gelu_bf16(_p(x), _p(bias), _p(y), x.size, bias.size)
+    return y
+
+
+def rope_f32(x, pos, n_dims, base=10000.0) -> np.ndarray:
+    """x f32 [tokens][heads][head_dim]."""
+    x = _c(x, np.float32)
+    T, H, D = x.shape
+    y = np.empty_like(x)
+    load().orc_rope_f32(_p(x), _p(_c(pos, np.int32)), _p(y), D, H, T, n_dims, base)
+    return y
+
+
+def qk_norm_rope(x, w, heads, head_dim, rope_mode, pos0=None, pos1=None, pos2=None, eps=1e-6, base=10000.0,
+                 dst=None, tok0=0) -> np.ndarray:
+    """x bf16 [T][heads*head_dim] -> dst bf16 [heads][dst_tokens][head_dim]."""
+    x = _c(x, np.uint16)
+    T = x.shape[0]
+    if dst is None:
+        dst = np.zeros((heads, T, head_dim), np.uint16)
+    ps = [None if p is None else _c(p, np.int32) for p in (pos0, pos1, pos2)]
+    load().orc_qk_norm_rope(_p(x), x.shape[1], _p(_c(w, np.uint16)), _p(dst), heads, head_dim, T, dst.shape[1], tok0,
+                            rope_mode, _p(ps[0]), _p(ps[1]), _p(ps[2]), eps, base)
+    return dst
+
+
+def softmax_f32(x, scale=1.0) -> np.ndarray:
+    x = _c(x, np.float32)
+    rows, cols = x.reshape(-1, x.shape[-1]).shape
+    y = np.empty_like(x)
+    load().orc_softmax_f32(_p(x), _p(y), rows, cols, scale)
+    return y
+
+
+def attention(q, k_a, vt_a, k_b=None, vt_b=None, na_split=0, scale=None) -> np.ndarray:
+    """q [H][tq][dh], k_a [H][na][dh], vt_a [H][dh][ld_a] (bf16) -> out bf16 [tq][H*dh]."""
+    q, k_a, vt_a = _c(q, np.uint16), _c(k_a, np.uint16), _c(vt_a, np.uint16)
+    H, tq, dh = q.shape
+    na = k_a.shape[1]
+    nb = 0 if k_b is None else k_b.shape[1]
+    kb = None if k_b is None else _c(k_b, np.uint16)
+    vb = None if vt_b is None else _c(vt_b, np.uint16)
+    scale = 1.0 / np.sqrt(dh) if scale is None else scale
+    out = np.empty((tq, H * dh), np.uint16)
+    load().orc_attention(_p(q), _p(k_a), _p(vt_a), na, vt_a.shape[2], _p(kb), _p(vb), nb,
+                         0 if vb is None else vb.shape[2], na_split, _p(out), H, dh, tq, float(scale))
+    return out
+
+
+def modulation(mod, tables) -> np.ndarray:
+    mod, tables = _c(mod, np.uint16), _c(tables, np.uint16)
+    per = mod.size
+    layers = tables.size // per
+    out = np.empty((layers, per), np.float32)
+    load().orc_modulation(_p(mod), _p(tables), _p(out), per, layers)
+    return out
+
+
+def flow_schedule(steps: int, shift: float):
+    t = np.empty(steps, np.float32)
+    s = np.empty(steps + 1, np.float32)
+    load().orc_flow_schedule(steps, shift, _p(t), _p(s))
+    return t, s
+
+
+def timestep_embedding(t: float, dim: int = 256) -> np.ndarray:
+    out = np.empty(dim, np.float32)
+    load().orc_timestep_embedding(t, dim, _p(out))
+    return out
+
+
+def fill_normal(n: int, seed: int, mean=0.0, std=1.0, dtype=F32) -> np.ndarray:
+    out = np.empty(n, np.float32 if dtype == F32 else np.uint16)
+    load().orc_fill_normal(_p(out), dtype, n, seed & (2**64 - 1), mean, std)
+    return out

@@ -1,0 +1,147 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol the public
+header declares, and the host-side IR (constructors, views, graph ordering,
+supports_op) behaves like the ggml calls it restates.  No kernel runs here."""
+from __future__ import annotations
+
+import ctypes as C
+
+import pytest
+
+
+def test_exports_every_declared_symbol(wx):
+    lib = wx.load()
+    names = wx.declared_symbols()
+    assert len(names) > 100
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_no_device_needed_to_load(wx):
+    assert wx.load().wamx_get_device_count() >= 0
+
+
+@pytest.fixture
+def ctx(wx):
+    lib = wx.load()
+    c = lib.wamx_init(4096)
+    yield c
+    lib.wamx_free(c)
+
+
+def shape(t):
+    return tuple(t.contents.ne)
+
+
+def strides(t):
+    return tuple(t.contents.nb)
+
+
+def test_mul_mat_shape_and_types(wx, ctx):
+    lib = wx.load()
+    w = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 3072, 9216)   # ne={K, M}
+    x = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 3072, 48)      # ne={K, N}
+    y = lib.wamx_mul_mat(ctx, w, x)
+    assert shape(y) == (9216, 48, 1, 1) and y.contents.type == wx.TYPE_F32
+    yb = lib.wamx_mul_mat_out_type(ctx, w, x, wx.TYPE_BF16)
+    assert yb.contents.type == wx.TYPE_BF16 and yb.contents.op == wx.OP["MUL_MAT"]
+    lib.wamx_mul_mat_set_prec(y, 10)
+    assert y.contents.op_params[0] == 10
+    bad = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 100, 48)
+    assert not lib.wamx_mul_mat(ctx, w, bad)
+    assert "mul_mat" in wx.last_error()
+    # batched broadcast over dim 2 (attention: K [128, n, H] x Q [128, T, H])
+    k = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 128, 3121, 24)
+    q = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 128, 48, 24)
+    assert shape(lib.wamx_mul_mat(ctx, k, q)) == (3121, 48, 24, 1)
+
+
+def test_permute_transpose_views(wx, ctx):
+    lib = wx.load()
+    t = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 128, 24, 48)  # [dh, H, T]
+    p = lib.wamx_permute(ctx, t, 0, 2, 1, 3)                    # -> [dh, T, H]
+    assert shape(p) == (128, 48, 24, 1)
+    assert strides(p)[:3] == (2, 2 * 128 * 24, 2 * 128)
+    assert not lib.wamx_is_contiguous(p)
+    c = lib.wamx_cont(ctx, p)
+    assert lib.wamx_is_contiguous(c) and shape(c) == shape(p)
+    v = lib.wamx_permute(ctx, t, 1, 2, 0, 3)                    # V layout [T, dh, H]
+    assert shape(v) == (48, 128, 24, 1)
+    tr = lib.wamx_transpose(ctx, lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 5, 7))
+    assert shape(tr) == (7, 5, 1, 1) and strides(tr)[:2] == (20, 4)
+    base = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 9216, 48)
+    view = lib.wamx_view_2d(ctx, base, 3072, 48, base.contents.nb[1], 3072 * 2)
+    assert shape(view) == (3072, 48, 1, 1) and view.contents.view_offs == 6144
+    assert C.addressof(view.contents.view_src.contents) == C.addressof(base.contents)
+    r = lib.wamx_reshape_3d(ctx, lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 3072, 48), 128, 24, 48)
+    assert shape(r) == (128, 24, 48, 1)
+    assert not lib.wamx_reshape_2d(ctx, p, 128 * 48, 24)  # non-contiguous source
+
+
+def test_concat_and_fused_constructors(wx, ctx):
+    lib = wx.load()
+    a = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 128, 1, 24)
+    b = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 128, 48, 24)
+    assert shape(lib.wamx_concat(ctx, a, b, 1)) == (128, 49, 24, 1)
+    h = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 3072, 48)
+    g = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 3072, 1)
+    gr = lib.wamx_gated_residual_bf16(ctx, h, h, g)
+    assert gr.contents.op == wx.OP["ADD"] and bool(gr.contents.src[2])
+    bias = lib.wamx_new_tensor_1d(ctx, wx.TYPE_BF16, 3072)
+    bg = lib.wamx_bias_gelu_bf16(ctx, h, bias)
+    assert bg.contents.op == wx.OP["UNARY"] and bg.contents.op_params[0] == 0
+    sc = lib.wamx_new_tensor_1d(ctx, wx.TYPE_F32, 3072)
+    nm = lib.wamx_norm_modulation_bf16(ctx, h, sc, sc, 1e-6)
+    assert nm.contents.op == wx.OP["NORM"] and nm.contents.type == wx.TYPE_BF16
+    rn = lib.wamx_rms_norm_bf16_f32(ctx, h, bias, 1e-6)
+    assert rn.contents.op == wx.OP["RMS_NORM"] and rn.contents.type == wx.TYPE_F32
+    w = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 3072, 14336)
+    lin = lib.wamx_linear(ctx, w, h, lib.wamx_new_tensor_1d(ctx, wx.TYPE_BF16, 14336), wx.EPI_BIAS_GELU, None, None)
+    assert shape(lin) == (14336, 48, 1, 1) and lin.contents.op == wx.OP["LINEAR"]
+    assert not lib.wamx_linear(ctx, w, h, bias, wx.EPI_BIAS, None, None)  # bias length must be M
+
+
+def test_graph_order_and_uid(wx, ctx):
+    lib = wx.load()
+    x = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 16, 4)
+    y = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 16, 4)
+    a = lib.wamx_add(ctx, x, y)
+    m = lib.wamx_mul(ctx, a, x)
+    s = lib.wamx_scale(ctx, m, 2.0)
+    g = lib.wamx_new_graph(ctx, 64)
+    lib.wamx_build_forward_expand(g, s)
+    assert lib.wamx_graph_n_nodes(g) == 3
+    ops = [lib.wamx_graph_node(g, i).contents.op for i in range(3)]
+    assert ops == [wx.OP["ADD"], wx.OP["MUL"], wx.OP["SCALE"]]
+    assert C.addressof(lib.wamx_graph_node(g, -1).contents) == C.addressof(s.contents)
+    lib.wamx_build_forward_expand(g, s)  # idempotent
+    assert lib.wamx_graph_n_nodes(g) == 3
+    assert lib.wamx_graph_uid(g) == 0
+    lib.wamx_graph_assign_uid(g)
+    uid = lib.wamx_graph_uid(g)
+    lib.wamx_graph_assign_uid(g)
+    assert uid != 0 and lib.wamx_graph_uid(g) == uid
+    g2 = lib.wamx_new_graph(ctx, 64)
+    lib.wamx_graph_assign_uid(g2)
+    assert lib.wamx_graph_uid(g2) != uid
+
+
+def test_supports_op(wx, ctx):
+    lib = wx.load()
+    x = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 64, 8)
+    assert lib.wamx_backend_supports_op(None, lib.wamx_soft_max_ext(ctx, x, None, 0.1, 0.0))
+    assert lib.wamx_backend_supports_op(None, lib.wamx_norm(ctx, x, 1e-6))
+    pos = lib.wamx_new_tensor_1d(ctx, wx.TYPE_I32, 8)
+    r = lib.wamx_rope_ext(ctx, lib.wamx_reshape_3d(ctx, x, 16, 4, 8), pos, None, 16, 0, 0, 10000.0, 1.0, 0.0,
+                          1.0, 32.0, 1.0)
+    assert r and lib.wamx_backend_supports_op(None, r)
+    # NEOX-mode rope is not built
+    assert not lib.wamx_rope_ext(ctx, lib.wamx_reshape_3d(ctx, x, 16, 4, 8), pos, None, 16, 2, 0, 10000.0, 1.0,
+                                 0.0, 1.0, 32.0, 1.0)
+
+
+def test_ggml_op_map(wx):
+    lib = wx.load()
+    n = lib.wamx_ggml_op_count()
+    names = {lib.wamx_ggml_op_name(i).decode(): lib.wamx_ggml_op_to_wamx(i) for i in range(n)}
+    for op in ("MUL_MAT", "NORM", "RMS_NORM", "ROPE", "SOFT_MAX", "ADD", "UNARY", "CONCAT", "CPY", "CONT"):
+        assert names[f"GGML_OP_{op}"] == wx.OP[op]

@@ -1,0 +1,258 @@
+"""Per-op parity of the HIP kernels (through the C ABI) against the CPU oracle
+on identical seeded inputs.
+
+Bar: bf16 inputs with fp32 accumulation -> max-rel <= 1e-2 and cosine >=
+0.9999 per op (the infinity-norm relative error max|got-ref|/max|ref|).
+Integer known-answer GEMMs are exact in fp32 and must match bit for bit.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_parity, cosine, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16(x):
+    import wamx
+    return wamx.f32_to_bf16(np.asarray(x, np.float32))
+
+
+def f32(h):
+    import wamx
+    return wamx.bf16_to_f32(h)
+
+
+def dev(be, a):
+    return be.array(np.ascontiguousarray(a))
+
+
+def gpu_mul_mat(wx, be, w, x, y_type):
+    M, K = w.shape
+    N = x.shape[0]
+    dw, dx = dev(be, w), dev(be, x)
+    es = 4 if y_type == wx.TYPE_F32 else 2
+    dy = be.empty(N * M * es)
+    x_type = wx.TYPE_BF16 if x.dtype == np.uint16 else wx.TYPE_F32
+    wx.check(be.lib.wamx_op_mul_mat(be.ptr, dw.ptr, K, dx.ptr, x_type, K, dy.ptr, y_type, M, M, N, K), "mul_mat")
+    return dy.download(np.float32 if y_type == wx.TYPE_F32 else np.uint16, (N, M))
+
+
+# --- GEMM -------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K", [(64, 48, 256), (96, 1, 136), (200, 64, 3072), (3072, 48, 3072),
+                                   (128, 65, 64), (300, 300, 520), (1000, 129, 72), (77, 33, 31)])
+@pytest.mark.parametrize("xt", ["f32", "bf16"])
+def test_mul_mat_integer_kat_exact(wx, be, M, N, K, xt):
+    print(f"mul_mat KAT M={M} N={N} K={K} x={xt}", flush=True)
+    rng = np.random.default_rng(M + 7 * N + 13 * K)
+    w = rng.integers(-4, 5, (M, K))
+    x = rng.integers(-4, 5, (N, K)).astype(np.float32)
+    xin = x if xt == "f32" else bf16(x)
+    ref = x.astype(np.float64) @ w.T.astype(np.float64)
+    got = gpu_mul_mat(wx, be, bf16(w), xin, wx.TYPE_F32)
+    assert np.array_equal(got.astype(np.float64), ref)
+    got_b = gpu_mul_mat(wx, be, bf16(w), xin, wx.TYPE_BF16)
+    assert np.array_equal(got_b, bf16(ref))
+
+
+def test_mul_mat_config1_single_gemm(wx, be, orc):
+    """W bf16 [3072 out x 3072 in] ~N(0,0.02), X f32 [256 x 3072] ~N(0,1), Y f32."""
+    print("mul_mat 3072x3072x256", flush=True)
+    w = orc.fill_normal(3072 * 3072, 0x5EED0000 + 1, 0.0, 0.02, orc.BF16).reshape(3072, 3072)
+    x = orc.fill_normal(256 * 3072, 0x5EED0000 + 2).reshape(256, 3072)
+    ref = orc.mul_mat(w, x)
+    got = gpu_mul_mat(wx, be, w, x, wx.TYPE_F32)
+    assert_parity(got, ref, what="mul_mat config 1")
+    assert rel_err(got, ref) < 1e-5  # fp32 accumulation of exact products
+
+
+@pytest.mark.parametrize("N", [48, 1, 384, 2048])
+def test_linear_epilogues(wx, be, orc, N):
+    print(f"linear epilogues N={N}", flush=True)
+    rng = np.random.default_rng(N)
+    M, K = (1536, 3072) if N <= 384 else (768, 1024)
+    w = bf16(rng.standard_normal((M, K)) * 0.02)
+    x = bf16(rng.standard_normal((N, K)))
+    b = bf16(rng.standard_normal(M) * 0.02)
+    h = bf16(rng.standard_normal((N, M)))
+    g = (rng.standard_normal(M) * 0.1).astype(np.float32)
+    dw, dx, db, dh, dg = dev(be, w), dev(be, x), dev(be, b), dev(be, h), dev(be, g)
+    dy = be.empty(N * M * 2)
+    for epi in (wx.EPI_NONE, wx.EPI_BIAS, wx.EPI_BIAS_GELU, wx.EPI_BIAS_GATED, wx.EPI_BIAS_RESIDUAL):
+        wx.check(be.lib.wamx_op_linear(be.ptr, dw.ptr, dx.ptr, wx.TYPE_BF16, db.ptr, epi, dh.ptr, dg.ptr, dy.ptr,
+                                       M, N, K), "linear")
+        got = dy.download(np.uint16, (N, M))
+        ref = orc.linear(w, x, b, epi, h, g)
+        assert_parity(f32(got), f32(ref), what=f"linear epi={epi} N={N}")
+        # at most one bf16 ulp apart almost everywhere (fp32 vs exact accumulation)
+        ulps = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+        assert np.mean(ulps > 1) < 1e-3, f"epi={epi}: {np.mean(ulps > 1)} of outputs differ by >1 ulp"
+
+
+def test_ffn_shapes_full_size(wx, be, orc):
+    """FFN GEMM shapes of the 2048-token block: up [14336 x 3072] + bias + GELU."""
+    print("ffn up 14336x3072 @ 2048 tokens", flush=True)
+    M, K, N = 14336, 3072, 2048
+    w = orc.fill_normal(M * K, 11, 0.0, 0.02, orc.BF16).reshape(M, K)
+    x = orc.fill_normal(N * K, 12, 0.0, 1.0, orc.BF16).reshape(N, K)
+    b = orc.fill_normal(M, 13, 0.0, 0.02, orc.BF16)
+    dw, dx, db = dev(be, w), dev(be, x), dev(be, b)
+    dy = be.empty(N * M * 2)
+    wx.check(be.lib.wamx_op_linear(be.ptr, dw.ptr, dx.ptr, wx.TYPE_BF16, db.ptr, wx.EPI_BIAS_GELU, None, None,
+                                   dy.ptr, M, N, K), "linear")
+    got = f32(dy.download(np.uint16, (N, M)))
+    ref = f32(orc.linear(w, x, b, orc.EPI_BIAS_GELU))
+    assert_parity(got, ref, what="ffn up")
+
+
+# --- norms / residual / gelu ----------------------------------------------------------
+@pytest.mark.parametrize("rows,cols", [(48, 3072), (1, 3072), (2048, 3072), (5, 256), (3, 1000)])
+def test_norm_modulation_bf16(wx, be, orc, rows, cols):
+    print(f"norm_mod bf16 {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows * cols)
+    x = bf16(rng.standard_normal((rows, cols)) * 2 + 0.3)
+    sc = (rng.standard_normal(cols) * 0.1).astype(np.float32)
+    sh = (rng.standard_normal(cols) * 0.1).astype(np.float32)
+    dx, ds, dh = dev(be, x), dev(be, sc), dev(be, sh)
+    dy = be.empty(rows * cols * 2)
+    wx.check(be.lib.wamx_op_norm_modulation_bf16(be.ptr, dx.ptr, cols, ds.ptr, dh.ptr, 0, dy.ptr, rows, cols, 1e-6))
+    got = dy.download(np.uint16, (rows, cols))
+    ref = orc.norm_mod_bf16(x, sc, sh, 1e-6)
+    assert_parity(f32(got), f32(ref), what="norm_mod_bf16")
+    assert np.mean(got != ref) < 0.02
+    # affine LayerNorm with bf16 weight/bias
+    w = bf16(1 + rng.standard_normal(cols) * 0.02)
+    b = bf16(rng.standard_normal(cols) * 0.02)
+    dw, db = dev(be, w), dev(be, b)
+    wx.check(be.lib.wamx_op_layer_norm_bf16(be.ptr, dx.ptr, cols, dw.ptr, db.ptr, dy.ptr, rows, cols, 1e-6))
+    assert_parity(f32(dy.download(np.uint16, (rows, cols))), f32(orc.layer_norm_bf16(x, w, b, 1e-6)),
+                  what="layer_norm_bf16")
+    # RMSNorm bf16 -> f32
+    dyf = be.empty(rows * cols * 4)
+    wx.check(be.lib.wamx_op_rms_norm_bf16_f32(be.ptr, dx.ptr, cols, dw.ptr, dyf.ptr, rows, cols, 1e-6))
+    got_r = dyf.download(np.float32, (rows, cols))
+    ref_r = orc.rms_norm_bf16_f32(x, w, 1e-6)
+    assert rel_err(got_r, ref_r) < 1e-5
+
+
+def test_norm_modulation_f32_and_gated_f32(wx, be, orc, rng):
+    rows, cols = 2048, 3072
+    print("norm_mod f32 2048x3072", flush=True)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    sc = (rng.standard_normal(cols) * 0.1).astype(np.float32)
+    sh = (rng.standard_normal(cols) * 0.1).astype(np.float32)
+    dx, ds, dh = dev(be, x), dev(be, sc), dev(be, sh)
+    dy = be.empty(rows * cols * 4)
+    wx.check(be.lib.wamx_op_norm_modulation_f32(be.ptr, dx.ptr, cols, ds.ptr, dh.ptr, 0, dy.ptr, rows, cols, 1e-6))
+    assert rel_err(dy.download(np.float32, (rows, cols)), orc.norm_mod_f32(x, sc, sh, 1e-6)) < 1e-4
+    b = rng.standard_normal((rows, cols)).astype(np.float32)
+    g = (rng.standard_normal(cols) * 0.1).astype(np.float32)
+    db, dg = dev(be, b), dev(be, g)
+    wx.check(be.lib.wamx_op_gated_residual_f32(be.ptr, dx.ptr, db.ptr, dg.ptr, 0, dy.ptr, rows, cols))
+    # unfused f32 product then sum: bit-exact against the oracle
+    assert np.array_equal(dy.download(np.float32, (rows, cols)), orc.gated_residual_f32(x, b, g))
+
+
+def test_gated_residual_and_bias_gelu_bf16(wx, be, orc, rng):
+    rows, cols = 48, 3072
+    h = bf16(rng.standard_normal((rows, cols)))
+    b = bf16(rng.standard_normal((rows, cols)))
+    g = (rng.standard_normal(cols) * 0.1).astype(np.float32)
+    dh, db, dg = dev(be, h), dev(be, b), dev(be, g)
+    dy = be.empty(rows * cols * 2)
+    wx.check(be.lib.wamx_op_gated_residual_bf16(be.ptr, dh.ptr, db.ptr, dg.ptr, wx.TYPE_F32, 0, dy.ptr, rows, cols))
+    assert np.array_equal(dy.download(np.uint16, (rows, cols)), orc.gated_residual_bf16(h, b, g))
+    gb = bf16(rng.standard_normal((rows, cols)) * 0.1)
+    dgb = dev(be, gb)
+    wx.check(be.lib.wamx_op_gated_residual_bf16(be.ptr, dh.ptr, db.ptr, dgb.ptr, wx.TYPE_BF16, cols, dy.ptr, rows,
+                                                cols))
+    assert np.array_equal(dy.download(np.uint16, (rows, cols)), orc.gated_residual_bf16(h, b, gb))
+    x = bf16(rng.standard_normal((rows, 14336)))
+    bias = bf16(rng.standard_normal(14336) * 0.02)
+    dx, dbias = dev(be, x), dev(be, bias)
+    dz = be.empty(x.nbytes)
+    wx.check(be.lib.wamx_op_bias_gelu_bf16(be.ptr, dx.ptr, dbias.ptr, dz.ptr, x.size, 14336))
+    got = dz.download(np.uint16, x.shape)
+    ref = orc.bias_gelu_bf16(x, bias)
+    assert_parity(f32(got), f32(ref), what="bias_gelu")
+    assert np.mean(got != ref) < 1e-3
+
+
+# --- RoPE / QK norm --------------------------------------------------------------------
+def test_rope_f32(wx, be, orc, rng):
+    T, H, D = 48, 24, 128
+    x = rng.standard_normal((T, H, D)).astype(np.float32)
+    pos = np.arange(1, T + 1, dtype=np.int32)
+    dx, dp = dev(be, x), dev(be, pos)
+    dy = be.empty(x.nbytes)
+    for n_dims in (128, 44):
+        wx.check(be.lib.wamx_op_rope_f32(be.ptr, dx.ptr, dp.ptr, dy.ptr, D, H, T, n_dims, 10000.0))
+        got = dy.download(np.float32, x.shape)
+        assert np.allclose(got, orc.rope_f32(x, pos, n_dims), atol=2e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_qk_norm_rope(wx, be, orc, rng, mode):
+    H, dh, T = 24, 128, 48 if mode == 0 else 200
+    print(f"qk_norm_rope mode={mode}", flush=True)
+    x = bf16(rng.standard_normal((T, 3 * H * dh)))  # packed qkv rows; q occupies the first H*dh
+    w = bf16(1 + rng.standard_normal(H * dh) * 0.02)
+    p0 = np.arange(1, T + 1, dtype=np.int32) if mode == 0 else np.zeros(T, np.int32)
+    p1 = (np.arange(T) // 20).astype(np.int32)
+    p2 = (np.arange(T) % 20).astype(np.int32)
+    tok0, total = 3, T + 5
+    dx, dw = dev(be, x), dev(be, w)
+    d0, d1, d2 = dev(be, p0), dev(be, p1), dev(be, p2)
+    ddst = dev(be, np.zeros((H, total, dh), np.uint16))
+    wx.check(be.lib.wamx_op_qk_norm_rope(be.ptr, dx.ptr, 3 * H * dh, dw.ptr, ddst.ptr, H, dh, T, total, tok0, mode,
+                                         d0.ptr, d1.ptr, d2.ptr, 1e-6, 10000.0))
+    got = ddst.download(np.uint16, (H, total, dh))
+    ref = np.zeros((H, total, dh), np.uint16)
+    orc.qk_norm_rope(np.ascontiguousarray(x[:, :H * dh]), w, H, dh, mode, p0, p1, p2, dst=ref, tok0=tok0)
+    assert_parity(f32(got), f32(ref), what=f"qk_norm_rope mode {mode}")
+    assert np.mean(got != ref) < 0.01
+    assert not got[:, :tok0].any() and not got[:, tok0 + T:].any()
+
+
+# --- attention ----------------------------------------------------------------------
+@pytest.mark.parametrize("H,tq,na,nb,split", [(24, 48, 3076, 48, 1), (4, 48, 1028, 48, 1), (2, 5, 64, 0, 0),
+                                              (3, 200, 200, 0, 0), (2, 48, 512, 0, 0), (1, 1, 4, 4, 2)])
+def test_joint_attention(wx, be, orc, H, tq, na, nb, split):
+    print(f"joint_attn H={H} tq={tq} na={na} nb={nb}", flush=True)
+    rng = np.random.default_rng(H * tq + na)
+    dh = 128
+    q = bf16(rng.standard_normal((H, tq, dh)))
+    ka = bf16(rng.standard_normal((H, na, dh)))
+    va = bf16(rng.standard_normal((H, dh, na)))
+    kb = bf16(rng.standard_normal((H, nb, dh))) if nb else None
+    vb = bf16(rng.standard_normal((H, dh, nb))) if nb else None
+    dq, dka, dva = dev(be, q), dev(be, ka), dev(be, va)
+    dkb = dev(be, kb) if nb else None
+    dvb = dev(be, vb) if nb else None
+    dout = be.empty(tq * H * dh * 2)
+    scale = 1.0 / np.sqrt(dh)
+    wx.check(be.lib.wamx_op_joint_attn(be.ptr, dq.ptr, dka.ptr, dva.ptr, na, dkb.ptr if nb else None,
+                                       dvb.ptr if nb else None, nb, split, dout.ptr, H, dh, tq, scale), "joint_attn")
+    got = dout.download(np.uint16, (tq, H * dh))
+    ref = orc.attention(q, ka, va, kb, vb, na_split=split, scale=scale)
+    assert_parity(f32(got), f32(ref), what="joint_attn")
+
+
+def test_softmax_and_fill(wx, be, orc, rng):
+    x = rng.standard_normal((24 * 48, 3121)).astype(np.float32) * 4
+    dx = dev(be, x)
+    dy = be.empty(x.nbytes)
+    wx.check(be.lib.wamx_op_soft_max_f32(be.ptr, dx.ptr, dy.ptr, x.shape[0], x.shape[1], 0.0883883))
+    assert rel_err(dy.download(np.float32, x.shape), orc.softmax_f32(x, 0.0883883)) < 1e-5
+    n = 1 << 20
+    d = be.empty(n * 4)
+    wx.check(be.lib.wamx_fill_normal(be.ptr, d.ptr, wx.TYPE_F32, n, 99, 0.0, 1.0))
+    got = d.download(np.float32, (n,))
+    ref = orc.fill_normal(n, 99)
+    # Same algorithm in f32 (device) and f64 (oracle) math: agreement to a few
+    # f32 ulps, a little more in the tails where log(u1) amplifies rounding.
+    assert np.max(np.abs(got - ref) / np.maximum(1.0, np.abs(ref))) < 1e-4
+    assert np.mean(np.abs(got - ref) > 1e-6 * np.maximum(1.0, np.abs(ref))) < 1e-3
+    assert cosine(got, ref) > 0.999999

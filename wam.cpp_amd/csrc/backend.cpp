@@ -1,0 +1,1054 @@
+// The HIP backend of libwamx: device registry, buffer types and buffers,
+// graph allocation, graph_compute dispatch with HIP-graph capture/replay, and
+// the single-op entry points.  Restates the ggml backend plugin interface of
+// llama.cpp b9866 (ggml-backend-impl.h: ggml_backend_i, ggml_backend_device_i,
+// ggml_backend_buffer_type_i, ggml_backend_buffer_i, ggml_backend_reg_i) that
+// wam.cpp's engine drives (weights.cpp:582-625, mot.cpp:526-594,
+// cache.cpp:113-130).
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <algorithm>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "common.h"
+#include "internal.h"
+
+using namespace wamx;
+
+static constexpr size_t kAlign = 256;
+static constexpr size_t kWorkspaceBytes = 96ull << 20;   // split-K / split-KV partials
+static constexpr int64_t kCounters = 1 << 15;            // per user (GEMM, attention)
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct wamx_device {
+    int index = 0;
+    char name[32] = {0};
+    char desc[256] = {0};
+};
+
+struct wamx_buffer_type {
+    wamx_device * dev = nullptr;
+    char name[32] = {0};
+};
+
+struct wamx_buffer {
+    wamx_buffer_type * buft = nullptr;
+    void * base = nullptr;
+    size_t size = 0;
+};
+
+struct GraphCacheEntry {
+    uint64_t signature = 0;
+    int n_nodes = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+struct wamx_backend {
+    wamx_device * dev = nullptr;
+    hipStream_t stream = nullptr;
+    void * workspace = nullptr;        // device scratch for split-K / split-KV partials
+    unsigned * counters = nullptr;     // 2 * kCounters arrival counters, zero between launches
+    bool use_graphs = true;
+    std::unordered_map<uint64_t, GraphCacheEntry> graphs;
+};
+
+struct wamx_backend_reg {
+    std::vector<wamx_device> devices;
+    std::vector<wamx_buffer_type> bufts;
+};
+
+// ---------------------------------------------------------------------------
+// Registry
+// ---------------------------------------------------------------------------
+static struct wamx_backend_reg * registry() {
+    static struct wamx_backend_reg * reg = [] {
+        auto * r = new struct wamx_backend_reg();
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+        r->devices.resize(n);
+        r->bufts.resize(n);
+        for (int i = 0; i < n; ++i) {
+            r->devices[i].index = i;
+            snprintf(r->devices[i].name, sizeof r->devices[i].name, "ROCm%d", i);
+            hipDeviceProp_t prop;
+            if (hipGetDeviceProperties(&prop, i) == hipSuccess)
+                snprintf(r->devices[i].desc, sizeof r->devices[i].desc, "%s (%s, %d CUs)", prop.name, prop.gcnArchName,
+                         prop.multiProcessorCount);
+            r->bufts[i].dev = &r->devices[i];
+            snprintf(r->bufts[i].name, sizeof r->bufts[i].name, "ROCm%d", i);
+        }
+        return r;
+    }();
+    return reg;
+}
+
+// ---------------------------------------------------------------------------
+// Buffer type / buffer interface
+// ---------------------------------------------------------------------------
+static const char * buft_get_name(wamx_buffer_type_t buft) { return buft->name; }
+static size_t buft_get_alignment(wamx_buffer_type_t) { return kAlign; }
+static size_t buft_get_max_size(wamx_buffer_type_t) { return SIZE_MAX; }
+static size_t buft_get_alloc_size(wamx_buffer_type_t, const wamx_tensor * t) { return align_up(wamx_nbytes(t), kAlign); }
+static bool buft_is_host(wamx_buffer_type_t) { return false; }
+
+static wamx_buffer_t buft_alloc_buffer(wamx_buffer_type_t buft, size_t size) {
+    if (!buft) return nullptr;
+    hipSetDevice(buft->dev->index);
+    auto * b = new (std::nothrow) wamx_buffer();
+    if (!b) return nullptr;
+    b->buft = buft;
+    b->size = align_up(std::max<size_t>(size, 1), kAlign);
+    if (hipMalloc(&b->base, b->size) != hipSuccess) {
+        set_errorf("hipMalloc(%zu) failed", b->size);
+        delete b;
+        return nullptr;
+    }
+    return b;
+}
+
+static void buffer_free(wamx_buffer_t b) {
+    if (!b) return;
+    if (b->base) hipFree(b->base);
+    delete b;
+}
+static void * buffer_get_base(wamx_buffer_t b) { return b ? b->base : nullptr; }
+static wamx_status buffer_init_tensor(wamx_buffer_t, wamx_tensor * t) {
+    if (t->view_src && t->view_src->data) t->data = (char *) t->view_src->data + t->view_offs;
+    return WAMX_STATUS_SUCCESS;
+}
+static void buffer_memset_tensor(wamx_buffer_t, wamx_tensor * t, uint8_t v, size_t off, size_t size) {
+    hipMemset((char *) t->data + off, v, size);
+}
+static void buffer_set_tensor(wamx_buffer_t, wamx_tensor * t, const void * data, size_t off, size_t size) {
+    hipMemcpy((char *) t->data + off, data, size, hipMemcpyHostToDevice);
+}
+static void buffer_get_tensor(wamx_buffer_t, const wamx_tensor * t, void * data, size_t off, size_t size) {
+    hipMemcpy(data, (const char *) t->data + off, size, hipMemcpyDeviceToHost);
+}
+static bool buffer_cpy_tensor(wamx_buffer_t, const wamx_tensor * src, wamx_tensor * dst) {
+    if (!src->data || !dst->data || wamx_nbytes(src) != wamx_nbytes(dst)) return false;
+    return hipMemcpy(dst->data, src->data, wamx_nbytes(src), hipMemcpyDeviceToDevice) == hipSuccess;
+}
+static void buffer_clear(wamx_buffer_t b, uint8_t v) {
+    if (b && b->base) hipMemset(b->base, v, b->size);
+}
+static void buffer_reset(wamx_buffer_t) {}
+
+static const wamx_buffer_type_i k_buft_iface = {
+    buft_get_name, buft_alloc_buffer, buft_get_alignment, buft_get_max_size, buft_get_alloc_size, buft_is_host,
+};
+static const wamx_buffer_i k_buffer_iface = {
+    buffer_free,       buffer_get_base,   buffer_init_tensor, buffer_memset_tensor, buffer_set_tensor,
+    buffer_get_tensor, buffer_cpy_tensor, buffer_clear,       buffer_reset,
+};
+
+// ---------------------------------------------------------------------------
+// Op dispatch
+// ---------------------------------------------------------------------------
+static int64_t es(const wamx_tensor * t) { return (int64_t) wamx_type_size(t->type); }
+
+static bool rows_contig(const wamx_tensor * t) { return t->nb[0] == (size_t) es(t); }
+
+static hipError_t run_mul_mat(wamx_backend * be, const wamx_tensor * node) {
+    const wamx_tensor * a = node->src[0];
+    const wamx_tensor * b = node->src[1];
+    GemmArgs g;
+    g.w = a->data;
+    g.w_type = a->type;
+    g.ldw = (int64_t) a->nb[1] / es(a);
+    g.w_bs2 = (int64_t) a->nb[2] / es(a);
+    g.w_bs3 = (int64_t) a->nb[3] / es(a);
+    g.x = b->data;
+    g.x_type = b->type;
+    g.ldx = (int64_t) b->nb[1] / es(b);
+    g.x_bs2 = (int64_t) b->nb[2] / es(b);
+    g.x_bs3 = (int64_t) b->nb[3] / es(b);
+    g.y = node->data;
+    g.y_type = node->type;
+    g.ldy = (int64_t) node->nb[1] / es(node);
+    g.y_bs2 = (int64_t) node->nb[2] / es(node);
+    g.y_bs3 = (int64_t) node->nb[3] / es(node);
+    g.M = a->ne[1];
+    g.N = b->ne[1];
+    g.K = a->ne[0];
+    g.B2 = b->ne[2];
+    g.B3 = b->ne[3];
+    g.r2 = b->ne[2] / a->ne[2];
+    g.r3 = b->ne[3] / a->ne[3];
+    g.ws = be->workspace;
+    g.ws_bytes = kWorkspaceBytes;
+    g.counters = be->counters;
+    g.max_counters = kCounters;
+    return launch_gemm(g, be->stream);
+}
+
+static hipError_t run_linear(wamx_backend * be, const wamx_tensor * node) {
+    const wamx_tensor * w = node->src[0];
+    const wamx_tensor * x = node->src[1];
+    GemmArgs g;
+    g.w = w->data;
+    g.w_type = WAMX_TYPE_BF16;
+    g.ldw = (int64_t) w->nb[1] / 2;
+    g.x = x->data;
+    g.x_type = x->type;
+    g.ldx = (int64_t) x->nb[1] / es(x);
+    g.y = node->data;
+    g.y_type = WAMX_TYPE_BF16;
+    g.ldy = (int64_t) node->nb[1] / 2;
+    g.M = w->ne[1];
+    g.N = x->ne[1];
+    g.K = w->ne[0];
+    g.epi = node->op_params[0];
+    g.bias = node->src[2] ? node->src[2]->data : nullptr;
+    g.res = node->src[3] ? node->src[3]->data : nullptr;
+    g.ldres = node->src[3] ? (int64_t) node->src[3]->nb[1] / 2 : 0;
+    g.gate = node->src[4] ? (const float *) node->src[4]->data : nullptr;
+    g.ws = be->workspace;
+    g.ws_bytes = kWorkspaceBytes;
+    g.counters = be->counters;
+    g.max_counters = kCounters;
+    return launch_gemm(g, be->stream);
+}
+
+static float param_f32(const wamx_tensor * t, int i) {
+    float v;
+    memcpy(&v, &t->op_params[i], 4);
+    return v;
+}
+
+static hipError_t run_joint_attn(wamx_backend * be, const wamx_tensor * node) {
+    const wamx_tensor * q = node->src[0];
+    AttnArgs a;
+    a.q = q->data;
+    a.k_a = node->src[1]->data;
+    a.vt_a = node->src[2]->data;
+    a.na = node->src[1]->ne[1];
+    a.vt_ld_a = (int64_t) node->src[2]->nb[1] / 2;
+    if (node->src[3]) {
+        a.k_b = node->src[3]->data;
+        a.vt_b = node->src[4]->data;
+        a.nb = node->src[3]->ne[1];
+        a.vt_ld_b = (int64_t) node->src[4]->nb[1] / 2;
+    }
+    a.na_split = node->op_params[0];
+    a.out = node->data;
+    a.heads = q->ne[2];
+    a.head_dim = q->ne[0];
+    a.tq = q->ne[1];
+    a.scale = param_f32(node, 1);
+    a.counters = be->counters + kCounters;
+    a.max_counters = kCounters;
+    if (attn_workspace_bytes(a) > kWorkspaceBytes) return hipErrorInvalidValue;
+    return launch_joint_attn(a, be->workspace, be->stream);
+}
+
+static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
+    hipStream_t s = be->stream;
+    wamx_tensor * s0 = node->src[0];
+    wamx_tensor * s1 = node->src[1];
+    switch (node->op) {
+        case WAMX_OP_NONE:
+        case WAMX_OP_VIEW:
+        case WAMX_OP_RESHAPE:
+        case WAMX_OP_PERMUTE:
+        case WAMX_OP_TRANSPOSE:
+            return hipSuccess;
+        case WAMX_OP_DUP:
+        case WAMX_OP_CONT:
+        case WAMX_OP_CPY:
+            return launch_copy(ref_of(s0), ref_of(node), s);
+        case WAMX_OP_ADD:
+            if (node->src[2]) {
+                const wamx_tensor * g = node->src[2];
+                return launch_gated_residual_bf16(s0->data, (int64_t) s0->nb[1] / 2, s1->data, (int64_t) s1->nb[1] / 2,
+                                                  g->data, g->type, g->ne[1] == 1 ? 0 : (int64_t) g->nb[1] / es(g),
+                                                  node->data, wamx_nrows(s0), s0->ne[0], s);
+            }
+            return launch_binary(0, ref_of(s0), ref_of(s1), ref_of(node), s);
+        case WAMX_OP_MUL:
+            return launch_binary(1, ref_of(s0), ref_of(s1), ref_of(node), s);
+        case WAMX_OP_REPEAT:
+            return launch_binary(2, ref_of(node), ref_of(s0), ref_of(node), s);
+        case WAMX_OP_SCALE:
+            return launch_unary(3, ref_of(s0), ref_of(node), param_f32(node, 0), s);
+        case WAMX_OP_CONCAT:
+            return launch_concat(ref_of(s0), ref_of(s1), ref_of(node), node->op_params[0], s);
+        case WAMX_OP_NORM: {
+            const float eps = param_f32(node, 0);
+            if (node->src[1]) {
+                const wamx_tensor * sc = node->src[1];
+                const wamx_tensor * sh = node->src[2];
+                const bool affine = sc->type == WAMX_TYPE_BF16;  // native-bf16.patch:393-400
+                const int64_t ss = sc->ne[1] == 1 ? 0 : (int64_t) sc->nb[1] / es(sc);
+                (void) sh;
+                return launch_norm_mod_bf16(s0->data, (int64_t) s0->nb[1] / 2, sc->data, sh->data, sc->type, ss,
+                                            node->data, (int64_t) node->nb[1] / 2, wamx_nrows(s0), s0->ne[0], eps,
+                                            affine, s);
+            }
+            return launch_norm_f32((const float *) s0->data, (int64_t) s0->nb[1] / 4, (float *) node->data,
+                                   (int64_t) node->nb[1] / 4, wamx_nrows(s0), s0->ne[0], eps, false, s);
+        }
+        case WAMX_OP_RMS_NORM: {
+            const float eps = param_f32(node, 0);
+            if (node->src[1])
+                return launch_rms_norm_bf16_f32(s0->data, (int64_t) s0->nb[1] / 2, node->src[1]->data,
+                                                (float *) node->data, (int64_t) node->nb[1] / 4, wamx_nrows(s0),
+                                                s0->ne[0], eps, s);
+            return launch_norm_f32((const float *) s0->data, (int64_t) s0->nb[1] / 4, (float *) node->data,
+                                   (int64_t) node->nb[1] / 4, wamx_nrows(s0), s0->ne[0], eps, true, s);
+        }
+        case WAMX_OP_MUL_MAT:
+            return run_mul_mat(be, node);
+        case WAMX_OP_SOFT_MAX:
+            return launch_softmax_f32(ref_of(s0), ref_of(node), param_f32(node, 0), s);
+        case WAMX_OP_ROPE:
+            return launch_rope_f32(ref_of(s0), (const int32_t *) s1->data, ref_of(node), node->op_params[1],
+                                   param_f32(node, 5), s);
+        case WAMX_OP_UNARY:
+            if (node->src[1])
+                return launch_bias_gelu_bf16(s0->data, s1->data, node->data, wamx_nelements(s0), s1->ne[0], s);
+            return launch_unary(node->op_params[0], ref_of(s0), ref_of(node), 1.0f, s);
+        case WAMX_OP_GET_ROWS:
+            return launch_get_rows(ref_of(s0), (const int32_t *) s1->data, ref_of(node), s);
+        case WAMX_OP_LINEAR:
+            return run_linear(be, node);
+        case WAMX_OP_QK_NORM_ROPE: {
+            const wamx_tensor * x = node->src[0];
+            return launch_qk_norm_rope(x->data, (int64_t) x->nb[1] / 2, node->src[1]->data, node->data, node->ne[2],
+                                       node->ne[0], x->ne[1], node->ne[1], node->op_params[0], node->op_params[1],
+                                       node->src[3] ? (const int32_t *) node->src[3]->data : nullptr,
+                                       node->src[4] ? (const int32_t *) node->src[4]->data : nullptr,
+                                       node->src[5] ? (const int32_t *) node->src[5]->data : nullptr,
+                                       param_f32(node, 2), param_f32(node, 3), s);
+        }
+        case WAMX_OP_JOINT_ATTN:
+            return run_joint_attn(be, node);
+        case WAMX_OP_MODULATION:
+            return launch_modulation(s0->data, s0->type, s1->data, s1->type, (float *) node->data,
+                                     wamx_nelements(s0), s1->ne[2] * s1->ne[3], s);
+        default:
+            return hipErrorNotSupported;
+    }
+}
+
+static bool supports(const wamx_tensor * t) {
+    auto ok_type = [](const wamx_tensor * x) {
+        return x && (x->type == WAMX_TYPE_F32 || x->type == WAMX_TYPE_BF16 || x->type == WAMX_TYPE_F16 ||
+                     x->type == WAMX_TYPE_I32);
+    };
+    const wamx_tensor * s0 = t->src[0];
+    const wamx_tensor * s1 = t->src[1];
+    switch (t->op) {
+        case WAMX_OP_NONE:
+        case WAMX_OP_VIEW:
+        case WAMX_OP_RESHAPE:
+        case WAMX_OP_PERMUTE:
+        case WAMX_OP_TRANSPOSE:
+            return true;
+        case WAMX_OP_DUP:
+        case WAMX_OP_CONT:
+        case WAMX_OP_CPY:
+            return ok_type(s0) && ok_type(t);
+        case WAMX_OP_ADD:
+            if (t->src[2])
+                return s0->type == WAMX_TYPE_BF16 && s1->type == WAMX_TYPE_BF16 && rows_contig(s0) && rows_contig(s1) &&
+                       rows_contig(t->src[2]) && s0->ne[2] == 1 && s0->ne[3] == 1;
+            return ok_type(s0) && ok_type(s1) && s0->type != WAMX_TYPE_I32;
+        case WAMX_OP_MUL:
+        case WAMX_OP_REPEAT:
+        case WAMX_OP_SCALE:
+        case WAMX_OP_CONCAT:
+        case WAMX_OP_GET_ROWS:
+            return ok_type(s0);
+        case WAMX_OP_NORM:
+            if (t->src[1])
+                return s0->type == WAMX_TYPE_BF16 && rows_contig(s0) && rows_contig(t->src[1]) &&
+                       rows_contig(t->src[2]) && s0->ne[2] == 1 && s0->ne[3] == 1 &&
+                       t->src[1]->ne[1] == t->src[2]->ne[1] &&
+                       (t->src[1]->ne[1] == 1 || t->src[1]->nb[1] / es(t->src[1]) == t->src[2]->nb[1] / es(t->src[2]));
+            return s0->type == WAMX_TYPE_F32 && rows_contig(s0);
+        case WAMX_OP_RMS_NORM:
+            return rows_contig(s0) && (t->src[1] ? s0->type == WAMX_TYPE_BF16 : s0->type == WAMX_TYPE_F32);
+        case WAMX_OP_MUL_MAT:
+            return (s0->type == WAMX_TYPE_BF16 || s0->type == WAMX_TYPE_F32) &&
+                   (s1->type == WAMX_TYPE_BF16 || s1->type == WAMX_TYPE_F32) && rows_contig(s0) && rows_contig(s1) &&
+                   wamx_is_contiguous(t);
+        case WAMX_OP_SOFT_MAX:
+            return s0->type == WAMX_TYPE_F32 && t->src[1] == nullptr;
+        case WAMX_OP_ROPE:
+            return s0->type == WAMX_TYPE_F32 && t->op_params[2] == 0;
+        case WAMX_OP_UNARY:
+            if (t->src[1]) return s0->type == WAMX_TYPE_BF16 && wamx_is_contiguous(s0);
+            return ok_type(s0) && t->op_params[0] >= 0 && t->op_params[0] <= 2;
+        case WAMX_OP_LINEAR:
+        case WAMX_OP_QK_NORM_ROPE:
+        case WAMX_OP_JOINT_ATTN:
+        case WAMX_OP_MODULATION:
+            return true;  // validated by their constructors
+        default:
+            return false;
+    }
+}
+
+// Signature of a graph: op, shapes and addresses of every node and source.
+// A captured HIP graph is replayed only when the signature is unchanged.
+static uint64_t graph_signature(wamx_cgraph * g) {
+    uint64_t h = 1469598103934665603ull;
+    auto mix = [&h](uint64_t v) {
+        h ^= v;
+        h *= 1099511628211ull;
+    };
+    const int n = wamx_graph_n_nodes(g);
+    for (int i = 0; i < n; ++i) {
+        const wamx_tensor * t = wamx_graph_node(g, i);
+        mix((uint64_t) t->op);
+        mix((uint64_t) (uintptr_t) t->data);
+        for (int d = 0; d < 4; ++d) mix((uint64_t) t->ne[d] ^ ((uint64_t) t->nb[d] << 20));
+        for (int k = 0; k < 16; ++k) mix((uint64_t) (uint32_t) t->op_params[k]);
+        for (int k = 0; k < WAMX_MAX_SRC; ++k)
+            if (t->src[k]) mix((uint64_t) (uintptr_t) t->src[k]->data);
+    }
+    return h;
+}
+
+static wamx_status run_nodes(wamx_backend * be, wamx_cgraph * g) {
+    const int n = wamx_graph_n_nodes(g);
+    for (int i = 0; i < n; ++i) {
+        wamx_tensor * node = wamx_graph_node(g, i);
+        for (int k = 0; k < WAMX_MAX_SRC; ++k) {
+            const wamx_tensor * s = node->src[k];
+            if (s && !s->data && wamx_nelements(s) > 0) {
+                set_errorf("graph_compute: node %d (%s '%s') source %d '%s' has no data", i, wamx_op_name(node->op),
+                           node->name, k, s->name);
+                return WAMX_STATUS_FAILED;
+            }
+        }
+        if (!node->data && wamx_nelements(node) > 0) {
+            set_errorf("graph_compute: node %d (%s '%s') is not allocated", i, wamx_op_name(node->op), node->name);
+            return WAMX_STATUS_ALLOC_FAILED;
+        }
+        const hipError_t err = compute_node(be, node);
+        if (err != hipSuccess) {
+            set_errorf("graph_compute: node %d (%s '%s') failed: %s", i, wamx_op_name(node->op), node->name,
+                       hipGetErrorString(err));
+            return WAMX_STATUS_FAILED;
+        }
+    }
+    return WAMX_STATUS_SUCCESS;
+}
+
+static void release_graph(GraphCacheEntry & e) {
+    if (e.exec) hipGraphExecDestroy(e.exec);
+    if (e.graph) hipGraphDestroy(e.graph);
+    e.exec = nullptr;
+    e.graph = nullptr;
+}
+
+static wamx_status graph_compute_impl(wamx_backend * be, wamx_cgraph * g) {
+    if (!be || !g) {
+        set_error("graph_compute: null argument");
+        return WAMX_STATUS_FAILED;
+    }
+    hipSetDevice(be->dev->index);
+    const int n = wamx_graph_n_nodes(g);
+    for (int i = 0; i < n; ++i) {
+        const wamx_tensor * node = wamx_graph_node(g, i);
+        if (!supports(node)) {
+            set_errorf("graph_compute: unsupported op %s at node %d ('%s')", wamx_op_name(node->op), i, node->name);
+            return WAMX_STATUS_FAILED;
+        }
+    }
+    const uint64_t uid = wamx_graph_uid(g);
+    if (!be->use_graphs || uid == 0) return run_nodes(be, g);
+
+    const uint64_t sig = graph_signature(g);
+    GraphCacheEntry & e = be->graphs[uid];
+    if (!e.exec || e.signature != sig || e.n_nodes != n) {
+        release_graph(e);
+        if (hipStreamBeginCapture(be->stream, hipStreamCaptureModeRelaxed) != hipSuccess) {
+            (void) hipGetLastError();
+            return run_nodes(be, g);
+        }
+        const wamx_status st = run_nodes(be, g);
+        hipGraph_t graph = nullptr;
+        const hipError_t end = hipStreamEndCapture(be->stream, &graph);
+        if (st != WAMX_STATUS_SUCCESS) {
+            if (graph) hipGraphDestroy(graph);
+            return st;
+        }
+        if (end != hipSuccess || !graph) {
+            set_errorf("graph_compute: stream capture failed: %s", hipGetErrorString(end));
+            return WAMX_STATUS_FAILED;
+        }
+        hipGraphExec_t exec = nullptr;
+        if (hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+            hipGraphDestroy(graph);
+            set_error("graph_compute: hipGraphInstantiate failed");
+            return WAMX_STATUS_FAILED;
+        }
+        e.graph = graph;
+        e.exec = exec;
+        e.signature = sig;
+        e.n_nodes = n;
+    }
+    const hipError_t err = hipGraphLaunch(e.exec, be->stream);
+    if (err != hipSuccess) {
+        set_errorf("graph_compute: hipGraphLaunch failed: %s", hipGetErrorString(err));
+        return WAMX_STATUS_FAILED;
+    }
+    return WAMX_STATUS_SUCCESS;
+}
+
+// ---------------------------------------------------------------------------
+// Backend / device / registry interfaces
+// ---------------------------------------------------------------------------
+static const char * be_get_name(wamx_backend_t be) { return be ? be->dev->name : ""; }
+static void be_free(wamx_backend_t be);
+static void be_set_tensor_async(wamx_backend_t be, wamx_tensor * t, const void * data, size_t off, size_t size) {
+    hipMemcpyAsync((char *) t->data + off, data, size, hipMemcpyHostToDevice, be->stream);
+}
+static void be_get_tensor_async(wamx_backend_t be, const wamx_tensor * t, void * data, size_t off, size_t size) {
+    hipMemcpyAsync(data, (const char *) t->data + off, size, hipMemcpyDeviceToHost, be->stream);
+}
+static bool be_cpy_tensor_async(wamx_backend_t src, wamx_backend_t, const wamx_tensor * a, wamx_tensor * b) {
+    if (!a->data || !b->data || wamx_nbytes(a) != wamx_nbytes(b)) return false;
+    return hipMemcpyAsync(b->data, a->data, wamx_nbytes(a), hipMemcpyDeviceToDevice, src->stream) == hipSuccess;
+}
+static void be_synchronize(wamx_backend_t be) {
+    if (be) hipStreamSynchronize(be->stream);
+}
+static wamx_status be_graph_compute(wamx_backend_t be, wamx_cgraph * g) { return graph_compute_impl(be, g); }
+
+static const wamx_backend_i k_backend_iface = {
+    be_get_name, be_free, be_set_tensor_async, be_get_tensor_async, be_cpy_tensor_async, be_synchronize, be_graph_compute,
+};
+
+static const char * dev_get_name(wamx_device_t d) { return d->name; }
+static const char * dev_get_description(wamx_device_t d) { return d->desc; }
+static void dev_get_memory(wamx_device_t d, size_t * free_b, size_t * total_b) {
+    hipSetDevice(d->index);
+    if (hipMemGetInfo(free_b, total_b) != hipSuccess) *free_b = *total_b = 0;
+}
+static wamx_backend_t dev_init_backend(wamx_device_t d, const char *) { return wamx_backend_init(d->index); }
+static wamx_buffer_type_t dev_get_buffer_type(wamx_device_t d) { return wamx_backend_buffer_type(d->index); }
+static bool dev_supports_op(wamx_device_t, const wamx_tensor * op) { return op && supports(op); }
+static bool dev_supports_buft(wamx_device_t d, wamx_buffer_type_t buft) { return buft && buft->dev == d; }
+static bool dev_offload_op(wamx_device_t, const wamx_tensor *) { return true; }
+
+static const wamx_device_i k_device_iface = {
+    dev_get_name, dev_get_description, dev_get_memory, dev_init_backend,
+    dev_get_buffer_type, dev_supports_op, dev_supports_buft, dev_offload_op,
+};
+
+static const char * reg_get_name(wamx_backend_reg_t) { return "ROCm"; }
+static size_t reg_get_device_count(wamx_backend_reg_t r) { return r->devices.size(); }
+static wamx_device_t reg_get_device(wamx_backend_reg_t r, size_t i) { return i < r->devices.size() ? &r->devices[i] : nullptr; }
+static void * reg_get_proc_address(wamx_backend_reg_t, const char * name);
+
+static const wamx_backend_reg_i k_reg_iface = {reg_get_name, reg_get_device_count, reg_get_device, reg_get_proc_address};
+
+// ---------------------------------------------------------------------------
+// Graph allocator
+// ---------------------------------------------------------------------------
+struct wamx_gallocr {
+    wamx_backend * be = nullptr;
+    wamx_buffer * buffer = nullptr;
+};
+
+struct FreeList {
+    std::map<size_t, size_t> blocks;  // offset -> size
+    size_t high = 0;
+    size_t alloc(size_t size) {
+        auto best = blocks.end();
+        for (auto it = blocks.begin(); it != blocks.end(); ++it)
+            if (it->second >= size && (best == blocks.end() || it->second < best->second)) best = it;
+        if (best != blocks.end()) {
+            const size_t off = best->first, bsz = best->second;
+            blocks.erase(best);
+            if (bsz > size) blocks[off + size] = bsz - size;
+            return off;
+        }
+        // Grow: merge with a trailing free block if there is one.
+        if (!blocks.empty()) {
+            auto last = std::prev(blocks.end());
+            if (last->first + last->second == high) {
+                const size_t off = last->first;
+                blocks.erase(last);
+                high = off + size;
+                return off;
+            }
+        }
+        const size_t off = high;
+        high += size;
+        return off;
+    }
+    void release(size_t off, size_t size) {
+        auto it = blocks.emplace(off, size).first;
+        auto nx = std::next(it);
+        if (nx != blocks.end() && it->first + it->second == nx->first) {
+            it->second += nx->second;
+            blocks.erase(nx);
+        }
+        if (it != blocks.begin()) {
+            auto pv = std::prev(it);
+            if (pv->first + pv->second == it->first) {
+                pv->second += it->second;
+                blocks.erase(it);
+            }
+        }
+    }
+};
+
+static wamx_tensor * root_of(wamx_tensor * t) { return t->view_src ? t->view_src : t; }
+
+static bool gallocr_alloc(wamx_gallocr * ga, wamx_cgraph * g) {
+    const int n = wamx_graph_n_nodes(g);
+    std::vector<wamx_tensor *> order;  // tensors that need memory, in first-use order
+    std::unordered_map<wamx_tensor *, int> last_use;
+    std::unordered_map<wamx_tensor *, int> first_def;
+    const int kForever = 1 << 30;
+    auto needs = [](wamx_tensor * t) { return t && !t->data && !t->view_src && wamx_nelements(t) > 0; };
+    auto touch = [&](wamx_tensor * t, int i) {
+        wamx_tensor * r = root_of(t);
+        if (!needs(r)) return;
+        if (!first_def.count(r)) {
+            first_def[r] = i;
+            order.push_back(r);
+        }
+        int & lu = last_use[r];
+        lu = std::max(lu, i);
+        if ((r->flags & (WAMX_TENSOR_FLAG_OUTPUT | WAMX_TENSOR_FLAG_INPUT)) || r->op == WAMX_OP_NONE) lu = kForever;
+        if (t->flags & WAMX_TENSOR_FLAG_OUTPUT) lu = kForever;
+    };
+    for (int i = 0; i < n; ++i) {
+        wamx_tensor * node = wamx_graph_node(g, i);
+        for (int k = 0; k < WAMX_MAX_SRC; ++k)
+            if (node->src[k]) touch(node->src[k], i);
+        touch(node, i);
+    }
+    // Leaf inputs and tensors first touched as sources are live from the start.
+    FreeList fl;
+    std::unordered_map<wamx_tensor *, size_t> offset;
+    std::vector<std::vector<wamx_tensor *>> frees(n);
+    for (auto * t : order)
+        if (last_use[t] < n) frees[last_use[t]].push_back(t);
+    auto size_of = [](wamx_tensor * t) { return align_up(wamx_nbytes(t), kAlign); };
+    for (auto * t : order)
+        if (first_def[t] == 0 || t->op == WAMX_OP_NONE) offset[t] = fl.alloc(size_of(t));
+    for (int i = 0; i < n; ++i) {
+        wamx_tensor * node = wamx_graph_node(g, i);
+        for (int k = 0; k < WAMX_MAX_SRC; ++k) {
+            wamx_tensor * r = node->src[k] ? root_of(node->src[k]) : nullptr;
+            if (r && needs(r) && !offset.count(r)) offset[r] = fl.alloc(size_of(r));
+        }
+        wamx_tensor * r = root_of(node);
+        if (needs(r) && !offset.count(r)) offset[r] = fl.alloc(size_of(r));
+        for (auto * t : frees[i]) fl.release(offset[t], size_of(t));
+    }
+    const size_t total = std::max<size_t>(fl.high, kAlign);
+    if (!ga->buffer || ga->buffer->size < total) {
+        if (ga->buffer) buffer_free(ga->buffer);
+        ga->buffer = buft_alloc_buffer(wamx_backend_get_default_buffer_type(ga->be), total);
+        if (!ga->buffer) return false;
+    }
+    for (auto & kv : offset) {
+        kv.first->data = (char *) ga->buffer->base + kv.second;
+        kv.first->buffer = ga->buffer;
+    }
+    // Views (and their views) alias their allocated roots.
+    for (int i = 0; i < n; ++i) {
+        wamx_tensor * node = wamx_graph_node(g, i);
+        for (int k = -1; k < WAMX_MAX_SRC; ++k) {
+            wamx_tensor * t = k < 0 ? node : node->src[k];
+            if (t && t->view_src && t->view_src->data) {
+                t->data = (char *) t->view_src->data + t->view_offs;
+                t->buffer = t->view_src->buffer;
+            }
+        }
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+wamx_backend_reg_t wamx_backend_reg(void) { return registry(); }
+const wamx_backend_reg_i * wamx_backend_reg_iface(void) { return &k_reg_iface; }
+const wamx_device_i * wamx_device_iface(void) { return &k_device_iface; }
+const wamx_backend_i * wamx_backend_iface(void) { return &k_backend_iface; }
+const wamx_buffer_type_i * wamx_buffer_type_iface(void) { return &k_buft_iface; }
+const wamx_buffer_i * wamx_buffer_iface(void) { return &k_buffer_iface; }
+
+int wamx_get_device_count(void) { return (int) registry()->devices.size(); }
+
+wamx_backend_t wamx_backend_init(int device) {
+    clear_error();
+    struct wamx_backend_reg * reg = registry();
+    if (device < 0 || device >= (int) reg->devices.size()) {
+        set_errorf("wamx_backend_init: device %d not present (%zu devices)", device, reg->devices.size());
+        return nullptr;
+    }
+    if (hipSetDevice(device) != hipSuccess) {
+        set_errorf("wamx_backend_init: hipSetDevice(%d) failed", device);
+        return nullptr;
+    }
+    auto * be = new (std::nothrow) wamx_backend();
+    if (!be) return nullptr;
+    be->dev = &reg->devices[device];
+    const char * env = getenv("WAMX_DISABLE_HIP_GRAPHS");
+    be->use_graphs = !(env && env[0] && env[0] != '0');
+    // A blocking stream, so synchronous tensor_set/get on the null stream are
+    // ordered with the graph work (default priority).
+    if (hipStreamCreate(&be->stream) != hipSuccess || hipMalloc(&be->workspace, kWorkspaceBytes) != hipSuccess ||
+        hipMalloc((void **) &be->counters, 2 * kCounters * sizeof(unsigned)) != hipSuccess ||
+        hipMemset(be->counters, 0, 2 * kCounters * sizeof(unsigned)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        set_error("wamx_backend_init: stream or workspace allocation failed");
+        be_free(be);
+        return nullptr;
+    }
+    return be;
+}
+
+static void be_free(wamx_backend_t be) {
+    if (!be) return;
+    hipSetDevice(be->dev->index);
+    if (be->stream) hipStreamSynchronize(be->stream);
+    for (auto & kv : be->graphs) release_graph(kv.second);
+    if (be->workspace) hipFree(be->workspace);
+    if (be->counters) hipFree(be->counters);
+    if (be->stream) hipStreamDestroy(be->stream);
+    delete be;
+}
+
+void wamx_backend_free(wamx_backend_t be) { be_free(be); }
+const char * wamx_backend_name(wamx_backend_t be) { return be_get_name(be); }
+void * wamx_backend_stream(wamx_backend_t be) { return be ? (void *) be->stream : nullptr; }
+
+wamx_buffer_type_t wamx_backend_buffer_type(int device) {
+    struct wamx_backend_reg * reg = registry();
+    if (device < 0 || device >= (int) reg->bufts.size()) return nullptr;
+    return &reg->bufts[device];
+}
+wamx_buffer_type_t wamx_backend_get_default_buffer_type(wamx_backend_t be) {
+    return be ? wamx_backend_buffer_type(be->dev->index) : nullptr;
+}
+
+wamx_buffer_t wamx_buft_alloc_buffer(wamx_buffer_type_t buft, size_t size) { return buft_alloc_buffer(buft, size); }
+size_t wamx_buft_get_alignment(wamx_buffer_type_t buft) { return buft_get_alignment(buft); }
+size_t wamx_buft_get_alloc_size(wamx_buffer_type_t buft, const wamx_tensor * t) { return buft_get_alloc_size(buft, t); }
+wamx_buffer_t wamx_backend_alloc_buffer(wamx_backend_t be, size_t size) {
+    return buft_alloc_buffer(wamx_backend_get_default_buffer_type(be), size);
+}
+void wamx_buffer_free(wamx_buffer_t buf) { buffer_free(buf); }
+void * wamx_buffer_get_base(wamx_buffer_t buf) { return buffer_get_base(buf); }
+size_t wamx_buffer_get_size(wamx_buffer_t buf) { return buf ? buf->size : 0; }
+
+wamx_status wamx_tensor_alloc(wamx_buffer_t buf, wamx_tensor * t, void * addr) {
+    WAMX_REQUIRE(buf && t && addr, "wamx_tensor_alloc: null argument");
+    const char * base = (const char *) buf->base;
+    WAMX_REQUIRE((const char *) addr >= base && (const char *) addr + wamx_nbytes(t) <= base + buf->size,
+                 "wamx_tensor_alloc: tensor does not fit in the buffer");
+    t->data = addr;
+    t->buffer = buf;
+    return WAMX_STATUS_SUCCESS;
+}
+
+wamx_status wamx_backend_tensor_set(wamx_tensor * t, const void * data, size_t offset, size_t size) {
+    WAMX_REQUIRE(t && t->data, "tensor_set: tensor not allocated");
+    WAMX_REQUIRE(offset + size <= wamx_nbytes(t), "tensor_set: out of range");
+    WAMX_HIP_TRY(hipMemcpy((char *) t->data + offset, data, size, hipMemcpyHostToDevice));
+    return WAMX_STATUS_SUCCESS;
+}
+wamx_status wamx_backend_tensor_get(const wamx_tensor * t, void * data, size_t offset, size_t size) {
+    WAMX_REQUIRE(t && t->data, "tensor_get: tensor not allocated");
+    WAMX_REQUIRE(offset + size <= wamx_nbytes(t), "tensor_get: out of range");
+    WAMX_HIP_TRY(hipMemcpy(data, (const char *) t->data + offset, size, hipMemcpyDeviceToHost));
+    return WAMX_STATUS_SUCCESS;
+}
+wamx_status wamx_backend_tensor_copy(const wamx_tensor * src, wamx_tensor * dst) {
+    WAMX_REQUIRE(src && dst && src->data && dst->data, "tensor_copy: unallocated tensor");
+    WAMX_REQUIRE(wamx_nbytes(src) == wamx_nbytes(dst), "tensor_copy: size mismatch");
+    WAMX_HIP_TRY(hipMemcpy(dst->data, src->data, wamx_nbytes(src), hipMemcpyDeviceToDevice));
+    return WAMX_STATUS_SUCCESS;
+}
+wamx_status wamx_backend_tensor_memset(wamx_tensor * t, uint8_t value, size_t offset, size_t size) {
+    WAMX_REQUIRE(t && t->data && offset + size <= wamx_nbytes(t), "tensor_memset: bad range");
+    WAMX_HIP_TRY(hipMemset((char *) t->data + offset, value, size));
+    return WAMX_STATUS_SUCCESS;
+}
+void wamx_backend_synchronize(wamx_backend_t be) { be_synchronize(be); }
+
+wamx_gallocr_t wamx_gallocr_new(wamx_backend_t be) {
+    if (!be) return nullptr;
+    auto * ga = new (std::nothrow) wamx_gallocr();
+    if (ga) ga->be = be;
+    return ga;
+}
+bool wamx_gallocr_alloc_graph(wamx_gallocr_t ga, wamx_cgraph * g) { return ga && g && gallocr_alloc(ga, g); }
+size_t wamx_gallocr_get_buffer_size(wamx_gallocr_t ga) { return ga && ga->buffer ? ga->buffer->size : 0; }
+void wamx_gallocr_free(wamx_gallocr_t ga) {
+    if (!ga) return;
+    buffer_free(ga->buffer);
+    delete ga;
+}
+
+wamx_status wamx_backend_graph_compute(wamx_backend_t be, wamx_cgraph * g) {
+    clear_error();
+    return graph_compute_impl(be, g);
+}
+bool wamx_backend_supports_op(wamx_backend_t, const wamx_tensor * op) { return op && supports(op); }
+
+// --- single-op entry points ---------------------------------------------
+#define WAMX_LAUNCH(expr)                                                                  \
+    do {                                                                                   \
+        const hipError_t e__ = (expr);                                                     \
+        if (e__ != hipSuccess) {                                                           \
+            set_errorf("%s: launch failed: %s", __func__, hipGetErrorString(e__));         \
+            return WAMX_STATUS_FAILED;                                                     \
+        }                                                                                  \
+        return WAMX_STATUS_SUCCESS;                                                        \
+    } while (0)
+
+wamx_status wamx_op_mul_mat(wamx_backend_t be, const void * w, int64_t ldw, const void * x, int32_t x_type, int64_t ldx,
+                            void * y, int32_t y_type, int64_t ldy, int64_t M, int64_t N, int64_t K) {
+    WAMX_REQUIRE(be && w && x && y, "wamx_op_mul_mat: null argument");
+    WAMX_REQUIRE(x_type == WAMX_TYPE_F32 || x_type == WAMX_TYPE_BF16, "wamx_op_mul_mat: x type");
+    WAMX_REQUIRE(y_type == WAMX_TYPE_F32 || y_type == WAMX_TYPE_BF16, "wamx_op_mul_mat: y type");
+    WAMX_REQUIRE(M > 0 && N > 0 && K > 0 && ldw >= K && ldx >= K && ldy >= M, "wamx_op_mul_mat: sizes");
+    GemmArgs g;
+    g.w = w;
+    g.ldw = ldw;
+    g.x = x;
+    g.x_type = x_type;
+    g.ldx = ldx;
+    g.y = y;
+    g.y_type = y_type;
+    g.ldy = ldy;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.ws = be->workspace;
+    g.ws_bytes = kWorkspaceBytes;
+    g.counters = be->counters;
+    g.max_counters = kCounters;
+    WAMX_LAUNCH(launch_gemm(g, be->stream));
+}
+
+wamx_status wamx_op_linear(wamx_backend_t be, const void * w, const void * x, int32_t x_type, const void * bias,
+                           int32_t epilogue, const void * residual, const float * gate, void * y, int64_t M, int64_t N,
+                           int64_t K) {
+    WAMX_REQUIRE(be && w && x && y && M > 0 && N > 0 && K > 0, "wamx_op_linear: bad arguments");
+    WAMX_REQUIRE(epilogue >= WAMX_EPI_NONE && epilogue <= WAMX_EPI_BIAS_RESIDUAL, "wamx_op_linear: epilogue");
+    WAMX_REQUIRE(epilogue == WAMX_EPI_NONE || bias, "wamx_op_linear: bias required");
+    WAMX_REQUIRE((epilogue != WAMX_EPI_BIAS_GATED && epilogue != WAMX_EPI_BIAS_RESIDUAL) || residual,
+                 "wamx_op_linear: residual required");
+    WAMX_REQUIRE(epilogue != WAMX_EPI_BIAS_GATED || gate, "wamx_op_linear: gate required");
+    GemmArgs g;
+    g.w = w;
+    g.ldw = K;
+    g.x = x;
+    g.x_type = x_type;
+    g.ldx = K;
+    g.y = y;
+    g.y_type = WAMX_TYPE_BF16;
+    g.ldy = M;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.epi = epilogue;
+    g.bias = bias;
+    g.res = residual;
+    g.ldres = M;
+    g.gate = gate;
+    g.ws = be->workspace;
+    g.ws_bytes = kWorkspaceBytes;
+    g.counters = be->counters;
+    g.max_counters = kCounters;
+    WAMX_LAUNCH(launch_gemm(g, be->stream));
+}
+
+wamx_status wamx_op_norm_modulation_bf16(wamx_backend_t be, const void * x, int64_t ldx, const float * scale,
+                                         const float * shift, int64_t ss, void * y, int64_t rows, int64_t cols,
+                                         float eps) {
+    WAMX_REQUIRE(be && x && scale && shift && y && cols > 0, "wamx_op_norm_modulation_bf16: bad arguments");
+    WAMX_LAUNCH(launch_norm_mod_bf16(x, ldx, scale, shift, WAMX_TYPE_F32, ss, y, cols, rows, cols, eps, false,
+                                     be->stream));
+}
+
+wamx_status wamx_op_layer_norm_bf16(wamx_backend_t be, const void * x, int64_t ldx, const void * w, const void * b,
+                                    void * y, int64_t rows, int64_t cols, float eps) {
+    WAMX_REQUIRE(be && x && w && b && y && cols > 0, "wamx_op_layer_norm_bf16: bad arguments");
+    WAMX_LAUNCH(launch_norm_mod_bf16(x, ldx, w, b, WAMX_TYPE_BF16, 0, y, cols, rows, cols, eps, true, be->stream));
+}
+
+wamx_status wamx_op_rms_norm_bf16_f32(wamx_backend_t be, const void * x, int64_t ldx, const void * w, float * y,
+                                      int64_t rows, int64_t cols, float eps) {
+    WAMX_REQUIRE(be && x && w && y && cols > 0, "wamx_op_rms_norm_bf16_f32: bad arguments");
+    WAMX_LAUNCH(launch_rms_norm_bf16_f32(x, ldx, w, y, cols, rows, cols, eps, be->stream));
+}
+
+wamx_status wamx_op_norm_modulation_f32(wamx_backend_t be, const float * x, int64_t ldx, const float * scale,
+                                        const float * shift, int64_t ss, float * y, int64_t rows, int64_t cols,
+                                        float eps) {
+    WAMX_REQUIRE(be && x && scale && shift && y && cols > 0, "wamx_op_norm_modulation_f32: bad arguments");
+    WAMX_LAUNCH(launch_norm_mod_f32(x, ldx, scale, shift, ss, y, rows, cols, eps, be->stream));
+}
+
+wamx_status wamx_op_gated_residual_bf16(wamx_backend_t be, const void * h, const void * b, const void * g,
+                                        int32_t gate_type, int64_t gs, void * y, int64_t rows, int64_t cols) {
+    WAMX_REQUIRE(be && h && b && g && y, "wamx_op_gated_residual_bf16: bad arguments");
+    WAMX_REQUIRE(gate_type == WAMX_TYPE_F32 || gate_type == WAMX_TYPE_BF16, "wamx_op_gated_residual_bf16: gate type");
+    WAMX_LAUNCH(launch_gated_residual_bf16(h, cols, b, cols, g, gate_type, gs, y, rows, cols, be->stream));
+}
+
+wamx_status wamx_op_gated_residual_f32(wamx_backend_t be, const float * r, const float * b, const float * g, int64_t gs,
+                                       float * y, int64_t rows, int64_t cols) {
+    WAMX_REQUIRE(be && r && b && g && y, "wamx_op_gated_residual_f32: bad arguments");
+    WAMX_LAUNCH(launch_gated_residual_f32(r, cols, b, cols, g, gs, y, rows, cols, be->stream));
+}
+
+wamx_status wamx_op_bias_gelu_bf16(wamx_backend_t be, const void * x, const void * bias, void * y, int64_t n,
+                                   int64_t width) {
+    WAMX_REQUIRE(be && x && bias && y && width > 0, "wamx_op_bias_gelu_bf16: bad arguments");
+    WAMX_LAUNCH(launch_bias_gelu_bf16(x, bias, y, n, width, be->stream));
+}
+
+wamx_status wamx_op_rope_f32(wamx_backend_t be, const float * x, const int32_t * pos, float * y, int64_t head_dim,
+                             int64_t heads, int64_t tokens, int n_dims, float freq_base) {
+    WAMX_REQUIRE(be && x && pos && y && n_dims > 0 && n_dims <= head_dim && !(n_dims & 1), "wamx_op_rope_f32: bad args");
+    TensorRef rx{(void *) x, WAMX_TYPE_F32, {head_dim, heads, tokens, 1},
+                 {4, 4 * head_dim, 4 * head_dim * heads, 4 * head_dim * heads * tokens}};
+    TensorRef ry = rx;
+    ry.data = y;
+    WAMX_LAUNCH(launch_rope_f32(rx, pos, ry, n_dims, freq_base, be->stream));
+}
+
+wamx_status wamx_op_qk_norm_rope(wamx_backend_t be, const void * x, int64_t ldx, const void * w, void * dst,
+                                 int64_t heads, int64_t head_dim, int64_t tokens, int64_t dst_tokens, int64_t tok0,
+                                 int rope_mode, const int32_t * pos0, const int32_t * pos1, const int32_t * pos2,
+                                 float eps, float freq_base) {
+    WAMX_REQUIRE(be && x && w && dst, "wamx_op_qk_norm_rope: null argument");
+    WAMX_REQUIRE(rope_mode >= 0 && rope_mode <= 2, "wamx_op_qk_norm_rope: rope mode");
+    WAMX_REQUIRE(rope_mode == 2 || pos0, "wamx_op_qk_norm_rope: positions required");
+    WAMX_REQUIRE(rope_mode != 1 || (pos1 && pos2 && head_dim == 128), "wamx_op_qk_norm_rope: 3-D positions");
+    WAMX_REQUIRE(tok0 >= 0 && tok0 + tokens <= dst_tokens, "wamx_op_qk_norm_rope: token range");
+    WAMX_LAUNCH(launch_qk_norm_rope(x, ldx, w, dst, heads, head_dim, tokens, dst_tokens, tok0, rope_mode, pos0, pos1,
+                                    pos2, eps, freq_base, be->stream));
+}
+
+wamx_status wamx_op_joint_attn(wamx_backend_t be, const void * q, const void * k_a, const void * vt_a, int64_t na,
+                               const void * k_b, const void * vt_b, int64_t nb, int64_t na_split, void * out,
+                               int64_t heads, int64_t head_dim, int64_t tq, float scale) {
+    WAMX_REQUIRE(be && q && k_a && vt_a && out, "wamx_op_joint_attn: null argument");
+    WAMX_REQUIRE(head_dim == 128, "wamx_op_joint_attn: head_dim must be 128");
+    WAMX_REQUIRE(na % 4 == 0 && (!k_b || nb % 4 == 0),
+                 "wamx_op_joint_attn: key counts must be multiples of 4 (pad V^T rows)");
+    AttnArgs a;
+    a.q = q;
+    a.k_a = k_a;
+    a.vt_a = vt_a;
+    a.na = na;
+    a.vt_ld_a = na;
+    a.k_b = k_b;
+    a.vt_b = vt_b;
+    a.nb = k_b ? nb : 0;
+    a.vt_ld_b = a.nb;
+    a.na_split = na_split;
+    a.out = out;
+    a.heads = heads;
+    a.head_dim = head_dim;
+    a.tq = tq;
+    a.scale = scale;
+    a.counters = be->counters + kCounters;
+    a.max_counters = kCounters;
+    WAMX_REQUIRE(attn_workspace_bytes(a) <= kWorkspaceBytes, "wamx_op_joint_attn: workspace too small");
+    WAMX_LAUNCH(launch_joint_attn(a, be->workspace, be->stream));
+}
+
+wamx_status wamx_op_soft_max_f32(wamx_backend_t be, const float * x, float * y, int64_t rows, int64_t cols, float scale) {
+    WAMX_REQUIRE(be && x && y && cols > 0, "wamx_op_soft_max_f32: bad arguments");
+    TensorRef rx{(void *) x, WAMX_TYPE_F32, {cols, rows, 1, 1}, {4, 4 * cols, 4 * cols * rows, 4 * cols * rows}};
+    TensorRef ry = rx;
+    ry.data = y;
+    WAMX_LAUNCH(launch_softmax_f32(rx, ry, scale, be->stream));
+}
+
+wamx_status wamx_fill_normal(wamx_backend_t be, void * dst, int32_t type, int64_t n, uint64_t seed, float mean,
+                             float stdv) {
+    WAMX_REQUIRE(be && dst, "wamx_fill_normal: null argument");
+    WAMX_LAUNCH(launch_fill_normal(dst, type, n, seed, mean, stdv, be->stream));
+}
+
+void * wamx_device_malloc(wamx_backend_t be, size_t size) {
+    if (!be) return nullptr;
+    hipSetDevice(be->dev->index);
+    void * p = nullptr;
+    if (hipMalloc(&p, std::max<size_t>(size, 1)) != hipSuccess) {
+        set_errorf("hipMalloc(%zu) failed", size);
+        return nullptr;
+    }
+    return p;
+}
+void wamx_device_free(wamx_backend_t, void * p) {
+    if (p) hipFree(p);
+}
+wamx_status wamx_memcpy_h2d(wamx_backend_t be, void * dst, const void * src, size_t size) {
+    WAMX_REQUIRE(be, "null backend");
+    WAMX_HIP_TRY(hipMemcpy(dst, src, size, hipMemcpyHostToDevice));
+    return WAMX_STATUS_SUCCESS;
+}
+wamx_status wamx_memcpy_d2h(wamx_backend_t be, void * dst, const void * src, size_t size) {
+    WAMX_REQUIRE(be, "null backend");
+    WAMX_HIP_TRY(hipStreamSynchronize(be->stream));
+    WAMX_HIP_TRY(hipMemcpy(dst, src, size, hipMemcpyDeviceToHost));
+    return WAMX_STATUS_SUCCESS;
+}
+
+struct wamx_timer {
+    wamx_backend * be;
+    hipEvent_t a, b;
+};
+wamx_timer_t wamx_timer_new(wamx_backend_t be) {
+    if (!be) return nullptr;
+    auto * t = new wamx_timer{be, nullptr, nullptr};
+    hipEventCreate(&t->a);
+    hipEventCreate(&t->b);
+    return t;
+}
+void wamx_timer_start(wamx_timer_t t) {
+    if (t) hipEventRecord(t->a, t->be->stream);
+}
+float wamx_timer_stop_ms(wamx_timer_t t) {
+    if (!t) return -1.0f;
+    hipEventRecord(t->b, t->be->stream);
+    hipEventSynchronize(t->b);
+    float ms = -1.0f;
+    hipEventElapsedTime(&ms, t->a, t->b);
+    return ms;
+}
+void wamx_timer_free(wamx_timer_t t) {
+    if (!t) return;
+    hipEventDestroy(t->a);
+    hipEventDestroy(t->b);
+    delete t;
+}
+
+}  // extern "C"
+
+static void * reg_get_proc_address(wamx_backend_reg_t, const char * name) {
+    if (!name) return nullptr;
+    if (!strcmp(name, "wamx_backend_graph_compute")) return (void *) &wamx_backend_graph_compute;
+    if (!strcmp(name, "wamx_backend_supports_op")) return (void *) &wamx_backend_supports_op;
+    if (!strcmp(name, "wamx_backend_init")) return (void *) &wamx_backend_init;
+    return nullptr;
+}

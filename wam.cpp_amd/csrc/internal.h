@@ -1,0 +1,118 @@
+// Internal declarations of libwamx: kernel launchers and backend internals.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace wamx {
+
+const char * last_error_cstr();
+
+// ---------------------------------------------------------------------------
+// GEMM: y[b][n][m] = sum_k w[b/r][m][k] * x[b][n][k]  (the ggml MUL_MAT layout:
+// both operands K-contiguous, "NT").  w is bf16 (or f32 for the SIMT path),
+// x is bf16 or f32 (rounded to bf16 on load when w is bf16).
+// ---------------------------------------------------------------------------
+struct GemmArgs {
+    const void * w = nullptr;
+    int32_t w_type = WAMX_TYPE_BF16;
+    int64_t ldw = 0, w_bs2 = 0, w_bs3 = 0;   // element strides
+    const void * x = nullptr;
+    int32_t x_type = WAMX_TYPE_BF16;
+    int64_t ldx = 0, x_bs2 = 0, x_bs3 = 0;
+    void * y = nullptr;
+    int32_t y_type = WAMX_TYPE_F32;
+    int64_t ldy = 0, y_bs2 = 0, y_bs3 = 0;
+    int64_t M = 0, N = 0, K = 0;
+    int64_t B2 = 1, B3 = 1;                  // batches of y / x
+    int64_t r2 = 1, r3 = 1;                  // broadcast ratio: w batch = b / r
+    int32_t epi = WAMX_EPI_NONE;             // wamx_linear_epilogue
+    const void * bias = nullptr;             // bf16 [M]
+    const void * res = nullptr;              // bf16 [N][ldres]
+    int64_t ldres = 0;
+    const float * gate = nullptr;            // f32 [M]
+    void * ws = nullptr;                     // split-K partials (skinny path)
+    size_t ws_bytes = 0;
+    unsigned * counters = nullptr;           // split-K arrival counters, zero between launches
+    int64_t max_counters = 0;
+};
+
+hipError_t launch_gemm(const GemmArgs & a, hipStream_t s);
+
+// ---------------------------------------------------------------------------
+// Row-wise norms (bf16 / f32), bias+GELU, gated residuals.
+// ---------------------------------------------------------------------------
+hipError_t launch_norm_mod_bf16(const void * x, int64_t ldx, const void * scale, const void * shift, int32_t ss_type,
+                                int64_t ss, void * y, int64_t ldy, int64_t rows, int64_t cols, float eps, bool affine,
+                                hipStream_t s);
+hipError_t launch_rms_norm_bf16_f32(const void * x, int64_t ldx, const void * w, float * y, int64_t ldy, int64_t rows,
+                                    int64_t cols, float eps, hipStream_t s);
+hipError_t launch_norm_mod_f32(const float * x, int64_t ldx, const float * scale, const float * shift, int64_t ss,
+                               float * y, int64_t rows, int64_t cols, float eps, hipStream_t s);
+hipError_t launch_norm_f32(const float * x, int64_t ldx, float * y, int64_t ldy, int64_t rows, int64_t cols, float eps,
+                           bool rms, hipStream_t s);
+hipError_t launch_gated_residual_bf16(const void * h, int64_t ldh, const void * b, int64_t ldb, const void * g,
+                                      int32_t g_type, int64_t gs, void * y, int64_t rows, int64_t cols, hipStream_t s);
+hipError_t launch_gated_residual_f32(const float * r, int64_t ldr, const float * b, int64_t ldb, const float * g,
+                                     int64_t gs, float * y, int64_t rows, int64_t cols, hipStream_t s);
+hipError_t launch_bias_gelu_bf16(const void * x, const void * bias, void * y, int64_t n, int64_t width, hipStream_t s);
+
+// ---------------------------------------------------------------------------
+// Generic strided tensor kernels (ggml glue ops).  A TensorRef describes a
+// 4-D strided view: data + ne[] + byte strides nb[] + type.
+// ---------------------------------------------------------------------------
+struct TensorRef {
+    void * data;
+    int32_t type;
+    int64_t ne[4];
+    int64_t nb[4];
+};
+TensorRef ref_of(const wamx_tensor * t);
+
+// dst[i] = convert(src[i]) elementwise over dst's shape; src broadcast by modulo.
+hipError_t launch_copy(const TensorRef & src, const TensorRef & dst, hipStream_t s);
+// dst = a (op) b with b broadcast (ggml bin_bcast).  op: 0 add, 1 mul, 2 repeat b.
+hipError_t launch_binary(int op, const TensorRef & a, const TensorRef & b, const TensorRef & dst, hipStream_t s);
+// dst = unary(a) (0 gelu-tanh, 1 gelu-erf, 2 silu) or scale (op 3, with scale).
+hipError_t launch_unary(int op, const TensorRef & a, const TensorRef & dst, float scale, hipStream_t s);
+hipError_t launch_concat(const TensorRef & a, const TensorRef & b, const TensorRef & dst, int dim, hipStream_t s);
+hipError_t launch_get_rows(const TensorRef & a, const int32_t * rows, const TensorRef & dst, hipStream_t s);
+hipError_t launch_softmax_f32(const TensorRef & x, const TensorRef & y, float scale, hipStream_t s);
+hipError_t launch_rope_f32(const TensorRef & x, const int32_t * pos, const TensorRef & y, int n_dims, float freq_base,
+                           hipStream_t s);
+hipError_t launch_modulation(const void * mod, int32_t mod_type, const void * tables, int32_t tab_type, float * out,
+                             int64_t per_layer, int64_t layers, hipStream_t s);
+
+// ---------------------------------------------------------------------------
+// Fused attention-side kernels.
+// ---------------------------------------------------------------------------
+hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void * dst, int64_t heads, int64_t head_dim,
+                               int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode, const int32_t * pos0,
+                               const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s);
+
+struct AttnArgs {
+    const void * q = nullptr;      // bf16 [H][Tq][dh]
+    const void * k_a = nullptr;    // bf16 [H][na][dh]
+    const void * vt_a = nullptr;   // bf16 [H][dh][vt_ld_a]
+    int64_t na = 0, vt_ld_a = 0;
+    const void * k_b = nullptr;    // bf16 [H][nb][dh] or null
+    const void * vt_b = nullptr;   // bf16 [H][dh][vt_ld_b]
+    int64_t nb = 0, vt_ld_b = 0;
+    int64_t na_split = 0;          // reference key order: a[0,na_split), b, a[na_split,na)
+    void * out = nullptr;          // bf16 [Tq][H*dh]
+    int64_t heads = 0, head_dim = 0, tq = 0;
+    float scale = 1.0f;
+    unsigned * counters = nullptr; // split-KV arrival counters, zero between launches
+    int64_t max_counters = 0;
+};
+// Needs a workspace for split-KV partials; ws/ws_bytes from attn_workspace_bytes.
+size_t attn_workspace_bytes(const AttnArgs & a);
+hipError_t launch_joint_attn(const AttnArgs & a, void * ws, hipStream_t s);
+
+// Synthetic N(mean, std) fill: splitmix64(seed ^ index) -> Box-Muller.
+hipError_t launch_fill_normal(void * dst, int32_t type, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
+hipError_t launch_fill_f32(float * dst, int64_t n, float v, hipStream_t s);
+
+}  // namespace wamx

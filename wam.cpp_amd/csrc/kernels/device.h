@@ -1,0 +1,80 @@
+// Device-side helpers shared by the HIP kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wamx {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t) h << 16); }
+
+// Round-to-nearest-even f32 -> bf16, NaN kept quiet (same rule as the host helper).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t) ((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t) (u >> 16);
+}
+
+// The value a bf16 store of f would read back as.
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return (uint32_t) f32_to_bf16(lo) | ((uint32_t) f32_to_bf16(hi) << 16);
+}
+
+// GELU, tanh form of Hendrycks & Gimpel (arXiv:1606.08415):
+// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float kSqrt2OverPi = 0.7978845608028654f;
+    const float kCubic = 0.044715f;
+    return 0.5f * x * (1.0f + tanhf(kSqrt2OverPi * x * (1.0f + kCubic * x * x)));
+}
+
+// GELU with the exact Gaussian CDF: 0.5 x (1 + erf(x / sqrt 2)).
+__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024).  `red` needs
+// blockDim.x/64 floats of shared memory.  Every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float * red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
+__device__ __forceinline__ float load_as_f32(const void * p, int32_t type, int64_t i) {
+    if (type == 0) return ((const float *) p)[i];
+    if (type == 30) return bf16_to_f32(((const uint16_t *) p)[i]);
+    if (type == 26) return (float) ((const int32_t *) p)[i];
+    return (float) ((const _Float16 *) p)[i];
+}
+__device__ __forceinline__ void store_from_f32(void * p, int32_t type, int64_t i, float v) {
+    if (type == 0) ((float *) p)[i] = v;
+    else if (type == 30) ((uint16_t *) p)[i] = f32_to_bf16(v);
+    else if (type == 26) ((int32_t *) p)[i] = (int32_t) v;
+    else ((_Float16 *) p)[i] = (_Float16) v;
+}
+
+}  // namespace wamx

@@ -1,0 +1,314 @@
+// Strided glue kernels for the ggml ops the engine's graphs contain besides
+// the fused hot path (CPY/CONT/DUP, ADD/MUL with broadcast, SCALE, unary
+// GELU/GELU_ERF/SILU, CONCAT, GET_ROWS, SOFT_MAX, ROPE), the per-layer adaLN
+// modulation sum, and the seeded synthetic-weight generator.
+//
+// Tensors are 4-D strided views (ne[], byte strides nb[]); one thread per
+// destination element, index decomposed in ne[0]-fastest order so consecutive
+// threads touch consecutive destination elements.
+#include "../internal.h"
+#include "device.h"
+
+namespace wamx {
+
+struct Ref4 {
+    char * data;
+    int32_t type;
+    int64_t ne0, ne1, ne2, ne3;
+    int64_t nb0, nb1, nb2, nb3;
+};
+
+static Ref4 to_ref4(const TensorRef & t) {
+    return Ref4{(char *) t.data, t.type, t.ne[0], t.ne[1], t.ne[2], t.ne[3], t.nb[0], t.nb[1], t.nb[2], t.nb[3]};
+}
+
+__device__ __forceinline__ void unravel(int64_t i, const Ref4 & r, int64_t & i0, int64_t & i1, int64_t & i2,
+                                        int64_t & i3) {
+    i0 = i % r.ne0;
+    i /= r.ne0;
+    i1 = i % r.ne1;
+    i /= r.ne1;
+    i2 = i % r.ne2;
+    i3 = i / r.ne2;
+}
+
+__device__ __forceinline__ char * at(const Ref4 & r, int64_t i0, int64_t i1, int64_t i2, int64_t i3) {
+    return r.data + i0 * r.nb0 + i1 * r.nb1 + i2 * r.nb2 + i3 * r.nb3;
+}
+
+__device__ __forceinline__ float ld(const Ref4 & r, const char * p) {
+    switch (r.type) {
+        case WAMX_TYPE_F32: return *(const float *) p;
+        case WAMX_TYPE_BF16: return bf16_to_f32(*(const uint16_t *) p);
+        case WAMX_TYPE_I32: return (float) *(const int32_t *) p;
+        default: return (float) *(const _Float16 *) p;
+    }
+}
+__device__ __forceinline__ void st(const Ref4 & r, char * p, float v) {
+    switch (r.type) {
+        case WAMX_TYPE_F32: *(float *) p = v; break;
+        case WAMX_TYPE_BF16: *(uint16_t *) p = f32_to_bf16(v); break;
+        case WAMX_TYPE_I32: *(int32_t *) p = (int32_t) v; break;
+        default: *(_Float16 *) p = (_Float16) v; break;
+    }
+}
+
+// Element k of src (in its own ne0-fastest order) goes to element k of dst.
+__global__ void copy_kernel(Ref4 src, Ref4 dst, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t a0, a1, a2, a3, b0, b1, b2, b3;
+    unravel(i, src, a0, a1, a2, a3);
+    unravel(i, dst, b0, b1, b2, b3);
+    const char * ps = at(src, a0, a1, a2, a3);
+    char * pd = at(dst, b0, b1, b2, b3);
+    if (src.type == dst.type) {
+        if (src.type == WAMX_TYPE_F32 || src.type == WAMX_TYPE_I32) *(uint32_t *) pd = *(const uint32_t *) ps;
+        else *(uint16_t *) pd = *(const uint16_t *) ps;
+    } else {
+        st(dst, pd, ld(src, ps));
+    }
+}
+
+__global__ void binary_kernel(int op, Ref4 a, Ref4 b, Ref4 dst, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t i0, i1, i2, i3;
+    unravel(i, dst, i0, i1, i2, i3);
+    const float y = ld(b, at(b, i0 % b.ne0, i1 % b.ne1, i2 % b.ne2, i3 % b.ne3));
+    if (op == 2) {  // REPEAT: dst = b broadcast
+        st(dst, at(dst, i0, i1, i2, i3), y);
+        return;
+    }
+    const float x = ld(a, at(a, i0, i1, i2, i3));
+    st(dst, at(dst, i0, i1, i2, i3), op == 0 ? x + y : x * y);
+}
+
+__global__ void unary_kernel(int op, Ref4 a, Ref4 dst, float scale, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t i0, i1, i2, i3;
+    unravel(i, dst, i0, i1, i2, i3);
+    const float x = ld(a, at(a, i0, i1, i2, i3));
+    float y;
+    switch (op) {
+        case 0: y = gelu_tanh(x); break;
+        case 1: y = gelu_erf(x); break;
+        case 2: y = silu(x); break;
+        default: y = x * scale; break;
+    }
+    st(dst, at(dst, i0, i1, i2, i3), y);
+}
+
+__global__ void concat_kernel(Ref4 a, Ref4 b, Ref4 dst, int dim, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t c[4];
+    unravel(i, dst, c[0], c[1], c[2], c[3]);
+    const int64_t ane[4] = {a.ne0, a.ne1, a.ne2, a.ne3};
+    const char * src;
+    if (c[dim] < ane[dim]) {
+        src = at(a, c[0], c[1], c[2], c[3]);
+    } else {
+        c[dim] -= ane[dim];
+        src = at(b, c[0], c[1], c[2], c[3]);
+        c[dim] += ane[dim];
+    }
+    char * d = at(dst, c[0], c[1], c[2], c[3]);
+    if (dst.type == WAMX_TYPE_F32 || dst.type == WAMX_TYPE_I32) *(uint32_t *) d = *(const uint32_t *) src;
+    else *(uint16_t *) d = *(const uint16_t *) src;
+}
+
+// dst[i0, i1, i2] = a[i0, rows[i1, i2], i2 % a.ne2]
+__global__ void get_rows_kernel(Ref4 a, const int32_t * rows, int64_t rows_ld, Ref4 dst, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t i0, i1, i2, i3;
+    unravel(i, dst, i0, i1, i2, i3);
+    const int64_t r = rows[i1 + i2 * rows_ld];
+    st(dst, at(dst, i0, i1, i2, i3), ld(a, at(a, i0, r, i2 % a.ne2, i3 % a.ne3)));
+}
+
+// SOFT_MAX_EXT without mask: y = exp(s*x - max) / sum over ne0.  One
+// workgroup per row.
+__global__ __launch_bounds__(256) void softmax_kernel(Ref4 x, Ref4 y, float scale) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const int64_t r1 = row % x.ne1, r2 = (row / x.ne1) % x.ne2, r3 = row / (x.ne1 * x.ne2);
+    const char * xr = at(x, 0, r1, r2, r3);
+    char * yr = at(y, 0, r1, r2, r3);
+    float mx = -INFINITY;
+    for (int64_t c = threadIdx.x; c < x.ne0; c += 256) mx = fmaxf(mx, *(const float *) (xr + c * x.nb0) * scale);
+    mx = wave_max(mx);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sum = 0.0f;
+    for (int64_t c = threadIdx.x; c < x.ne0; c += 256) {
+        const float e = expf(*(const float *) (xr + c * x.nb0) * scale - mx);
+        *(float *) (yr + c * y.nb0) = e;
+        sum += e;
+    }
+    sum = block_sum(sum, red);
+    const float inv = 1.0f / sum;
+    for (int64_t c = threadIdx.x; c < x.ne0; c += 256) *(float *) (yr + c * y.nb0) *= inv;
+}
+
+// ROPE mode NORMAL on [head_dim, heads, tokens(, ne3)]: pairs (2i, 2i+1) for
+// 2i < n_dims rotate by pos[token] * theta_scale^i; the rest is copied.
+__global__ void rope_kernel(Ref4 x, const int32_t * pos, Ref4 y, int n_dims, float theta_scale, int64_t npairs) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= npairs) return;
+    const int64_t half = (x.ne0 + 1) / 2;
+    const int64_t ip = i % half;
+    int64_t rest = i / half;
+    const int64_t i1 = rest % x.ne1;
+    rest /= x.ne1;
+    const int64_t i2 = rest % x.ne2, i3 = rest / x.ne2;
+    const int64_t e = 2 * ip;
+    const char * px = at(x, e, i1, i2, i3);
+    char * py = at(y, e, i1, i2, i3);
+    const float a = *(const float *) px;
+    if (e + 1 >= x.ne0) {
+        *(float *) py = a;
+        return;
+    }
+    const float b = *(const float *) (px + x.nb0);
+    if (e < n_dims) {
+        const float theta = (float) pos[i2] * powf(theta_scale, (float) ip);
+        float sn, cs;
+        sincosf(theta, &sn, &cs);
+        *(float *) py = a * cs - b * sn;
+        *(float *) (py + y.nb0) = a * sn + b * cs;
+    } else {
+        *(float *) py = a;
+        *(float *) (py + y.nb0) = b;
+    }
+}
+
+// out[l][j] = f32(mod[j]) + f32(tables[l][j])  (modulation_add, mot.cpp:137-145).
+__global__ void modulation_kernel(const void * mod, int32_t mod_type, const void * tables, int32_t tab_type, float * out,
+                                  int64_t per_layer, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t j = i % per_layer;
+    out[i] = load_as_f32(mod, mod_type, j) + load_as_f32(tables, tab_type, i);
+}
+
+// splitmix64 (Steele, Lea, Flood: "Fast splittable pseudorandom number
+// generators", OOPSLA 2014) on seed + (i+1)*golden gamma, then Box-Muller
+// with two 24-bit uniforms in (0, 1).
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ void fill_normal_kernel(void * dst, int32_t type, int64_t n, uint64_t seed, float mean, float stdv) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t z = splitmix64(seed + (uint64_t) (i + 1) * 0x9E3779B97F4A7C15ull);
+    const float u1 = ((float) (z >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    const float u2 = ((float) ((z >> 16) & 0xFFFFFFull) + 0.5f) * (1.0f / 16777216.0f);
+    const float r = sqrtf(-2.0f * logf(u1));
+    const float v = mean + stdv * r * cosf(6.283185307179586f * u2);
+    if (type == WAMX_TYPE_F32) ((float *) dst)[i] = v;
+    else ((uint16_t *) dst)[i] = f32_to_bf16(v);
+}
+
+__global__ void fill_f32_kernel(float * dst, int64_t n, float v) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = v;
+}
+
+// ---------------------------------------------------------------------------
+static int64_t nel(const TensorRef & t) { return t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3]; }
+static dim3 grid1d(int64_t n) { return dim3((unsigned) ((n + 255) / 256)); }
+
+hipError_t launch_copy(const TensorRef & src, const TensorRef & dst, hipStream_t s) {
+    const int64_t n = nel(dst);
+    if (n <= 0) return hipSuccess;
+    if (nel(src) != n) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(copy_kernel, grid1d(n), dim3(256), 0, s, to_ref4(src), to_ref4(dst), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_binary(int op, const TensorRef & a, const TensorRef & b, const TensorRef & dst, hipStream_t s) {
+    const int64_t n = nel(dst);
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(binary_kernel, grid1d(n), dim3(256), 0, s, op, to_ref4(a), to_ref4(b), to_ref4(dst), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_unary(int op, const TensorRef & a, const TensorRef & dst, float scale, hipStream_t s) {
+    const int64_t n = nel(dst);
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(unary_kernel, grid1d(n), dim3(256), 0, s, op, to_ref4(a), to_ref4(dst), scale, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_concat(const TensorRef & a, const TensorRef & b, const TensorRef & dst, int dim, hipStream_t s) {
+    const int64_t n = nel(dst);
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(concat_kernel, grid1d(n), dim3(256), 0, s, to_ref4(a), to_ref4(b), to_ref4(dst), dim, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_get_rows(const TensorRef & a, const int32_t * rows, const TensorRef & dst, hipStream_t s) {
+    const int64_t n = nel(dst);
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(get_rows_kernel, grid1d(n), dim3(256), 0, s, to_ref4(a), rows, dst.ne[1], to_ref4(dst), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax_f32(const TensorRef & x, const TensorRef & y, float scale, hipStream_t s) {
+    const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(softmax_kernel, dim3((unsigned) rows), dim3(256), 0, s, to_ref4(x), to_ref4(y), scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_f32(const TensorRef & x, const int32_t * pos, const TensorRef & y, int n_dims, float freq_base,
+                           hipStream_t s) {
+    const int64_t npairs = (x.ne[0] + 1) / 2 * x.ne[1] * x.ne[2] * x.ne[3];
+    if (npairs <= 0) return hipSuccess;
+    const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
+    hipLaunchKernelGGL(rope_kernel, grid1d(npairs), dim3(256), 0, s, to_ref4(x), pos, to_ref4(y), n_dims, theta_scale,
+                       npairs);
+    return hipGetLastError();
+}
+
+hipError_t launch_modulation(const void * mod, int32_t mod_type, const void * tables, int32_t tab_type, float * out,
+                             int64_t per_layer, int64_t layers, hipStream_t s) {
+    const int64_t n = per_layer * layers;
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(modulation_kernel, grid1d(n), dim3(256), 0, s, mod, mod_type, tables, tab_type, out, per_layer, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(void * dst, int32_t type, int64_t n, uint64_t seed, float mean, float stdv, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (type != WAMX_TYPE_F32 && type != WAMX_TYPE_BF16) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(fill_normal_kernel, grid1d(n), dim3(256), 0, s, dst, type, n, seed, mean, stdv);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_f32(float * dst, int64_t n, float v, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_f32_kernel, grid1d(n), dim3(256), 0, s, dst, n, v);
+    return hipGetLastError();
+}
+
+TensorRef ref_of(const wamx_tensor * t) {
+    TensorRef r;
+    r.data = t->data;
+    r.type = t->type;
+    for (int i = 0; i < 4; ++i) {
+        r.ne[i] = t->ne[i];
+        r.nb[i] = (int64_t) t->nb[i];
+    }
+    return r;
+}
+
+}  // namespace wamx
