@@ -166,15 +166,138 @@ def workload_ffn(be, args):
             "roofline": roof, "cpu_baseline": cpu}
 
 
-WORKLOADS = {"ffn": workload_ffn, "gemm": workload_gemm}
+def _gwp_inputs(cfg, seed):
+    import oracle
+    A, T = cfg["action_dim"], cfg["action_chunk"]
+    return (oracle.fill_normal(A, seed + 1), oracle.fill_normal(cfg["z_dim"] * 4 * cfg["grid_h"] * cfg["grid_w"], seed + 2),
+            oracle.fill_normal(cfg["n_lang"] * cfg["t5_hidden"], seed + 3), oracle.fill_normal(T * A, seed + 4))
+
+
+def _read_weights(be, m, keep):
+    out = {}
+    lib = be.lib
+    for i in range(lib.wamx_gwp_n_weights(m)):
+        name = lib.wamx_gwp_weight_name(m, i).decode()
+        if not keep(name):
+            continue
+        t = lib.wamx_gwp_weight(m, name.encode())
+        n = lib.wamx_nelements(t)
+        a = np.empty(n, np.uint16)
+        wamx.check(lib.wamx_backend_tensor_get(t, a.ctypes.data, 0, n * 2), name)
+        out[name] = a
+    return out
+
+
+def workload_chunk(be, args):
+    """Full synthetic GWP-0.5-shaped action chunk: prompt projection, prefix
+    pass over 1 state + 3x1024 visual tokens with 512 prompt tokens, then 10
+    flow-matching denoise steps of the 48-token action expert, 30 layers at
+    width 3072 (24x128 heads, FFN 14336) in both experts."""
+    import ctypes as C
+    import oracle
+    lib = be.lib
+    c = lib.wamx_gwp_default_config()
+    cfg = {k: getattr(c, k) for k, _ in wamx.GwpConfig._fields_}
+    m = lib.wamx_gwp_create(be.ptr, C.byref(c))
+    if not m:
+        raise RuntimeError(wamx.last_error())
+    wamx.check(lib.wamx_gwp_init_synthetic(m, 0x5EED0003, 0.02), "init_synthetic")
+    state, latent, prompt, noise = _gwp_inputs(cfg, 0x5EED0003)
+    wamx.check(lib.wamx_gwp_set_inputs(m, state.ctypes.data, latent.ctypes.data, prompt.ctypes.data,
+                                       noise.ctypes.data), "set_inputs")
+    tm = wamx.GwpTiming()
+    for _ in range(max(1, args.warmup)):
+        wamx.check(lib.wamx_gwp_predict(m, None), "predict")
+    be.sync()
+    phases = np.zeros(3)
+    t = wamx.Timer(be)
+    t.start()
+    for _ in range(args.steps):
+        wamx.check(lib.wamx_gwp_predict(m, None), "predict")
+    ms = t.stop_ms() / args.steps
+    for _ in range(3):
+        wamx.check(lib.wamx_gwp_predict(m, C.byref(tm)), "predict")
+        phases += np.array([tm.prompt_ms, tm.prefix_ms, tm.denoise_ms]) / 3
+    action = np.empty(noise.size, np.float32)
+    wamx.check(lib.wamx_gwp_get_action(m, action.ctypes.data), "get_action")
+    if not np.all(np.isfinite(action)):
+        raise RuntimeError("non-finite action chunk")
+    params = int(lib.wamx_gwp_param_count(m))
+    nodes = [int(lib.wamx_gwp_graph_nodes(m, i)) for i in range(3)]
+
+    # Dominant kernel: the visual FFN-up GEMM of the prefix pass (3072 tokens x
+    # W[14336 x 3072], bias + GELU epilogue), timed standalone on the stream.
+    T, D, F = cfg["grid_h"] * cfg["grid_w"], cfg["hidden"], cfg["ffn_dim"]
+    w_up = lib.wamx_gwp_weight(m, b"gwp.blocks.0.visual_expert.ffn.net.0.proj.weight")
+    b_up = lib.wamx_gwp_weight(m, b"gwp.blocks.0.visual_expert.ffn.net.0.proj.bias")
+    dx = be.array(oracle.fill_normal(T * D, 5, 0.0, 1.0, oracle.BF16))
+    dy = be.empty(T * F * 2)
+
+    def up():
+        wamx.check(lib.wamx_op_linear(be.ptr, w_up.contents.data, dx.ptr, wamx.TYPE_BF16, b_up.contents.data,
+                                      wamx.EPI_BIAS_GELU, None, None, dy.ptr, F, T, D), "linear")
+    up_ms = time_op(be, up, 20)
+    flops = 2.0 * T * D * F
+    # The 48-token FFN-up of the action expert (HBM-bound weight streaming).
+    w_aup = lib.wamx_gwp_weight(m, b"gwp.blocks.0.action_expert.ffn.net.0.proj.weight")
+    b_aup = lib.wamx_gwp_weight(m, b"gwp.blocks.0.action_expert.ffn.net.0.proj.bias")
+    Ta, Da, Fa = cfg["action_chunk"], cfg["action_hidden"], cfg["action_ffn_dim"]
+    dxa = be.array(oracle.fill_normal(Ta * Da, 6, 0.0, 1.0, oracle.BF16))
+    dya = be.empty(Ta * Fa * 2)
+
+    def aup():
+        wamx.check(lib.wamx_op_linear(be.ptr, w_aup.contents.data, dxa.ptr, wamx.TYPE_BF16, b_aup.contents.data,
+                                      wamx.EPI_BIAS_GELU, None, None, dya.ptr, Fa, Ta, Da), "linear")
+    aup_ms = time_op(be, aup, 50)
+    aup_bytes = Fa * Da * 2 + Ta * Da * 2 + Ta * Fa * 2 + Fa * 2
+    roof = {"bound": "mfma", "achieved": flops / (up_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": flops / (up_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "traffic": None,
+            "kernel": "gemm_tile: prefix visual FFN-up 3072 tok x [14336 x 3072] + bias + GELU",
+            "kernel_ms": up_ms, "flops_per_launch": flops,
+            "skinny": {"kernel": "gemm_skinny: denoise FFN-up 48 tok x [14336 x 3072] + bias + GELU",
+                       "kernel_ms": aup_ms, "achieved_gbs": aup_bytes / (aup_ms * 1e-3) / 1e9,
+                       "frac_hbm": aup_bytes / (aup_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}}
+
+    # CPU baseline: the oracle on layer 0 (prompt K/V, prefix layer, one
+    # denoise step) at full width, scaled by layers and steps.
+    L, S = cfg["n_layers"], cfg["num_steps"]
+    w = _read_weights(be, m, lambda n: not n.startswith("gwp.blocks.") or n.startswith("gwp.blocks.0.")
+                      or "scale_shift_table" in n)
+    lib.wamx_gwp_free(m)
+    ref = oracle.Gwp(cfg, w)
+    t0 = time.perf_counter()
+    ref.prompt(prompt, layers=1)
+    t1 = time.perf_counter()
+    ref.prefix(state, latent, prompt, layers=1)
+    t2 = time.perf_counter()
+    ref.denoise(noise, layers=1, steps=1)
+    t3 = time.perf_counter()
+    ref.close()
+    cpu_ms = ((t1 - t0) + (t2 - t1)) * 1e3 * L + (t3 - t2) * 1e3 * L * S
+    cores, model = cpu_info()
+    cpu = {"value": cpu_ms, "unit": "ms per action chunk", "cores": oracle.num_threads(), "kind": "port",
+           "sample": f"layer 0 only (prompt K/V + prefix layer + 1 denoise step, {(t3 - t0):.1f} s), scaled x{L} "
+                     f"layers and x{S} steps, on {model} ({cores} logical CPUs)"}
+    return {"metric": "ms per action chunk (GWP-0.5-shape MoT, bf16, 1 GPU); GEMM % of MFMA peak", "unit": "ms",
+            "value": ms, "ms_per_step": ms, "higher_is_better": False, "dtype": "bf16",
+            "config": {"workload": "GWP-0.5-shaped MoT action chunk: 30 layers, d=3072, 24x128 heads, FFN 14336, "
+                                   "prefix 1 state + 3x1024 visual tokens, 512 prompt tokens, 10 denoise steps on "
+                                   "a 48x32 action chunk, batch 1",
+                       "params": params, "graph_nodes": nodes,
+                       "phase_ms": {"prompt": phases[0], "prefix": phases[1], "denoise": phases[2]},
+                       "gemm_mfma_frac": roof["frac"]},
+            "roofline": roof, "cpu_baseline": cpu}
+
+
+WORKLOADS = {"chunk": workload_chunk, "ffn": workload_ffn, "gemm": workload_gemm}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="ffn", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="chunk", choices=sorted(WORKLOADS))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "

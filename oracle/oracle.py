@@ -250,3 +250,98 @@ def fill_normal(n: int, seed: int, mean=0.0, std=1.0, dtype=F32) -> np.ndarray:
     out = np.empty(n, np.float32 if dtype == F32 else np.uint16)
     load().orc_fill_normal(_p(out), dtype, n, seed & (2**64 - 1), mean, std)
     return out
+
+
+# ---------------------------------------------------------------------------
+# Full MoT step (oracle_mot.c)
+# ---------------------------------------------------------------------------
+class GwpConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "n_layers", "hidden", "n_heads", "head_dim", "ffn_dim", "action_hidden", "action_ffn_dim",
+        "action_chunk", "action_dim", "grid_h", "grid_w", "n_lang", "t5_hidden", "z_dim",
+        "num_steps", "enc_hidden")] + [("shift", C.c_float), ("eps", C.c_float)]
+
+
+_WEIGHT_FN = C.CFUNCTYPE(C.c_void_p, C.c_void_p, C.c_char_p)
+
+
+class Gwp:
+    """CPU restatement of the synthetic GWP-0.5 MoT over named bf16 weights."""
+
+    def __init__(self, cfg: dict, weights: dict):
+        lib = load()
+        for name, res, args in (
+                ("orc_gwp_new", C.c_void_p, [C.POINTER(GwpConfig), _WEIGHT_FN, C.c_void_p]),
+                ("orc_gwp_free", None, [C.c_void_p]),
+                ("orc_gwp_prompt", C.c_int, [C.c_void_p, C.c_void_p, C.c_int]),
+                ("orc_gwp_prefix", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]),
+                ("orc_gwp_denoise", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
+                ("orc_gwp_prefix_key", C.c_void_p, [C.c_void_p, C.c_int]),
+                ("orc_gwp_prefix_value", C.c_void_p, [C.c_void_p, C.c_int]),
+                ("orc_gwp_prompt_key", C.c_void_p, [C.c_void_p, C.c_int]),
+                ("orc_gwp_action_prompt", C.c_void_p, [C.c_void_p])):
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        self.lib = lib
+        self.cfg = dict(cfg)
+        self.weights = {k.encode(): np.ascontiguousarray(v, np.uint16) for k, v in weights.items()}
+
+        def lookup(_user, name):
+            a = self.weights.get(name)
+            return None if a is None else a.ctypes.data
+
+        self._cb = _WEIGHT_FN(lookup)
+        c = GwpConfig(**{k: self.cfg[k] for k, _ in GwpConfig._fields_})
+        self.ptr = lib.orc_gwp_new(C.byref(c), self._cb, None)
+        c_ = self.cfg
+        self.d = c_["n_heads"] * c_["head_dim"]
+        self.P = 1 + c_["grid_h"] * c_["grid_w"]
+
+    def close(self):
+        if self.ptr:
+            self.lib.orc_gwp_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prompt(self, prompt, layers=0):
+        p = _c(prompt, np.float32)
+        if self.lib.orc_gwp_prompt(self.ptr, _p(p), layers) != 0:
+            raise RuntimeError("oracle prompt projection failed (missing weight)")
+
+    def prefix(self, state, latent, prompt, layers=0):
+        s, lt, p = _c(state, np.float32), _c(latent, np.float32), _c(prompt, np.float32)
+        if self.lib.orc_gwp_prefix(self.ptr, _p(s), _p(lt), _p(p), layers) != 0:
+            raise RuntimeError("oracle prefix failed (missing weight)")
+
+    def denoise(self, noise, layers=0, steps=0):
+        n = _c(noise, np.float32)
+        out = np.empty_like(n)
+        if self.lib.orc_gwp_denoise(self.ptr, _p(n), _p(out), layers, steps) != 0:
+            raise RuntimeError("oracle denoise failed (missing weight)")
+        return out
+
+    def _arr(self, ptr, shape):
+        n = int(np.prod(shape))
+        return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_uint16)), shape=(n,)).reshape(shape).copy()
+
+    def prefix_key(self, layer):
+        c = self.cfg
+        return self._arr(self.lib.orc_gwp_prefix_key(self.ptr, layer), (c["n_heads"], self.P, c["head_dim"]))
+
+    def prefix_value(self, layer):
+        c = self.cfg
+        return self._arr(self.lib.orc_gwp_prefix_value(self.ptr, layer), (c["n_heads"], c["head_dim"], self.P))
+
+    def prompt_key(self, layer):
+        c = self.cfg
+        return self._arr(self.lib.orc_gwp_prompt_key(self.ptr, layer), (c["n_heads"], c["n_lang"], c["head_dim"]))
+
+    def action_prompt(self):
+        c = self.cfg
+        return self._arr(self.lib.orc_gwp_action_prompt(self.ptr), (c["n_lang"], c["action_hidden"]))

@@ -1,0 +1,47 @@
+/*
+ * oracle_mot — CPU restatement of the synthetic GWP-0.5 MoT action step
+ * (test infrastructure only; see oracle.h for the rules).
+ */
+#ifndef WAMX_ORACLE_MOT_H
+#define WAMX_ORACLE_MOT_H
+
+#include <stdarg.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same fields and meaning as wamx_gwp_config. */
+typedef struct orc_gwp_config {
+    int32_t n_layers, hidden, n_heads, head_dim, ffn_dim, action_hidden, action_ffn_dim, action_chunk, action_dim;
+    int32_t grid_h, grid_w, n_lang, t5_hidden, z_dim, num_steps, enc_hidden;
+    float shift, eps;
+} orc_gwp_config;
+
+/* Returns the bf16 array of the named weight (names as in the wamx driver:
+ * gwp.blocks.<l>.<expert>.attn1.to_qkv.weight, ...), or NULL. */
+typedef const uint16_t * (*orc_weight_fn)(void * user, const char * name);
+
+typedef struct orc_gwp orc_gwp;
+
+orc_gwp * orc_gwp_new(const orc_gwp_config * cfg, orc_weight_fn wf, void * user);
+void      orc_gwp_free(orc_gwp * g);
+/* prompt f32 [n_lang][t5_hidden] -> action prompt and per-layer prompt K/V. */
+/* layers > 0 limits the per-layer prompt K/V to the first `layers` blocks. */
+int orc_gwp_prompt(orc_gwp * g, const float * prompt, int layers);
+/* state f32 [action_dim], latent f32 [z][2gh][2gw], prompt as above.
+ * layers > 0 limits the pass to the first `layers` blocks (timing samples). */
+int orc_gwp_prefix(orc_gwp * g, const float * state, const float * latent, const float * prompt, int layers);
+/* noise f32 [chunk][action_dim] -> action f32; layers/steps > 0 limit the work. */
+int orc_gwp_denoise(orc_gwp * g, const float * noise, float * action_out, int layers, int steps);
+const uint16_t * orc_gwp_prefix_key(orc_gwp * g, int layer);    /* [H][P][dh] */
+const uint16_t * orc_gwp_prefix_value(orc_gwp * g, int layer);  /* [H][dh][P] */
+const uint16_t * orc_gwp_prompt_key(orc_gwp * g, int layer);    /* [H][n_lang][dh] */
+const uint16_t * orc_gwp_action_prompt(orc_gwp * g);            /* [n_lang][action_hidden] */
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

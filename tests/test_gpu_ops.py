@@ -254,5 +254,5 @@ def test_softmax_and_fill(wx, be, orc, rng):
     # Same algorithm in f32 (device) and f64 (oracle) math: agreement to a few
     # f32 ulps, a little more in the tails where log(u1) amplifies rounding.
     assert np.max(np.abs(got - ref) / np.maximum(1.0, np.abs(ref))) < 1e-4
-    assert np.mean(np.abs(got - ref) > 1e-6 * np.maximum(1.0, np.abs(ref))) < 1e-3
+    assert np.mean(np.abs(got - ref) > 1e-6 * np.maximum(1.0, np.abs(ref))) < 1e-2
     assert cosine(got, ref) > 0.999999

@@ -21,8 +21,7 @@
 using namespace wamx;
 
 static constexpr size_t kAlign = 256;
-static constexpr size_t kWorkspaceBytes = 96ull << 20;   // split-K / split-KV partials
-static constexpr int64_t kCounters = 1 << 15;            // per user (GEMM, attention)
+static constexpr size_t kWorkspaceBytes = 64ull << 20;  // K-split GEMM partials
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -53,8 +52,7 @@ struct GraphCacheEntry {
 struct wamx_backend {
     wamx_device * dev = nullptr;
     hipStream_t stream = nullptr;
-    void * workspace = nullptr;        // device scratch for split-K / split-KV partials
-    unsigned * counters = nullptr;     // 2 * kCounters arrival counters, zero between launches
+    void * workspace = nullptr;  // K-split partials, reused by consecutive GEMMs on the stream
     bool use_graphs = true;
     std::unordered_map<uint64_t, GraphCacheEntry> graphs;
 };
@@ -184,8 +182,6 @@ static hipError_t run_mul_mat(wamx_backend * be, const wamx_tensor * node) {
     g.r3 = b->ne[3] / a->ne[3];
     g.ws = be->workspace;
     g.ws_bytes = kWorkspaceBytes;
-    g.counters = be->counters;
-    g.max_counters = kCounters;
     return launch_gemm(g, be->stream);
 }
 
@@ -212,8 +208,6 @@ static hipError_t run_linear(wamx_backend * be, const wamx_tensor * node) {
     g.gate = node->src[4] ? (const float *) node->src[4]->data : nullptr;
     g.ws = be->workspace;
     g.ws_bytes = kWorkspaceBytes;
-    g.counters = be->counters;
-    g.max_counters = kCounters;
     return launch_gemm(g, be->stream);
 }
 
@@ -243,10 +237,7 @@ static hipError_t run_joint_attn(wamx_backend * be, const wamx_tensor * node) {
     a.head_dim = q->ne[0];
     a.tq = q->ne[1];
     a.scale = param_f32(node, 1);
-    a.counters = be->counters + kCounters;
-    a.max_counters = kCounters;
-    if (attn_workspace_bytes(a) > kWorkspaceBytes) return hipErrorInvalidValue;
-    return launch_joint_attn(a, be->workspace, be->stream);
+    return launch_joint_attn(a, be->stream);
 }
 
 static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
@@ -317,6 +308,10 @@ static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
             return launch_unary(node->op_params[0], ref_of(s0), ref_of(node), 1.0f, s);
         case WAMX_OP_GET_ROWS:
             return launch_get_rows(ref_of(s0), (const int32_t *) s1->data, ref_of(node), s);
+        case WAMX_OP_IM2COL: {
+            const int32_t * pp = node->op_params;
+            return launch_im2col(ref_of(s1), ref_of(node), pp[7], pp[8], pp[0], pp[1], pp[2], pp[3], pp[4], pp[5], s);
+        }
         case WAMX_OP_LINEAR:
             return run_linear(be, node);
         case WAMX_OP_QK_NORM_ROPE: {
@@ -387,6 +382,7 @@ static bool supports(const wamx_tensor * t) {
         case WAMX_OP_UNARY:
             if (t->src[1]) return s0->type == WAMX_TYPE_BF16 && wamx_is_contiguous(s0);
             return ok_type(s0) && t->op_params[0] >= 0 && t->op_params[0] <= 2;
+        case WAMX_OP_IM2COL:
         case WAMX_OP_LINEAR:
         case WAMX_OP_QK_NORM_ROPE:
         case WAMX_OP_JOINT_ATTN:
@@ -624,7 +620,10 @@ static bool gallocr_alloc(wamx_gallocr * ga, wamx_cgraph * g) {
         }
         int & lu = last_use[r];
         lu = std::max(lu, i);
-        if ((r->flags & (WAMX_TENSOR_FLAG_OUTPUT | WAMX_TENSOR_FLAG_INPUT)) || r->op == WAMX_OP_NONE) lu = kForever;
+        // Graph inputs and outputs stay put; unallocated leaves without the
+        // input flag are scratch (written in place by a later node) and are
+        // recycled after their last reader like any intermediate.
+        if (r->flags & (WAMX_TENSOR_FLAG_OUTPUT | WAMX_TENSOR_FLAG_INPUT)) lu = kForever;
         if (t->flags & WAMX_TENSOR_FLAG_OUTPUT) lu = kForever;
     };
     for (int i = 0; i < n; ++i) {
@@ -641,7 +640,7 @@ static bool gallocr_alloc(wamx_gallocr * ga, wamx_cgraph * g) {
         if (last_use[t] < n) frees[last_use[t]].push_back(t);
     auto size_of = [](wamx_tensor * t) { return align_up(wamx_nbytes(t), kAlign); };
     for (auto * t : order)
-        if (first_def[t] == 0 || t->op == WAMX_OP_NONE) offset[t] = fl.alloc(size_of(t));
+        if (first_def[t] == 0 || (t->flags & WAMX_TENSOR_FLAG_INPUT)) offset[t] = fl.alloc(size_of(t));
     for (int i = 0; i < n; ++i) {
         wamx_tensor * node = wamx_graph_node(g, i);
         for (int k = 0; k < WAMX_MAX_SRC; ++k) {
@@ -708,10 +707,7 @@ wamx_backend_t wamx_backend_init(int device) {
     be->use_graphs = !(env && env[0] && env[0] != '0');
     // A blocking stream, so synchronous tensor_set/get on the null stream are
     // ordered with the graph work (default priority).
-    if (hipStreamCreate(&be->stream) != hipSuccess || hipMalloc(&be->workspace, kWorkspaceBytes) != hipSuccess ||
-        hipMalloc((void **) &be->counters, 2 * kCounters * sizeof(unsigned)) != hipSuccess ||
-        hipMemset(be->counters, 0, 2 * kCounters * sizeof(unsigned)) != hipSuccess ||
-        hipDeviceSynchronize() != hipSuccess) {
+    if (hipStreamCreate(&be->stream) != hipSuccess || hipMalloc(&be->workspace, kWorkspaceBytes) != hipSuccess) {
         set_error("wamx_backend_init: stream or workspace allocation failed");
         be_free(be);
         return nullptr;
@@ -725,7 +721,6 @@ static void be_free(wamx_backend_t be) {
     if (be->stream) hipStreamSynchronize(be->stream);
     for (auto & kv : be->graphs) release_graph(kv.second);
     if (be->workspace) hipFree(be->workspace);
-    if (be->counters) hipFree(be->counters);
     if (be->stream) hipStreamDestroy(be->stream);
     delete be;
 }
@@ -839,8 +834,6 @@ wamx_status wamx_op_mul_mat(wamx_backend_t be, const void * w, int64_t ldw, cons
     g.K = K;
     g.ws = be->workspace;
     g.ws_bytes = kWorkspaceBytes;
-    g.counters = be->counters;
-    g.max_counters = kCounters;
     WAMX_LAUNCH(launch_gemm(g, be->stream));
 }
 
@@ -872,8 +865,6 @@ wamx_status wamx_op_linear(wamx_backend_t be, const void * w, const void * x, in
     g.gate = gate;
     g.ws = be->workspace;
     g.ws_bytes = kWorkspaceBytes;
-    g.counters = be->counters;
-    g.max_counters = kCounters;
     WAMX_LAUNCH(launch_gemm(g, be->stream));
 }
 
@@ -969,10 +960,7 @@ wamx_status wamx_op_joint_attn(wamx_backend_t be, const void * q, const void * k
     a.head_dim = head_dim;
     a.tq = tq;
     a.scale = scale;
-    a.counters = be->counters + kCounters;
-    a.max_counters = kCounters;
-    WAMX_REQUIRE(attn_workspace_bytes(a) <= kWorkspaceBytes, "wamx_op_joint_attn: workspace too small");
-    WAMX_LAUNCH(launch_joint_attn(a, be->workspace, be->stream));
+    WAMX_LAUNCH(launch_joint_attn(a, be->stream));
 }
 
 wamx_status wamx_op_soft_max_f32(wamx_backend_t be, const float * x, float * y, int64_t rows, int64_t cols, float scale) {

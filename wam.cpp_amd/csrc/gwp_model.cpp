@@ -1,0 +1,689 @@
+// Synthetic GWP-0.5-shaped Mixture-of-Transformers driver.
+//
+// Builds the three graphs wam.cpp submits per request in its BF16 latency
+// profile and runs them through this backend's graph_compute:
+//   1. prompt projection: action text embedder + per-layer cross-attention
+//      K/V of the prompt (src/models/gwp05/engine/cache.cpp:53-137),
+//   2. prefix pass: state token through the action expert and the visual
+//      tokens through the visual expert, joint self-attention, per-layer K/V
+//      written to the resident prefix cache (cache.cpp:139-485),
+//   3. unrolled denoise: num_steps flow-matching steps of the action expert
+//      attending [state, action, reference] keys and the cached prompt K/V
+//      (mot.cpp:358-594).
+// Op order and bf16 rounding points follow those files; the fused ops of this
+// backend (LINEAR, QK_NORM_ROPE, JOINT_ATTN, MODULATION) replace the unfused
+// ggml subgraphs with the same rounding points.
+#include <math.h>
+#include <stdio.h>
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+using namespace wamx;
+
+namespace {
+
+struct Mlp3 {  // action/state encoder and action decoder (mot.cpp:16-55)
+    wamx_tensor *in_w, *in_b, *mid_w, *mid_b, *out_w, *out_b;
+};
+
+struct Cond {  // condition embedder (mot.cpp:63-99)
+    wamx_tensor *t1_w, *t1_b, *t2_w, *t2_b, *tp_w, *tp_b, *x1_w, *x1_b, *x2_w, *x2_b;
+};
+
+struct ExpertLayer {  // one expert of one MoT block
+    wamx_tensor *qkv_w, *qkv_b, *norm_q, *norm_k, *o_w, *o_b;
+    wamx_tensor *n2_w, *n2_b;
+    wamx_tensor *cq_w, *cq_b, *ck_w, *ck_b, *cv_w, *cv_b, *cnq, *cnk, *co_w, *co_b;
+    wamx_tensor *up_w, *up_b, *dn_w, *dn_b;
+};
+
+uint64_t fnv1a(const std::string & s) {
+    uint64_t h = 1469598103934665603ull;
+    for (unsigned char c : s) {
+        h ^= c;
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+struct wamx_gwp_model {
+    wamx_backend_t be = nullptr;
+    wamx_gwp_config cfg{};
+    int64_t P = 0, Ppad = 0, nimg = 0, NLpad = 0, Tpad = 0;
+
+    wamx_context * wctx = nullptr;
+    wamx_buffer_t wbuf = nullptr;
+    std::vector<std::pair<std::string, wamx_tensor *>> weights;
+    std::map<std::string, wamx_tensor *> by_name;
+
+    wamx_tensor *patch_w = nullptr, *patch_b = nullptr, *action_sst = nullptr;
+    wamx_tensor *a_tables = nullptr, *v_tables = nullptr;  // [d, 6, L] bf16
+    Mlp3 state_enc{}, action_enc{}, action_dec{};
+    Cond acond{}, vcond{};
+    std::vector<ExpertLayer> act, vis;
+
+    // Resident storage (prefix / prompt caches) and inputs.
+    wamx_context * sctx = nullptr;
+    wamx_buffer_t sbuf = nullptr;
+    wamx_tensor * action_prompt = nullptr;
+    std::vector<wamx_tensor *> pk, pv_raw, pv;    // prefix K [dh,P,H]; V^T [Ppad,dh,H] and its [P,dh,H] view
+    std::vector<wamx_tensor *> lk, lv_raw, lv;    // prompt K [dh,NL,H]; V^T
+    wamx_tensor *in_state = nullptr, *in_latent = nullptr, *in_prompt = nullptr, *in_action = nullptr;
+    wamx_tensor *in_apos = nullptr, *in_spos = nullptr, *in_vt = nullptr, *in_vh = nullptr, *in_vw = nullptr;
+    wamx_tensor *in_freq0 = nullptr, *in_freqs = nullptr, *in_dts = nullptr;
+
+    // Graphs: 0 prompt, 1 prefix, 2 denoise.
+    wamx_context * gctx[3] = {nullptr, nullptr, nullptr};
+    wamx_cgraph * graph[3] = {nullptr, nullptr, nullptr};
+    wamx_gallocr_t galloc[3] = {nullptr, nullptr, nullptr};
+    wamx_tensor * action_out = nullptr;
+    wamx_timer_t timer = nullptr;
+
+    ~wamx_gwp_model() {
+        for (int i = 0; i < 3; ++i) {
+            wamx_gallocr_free(galloc[i]);
+            wamx_free(gctx[i]);
+        }
+        wamx_timer_free(timer);
+        wamx_buffer_free(sbuf);
+        wamx_free(sctx);
+        wamx_buffer_free(wbuf);
+        wamx_free(wctx);
+    }
+
+    wamx_tensor * add_weight(const std::string & name, int64_t ne0, int64_t ne1 = 1, int64_t ne2 = 1, int64_t ne3 = 1) {
+        wamx_tensor * t = wamx_new_tensor_4d(wctx, WAMX_TYPE_BF16, ne0, ne1, ne2, ne3);
+        if (!t) return nullptr;
+        wamx_set_name(t, name.c_str());
+        weights.push_back({name, t});
+        by_name[name] = t;
+        return t;
+    }
+    // Linear layer [out][in]: ggml ne = {in, out}.
+    void add_linear(const std::string & prefix, int64_t in, int64_t out, wamx_tensor ** w, wamx_tensor ** b) {
+        *w = add_weight(prefix + ".weight", in, out);
+        *b = add_weight(prefix + ".bias", out);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Graph-building helpers (ctx-local)
+// ---------------------------------------------------------------------------
+namespace {
+
+struct Builder {
+    wamx_gwp_model * m;
+    wamx_context * ctx;
+    const wamx_gwp_config & c;
+    float scale;
+
+    Builder(wamx_gwp_model * model, wamx_context * context)
+        : m(model), ctx(context), c(model->cfg), scale(1.0f / sqrtf((float) model->cfg.head_dim)) {}
+
+    wamx_tensor * lin(wamx_tensor * w, wamx_tensor * b, wamx_tensor * x, int epi = WAMX_EPI_BIAS,
+                      wamx_tensor * res = nullptr, wamx_tensor * gate = nullptr) {
+        return wamx_linear(ctx, w, x, b, epi, res, gate);
+    }
+
+    // action_encoder / action_decoder (mot.cpp:16-55): linear + GELU_ERF x2 + linear.
+    wamx_tensor * mlp3(const Mlp3 & p, wamx_tensor * x) {
+        wamx_tensor * h = wamx_gelu_erf(ctx, lin(p.in_w, p.in_b, x));
+        h = wamx_gelu_erf(ctx, lin(p.mid_w, p.mid_b, h));
+        return lin(p.out_w, p.out_b, h);
+    }
+
+    // build_condition time branch (mot.cpp:69-82): temb and the 6-way modulation.
+    void condition(const Cond & p, wamx_tensor * freq, wamx_tensor ** temb, wamx_tensor ** mod) {
+        wamx_tensor * t = lin(p.t1_w, p.t1_b, freq);
+        t = lin(p.t2_w, p.t2_b, wamx_silu(ctx, t));
+        *temb = t;
+        *mod = lin(p.tp_w, p.tp_b, wamx_silu(ctx, t));
+    }
+
+    // build_condition text branch (mot.cpp:84-92): linear + GELU + linear.
+    wamx_tensor * text(const Cond & p, wamx_tensor * prompt) {
+        wamx_tensor * h = wamx_gelu(ctx, lin(p.x1_w, p.x1_b, prompt));
+        return lin(p.x2_w, p.x2_b, h);
+    }
+
+    // View (layer l, part i) of a modulation tensor [width, 6, L] (f32).
+    wamx_tensor * part(wamx_tensor * mods, int64_t width, int l, int i) {
+        return wamx_view_1d(ctx, mods, width, (size_t) ((int64_t) l * 6 + i) * width * sizeof(float));
+    }
+
+    // Column view [ne0 = cols, ne1 = rows] of a packed projection output.
+    wamx_tensor * cols(wamx_tensor * x, int64_t ncols, int64_t off_elems) {
+        return wamx_view_2d(ctx, x, ncols, x->ne[1], x->nb[1], (size_t) off_elems * 2);
+    }
+
+    // V part of a packed [3d, tokens] projection, transposed into a V^T view
+    // [tokens, dh, H] of `dst` (ggml_cont(ggml_permute(v, 1, 2, 0, 3)),
+    // mot.cpp:397-401, written in place as cache.cpp:316-339 stores it).
+    wamx_tensor * store_v(wamx_tensor * qkv, int64_t v_off, wamx_tensor * dst_view) {
+        const int64_t dh = c.head_dim, H = c.n_heads, T = qkv->ne[1];
+        wamx_tensor * v = wamx_view_3d(ctx, qkv, dh, H, T, (size_t) dh * 2, qkv->nb[1], (size_t) v_off * 2);
+        wamx_tensor * vp = wamx_permute(ctx, v, 1, 2, 0, 3);
+        return wamx_cpy(ctx, vp, dst_view);
+    }
+
+    // V^T view of `raw` [ld, dh, H] covering key columns [k0, k0+n).
+    wamx_tensor * vt_view(wamx_tensor * raw, int64_t k0, int64_t n) {
+        return wamx_view_3d(ctx, raw, n, raw->ne[1], raw->ne[2], raw->nb[1], raw->nb[2], (size_t) k0 * 2);
+    }
+
+    // expert_cross_ffn with cached prompt K/V (mot.cpp:284-347, cached branch).
+    wamx_tensor * cross_ffn_cached(const ExpertLayer & e, wamx_tensor * h, wamx_tensor * pk, wamx_tensor * pv,
+                                   wamx_tensor * cshift, wamx_tensor * cscale, wamx_tensor * cgate) {
+        const int64_t T = h->ne[1];
+        wamx_tensor * n = wamx_layer_norm_bf16(ctx, h, e.n2_w, e.n2_b, c.eps);
+        wamx_tensor * q = lin(e.cq_w, e.cq_b, n);
+        wamx_tensor * Q = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, c.head_dim, T, c.n_heads);
+        Q = wamx_qk_norm_rope(ctx, q, e.cnq, Q, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
+        wamx_tensor * att = wamx_joint_attn(ctx, Q, pk, pv, nullptr, nullptr, 0, scale);
+        h = lin(e.co_w, e.co_b, att, WAMX_EPI_BIAS_RESIDUAL, h);
+        return ffn(e, h, cshift, cscale, cgate);
+    }
+
+    // expert_cross_ffn against uncached text (build_attention, text_encoder.cpp:26-73).
+    wamx_tensor * cross_ffn_uncached(const ExpertLayer & e, wamx_tensor * h, wamx_tensor * txt, wamx_tensor * cshift,
+                                     wamx_tensor * cscale, wamx_tensor * cgate) {
+        const int64_t T = h->ne[1], NL = txt->ne[1];
+        wamx_tensor * n = wamx_layer_norm_bf16(ctx, h, e.n2_w, e.n2_b, c.eps);
+        wamx_tensor * q = lin(e.cq_w, e.cq_b, n);
+        wamx_tensor * k = lin(e.ck_w, e.ck_b, txt);
+        wamx_tensor * v = lin(e.cv_w, e.cv_b, txt);
+        wamx_tensor * Q = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, c.head_dim, T, c.n_heads);
+        Q = wamx_qk_norm_rope(ctx, q, e.cnq, Q, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
+        wamx_tensor * K = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, c.head_dim, NL, c.n_heads);
+        K = wamx_qk_norm_rope(ctx, k, e.cnk, K, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
+        wamx_tensor * vraw = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, round_up(NL, 4), c.head_dim, c.n_heads);
+        wamx_tensor * V = store_v(v, 0, vt_view(vraw, 0, NL));
+        wamx_tensor * att = wamx_joint_attn(ctx, Q, K, V, nullptr, nullptr, 0, scale);
+        h = lin(e.co_w, e.co_b, att, WAMX_EPI_BIAS_RESIDUAL, h);
+        return ffn(e, h, cshift, cscale, cgate);
+    }
+
+    // FFN half (mot.cpp:339-346): modulated norm, up + bias + GELU-tanh, down +
+    // bias + gated residual.
+    wamx_tensor * ffn(const ExpertLayer & e, wamx_tensor * h, wamx_tensor * cshift, wamx_tensor * cscale,
+                      wamx_tensor * cgate) {
+        wamx_tensor * n = wamx_norm_modulation_bf16(ctx, h, cscale, cshift, c.eps);
+        wamx_tensor * u = lin(e.up_w, e.up_b, n, WAMX_EPI_BIAS_GELU);
+        return lin(e.dn_w, e.dn_b, u, WAMX_EPI_BIAS_GATED, h, cgate);
+    }
+};
+
+// Make `t` depend on `dep` without reading it (views ignore src[1]).
+wamx_tensor * after(wamx_tensor * t, wamx_tensor * dep) {
+    if (t && dep && t->op == WAMX_OP_VIEW && !t->src[1]) t->src[1] = dep;
+    return t;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Model construction
+// ---------------------------------------------------------------------------
+static bool create_weights(wamx_gwp_model * m) {
+    const wamx_gwp_config & c = m->cfg;
+    const int64_t d = (int64_t) c.n_heads * c.head_dim, da = c.action_hidden, E = c.enc_hidden, A = c.action_dim;
+    const int64_t L = c.n_layers;
+    m->wctx = wamx_init(64 * L + 256);
+    if (!m->wctx) return false;
+    m->patch_w = m->add_weight("gwp.patch_embedding.weight", 2, 2, c.z_dim, d);
+    m->patch_b = m->add_weight("gwp.patch_embedding.bias", d);
+    auto mlp = [&](const std::string & p, int64_t in, int64_t out, Mlp3 & r) {
+        m->add_linear(p + ".in_proj", in, E, &r.in_w, &r.in_b);
+        m->add_linear(p + ".mid_proj", E, E, &r.mid_w, &r.mid_b);
+        m->add_linear(p + ".out_proj", E, out, &r.out_w, &r.out_b);
+    };
+    mlp("gwp.state_encoder", A, da, m->state_enc);
+    mlp("gwp.action_encoder", A, da, m->action_enc);
+    mlp("gwp.action_decoder", da, A, m->action_dec);
+    auto cond = [&](const std::string & p, int64_t w, Cond & r) {
+        m->add_linear(p + ".time_embedder.linear_1", 256, w, &r.t1_w, &r.t1_b);
+        m->add_linear(p + ".time_embedder.linear_2", w, w, &r.t2_w, &r.t2_b);
+        m->add_linear(p + ".time_proj", w, 6 * w, &r.tp_w, &r.tp_b);
+        m->add_linear(p + ".text_embedder.linear_1", c.t5_hidden, w, &r.x1_w, &r.x1_b);
+        m->add_linear(p + ".text_embedder.linear_2", w, w, &r.x2_w, &r.x2_b);
+    };
+    cond("gwp.action_condition_embedder", da, m->acond);
+    cond("gwp.condition_embedder", d, m->vcond);
+    m->action_sst = m->add_weight("gwp.action_scale_shift_table", da, 2);
+    // Per-layer scale_shift_table [6][width] of each expert, packed [width, 6, L].
+    m->a_tables = m->add_weight("gwp.blocks.action_expert.scale_shift_table", da, 6, L);
+    m->v_tables = m->add_weight("gwp.blocks.visual_expert.scale_shift_table", d, 6, L);
+    auto expert = [&](const std::string & p, int64_t w, int64_t ffn, ExpertLayer & e) {
+        m->add_linear(p + ".attn1.to_qkv", w, 3 * d, &e.qkv_w, &e.qkv_b);
+        e.norm_q = m->add_weight(p + ".attn1.norm_q.weight", d);
+        e.norm_k = m->add_weight(p + ".attn1.norm_k.weight", d);
+        m->add_linear(p + ".attn1.to_out.0", d, w, &e.o_w, &e.o_b);
+        e.n2_w = m->add_weight(p + ".norm2.weight", w);
+        e.n2_b = m->add_weight(p + ".norm2.bias", w);
+        m->add_linear(p + ".attn2.to_q", w, d, &e.cq_w, &e.cq_b);
+        m->add_linear(p + ".attn2.to_k", w, d, &e.ck_w, &e.ck_b);
+        m->add_linear(p + ".attn2.to_v", w, d, &e.cv_w, &e.cv_b);
+        e.cnq = m->add_weight(p + ".attn2.norm_q.weight", d);
+        e.cnk = m->add_weight(p + ".attn2.norm_k.weight", d);
+        m->add_linear(p + ".attn2.to_out.0", d, w, &e.co_w, &e.co_b);
+        m->add_linear(p + ".ffn.net.0.proj", w, ffn, &e.up_w, &e.up_b);
+        m->add_linear(p + ".ffn.net.2", ffn, w, &e.dn_w, &e.dn_b);
+    };
+    m->act.resize(L);
+    m->vis.resize(L);
+    for (int64_t l = 0; l < L; ++l) {
+        const std::string b = "gwp.blocks." + std::to_string(l);
+        expert(b + ".action_expert", da, c.action_ffn_dim, m->act[l]);
+        expert(b + ".visual_expert", d, c.ffn_dim, m->vis[l]);
+    }
+    for (auto & kv : m->weights)
+        if (!kv.second) return false;
+    m->wbuf = wamx_backend_alloc_ctx_tensors(m->wctx, m->be);
+    return m->wbuf != nullptr;
+}
+
+static bool create_storage(wamx_gwp_model * m) {
+    const wamx_gwp_config & c = m->cfg;
+    const int64_t dh = c.head_dim, H = c.n_heads, L = c.n_layers;
+    m->sctx = wamx_init(16 * L + 64);
+    if (!m->sctx) return false;
+    wamx_context * s = m->sctx;
+    m->action_prompt = wamx_new_tensor_2d(s, WAMX_TYPE_BF16, c.action_hidden, c.n_lang);
+    for (int64_t l = 0; l < L; ++l) {
+        m->pk.push_back(wamx_new_tensor_3d(s, WAMX_TYPE_BF16, dh, m->P, H));
+        m->pv_raw.push_back(wamx_new_tensor_3d(s, WAMX_TYPE_BF16, m->Ppad, dh, H));
+        m->lk.push_back(wamx_new_tensor_3d(s, WAMX_TYPE_BF16, dh, c.n_lang, H));
+        m->lv_raw.push_back(wamx_new_tensor_3d(s, WAMX_TYPE_BF16, m->NLpad, dh, H));
+    }
+    m->in_state = wamx_new_tensor_2d(s, WAMX_TYPE_F32, c.action_dim, 1);
+    m->in_latent = wamx_new_tensor_4d(s, WAMX_TYPE_F32, 2 * c.grid_w, 2 * c.grid_h, c.z_dim, 1);
+    m->in_prompt = wamx_new_tensor_2d(s, WAMX_TYPE_F32, c.t5_hidden, c.n_lang);
+    m->in_action = wamx_new_tensor_2d(s, WAMX_TYPE_BF16, c.action_dim, c.action_chunk);
+    m->in_apos = wamx_new_tensor_1d(s, WAMX_TYPE_I32, c.action_chunk);
+    m->in_spos = wamx_new_tensor_1d(s, WAMX_TYPE_I32, 1);
+    m->in_vt = wamx_new_tensor_1d(s, WAMX_TYPE_I32, m->nimg);
+    m->in_vh = wamx_new_tensor_1d(s, WAMX_TYPE_I32, m->nimg);
+    m->in_vw = wamx_new_tensor_1d(s, WAMX_TYPE_I32, m->nimg);
+    m->in_freq0 = wamx_new_tensor_2d(s, WAMX_TYPE_F32, 256, 1);
+    m->in_freqs = wamx_new_tensor_2d(s, WAMX_TYPE_F32, 256, c.num_steps);
+    m->in_dts = wamx_new_tensor_1d(s, WAMX_TYPE_F32, c.num_steps);
+    m->sbuf = wamx_backend_alloc_ctx_tensors(s, m->be);
+    if (!m->sbuf) return false;
+    // Views of the padded V^T storage covering the real key columns.
+    for (int64_t l = 0; l < L; ++l) {
+        wamx_tensor * r = m->pv_raw[l];
+        m->pv.push_back(wamx_view_3d(s, r, m->P, dh, H, r->nb[1], r->nb[2], 0));
+        wamx_tensor * q = m->lv_raw[l];
+        m->lv.push_back(wamx_view_3d(s, q, c.n_lang, dh, H, q->nb[1], q->nb[2], 0));
+    }
+    // Zero the storage once so padded V^T columns hold finite values.
+    for (auto * t : m->pv_raw) wamx_backend_tensor_memset(t, 0, 0, wamx_nbytes(t));
+    for (auto * t : m->lv_raw) wamx_backend_tensor_memset(t, 0, 0, wamx_nbytes(t));
+    // Constant inputs: positions (semantics.cpp:210-257), schedule and
+    // timestep embeddings (scheduler.cpp:26-55, text_encoder.cpp:1-12).
+    std::vector<int32_t> apos(c.action_chunk), vt(m->nimg, 0), vh(m->nimg), vw(m->nimg);
+    for (int i = 0; i < c.action_chunk; ++i) apos[i] = i + 1;
+    for (int64_t y = 0; y < c.grid_h; ++y)
+        for (int64_t x = 0; x < c.grid_w; ++x) {
+            vh[y * c.grid_w + x] = (int32_t) y;
+            vw[y * c.grid_w + x] = (int32_t) x;
+        }
+    const int32_t spos = 0;
+    wamx_backend_tensor_set(m->in_apos, apos.data(), 0, apos.size() * 4);
+    wamx_backend_tensor_set(m->in_spos, &spos, 0, 4);
+    wamx_backend_tensor_set(m->in_vt, vt.data(), 0, vt.size() * 4);
+    wamx_backend_tensor_set(m->in_vh, vh.data(), 0, vh.size() * 4);
+    wamx_backend_tensor_set(m->in_vw, vw.data(), 0, vw.size() * 4);
+    auto embed = [](float t, float * out) {
+        for (int i = 0; i < 128; ++i) {
+            const float f = expf(-logf(10000.0f) * (float) i / 128.0f);
+            out[i] = cosf(t * f);
+            out[i + 128] = sinf(t * f);
+        }
+    };
+    std::vector<float> f0(256);
+    embed(0.0f, f0.data());
+    wamx_backend_tensor_set(m->in_freq0, f0.data(), 0, 256 * 4);
+    // Flow-match Euler schedule, f32 endpoint then f64 linspace + shift.
+    const int S = c.num_steps;
+    std::vector<float> sig(S + 1), ts(S), freqs(256 * (size_t) S), dts(S);
+    const float train = 1.0f / 1000.0f;
+    const float smin = c.shift * train / (1.0f + (c.shift - 1.0f) * train);
+    const double tmin = (double) smin * 1000.0;
+    for (int i = 0; i < S; ++i) {
+        const double t = S == 1 ? 1000.0 : 1000.0 + (tmin - 1000.0) * i / (S - 1);
+        const double g = t / 1000.0;
+        sig[i] = (float) ((double) c.shift * g / (1.0 + ((double) c.shift - 1.0) * g));
+        ts[i] = sig[i] * 1000.0f;
+    }
+    sig[S] = 0.0f;
+    for (int i = 0; i < S; ++i) {
+        embed(ts[i], &freqs[256 * (size_t) i]);
+        dts[i] = sig[i + 1] - sig[i];
+    }
+    wamx_backend_tensor_set(m->in_freqs, freqs.data(), 0, freqs.size() * 4);
+    wamx_backend_tensor_set(m->in_dts, dts.data(), 0, dts.size() * 4);
+    return true;
+}
+
+// Graph 1: prompt projection (cache.cpp:53-137, build_cross_kv mot.cpp:101-128).
+static bool build_prompt_graph(wamx_gwp_model * m) {
+    const wamx_gwp_config & c = m->cfg;
+    wamx_context * ctx = m->gctx[0] = wamx_init(64 * c.n_layers + 256);
+    Builder b(m, ctx);
+    wamx_cgraph * g = m->graph[0] = wamx_new_graph(ctx, 64 * c.n_layers + 256);
+    wamx_tensor * txt = b.text(m->acond, m->in_prompt);
+    wamx_build_forward_expand(g, wamx_cpy(ctx, txt, m->action_prompt));
+    const int64_t d = (int64_t) c.n_heads * c.head_dim;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const ExpertLayer & e = m->act[l];
+        wamx_tensor * k = b.lin(e.ck_w, e.ck_b, txt);
+        wamx_tensor * v = b.lin(e.cv_w, e.cv_b, txt);
+        wamx_build_forward_expand(
+            g, wamx_qk_norm_rope(ctx, k, e.cnk, m->lk[l], 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f));
+        (void) d;
+        wamx_build_forward_expand(g, b.store_v(v, 0, b.vt_view(m->lv_raw[l], 0, c.n_lang)));
+    }
+    wamx_graph_assign_uid(g);
+    m->galloc[0] = wamx_gallocr_new(m->be);
+    return m->galloc[0] && wamx_gallocr_alloc_graph(m->galloc[0], g);
+}
+
+// Graph 2: prefix pass (cache.cpp:139-485).
+static bool build_prefix_graph(wamx_gwp_model * m) {
+    const wamx_gwp_config & c = m->cfg;
+    const int64_t d = (int64_t) c.n_heads * c.head_dim, da = c.action_hidden, dh = c.head_dim, H = c.n_heads;
+    const int64_t nimg = m->nimg, P = m->P;
+    wamx_context * ctx = m->gctx[1] = wamx_init(160 * c.n_layers + 512);
+    Builder b(m, ctx);
+    wamx_cgraph * g = m->graph[1] = wamx_new_graph(ctx, 160 * c.n_layers + 512);
+
+    wamx_tensor * sh = b.mlp3(m->state_enc, m->in_state);  // [da, 1]
+    // Patch embedding: conv 2x2 stride 2 as im2col + bf16 MUL_MAT + bias (cache.cpp:203-218).
+    wamx_tensor * cols = wamx_im2col(ctx, m->patch_w, m->in_latent, 2, 2, 0, 0, 1, 1, WAMX_TYPE_BF16);
+    cols = wamx_reshape_2d(ctx, cols, cols->ne[0], nimg);
+    wamx_tensor * pw = wamx_reshape_2d(ctx, m->patch_w, 4 * (int64_t) c.z_dim, d);
+    wamx_tensor * vh = b.lin(pw, m->patch_b, cols);  // [d, nimg]
+
+    wamx_tensor *stemb, *smod, *vtemb, *vmod;
+    b.condition(m->acond, m->in_freq0, &stemb, &smod);
+    // Every visual token has the timestep-0 embedding; its condition rows are
+    // identical, so one row is computed and broadcast (bit-identical).
+    b.condition(m->vcond, m->in_freq0, &vtemb, &vmod);
+    wamx_tensor * vtext = b.text(m->vcond, m->in_prompt);
+    wamx_tensor * amods = wamx_modulation(ctx, smod, m->a_tables);  // [da, 6, L] f32
+    wamx_tensor * vmods = wamx_modulation(ctx, vmod, m->v_tables);  // [d, 6, L] f32
+
+    for (int l = 0; l < c.n_layers; ++l) {
+        const ExpertLayer & ea = m->act[l];
+        const ExpertLayer & ev = m->vis[l];
+        wamx_tensor * sn = wamx_norm_modulation_bf16(ctx, sh, b.part(amods, da, l, 1), b.part(amods, da, l, 0), c.eps);
+        wamx_tensor * sqkv = b.lin(ea.qkv_w, ea.qkv_b, sn);
+        wamx_tensor * vn = wamx_norm_modulation_bf16(ctx, vh, b.part(vmods, d, l, 1), b.part(vmods, d, l, 0), c.eps);
+        wamx_tensor * vqkv = b.lin(ev.qkv_w, ev.qkv_b, vn);
+        // Q [dh, P, H] and K (prefix storage) in [state, visual] order: 1-D rope at
+        // position 0 for the state, 3-D {44,42,42} rope for the visual tokens.
+        wamx_tensor * Q = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, dh, P, H);
+        Q = wamx_qk_norm_rope(ctx, b.cols(sqkv, d, 0), ea.norm_q, Q, 0, 0, m->in_spos, nullptr, nullptr, c.eps, 10000.0f);
+        Q = wamx_qk_norm_rope(ctx, b.cols(vqkv, d, 0), ev.norm_q, Q, 1, 1, m->in_vt, m->in_vh, m->in_vw, c.eps,
+                              10000.0f);
+        wamx_tensor * K = wamx_qk_norm_rope(ctx, b.cols(sqkv, d, d), ea.norm_k, m->pk[l], 0, 0, m->in_spos, nullptr,
+                                            nullptr, c.eps, 10000.0f);
+        K = wamx_qk_norm_rope(ctx, b.cols(vqkv, d, d), ev.norm_k, K, 1, 1, m->in_vt, m->in_vh, m->in_vw, c.eps,
+                              10000.0f);
+        wamx_tensor * v0 = b.store_v(sqkv, 2 * d, b.vt_view(m->pv_raw[l], 0, 1));
+        wamx_tensor * v1 = b.store_v(vqkv, 2 * d, after(b.vt_view(m->pv_raw[l], 1, nimg), v0));
+        wamx_tensor * V = after(b.vt_view(m->pv_raw[l], 0, P), v1);
+        wamx_set_output(K);
+        wamx_set_output(V);
+        wamx_build_forward_expand(g, K);
+        wamx_build_forward_expand(g, V);
+        if (l + 1 == c.n_layers) break;  // the last layer's K/V are the outputs
+        wamx_tensor * att = wamx_joint_attn(ctx, Q, K, V, nullptr, nullptr, 0, b.scale);  // [d, P]
+        wamx_tensor * satt = wamx_view_2d(ctx, att, d, 1, att->nb[1], 0);
+        wamx_tensor * vatt = wamx_view_2d(ctx, att, d, nimg, att->nb[1], att->nb[1]);
+        sh = b.lin(ea.o_w, ea.o_b, satt, WAMX_EPI_BIAS_GATED, sh, b.part(amods, da, l, 2));
+        vh = b.lin(ev.o_w, ev.o_b, vatt, WAMX_EPI_BIAS_GATED, vh, b.part(vmods, d, l, 2));
+        sh = b.cross_ffn_cached(ea, sh, m->lk[l], m->lv[l], b.part(amods, da, l, 3), b.part(amods, da, l, 4),
+                                b.part(amods, da, l, 5));
+        vh = b.cross_ffn_uncached(ev, vh, vtext, b.part(vmods, d, l, 3), b.part(vmods, d, l, 4),
+                                  b.part(vmods, d, l, 5));
+    }
+    wamx_graph_assign_uid(g);
+    m->galloc[1] = wamx_gallocr_new(m->be);
+    return m->galloc[1] && wamx_gallocr_alloc_graph(m->galloc[1], g);
+}
+
+// Graph 3: unrolled denoise (mot.cpp:498-594 over build_cached_action_body).
+static bool build_denoise_graph(wamx_gwp_model * m) {
+    const wamx_gwp_config & c = m->cfg;
+    const int64_t da = c.action_hidden, dh = c.head_dim, H = c.n_heads, T = c.action_chunk;
+    const int64_t d = dh * H;
+    wamx_context * ctx = m->gctx[2] = wamx_init((size_t) (40 * c.n_layers + 64) * c.num_steps + 64);
+    Builder b(m, ctx);
+    wamx_cgraph * g = m->graph[2] = wamx_new_graph(ctx, (size_t) (40 * c.n_layers + 64) * c.num_steps + 64);
+    wamx_tensor * action = m->in_action;  // bf16 [A, T]
+    for (int s = 0; s < c.num_steps; ++s) {
+        wamx_tensor * freq = wamx_view_2d(ctx, m->in_freqs, 256, 1, m->in_freqs->nb[1], (size_t) s * 256 * 4);
+        wamx_tensor * dt = wamx_view_1d(ctx, m->in_dts, 1, (size_t) s * 4);
+        wamx_tensor * h = b.mlp3(m->action_enc, action);  // [da, T]
+        wamx_tensor *temb, *mod;
+        b.condition(m->acond, freq, &temb, &mod);
+        wamx_tensor * mods = wamx_modulation(ctx, mod, m->a_tables);  // [da, 6, L]
+        for (int l = 0; l < c.n_layers; ++l) {
+            const ExpertLayer & e = m->act[l];
+            wamx_tensor * n = wamx_norm_modulation_bf16(ctx, h, b.part(mods, da, l, 1), b.part(mods, da, l, 0), c.eps);
+            wamx_tensor * qkv = b.lin(e.qkv_w, e.qkv_b, n);
+            wamx_tensor * Q = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, dh, T, H);
+            Q = wamx_qk_norm_rope(ctx, b.cols(qkv, d, 0), e.norm_q, Q, 0, 0, m->in_apos, nullptr, nullptr, c.eps,
+                                  10000.0f);
+            wamx_tensor * Ka = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, dh, T, H);
+            Ka = wamx_qk_norm_rope(ctx, b.cols(qkv, d, d), e.norm_k, Ka, 0, 0, m->in_apos, nullptr, nullptr, c.eps,
+                                   10000.0f);
+            wamx_tensor * vraw = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, m->Tpad, dh, H);
+            wamx_tensor * Va = b.store_v(qkv, 2 * d, b.vt_view(vraw, 0, T));
+            // Keys [state, action, reference]: prefix cache split after the state token.
+            wamx_tensor * att = wamx_joint_attn(ctx, Q, m->pk[l], m->pv[l], Ka, Va, 1, b.scale);
+            h = b.lin(e.o_w, e.o_b, att, WAMX_EPI_BIAS_GATED, h, b.part(mods, da, l, 2));
+            h = b.cross_ffn_cached(e, h, m->lk[l], m->lv[l], b.part(mods, da, l, 3), b.part(mods, da, l, 4),
+                                   b.part(mods, da, l, 5));
+        }
+        // Output modulation: f32(action_scale_shift_table) + f32(temb) (mot.cpp:468-486).
+        wamx_tensor * tab = wamx_reshape_3d(ctx, m->action_sst, da, 1, 2);
+        wamx_tensor * om = wamx_modulation(ctx, temb, tab);  // [da, 1, 2]: row 0 shift, row 1 scale
+        wamx_tensor * oshift = wamx_view_1d(ctx, om, da, 0);
+        wamx_tensor * oscale = wamx_view_1d(ctx, om, da, (size_t) da * 4);
+        wamx_tensor * n = wamx_norm_modulation_bf16(ctx, h, oscale, oshift, c.eps);
+        wamx_tensor * pred = b.mlp3(m->action_dec, n);  // bf16 [A, T]
+        // scheduler_step (weights.cpp:885-902): bf16(f32(a) + f32(v) * dt).
+        wamx_tensor * a32 = wamx_cast(ctx, action, WAMX_TYPE_F32);
+        wamx_tensor * v32 = wamx_cast(ctx, pred, WAMX_TYPE_F32);
+        action = wamx_cast(ctx, wamx_add(ctx, a32, wamx_mul(ctx, v32, dt)), WAMX_TYPE_BF16);
+    }
+    m->action_out = action;
+    wamx_set_output(action);
+    wamx_build_forward_expand(g, action);
+    wamx_graph_assign_uid(g);
+    m->galloc[2] = wamx_gallocr_new(m->be);
+    return m->galloc[2] && wamx_gallocr_alloc_graph(m->galloc[2], g);
+}
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+wamx_gwp_config wamx_gwp_default_config(void) {
+    wamx_gwp_config c{};
+    c.n_layers = 30;
+    c.hidden = 3072;
+    c.n_heads = 24;
+    c.head_dim = 128;
+    c.ffn_dim = 14336;
+    c.action_hidden = 3072;
+    c.action_ffn_dim = 14336;
+    c.action_chunk = 48;
+    c.action_dim = 32;
+    c.grid_h = 32;  // 3 camera views of 32x32 visual tokens side by side
+    c.grid_w = 96;
+    c.n_lang = 512;
+    c.t5_hidden = 4096;
+    c.z_dim = 48;
+    c.num_steps = 10;
+    c.enc_hidden = 128;
+    c.shift = 5.0f;
+    c.eps = 1e-6f;
+    return c;
+}
+
+wamx_gwp_t wamx_gwp_create(wamx_backend_t be, const wamx_gwp_config * cfg) {
+    clear_error();
+    if (!be || !cfg) {
+        set_error("wamx_gwp_create: null argument");
+        return nullptr;
+    }
+    const wamx_gwp_config & c = *cfg;
+    if (c.n_layers < 1 || c.n_heads < 1 || c.head_dim != 128 || c.hidden != c.n_heads * c.head_dim ||
+        c.action_hidden < 1 || c.ffn_dim < 1 || c.action_ffn_dim < 1 || c.action_chunk < 1 || c.action_chunk > 64 ||
+        c.action_dim < 1 || c.grid_h < 1 || c.grid_w < 1 || c.n_lang < 1 || c.t5_hidden < 1 || c.z_dim < 1 ||
+        c.num_steps < 1 || c.enc_hidden < 1 || !(c.shift > 0.0f) || !(c.eps >= 0.0f)) {
+        set_error("wamx_gwp_create: invalid configuration (head_dim 128, hidden = heads*128, chunk <= 64)");
+        return nullptr;
+    }
+    auto m = std::make_unique<wamx_gwp_model>();
+    m->be = be;
+    m->cfg = c;
+    m->nimg = (int64_t) c.grid_h * c.grid_w;
+    m->P = 1 + m->nimg;
+    m->Ppad = round_up(m->P, 8);
+    m->NLpad = round_up(c.n_lang, 8);
+    m->Tpad = round_up(c.action_chunk, 8);
+    if (!create_weights(m.get())) {
+        set_errorf("wamx_gwp_create: weight allocation failed: %s", wamx_last_error());
+        return nullptr;
+    }
+    if (!create_storage(m.get())) {
+        set_errorf("wamx_gwp_create: cache allocation failed: %s", wamx_last_error());
+        return nullptr;
+    }
+    if (!build_prompt_graph(m.get()) || !build_prefix_graph(m.get()) || !build_denoise_graph(m.get())) {
+        set_errorf("wamx_gwp_create: graph construction failed: %s", wamx_last_error());
+        return nullptr;
+    }
+    m->timer = wamx_timer_new(be);
+    return m.release();
+}
+
+void wamx_gwp_free(wamx_gwp_t m) { delete m; }
+int wamx_gwp_n_weights(wamx_gwp_t m) { return m ? (int) m->weights.size() : 0; }
+const char * wamx_gwp_weight_name(wamx_gwp_t m, int i) {
+    return (m && i >= 0 && i < (int) m->weights.size()) ? m->weights[i].first.c_str() : nullptr;
+}
+wamx_tensor * wamx_gwp_weight(wamx_gwp_t m, const char * name) {
+    if (!m || !name) return nullptr;
+    auto it = m->by_name.find(name);
+    return it == m->by_name.end() ? nullptr : it->second;
+}
+uint64_t wamx_gwp_param_count(wamx_gwp_t m) {
+    uint64_t n = 0;
+    if (m)
+        for (auto & kv : m->weights) n += (uint64_t) wamx_nelements(kv.second);
+    return n;
+}
+
+wamx_status wamx_gwp_init_synthetic(wamx_gwp_t m, uint64_t seed, float wstd) {
+    WAMX_REQUIRE(m, "wamx_gwp_init_synthetic: null model");
+    for (auto & kv : m->weights) {
+        const std::string & n = kv.first;
+        float mean = 0.0f, sd = wstd;
+        auto ends = [&](const char * s) {
+            const size_t k = strlen(s);
+            return n.size() >= k && n.compare(n.size() - k, k, s) == 0;
+        };
+        if (ends(".bias")) {
+            sd = 0.02f;
+        } else if (ends("norm_q.weight") || ends("norm_k.weight") || ends("norm2.weight")) {
+            mean = 1.0f;
+            sd = 0.02f;
+        } else if (n.find("scale_shift_table") != std::string::npos) {
+            sd = 0.1f;
+        }
+        const wamx_status st = wamx_fill_normal(m->be, kv.second->data, WAMX_TYPE_BF16, wamx_nelements(kv.second),
+                                                seed ^ fnv1a(n), mean, sd);
+        if (st != WAMX_STATUS_SUCCESS) return st;
+    }
+    wamx_backend_synchronize(m->be);
+    return WAMX_STATUS_SUCCESS;
+}
+
+wamx_status wamx_gwp_set_inputs(wamx_gwp_t m, const float * state, const float * latent, const float * prompt,
+                                const float * noise) {
+    WAMX_REQUIRE(m && state && latent && prompt && noise, "wamx_gwp_set_inputs: null argument");
+    wamx_status st = wamx_backend_tensor_set(m->in_state, state, 0, wamx_nbytes(m->in_state));
+    if (st == WAMX_STATUS_SUCCESS) st = wamx_backend_tensor_set(m->in_latent, latent, 0, wamx_nbytes(m->in_latent));
+    if (st == WAMX_STATUS_SUCCESS) st = wamx_backend_tensor_set(m->in_prompt, prompt, 0, wamx_nbytes(m->in_prompt));
+    if (st != WAMX_STATUS_SUCCESS) return st;
+    // The action state is bf16 in the native profile (mot.cpp:523-525, set_f32_tensor).
+    const int64_t n = wamx_nelements(m->in_action);
+    std::vector<uint16_t> a(n);
+    for (int64_t i = 0; i < n; ++i) a[i] = f32_to_bf16_host(noise[i]);
+    return wamx_backend_tensor_set(m->in_action, a.data(), 0, n * 2);
+}
+
+static wamx_status run_graph(wamx_gwp_t m, int which) {
+    WAMX_REQUIRE(m && m->graph[which], "wamx_gwp: graph %d missing", which);
+    return wamx_backend_graph_compute(m->be, m->graph[which]);
+}
+wamx_status wamx_gwp_run_prompt(wamx_gwp_t m) { return run_graph(m, 0); }
+wamx_status wamx_gwp_run_prefix(wamx_gwp_t m) { return run_graph(m, 1); }
+wamx_status wamx_gwp_run_denoise(wamx_gwp_t m) { return run_graph(m, 2); }
+
+wamx_status wamx_gwp_predict(wamx_gwp_t m, wamx_gwp_timing * timing) {
+    WAMX_REQUIRE(m, "wamx_gwp_predict: null model");
+    float ms[3] = {0, 0, 0};
+    for (int i = 0; i < 3; ++i) {
+        if (timing) wamx_timer_start(m->timer);
+        const wamx_status st = run_graph(m, i);
+        if (st != WAMX_STATUS_SUCCESS) return st;
+        if (timing) ms[i] = wamx_timer_stop_ms(m->timer);
+    }
+    if (timing) {
+        timing->prompt_ms = ms[0];
+        timing->prefix_ms = ms[1];
+        timing->denoise_ms = ms[2];
+        timing->total_ms = ms[0] + ms[1] + ms[2];
+    }
+    return WAMX_STATUS_SUCCESS;
+}
+
+wamx_status wamx_gwp_get_action(wamx_gwp_t m, float * out) {
+    WAMX_REQUIRE(m && out && m->action_out && m->action_out->data, "wamx_gwp_get_action: no action");
+    wamx_backend_synchronize(m->be);
+    const int64_t n = wamx_nelements(m->action_out);
+    std::vector<uint16_t> a(n);
+    const wamx_status st = wamx_backend_tensor_get(m->action_out, a.data(), 0, n * 2);
+    if (st != WAMX_STATUS_SUCCESS) return st;
+    for (int64_t i = 0; i < n; ++i) out[i] = bf16_to_f32_host(a[i]);
+    return WAMX_STATUS_SUCCESS;
+}
+
+wamx_tensor * wamx_gwp_prefix_key(wamx_gwp_t m, int layer) {
+    return (m && layer >= 0 && layer < m->cfg.n_layers) ? m->pk[layer] : nullptr;
+}
+wamx_tensor * wamx_gwp_prefix_value(wamx_gwp_t m, int layer) {
+    return (m && layer >= 0 && layer < m->cfg.n_layers) ? m->pv[layer] : nullptr;
+}
+int wamx_gwp_graph_nodes(wamx_gwp_t m, int which) {
+    return (m && which >= 0 && which < 3) ? wamx_graph_n_nodes(m->graph[which]) : 0;
+}
+
+}  // extern "C"

@@ -33,13 +33,13 @@ struct GemmArgs {
     const void * res = nullptr;              // bf16 [N][ldres]
     int64_t ldres = 0;
     const float * gate = nullptr;            // f32 [M]
-    void * ws = nullptr;                     // split-K partials (skinny path)
+    void * ws = nullptr;                     // K-split partials of the skinny path
     size_t ws_bytes = 0;
-    unsigned * counters = nullptr;           // split-K arrival counters, zero between launches
-    int64_t max_counters = 0;
 };
 
 hipError_t launch_gemm(const GemmArgs & a, hipStream_t s);
+// Workspace the skinny path needs for an M x N x K product (0 when unsplit).
+size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 // ---------------------------------------------------------------------------
 // Row-wise norms (bf16 / f32), bias+GELU, gated residuals.
@@ -82,6 +82,8 @@ hipError_t launch_get_rows(const TensorRef & a, const int32_t * rows, const Tens
 hipError_t launch_softmax_f32(const TensorRef & x, const TensorRef & y, float scale, hipStream_t s);
 hipError_t launch_rope_f32(const TensorRef & x, const int32_t * pos, const TensorRef & y, int n_dims, float freq_base,
                            hipStream_t s);
+hipError_t launch_im2col(const TensorRef & src, const TensorRef & dst, int KW, int KH, int s0, int s1, int p0, int p1,
+                         int d0, int d1, hipStream_t s);
 hipError_t launch_modulation(const void * mod, int32_t mod_type, const void * tables, int32_t tab_type, float * out,
                              int64_t per_layer, int64_t layers, hipStream_t s);
 
@@ -104,12 +106,8 @@ struct AttnArgs {
     void * out = nullptr;          // bf16 [Tq][H*dh]
     int64_t heads = 0, head_dim = 0, tq = 0;
     float scale = 1.0f;
-    unsigned * counters = nullptr; // split-KV arrival counters, zero between launches
-    int64_t max_counters = 0;
 };
-// Needs a workspace for split-KV partials; ws/ws_bytes from attn_workspace_bytes.
-size_t attn_workspace_bytes(const AttnArgs & a);
-hipError_t launch_joint_attn(const AttnArgs & a, void * ws, hipStream_t s);
+hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s);
 
 // Synthetic N(mean, std) fill: splitmix64(seed ^ index) -> Box-Muller.
 hipError_t launch_fill_normal(void * dst, int32_t type, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);

@@ -9,10 +9,9 @@
 // joint_attn: softmax(scale * Q K^T) V per head over keys taken from two
 //   sources without concatenating them (mot.cpp:402-445 builds the CONCAT and
 //   three GEMM/softmax nodes; the math here is the same with fp32 scores and
-//   bf16 probabilities).  Split-KV ("flash-decoding"): every wave streams its
-//   32-key blocks of K and V^T once from HBM, keeps an online softmax per
-//   query, waves of a workgroup merge in LDS, and the last workgroup of a
-//   (head, query group) merges the split partials in split order.
+//   bf16 probabilities).  Every wave streams its 32-key blocks of K and V^T
+//   once, keeps an online softmax per query, and the waves of the workgroup
+//   merge their states in LDS in wave order.
 #include "../internal.h"
 #include "device.h"
 
@@ -104,10 +103,7 @@ hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void
 // joint_attn
 // ---------------------------------------------------------------------------
 constexpr int kDh = 128;         // head_dim
-constexpr int kQG = 48;          // queries per workgroup (3 MFMA column tiles of 16)
-constexpr int kQT = kQG / 16;
 constexpr int kKB = 32;          // keys per block
-constexpr int kAttnWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
@@ -119,14 +115,11 @@ struct AttnParams {
     int64_t seg_blocks[2];
     int64_t nblocks;
     uint16_t * out;
-    float * ws;              // partials [H][qgroups][splits][kQG][kDh + 2]
-    unsigned * counters;     // [H][qgroups]
-    int64_t heads, tq, qgroups;
-    int splits;
+    int64_t heads, tq;
     float scale_log2;
 };
 
-// Unpack 4 bf16 packed in a uint2 with keys >= valid replaced by zero.
+// Zero the bf16 values of keys >= valid in 4 packed keys starting at first_key.
 __device__ __forceinline__ uint2 mask4(uint2 v, int first_key, int valid) {
     uint32_t lo = v.x, hi = v.y;
     if (first_key + 0 >= valid) lo &= 0xffff0000u;
@@ -136,101 +129,119 @@ __device__ __forceinline__ uint2 mask4(uint2 v, int first_key, int valid) {
     return make_uint2(lo, hi);
 }
 
-__global__ __launch_bounds__(256) void joint_attn_kernel(AttnParams p) {
-    __shared__ float s_m[kAttnWaves][kQG];
-    __shared__ float s_l[kAttnWaves][kQG];
-    __shared__ float s_o[kQG][kDh + 1];
-    __shared__ int s_last;
+// One 32-key block's operands in registers: K as two 16-key A fragments
+// (lane = key c16 of the tile, dims [32g, 32g+32) as four k-steps) and V^T as
+// 8 dim tiles of keys {4g..4g+3} and {16+4g..16+4g+3} (the S^T accumulator
+// layout, so P needs no shuffle before the PV MFMA).
+struct KvBlock {
+    uint4 k[2][4];
+    uint2 va[8], vb[8];
+    int valid;
+};
+
+// Branch-free loads: rows and columns are clamped into the segment and the
+// out-of-range keys are masked (scores to -inf, V to zero) by the consumer.
+__device__ __forceinline__ void load_block(const AttnParams & p, int64_t b, int64_t h, int g, int c16, KvBlock & kv) {
+    const int seg = b < p.seg_blocks[0] ? 0 : 1;
+    const int64_t lb = seg == 0 ? b : b - p.seg_blocks[0];
+    const int64_t k0 = lb * kKB;
+    const int valid = (int) min((int64_t) kKB, p.seg_len[seg] - k0);
+    kv.valid = valid;
+    const uint16_t * kbase = p.k[seg] + (h * p.seg_len[seg] + k0) * kDh;
+    const uint16_t * vbase = p.vt[seg] + h * kDh * p.vt_ld[seg] + k0;
+    const int64_t vld = p.vt_ld[seg];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+        const int key = min(16 * kt + c16, valid - 1);
+        const uint4 * src = (const uint4 *) (kbase + (int64_t) key * kDh + 32 * g);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kv.k[kt][c] = src[c];
+    }
+    const int last = ((valid - 1) >> 2) << 2;  // last 4-aligned chunk inside the block
+    const int ka = min(4 * g, last), kb = min(16 + 4 * g, last);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+        const uint16_t * row = vbase + (int64_t) (16 * dt + c16) * vld;
+        kv.va[dt] = *(const uint2 *) (row + ka);
+        kv.vb[dt] = *(const uint2 *) (row + kb);
+    }
+}
+
+// softmax(scale * Q K^T) V for one (head, group of 16*QT queries) per
+// workgroup; the NW waves take key blocks round-robin, each with one block of
+// prefetch, and merge their online-softmax states in LDS in wave order.
+template <int QT, int NW>
+__global__ __launch_bounds__(NW * 64) void joint_attn_kernel(AttnParams p) {
+    constexpr int QG = 16 * QT;
+    __shared__ float s_m[NW][QG];
+    __shared__ float s_l[NW][QG];
+    __shared__ float s_o[QG][kDh + 1];
+    __shared__ float s_lstar[QG];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    const int split = blockIdx.x;
-    const int64_t h = blockIdx.y, qg = blockIdx.z;
-    const int64_t q0 = qg * kQG;
+    const int64_t h = blockIdx.x, qg = blockIdx.y;
+    const int64_t q0 = qg * QG;
 
     // Q fragments: B operand of S^T = K Q^T.  Lane (query c16 of tile t,
     // group g) holds dims [32g, 32g+32) as four 8-element k-steps.
-    bf16x8_t qf[kQT][4];
+    bf16x8_t qf[QT][4];
 #pragma unroll
-    for (int t = 0; t < kQT; ++t) {
-        const int64_t qi = q0 + 16 * t + c16;
-        const bool ok = qi < p.tq;
-        const uint4 * src = (const uint4 *) (p.q + (h * p.tq + (ok ? qi : 0)) * kDh + 32 * g);
+    for (int t = 0; t < QT; ++t) {
+        const int64_t qi = min(q0 + 16 * t + c16, p.tq - 1);
+        const uint4 * src = (const uint4 *) (p.q + (h * p.tq + qi) * kDh + 32 * g);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            uint4 u = ok ? src[c] : make_uint4(0, 0, 0, 0);
-            qf[t][c] = __builtin_bit_cast(bf16x8_t, u);
-        }
+        for (int c = 0; c < 4; ++c) qf[t][c] = __builtin_bit_cast(bf16x8_t, src[c]);
     }
 
-    f32x4_t o[kQT][8];
+    f32x4_t o[QT][8];
 #pragma unroll
-    for (int t = 0; t < kQT; ++t)
+    for (int t = 0; t < QT; ++t)
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) o[t][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m_run[kQT], l_run[kQT];
+    float m_run[QT], l_run[QT];
 #pragma unroll
-    for (int t = 0; t < kQT; ++t) {
+    for (int t = 0; t < QT; ++t) {
         m_run[t] = -INFINITY;
         l_run[t] = 0.0f;
     }
 
-    const int64_t stride = (int64_t) p.splits * kAttnWaves;
-    for (int64_t b = (int64_t) split * kAttnWaves + wave; b < p.nblocks; b += stride) {
-        const int seg = b < p.seg_blocks[0] ? 0 : 1;
-        const int64_t lb = seg == 0 ? b : b - p.seg_blocks[0];
-        const int64_t k0 = lb * kKB;
-        const int valid = (int) min((int64_t) kKB, p.seg_len[seg] - k0);
-        const uint16_t * kbase = p.k[seg] + (h * p.seg_len[seg] + k0) * kDh;
-        const uint16_t * vbase = p.vt[seg] + h * kDh * p.vt_ld[seg] + k0;
-        const int64_t vld = p.vt_ld[seg];
-
-        // S^T tiles: two 16-key tiles x kQT query tiles.
-        f32x4_t st[2][kQT];
+    KvBlock cur, nxt;
+    int64_t b = wave;
+    if (b < p.nblocks) load_block(p, b, h, g, c16, cur);
+    for (; b < p.nblocks; b += NW) {
+        if (b + NW < p.nblocks) load_block(p, b + NW, h, g, c16, nxt);
+        const int valid = cur.valid;
+        // S^T tiles: two 16-key tiles x QT query tiles.
+        f32x4_t st[2][QT];
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            const int key = 16 * kt + c16;
-            const bool ok = key < valid;
-            const uint4 * ksrc = (const uint4 *) (kbase + (int64_t) (ok ? key : 0) * kDh + 32 * g);
-            uint4 kr[4];
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) kr[c] = ok ? ksrc[c] : make_uint4(0, 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < kQT; ++t) {
+            for (int t = 0; t < QT; ++t) {
                 f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[c]), qf[t][c], acc, 0,
-                                                                  0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cur.k[kt][c]),
+                                                                  qf[t][c], acc, 0, 0, 0);
                 st[kt][t] = acc;
             }
-        }
-        // V^T fragments: lane (dim row c16 of dim tile dt, group g) holds keys
-        // 4g..4g+3 and 16+4g..16+4g+3, matching the S^T accumulator layout.
         uint2 va[8], vb[8];
+        const bool full = valid == kKB;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
-            const uint16_t * row = vbase + (int64_t) (16 * dt + c16) * vld;
-            const bool full = valid == kKB;
-            const int ka = 4 * g, kb = 16 + 4 * g;
-            va[dt] = (full || ka < valid) ? *(const uint2 *) (row + ka) : make_uint2(0, 0);
-            vb[dt] = (full || kb < valid) ? *(const uint2 *) (row + kb) : make_uint2(0, 0);
-            if (!full) {
-                va[dt] = mask4(va[dt], ka, valid);
-                vb[dt] = mask4(vb[dt], kb, valid);
-            }
+            va[dt] = full ? cur.va[dt] : mask4(cur.va[dt], 4 * g, valid);
+            vb[dt] = full ? cur.vb[dt] : mask4(cur.vb[dt], 16 + 4 * g, valid);
         }
         // Online softmax per query (lane's query c16 of tile t; its 8 keys are
         // keys 4g+r and 16+4g+r; the rest of the block lives in lanes ^16, ^32).
 #pragma unroll
-        for (int t = 0; t < kQT; ++t) {
+        for (int t = 0; t < QT; ++t) {
             float sv[8];
             float mx = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const bool oka = 4 * g + r < valid, okb = 16 + 4 * g + r < valid;
-                sv[r] = oka ? st[0][t][r] * p.scale_log2 : -INFINITY;
-                sv[4 + r] = okb ? st[1][t][r] * p.scale_log2 : -INFINITY;
+                sv[r] = (4 * g + r < valid) ? st[0][t][r] * p.scale_log2 : -INFINITY;
+                sv[4 + r] = (16 + 4 * g + r < valid) ? st[1][t][r] * p.scale_log2 : -INFINITY;
                 mx = fmaxf(mx, fmaxf(sv[r], sv[4 + r]));
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -238,24 +249,18 @@ __global__ __launch_bounds__(256) void joint_attn_kernel(AttnParams p) {
             const float m_new = fmaxf(m_run[t], mx);
             const float corr = exp2f(m_run[t] - m_new);
             float ps = 0.0f;
-            uint32_t pk[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float pa = exp2f(sv[r] - m_new);
-                const float pb = exp2f(sv[4 + r] - m_new);
-                sv[r] = round_bf16(pa);
-                sv[4 + r] = round_bf16(pb);
-                ps += sv[r] + sv[4 + r];
+            for (int r = 0; r < 8; ++r) {
+                sv[r] = round_bf16(exp2f(sv[r] - m_new));
+                ps += sv[r];
             }
-            pk[0] = pack_bf16x2(sv[0], sv[1]);
-            pk[1] = pack_bf16x2(sv[2], sv[3]);
-            pk[2] = pack_bf16x2(sv[4], sv[5]);
-            pk[3] = pack_bf16x2(sv[6], sv[7]);
             ps += __shfl_xor(ps, 16, 64);
             ps += __shfl_xor(ps, 32, 64);
             l_run[t] = l_run[t] * corr + ps;
             m_run[t] = m_new;
-            const bf16x8_t pfrag = __builtin_bit_cast(bf16x8_t, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+            const bf16x8_t pfrag = __builtin_bit_cast(
+                bf16x8_t, make_uint4(pack_bf16x2(sv[0], sv[1]), pack_bf16x2(sv[2], sv[3]), pack_bf16x2(sv[4], sv[5]),
+                                     pack_bf16x2(sv[6], sv[7])));
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
@@ -264,30 +269,31 @@ __global__ __launch_bounds__(256) void joint_attn_kernel(AttnParams p) {
                 o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag, pfrag, o[t][dt], 0, 0, 0);
             }
         }
+        cur = nxt;
     }
 
-    // --- merge the four waves of this workgroup (in wave order) ------------
+    // --- merge the waves of this workgroup (in wave order) ----------------
     // O^T accumulator: lane holds query c16 of tile t, dims 16dt + 4g + r.
 #pragma unroll
-    for (int t = 0; t < kQT; ++t) {
+    for (int t = 0; t < QT; ++t) {
         if (g == 0) {
             s_m[wave][16 * t + c16] = m_run[t];
             s_l[wave][16 * t + c16] = l_run[t];
         }
     }
     __syncthreads();
-    float fac[kQT];
+    float fac[QT];
 #pragma unroll
-    for (int t = 0; t < kQT; ++t) {
+    for (int t = 0; t < QT; ++t) {
         const int q = 16 * t + c16;
         float mstar = -INFINITY;
-        for (int w = 0; w < kAttnWaves; ++w) mstar = fmaxf(mstar, s_m[w][q]);
+        for (int w = 0; w < NW; ++w) mstar = fmaxf(mstar, s_m[w][q]);
         fac[t] = (m_run[t] == -INFINITY) ? 0.0f : exp2f(m_run[t] - mstar);
     }
-    for (int w = 0; w < kAttnWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
         if (wave == w) {
 #pragma unroll
-            for (int t = 0; t < kQT; ++t)
+            for (int t = 0; t < QT; ++t)
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
@@ -299,90 +305,31 @@ __global__ __launch_bounds__(256) void joint_attn_kernel(AttnParams p) {
         }
         __syncthreads();
     }
-    // Per-query merged max and denominator (thread q < kQG computes them).
-    __shared__ float s_mstar[kQG], s_lstar[kQG];
-    if (tid < kQG) {
+    if (tid < QG) {
         float mstar = -INFINITY;
-        for (int w = 0; w < kAttnWaves; ++w) mstar = fmaxf(mstar, s_m[w][tid]);
+        for (int w = 0; w < NW; ++w) mstar = fmaxf(mstar, s_m[w][tid]);
         float l = 0.0f;
-        for (int w = 0; w < kAttnWaves; ++w)
+        for (int w = 0; w < NW; ++w)
             if (s_m[w][tid] != -INFINITY) l += s_l[w][tid] * exp2f(s_m[w][tid] - mstar);
-        s_mstar[tid] = mstar;
         s_lstar[tid] = l;
     }
     __syncthreads();
-
-    const int64_t nq = min((int64_t) kQG, p.tq - q0);
-    if (p.splits == 1) {
-        for (int e = tid; e < nq * kDh; e += 256) {
-            const int q = e / kDh, d = e % kDh;
-            const float l = s_lstar[q];
-            p.out[(q0 + q) * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? s_o[q][d] / l : 0.0f);
-        }
-        return;
-    }
-
-    // --- split-KV: publish the partial, last workgroup merges -------------
-    const int64_t slot = (h * p.qgroups + qg) * p.splits;
-    float * part = p.ws + (slot + split) * (int64_t) kQG * (kDh + 2);
-    for (int e = tid; e < kQG * kDh; e += 256) part[e] = s_o[e / kDh][e % kDh];
-    if (tid < kQG) {
-        part[kQG * kDh + tid] = s_mstar[tid];
-        part[kQG * kDh + kQG + tid] = s_lstar[tid];
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&p.counters[h * p.qgroups + qg], 1u);
-        s_last = prev == (unsigned) (p.splits - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const float * base = p.ws + slot * (int64_t) kQG * (kDh + 2);
-    const int64_t pstride = (int64_t) kQG * (kDh + 2);
-    for (int e = tid; e < nq * kDh; e += 256) {
+    const int64_t nq = min((int64_t) QG, p.tq - q0);
+    for (int e = tid; e < nq * kDh; e += NW * 64) {
         const int q = e / kDh, d = e % kDh;
-        float mstar = -INFINITY;
-        for (int sp = 0; sp < p.splits; ++sp) mstar = fmaxf(mstar, base[sp * pstride + kQG * kDh + q]);
-        float acc = 0.0f, l = 0.0f;
-        for (int sp = 0; sp < p.splits; ++sp) {
-            const float ms = base[sp * pstride + kQG * kDh + q];
-            if (ms == -INFINITY) continue;
-            const float f = exp2f(ms - mstar);
-            acc += base[sp * pstride + q * kDh + d] * f;
-            l += base[sp * pstride + kQG * kDh + kQG + q] * f;
-        }
-        p.out[(q0 + q) * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? acc / l : 0.0f);
+        const float l = s_lstar[q];
+        p.out[(q0 + q) * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? s_o[q][d] / l : 0.0f);
     }
-    if (tid == 0) atomicExch(&p.counters[h * p.qgroups + qg], 0u);
 }
 
 // Softmax is order-free, so the keys are visited per source in 32-key blocks
 // aligned to each source's start: source a ([state, reference] prefix cache,
 // na keys) and source b (the current action tokens, nb keys).  The complete
 // MoT order [state, action, reference] (mot.cpp:402-403) only fixes the
-// reference's fp32 summation order, which split-KV reassociates anyway.
-static void attn_plan(const AttnArgs & a, int64_t & nblocks, int64_t & qgroups, int & splits) {
-    const int64_t seg1 = a.k_b ? a.nb : 0;
-    nblocks = (a.na + kKB - 1) / kKB + (seg1 + kKB - 1) / kKB;
-    qgroups = (a.tq + kQG - 1) / kQG;
-    // Enough workgroups to cover the chip, at least two key blocks per wave.
-    const int64_t wgs = a.heads * qgroups;
-    int64_t sp = 1;
-    while (wgs * sp < 256 && (nblocks + (sp * 2 * kAttnWaves) - 1) / (sp * 2 * kAttnWaves) >= 2) sp *= 2;
-    splits = (int) sp;
-}
-
-size_t attn_workspace_bytes(const AttnArgs & a) {
-    int64_t nblocks, qgroups;
-    int splits;
-    attn_plan(a, nblocks, qgroups, splits);
-    if (splits == 1) return 0;
-    return (size_t) a.heads * qgroups * splits * kQG * (kDh + 2) * sizeof(float);
-}
-
-hipError_t launch_joint_attn(const AttnArgs & a, void * ws, hipStream_t s) {
+// reference's fp32 summation order, which the online softmax reassociates.
+// One workgroup per (head, query group): its waves split the key blocks and
+// merge in LDS, so no partial state crosses workgroups.
+hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     if (a.head_dim != kDh) return hipErrorInvalidValue;
     if (a.tq <= 0) return hipSuccess;
     AttnParams p{};
@@ -397,26 +344,26 @@ hipError_t launch_joint_attn(const AttnArgs & a, void * ws, hipStream_t s) {
     p.seg_len[1] = a.k_b ? a.nb : 0;
     p.seg_blocks[0] = (p.seg_len[0] + kKB - 1) / kKB;
     p.seg_blocks[1] = (p.seg_len[1] + kKB - 1) / kKB;
-    int64_t nblocks, qgroups;
-    int splits;
-    attn_plan(a, nblocks, qgroups, splits);
-    p.nblocks = nblocks;
+    p.nblocks = p.seg_blocks[0] + p.seg_blocks[1];
     p.out = (uint16_t *) a.out;
     p.heads = a.heads;
     p.tq = a.tq;
-    p.qgroups = qgroups;
-    p.splits = splits;
     p.scale_log2 = a.scale * kLog2e;
-    p.ws = (float *) ws;
-    p.counters = a.counters;
-    if (splits > 1 && (!ws || !a.counters || a.heads * qgroups > a.max_counters)) return hipErrorInvalidValue;
     // 8-byte V^T loads of 4 keys need rows padded to a multiple of 4 keys.
     for (int i = 0; i < 2; ++i)
         if (p.seg_len[i] > 0 &&
             (p.vt_ld[i] % 4 != 0 || p.vt_ld[i] < p.seg_len[i] || ((uintptr_t) p.vt[i] & 7) || ((uintptr_t) p.k[i] & 15)))
             return hipErrorInvalidValue;
-    hipLaunchKernelGGL(joint_attn_kernel, dim3((unsigned) splits, (unsigned) a.heads, (unsigned) qgroups), dim3(256), 0,
-                       s, p);
+    // Few queries (the 48-token denoise step): 16-query groups and 8 waves per
+    // workgroup to spread the key stream over more CUs; many queries (the
+    // prefix pass): 48-query groups, 4 waves.
+    if (a.tq <= 64) {
+        const int64_t qgroups = (a.tq + 15) / 16;
+        hipLaunchKernelGGL((joint_attn_kernel<1, 8>), dim3((unsigned) a.heads, (unsigned) qgroups), dim3(512), 0, s, p);
+    } else {
+        const int64_t qgroups = (a.tq + 47) / 48;
+        hipLaunchKernelGGL((joint_attn_kernel<3, 4>), dim3((unsigned) a.heads, (unsigned) qgroups), dim3(256), 0, s, p);
+    }
     return hipGetLastError();
 }
 

@@ -187,6 +187,21 @@ __global__ void rope_kernel(Ref4 x, const int32_t * pos, Ref4 y, int n_dims, flo
     }
 }
 
+// ggml_im2col, 2-D: dst[n][oh][ow][ic*KH*KW + kh*KW + kw] =
+// src[n][ic][oh*s1 + kh*d1 - p1][ow*s0 + kw*d0 - p0] (zero outside).
+__global__ void im2col_kernel(Ref4 src, Ref4 dst, int KW, int KH, int s0, int s1, int p0, int p1, int d0, int d1,
+                              int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t c, ow, oh, b;
+    unravel(i, dst, c, ow, oh, b);
+    const int64_t kw = c % KW, kh = (c / KW) % KH, ic = c / (KW * KH);
+    const int64_t iw = ow * s0 + kw * d0 - p0, ih = oh * s1 + kh * d1 - p1;
+    float v = 0.0f;
+    if (iw >= 0 && iw < src.ne0 && ih >= 0 && ih < src.ne1) v = ld(src, at(src, iw, ih, ic, b));
+    st(dst, at(dst, c, ow, oh, b), v);
+}
+
 // out[l][j] = f32(mod[j]) + f32(tables[l][j])  (modulation_add, mot.cpp:137-145).
 __global__ void modulation_kernel(const void * mod, int32_t mod_type, const void * tables, int32_t tab_type, float * out,
                                   int64_t per_layer, int64_t n) {
@@ -276,6 +291,15 @@ hipError_t launch_rope_f32(const TensorRef & x, const int32_t * pos, const Tenso
     const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
     hipLaunchKernelGGL(rope_kernel, grid1d(npairs), dim3(256), 0, s, to_ref4(x), pos, to_ref4(y), n_dims, theta_scale,
                        npairs);
+    return hipGetLastError();
+}
+
+hipError_t launch_im2col(const TensorRef & src, const TensorRef & dst, int KW, int KH, int s0, int s1, int p0, int p1,
+                         int d0, int d1, hipStream_t s) {
+    const int64_t n = nel(dst);
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(im2col_kernel, grid1d(n), dim3(256), 0, s, to_ref4(src), to_ref4(dst), KW, KH, s0, s1, p0, p1,
+                       d0, d1, n);
     return hipGetLastError();
 }
 

@@ -10,12 +10,13 @@
 //  * gemm_tile   — MFMA 32x32x16 bf16, LDS double-buffered 128x128x64 tiles,
 //                  128-bit global loads, for token counts above 64.
 //  * gemm_skinny — N <= 64 tokens (the 48-token action expert): HBM-bound
-//                  weight streaming with MFMA 16x16x32, split-K across
-//                  workgroups, deterministic in-kernel reduction by the last
-//                  workgroup of each feature block.
+//                  weight streaming with MFMA 16x16x32, K split across the
+//                  waves of a workgroup and reduced in LDS.
 //  * gemm_simt   — f32 weights (generic MUL_MAT only), plain FMA.
 #include "../internal.h"
 #include "device.h"
+
+#include <algorithm>
 
 namespace wamx {
 
@@ -26,8 +27,6 @@ struct GemmParams {
     const uint16_t * bias;
     const uint16_t * res;
     const float * gate;
-    float * ws;          // split-K partials
-    unsigned * counters; // split-K arrival counters (zero between launches)
     int64_t ldw, w_bs2, w_bs3;
     int64_t ldx, x_bs2, x_bs3;
     int64_t ldy, y_bs2, y_bs3;
@@ -35,7 +34,6 @@ struct GemmParams {
     int64_t M, N, K;
     int64_t B2, r2, r3;
     int32_t y_type, epi;
-    int32_t splits, kslice;  // skinny: number of K slices and their length
 };
 
 // Epilogue for one output element (row n, col m) from the fp32 accumulator.
@@ -250,135 +248,164 @@ __global__ __launch_bounds__(256) void gemm_tile(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// gemm_skinny: N <= 64 tokens.  Grid = (feature blocks of 64) x (K slices).
-// The workgroup stages its K slice of x (all tokens, bf16) in LDS once; each
-// wave then streams 16 weight rows of the slice straight from HBM into
-// registers and feeds MFMA 16x16x32.  The k order inside a 128-wide step is
-// permuted so every lane reads 64 contiguous bytes of its weight row (the dot
-// product is order-free as long as x uses the same permutation).
-// Split-K partials go to ws; the last workgroup to finish a feature block
-// sums them in slice order (deterministic) and applies the epilogue.
+// gemm_skinny: N <= 64 tokens (the 48-token action expert), HBM-bound weight
+// streaming in two kernels.
+//
+// gemm_skinny_part: grid = (feature blocks of 128) x (K splits).  The
+//   workgroup stages its K slice of the activations (all tokens, bf16) in LDS
+//   once; each of its 8 waves then streams 16 weight rows of the slice from
+//   HBM with a 4-step-deep branch-free prefetch and feeds MFMA 16x16x32 with
+//   activation fragments read from LDS.  Activation bytes per workgroup are
+//   48/128 of its weight bytes.  With one K split the epilogue is applied
+//   directly; otherwise fp32 partials go to a workspace.
+// gemm_skinny_reduce: sums the K-split partials in split order
+//   (deterministic) and applies the epilogue.  The kernel boundary orders the
+//   partial writes before the reads; no device-scope fences are needed.
+// Inside a 128-wide K step the k order is permuted so each lane reads 64
+// contiguous bytes of its weight row (a dot product is order-free as long as
+// the activation fragment uses the same permutation).
 // ---------------------------------------------------------------------------
-constexpr int kSkinnyMB = 64;
-constexpr int kSkinnyMaxSlice = 512;
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyFeat = 16 * kSkinnyWaves;  // features per workgroup
+constexpr int kSkinnyDepth = 4;                  // weight prefetch depth (128-wide steps)
 
-template <bool XF32>
-__global__ __launch_bounds__(256) void gemm_skinny(GemmParams p) {
-    extern __shared__ __align__(16) uint16_t xs[];  // [64 tokens][kslice + 8]
-    __shared__ int s_last;
+template <bool XF32, int NT>
+__global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams p, float * part, int ks) {
+    extern __shared__ __align__(16) uint16_t xs[];  // [16*NT][ks + 8]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pitch = p.kslice + 8;
+    const int g = lane >> 4, r16 = lane & 15;
     const int64_t N = p.N, M = p.M, K = p.K;
-    const int ntiles = (int) ((N + 15) / 16);
+    const int pitch = ks + 8;
+    const int64_t m0 = (int64_t) blockIdx.x * kSkinnyFeat;
+    const int64_t kb = (int64_t) blockIdx.y * ks;
+    const int64_t ke = min(K, kb + ks);
+    const int klen = (int) (ke - kb);
 
-    // XCD-aware mapping: workgroups are dealt round-robin to the 8 XCDs, so
-    // keep all K slices of one feature block on the same XCD (same L2).
-    const int64_t nfb = (M + kSkinnyMB - 1) / kSkinnyMB;
-    const int64_t lin = blockIdx.x;
-    const int64_t xcd = lin & 7, q = lin >> 3;
-    const int64_t fb = (q / p.splits) * 8 + xcd;
-    const int split = (int) (q % p.splits);
-    if (fb >= nfb) return;  // padding workgroups of the XCD-aware grid
-    const int64_t m0 = fb * kSkinnyMB;
-    const int64_t kb = (int64_t) split * p.kslice;
-    const int64_t klen = min((int64_t) p.kslice, K - kb);
-
-    // Stage x[0..N)[kb..kb+klen) as bf16; pad tokens to 16*ntiles and k to a
-    // multiple of 128 with zeros.
-    const int kpad = (int) ((klen + 127) / 128) * 128;
-    const int chunks_per_row = kpad / 8;
-    for (int c = tid; c < 16 * ntiles * chunks_per_row; c += 256) {
-        const int r = c / chunks_per_row, kc = c % chunks_per_row;
-        const int64_t k = kb + kc * 8;
+    // Stage x[0..N)[kb..ke) as bf16 (rows past N and columns past ke are zero).
+    const int cpr = ks / 8;
+    for (int c = tid; c < 16 * NT * cpr; c += kSkinnyWaves * 64) {
+        const int r = c / cpr, kc = c % cpr;
         uint4 v = make_uint4(0, 0, 0, 0);
-        if (r < N && kc * 8 < klen) v = load_x8<XF32>(p.x, r * p.ldx + k);
+        if (r < N && kc * 8 < klen) v = load_x8<XF32>(p.x, r * p.ldx + kb + kc * 8);
         *(uint4 *) (xs + r * pitch + kc * 8) = v;
     }
-    __syncthreads();
 
-    const int64_t mrow = m0 + wave * 16 + (lane & 15);
-    const bool row_ok = mrow < M;
-    const uint16_t * wrow = p.w + (row_ok ? mrow : 0) * p.ldw + kb;
-    const int g = lane >> 4;  // which 32-wide k group of the 128-wide step
-
-    f32x4_t acc[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const int nsteps = kpad / 128;
-    uint4 wcur[4], wnext[4];
-    auto wload = [&](int st, uint4 * dst) {
+    const int64_t mrow = m0 + 16 * wave + r16;
+    const uint16_t * wrow = p.w + min(mrow, M - 1) * p.ldw + kb;
+    const int nsteps = (klen + 127) / 128;
+    uint4 wbuf[kSkinnyDepth][4];
+    auto wload = [&](int st, uint4 (&d)[4]) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const int kk = st * 128 + 32 * g + 8 * c;
-            dst[c] = (row_ok && kk < klen) ? *(const uint4 *) (wrow + kk) : make_uint4(0, 0, 0, 0);
+            const int k = st * 128 + 32 * g + 8 * c;
+            const bool kin = k < klen;
+            uint4 v = *(const uint4 *) (wrow + (kin ? k : klen - 8));
+            const uint32_t mask = kin ? 0xffffffffu : 0u;
+            v.x &= mask;
+            v.y &= mask;
+            v.z &= mask;
+            v.w &= mask;
+            d[c] = v;
         }
     };
-    wload(0, wcur);
-    for (int st = 0; st < nsteps; ++st) {
-        if (st + 1 < nsteps) wload(st + 1, wnext);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const bf16x8_t bfrag = __builtin_bit_cast(bf16x8_t, wcur[c]);
-            const int kk = st * 128 + 32 * g + 8 * c;
+    for (int i = 0; i < kSkinnyDepth; ++i) wload(min(i, nsteps - 1), wbuf[i]);
+    __syncthreads();
+
+    f32x4_t acc[NT];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                if (t < ntiles) {
-                    const bf16x8_t afrag = *(const bf16x8_t *) (xs + (16 * t + (lane & 15)) * pitch + kk);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag, acc[t], 0, 0, 0);
+    for (int t = 0; t < NT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int st0 = 0; st0 < nsteps; st0 += kSkinnyDepth) {
+#pragma unroll
+        for (int i = 0; i < kSkinnyDepth; ++i) {
+            const int st = st0 + i;
+            if (st < nsteps) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int kk = st * 128 + 32 * g + 8 * c;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const bf16x8_t a = *(const bf16x8_t *) (xs + (16 * t + r16) * pitch + kk);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, wbuf[i][c]),
+                                                                         acc[t], 0, 0, 0);
+                    }
                 }
             }
-        }
-        if (st + 1 < nsteps) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) wcur[c] = wnext[c];
+            wload(min(st + kSkinnyDepth, nsteps - 1), wbuf[i]);
         }
     }
 
-    // 16x16 fragment: lane holds column (lane & 15) = feature, register r holds
-    // row 4*(lane/16) + r = token within the tile.
-    const int64_t m = m0 + wave * 16 + (lane & 15);
-    if (p.splits == 1) {
-        if (m < M) {
+    // 16x16 fragment: lane holds column (lane & 15) = feature, register r
+    // holds row 4*(lane/16) + r = token within the tile.
+    if (mrow >= M) return;
+    if (gridDim.y == 1) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int64_t n = 16 * t + 4 * g + r;
-                    if (t < ntiles && n < N) store_out(p, p.y, p.res, n, m, acc[t][r]);
-                }
-        }
-        return;
-    }
-
-    float * part = p.ws + (int64_t) split * 64 * M;
-    if (m < M) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t n = 16 * t + 4 * g + r;
-                if (t < ntiles && n < N) part[n * M + m] = acc[t][r];
+                if (n < N) store_out(p, p.y, p.res, n, mrow, acc[t][r]);
             }
+        return;
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&p.counters[fb], 1u);
-        s_last = (prev == (unsigned) (p.splits - 1));
+    float * pp = part + (int64_t) blockIdx.y * N * M;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t n = 16 * t + 4 * g + r;
+            if (n < N) pp[n * M + mrow] = acc[t][r];
+        }
+}
+
+__global__ __launch_bounds__(256) void gemm_skinny_reduce(GemmParams p, const float * part, int splits) {
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = p.N * p.M;
+    if (i >= total) return;
+    float s = part[i];
+    for (int sp = 1; sp < splits; ++sp) s += part[(int64_t) sp * total + i];
+    store_out(p, p.y, p.res, i / p.M, i % p.M, s);
+}
+
+// K split of the skinny path: ~512 workgroups, slices of 256..1024 columns.
+static void skinny_plan(int64_t M, int64_t K, int & splits, int & ks) {
+    const int64_t nfb = (M + kSkinnyFeat - 1) / kSkinnyFeat;
+    int64_t s = (512 + nfb - 1) / nfb;                // aim at ~512 workgroups
+    s = std::max<int64_t>(1, std::min<int64_t>(s, K / 256));
+    int64_t k = ((K + s - 1) / s + 127) / 128 * 128;  // slice length, multiple of 128
+    k = std::min<int64_t>(k, 1024);
+    splits = (int) ((K + k - 1) / k);
+    ks = (int) k;
+}
+
+size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    int splits, ks;
+    skinny_plan(M, K, splits, ks);
+    return splits > 1 ? (size_t) splits * N * M * sizeof(float) : 0;
+}
+
+template <bool XF32>
+static hipError_t run_skinny(const GemmParams & p, void * ws, size_t ws_bytes, hipStream_t s) {
+    int splits, ks;
+    skinny_plan(p.M, p.K, splits, ks);
+    if (splits > 1 && (!ws || (size_t) splits * p.N * p.M * sizeof(float) > ws_bytes)) return hipErrorInvalidValue;
+    const int nt = (int) ((p.N + 15) / 16);
+    const size_t lds = (size_t) 16 * nt * (ks + 8) * sizeof(uint16_t);
+    const dim3 grid((unsigned) ((p.M + kSkinnyFeat - 1) / kSkinnyFeat), (unsigned) splits);
+    const dim3 block(kSkinnyWaves * 64);
+    float * part = (float *) ws;
+    switch (nt) {
+        case 1: hipLaunchKernelGGL((gemm_skinny_part<XF32, 1>), grid, block, lds, s, p, part, ks); break;
+        case 2: hipLaunchKernelGGL((gemm_skinny_part<XF32, 2>), grid, block, lds, s, p, part, ks); break;
+        case 3: hipLaunchKernelGGL((gemm_skinny_part<XF32, 3>), grid, block, lds, s, p, part, ks); break;
+        default: hipLaunchKernelGGL((gemm_skinny_part<XF32, 4>), grid, block, lds, s, p, part, ks); break;
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    // Last arrival: reduce the slices in order and run the epilogue.
-    for (int e = tid; e < N * kSkinnyMB; e += 256) {
-        const int64_t n = e / kSkinnyMB, mm = m0 + e % kSkinnyMB;
-        if (mm >= M) continue;
-        float s = 0.0f;
-        for (int sp = 0; sp < p.splits; ++sp) s += p.ws[((int64_t) sp * 64 + n) * M + mm];
-        store_out(p, p.y, p.res, n, mm, s);
+    if (splits > 1) {
+        const int64_t total = p.N * p.M;
+        hipLaunchKernelGGL(gemm_skinny_reduce, dim3((unsigned) ((total + 255) / 256)), dim3(256), 0, s, p,
+                           (const float *) part, splits);
     }
-    if (tid == 0) atomicExch(&p.counters[fb], 0u);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -427,8 +454,6 @@ hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
     p.bias = (const uint16_t *) a.bias;
     p.res = (const uint16_t *) a.res;
     p.gate = a.gate;
-    p.ws = (float *) a.ws;
-    p.counters = a.counters;
     p.ldw = a.ldw; p.w_bs2 = a.w_bs2; p.w_bs3 = a.w_bs3;
     p.ldx = a.ldx; p.x_bs2 = a.x_bs2; p.x_bs3 = a.x_bs3;
     p.ldy = a.ldy; p.y_bs2 = a.y_bs2; p.y_bs3 = a.y_bs3;
@@ -452,33 +477,16 @@ hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
     const bool vec = a.K % 8 == 0 && a.ldw % 8 == 0 && a.ldx % 8 == 0 && aligned16(a.w) && aligned16(a.x) &&
                      a.w_bs2 % 8 == 0 && a.w_bs3 % 8 == 0 && a.x_bs2 % 8 == 0 && a.x_bs3 % 8 == 0;
 
-    if (vec && batches == 1 && a.N <= 64 && a.ws && a.counters) {
-        // Split K so the grid covers the chip while the partials stay a small
-        // fraction of the weight bytes.
-        const int64_t nfb = (a.M + kSkinnyMB - 1) / kSkinnyMB;
-        int64_t splits = 1;
-        const int64_t target_wg = 1024;
-        while (nfb * splits < target_wg && (a.K + splits * 2 - 1) / (splits * 2) >= 128) splits *= 2;
-        int64_t kslice = (a.K + splits - 1) / splits;
-        kslice = (kslice + 127) / 128 * 128;
-        while (kslice > kSkinnyMaxSlice) {
-            splits *= 2;
-            kslice = ((a.K + splits - 1) / splits + 127) / 128 * 128;
-        }
-        splits = (a.K + kslice - 1) / kslice;
-        if (splits * 64 * a.M * 4 <= (int64_t) a.ws_bytes && nfb <= a.max_counters) {
-            p.splits = (int32_t) splits;
-            p.kslice = (int32_t) kslice;
-            const int64_t per_xcd = (nfb + 7) / 8;
-            const int64_t grid = per_xcd * splits * 8;
-            const size_t lds = (size_t) 64 * (kslice + 8) * sizeof(uint16_t);
-            static bool once = (allow_lds(gemm_skinny<true>, (size_t) 64 * (kSkinnyMaxSlice + 8) * 2),
-                                allow_lds(gemm_skinny<false>, (size_t) 64 * (kSkinnyMaxSlice + 8) * 2), true);
-            (void) once;
-            if (xf32) hipLaunchKernelGGL(gemm_skinny<true>, dim3((unsigned) grid), dim3(256), lds, s, p);
-            else hipLaunchKernelGGL(gemm_skinny<false>, dim3((unsigned) grid), dim3(256), lds, s, p);
-            return hipGetLastError();
-        }
+    if (vec && batches == 1 && a.N <= 64) {
+        // K slices up to 1024 columns: 64 x 1032 bf16 = 132 KB of LDS.
+        constexpr size_t kMaxLds = 160 * 1024;
+        static bool once = (allow_lds(gemm_skinny_part<true, 1>, kMaxLds), allow_lds(gemm_skinny_part<false, 1>, kMaxLds),
+                            allow_lds(gemm_skinny_part<true, 2>, kMaxLds), allow_lds(gemm_skinny_part<false, 2>, kMaxLds),
+                            allow_lds(gemm_skinny_part<true, 3>, kMaxLds), allow_lds(gemm_skinny_part<false, 3>, kMaxLds),
+                            allow_lds(gemm_skinny_part<true, 4>, kMaxLds), allow_lds(gemm_skinny_part<false, 4>, kMaxLds),
+                            true);
+        (void) once;
+        return xf32 ? run_skinny<true>(p, a.ws, a.ws_bytes, s) : run_skinny<false>(p, a.ws, a.ws_bytes, s);
     }
     if (vec) return xf32 ? run_tile<128, 128, true, true>(p, batches, s) : run_tile<128, 128, false, true>(p, batches, s);
     return xf32 ? run_tile<128, 128, true, false>(p, batches, s) : run_tile<128, 128, false, false>(p, batches, s);
