@@ -41,36 +41,52 @@ struct GemmParams {
 // (native-bf16.patch:273-275), the bias ADD is a bf16 + bf16 -> bf16 op
 // (weights.cpp:826-828), bias_gelu_bf16 (patch:507-514) and
 // gated_residual_bf16 (patch:79-91) read bf16 and round once.
+// Kinds: 0 f32 out, 1 bf16 out, 2 bias, 3 bias+GELU, 4 bias+gated residual,
+// 5 bias+residual.
+enum { kEpiF32 = 0, kEpiBf16, kEpiBias, kEpiBiasGelu, kEpiBiasGated, kEpiBiasResidual };
+
+__host__ __device__ __forceinline__ int epi_kind(const GemmParams & p) {
+    switch (p.epi) {
+        case WAMX_EPI_NONE: return p.y_type == WAMX_TYPE_F32 ? kEpiF32 : kEpiBf16;
+        case WAMX_EPI_BIAS: return kEpiBias;
+        case WAMX_EPI_BIAS_GELU: return kEpiBiasGelu;
+        case WAMX_EPI_BIAS_GATED: return kEpiBiasGated;
+        default: return kEpiBiasResidual;
+    }
+}
+
+template <int E>
+__device__ __forceinline__ void store_out_t(const GemmParams & p, void * yb, const uint16_t * resb, int64_t n,
+                                            int64_t m, float acc) {
+    const int64_t yi = n * p.ldy + m;
+    if constexpr (E == kEpiF32) {
+        ((float *) yb)[yi] = acc;
+    } else if constexpr (E == kEpiBf16) {
+        ((uint16_t *) yb)[yi] = f32_to_bf16(acc);
+    } else if constexpr (E == kEpiBias) {
+        ((uint16_t *) yb)[yi] = f32_to_bf16(round_bf16(acc) + bf16_to_f32(p.bias[m]));
+    } else if constexpr (E == kEpiBiasGelu) {
+        ((uint16_t *) yb)[yi] = f32_to_bf16(gelu_tanh(round_bf16(acc) + bf16_to_f32(p.bias[m])));
+    } else if constexpr (E == kEpiBiasGated) {
+        const float o = round_bf16(round_bf16(acc) + bf16_to_f32(p.bias[m]));
+        const float h = bf16_to_f32(resb[n * p.ldres + m]);
+        ((uint16_t *) yb)[yi] = f32_to_bf16(fmaf(o, p.gate[m], h));
+    } else {
+        const float o = round_bf16(round_bf16(acc) + bf16_to_f32(p.bias[m]));
+        const float h = bf16_to_f32(resb[n * p.ldres + m]);
+        ((uint16_t *) yb)[yi] = f32_to_bf16(h + o);
+    }
+}
+
 __device__ __forceinline__ void store_out(const GemmParams & p, void * yb, const uint16_t * resb, int64_t n, int64_t m,
                                           float acc) {
-    const int64_t yi = n * p.ldy + m;
-    switch (p.epi) {
-        case WAMX_EPI_NONE:
-            if (p.y_type == WAMX_TYPE_F32) ((float *) yb)[yi] = acc;
-            else ((uint16_t *) yb)[yi] = f32_to_bf16(acc);
-            return;
-        case WAMX_EPI_BIAS: {
-            const float v = round_bf16(acc) + bf16_to_f32(p.bias[m]);
-            ((uint16_t *) yb)[yi] = f32_to_bf16(v);
-            return;
-        }
-        case WAMX_EPI_BIAS_GELU: {
-            const float v = round_bf16(acc) + bf16_to_f32(p.bias[m]);
-            ((uint16_t *) yb)[yi] = f32_to_bf16(gelu_tanh(v));
-            return;
-        }
-        case WAMX_EPI_BIAS_GATED: {
-            const float o = round_bf16(round_bf16(acc) + bf16_to_f32(p.bias[m]));
-            const float h = bf16_to_f32(resb[n * p.ldres + m]);
-            ((uint16_t *) yb)[yi] = f32_to_bf16(fmaf(o, p.gate[m], h));
-            return;
-        }
-        default: {  // WAMX_EPI_BIAS_RESIDUAL
-            const float o = round_bf16(round_bf16(acc) + bf16_to_f32(p.bias[m]));
-            const float h = bf16_to_f32(resb[n * p.ldres + m]);
-            ((uint16_t *) yb)[yi] = f32_to_bf16(h + o);
-            return;
-        }
+    switch (epi_kind(p)) {
+        case kEpiF32: store_out_t<kEpiF32>(p, yb, resb, n, m, acc); return;
+        case kEpiBf16: store_out_t<kEpiBf16>(p, yb, resb, n, m, acc); return;
+        case kEpiBias: store_out_t<kEpiBias>(p, yb, resb, n, m, acc); return;
+        case kEpiBiasGelu: store_out_t<kEpiBiasGelu>(p, yb, resb, n, m, acc); return;
+        case kEpiBiasGated: store_out_t<kEpiBiasGated>(p, yb, resb, n, m, acc); return;
+        default: store_out_t<kEpiBiasResidual>(p, yb, resb, n, m, acc); return;
     }
 }
 
@@ -98,35 +114,123 @@ __device__ __forceinline__ uint16_t load_x1(const void * x, int64_t idx) {
 }
 
 // ---------------------------------------------------------------------------
-// gemm_tile: TR tokens x TC features per 256-thread workgroup, BK = 64.
-// Four waves in a 2x2 grid; each wave owns (TR/2) x (TC/2) built from 32x32
-// MFMA fragments.  LDS rows are padded by 16 bytes so the 128-bit fragment
-// reads of 32 consecutive rows hit distinct banks.
+// gemm_tile: BM tokens x BN features per workgroup of WM x WN waves, BK = 64.
+// Each wave owns (BM/WM) x (BN/WN) built from 32x32 MFMA fragments; operand
+// tiles are double-buffered in LDS with rows padded by 16 bytes, so the
+// 128-bit fragment reads of 32 consecutive rows hit distinct banks.  LDS
+// read traffic per MAC is (1/wave_rows + 1/wave_cols), which is why the large
+// configurations give each wave a 128 x 128 (or 96 x 96) output block held in
+// the accumulation registers.
+//
+// Tile order: workgroups are dispatched round-robin over the 8 XCDs (linear
+// id % 8), each with its own L2.  XCD x is given a contiguous range of the
+// logical tile order, and that order walks feature tiles inside groups of
+// kTileGroup token tiles, so the tiles resident on one XCD at a time share
+// their activation and weight panels in that XCD's L2.
 // ---------------------------------------------------------------------------
 constexpr int kBK = 64;
 constexpr int kPitch = kBK + 8;  // elements per LDS row
+constexpr int kTileGroup = 4;
+constexpr int kXcds = 8;
 
-template <int TR, int TC, bool XF32, bool VEC>
-__global__ __launch_bounds__(256) void gemm_tile(GemmParams p) {
-    constexpr int FR = TR / 64;  // 32-row fragments per wave
-    constexpr int FC = TC / 64;
-    constexpr int CPR = kBK / 8;  // 16-byte chunks per row per K tile
-    constexpr int A_PER = TR * CPR / 256;
-    constexpr int B_PER = TC * CPR / 256;
-    static_assert(A_PER * 256 == TR * CPR && B_PER * 256 == TC * CPR, "tile/thread mismatch");
+__device__ __forceinline__ void tile_coords(int pid, int nt_m, int nt_n, int & tm, int & tn) {
+    const int T = nt_m * nt_n;
+    const int q = T / kXcds, r = T % kXcds;
+    const int xcd = pid % kXcds, j = pid / kXcds;
+    const int L = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + j;
+    const int per_group = kTileGroup * nt_m;
+    const int first_n = (L / per_group) * kTileGroup;
+    const int gsize = min(nt_n - first_n, kTileGroup);
+    const int in = L % per_group;
+    tn = first_n + in % gsize;
+    tm = in / gsize;
+}
+
+template <int BM, int BN, int WM, int WN>
+struct TileCfg {
+    static constexpr int kThreads = 64 * WM * WN;
+    static constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
+    static constexpr int FR = kWaveM / 32, FC = kWaveN / 32;
+    static constexpr int CPR = kBK / 8;  // 16-byte chunks per row per K tile
+    static constexpr int A_PER = BM * CPR / kThreads, B_PER = BN * CPR / kThreads;
+    static constexpr size_t kLds = 2 * (size_t) (BM + BN) * kPitch * sizeof(uint16_t);
+    static_assert(FR * 32 * WM == BM && FC * 32 * WN == BN, "wave tile must be whole 32x32 fragments");
+    static_assert(A_PER * kThreads == BM * CPR && B_PER * kThreads == BN * CPR, "tile/thread mismatch");
+    static_assert(kLds <= 160 * 1024, "LDS budget");
+};
+
+// Accumulator fragments -> global, one epilogue kind.  32x32 fragment: lane
+// holds feature (lane & 31); register v holds token 8*(v/4) + 4*(lane/32) + v%4.
+// The per-feature bias / gate are loaded once per fragment column and the 16
+// residual values of a fragment are loaded together before any store, so the
+// epilogue waits for memory once per fragment rather than once per element.
+template <int E, int FR, int FC>
+__device__ __forceinline__ void tile_store(const GemmParams & p, char * __restrict__ y,
+                                           const uint16_t * __restrict__ resb, f32x16_t (&acc)[FR][FC], int64_t nb,
+                                           int64_t mb, int lane) {
+    constexpr bool kBias = E >= kEpiBias, kRes = E >= kEpiBiasGated;
+    const uint16_t * __restrict__ bias = p.bias;
+    const float * __restrict__ gate = p.gate;
+#pragma unroll
+    for (int j = 0; j < FC; ++j) {
+        const int64_t m = mb + 32 * j + (lane & 31);
+        if (m >= p.M) continue;
+        const float bv = kBias ? bf16_to_f32(bias[m]) : 0.0f;
+        const float gv = E == kEpiBiasGated ? gate[m] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < FR; ++i) {
+            float h[16];
+            if constexpr (kRes) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t n = min(nb + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3), p.N - 1);
+                    h[v] = bf16_to_f32(resb[n * p.ldres + m]);
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t n = nb + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (n >= p.N) continue;
+                const float a = acc[i][j][v];
+                const int64_t yi = n * p.ldy + m;
+                if constexpr (E == kEpiF32) {
+                    ((float *) y)[yi] = a;
+                } else if constexpr (E == kEpiBf16) {
+                    ((uint16_t *) y)[yi] = f32_to_bf16(a);
+                } else if constexpr (E == kEpiBias) {
+                    ((uint16_t *) y)[yi] = f32_to_bf16(round_bf16(a) + bv);
+                } else if constexpr (E == kEpiBiasGelu) {
+                    ((uint16_t *) y)[yi] = f32_to_bf16(gelu_tanh(round_bf16(a) + bv));
+                } else if constexpr (E == kEpiBiasGated) {
+                    ((uint16_t *) y)[yi] = f32_to_bf16(fmaf(round_bf16(round_bf16(a) + bv), gv, h[v]));
+                } else {
+                    ((uint16_t *) y)[yi] = f32_to_bf16(h[v] + round_bf16(round_bf16(a) + bv));
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, bool XF32, bool VEC>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_tile(GemmParams p, int nt_m, int nt_n) {
+    using C = TileCfg<BM, BN, WM, WN>;
+    constexpr int NTH = C::kThreads, FR = C::FR, FC = C::FC, CPR = C::CPR;
+    constexpr int A_PER = C::A_PER, B_PER = C::B_PER;
 
     extern __shared__ __align__(16) uint16_t lds[];
     uint16_t * buf0 = lds;
-    uint16_t * buf1 = lds + (TR + TC) * kPitch;
+    uint16_t * buf1 = lds + (BM + BN) * kPitch;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = wave >> 1, wc = wave & 1;
+    const int wr = wave / WN, wc = wave % WN;
     const int64_t bz = blockIdx.z;
     const int64_t b2 = bz % p.B2, b3 = bz / p.B2;
     const uint16_t * w = p.w + (b2 / p.r2) * p.w_bs2 + (b3 / p.r3) * p.w_bs3;
     const char * x = (const char *) p.x + (b2 * p.x_bs2 + b3 * p.x_bs3) * (XF32 ? 4 : 2);
     char * y = (char *) p.y + (b2 * p.y_bs2 + b3 * p.y_bs3) * (p.y_type == WAMX_TYPE_F32 ? 4 : 2);
-    const int64_t n0 = (int64_t) blockIdx.y * TR, m0 = (int64_t) blockIdx.x * TC;
+    int tm, tn;
+    tile_coords((int) blockIdx.x, nt_m, nt_n, tm, tn);
+    const int64_t n0 = (int64_t) tn * BM, m0 = (int64_t) tm * BN;
     const int64_t N = p.N, M = p.M, K = p.K;
 
     uint4 ra[A_PER], rb[B_PER];
@@ -135,7 +239,7 @@ __global__ __launch_bounds__(256) void gemm_tile(GemmParams p) {
     auto gload = [&](int64_t k0) {
 #pragma unroll
         for (int i = 0; i < A_PER; ++i) {
-            const int c = tid + 256 * i, r = c / CPR, kc = c % CPR;
+            const int c = tid + NTH * i, r = c / CPR, kc = c % CPR;
             const int64_t n = n0 + r, k = k0 + kc * 8;
             if constexpr (VEC && XF32) {
                 const bool ok = n < N && k < K;
@@ -153,7 +257,7 @@ __global__ __launch_bounds__(256) void gemm_tile(GemmParams p) {
         }
 #pragma unroll
         for (int i = 0; i < B_PER; ++i) {
-            const int c = tid + 256 * i, r = c / CPR, kc = c % CPR;
+            const int c = tid + NTH * i, r = c / CPR, kc = c % CPR;
             const int64_t m = m0 + r, k = k0 + kc * 8;
             if constexpr (VEC) {
                 rb[i] = (m < M && k < K) ? *(const uint4 *) (w + m * p.ldw + k) : make_uint4(0, 0, 0, 0);
@@ -168,7 +272,7 @@ __global__ __launch_bounds__(256) void gemm_tile(GemmParams p) {
     auto sstore = [&](uint16_t * buf) {
 #pragma unroll
         for (int i = 0; i < A_PER; ++i) {
-            const int c = tid + 256 * i, r = c / CPR, kc = c % CPR;
+            const int c = tid + NTH * i, r = c / CPR, kc = c % CPR;
             if constexpr (VEC && XF32) {
                 const float4 a = raf[2 * i], b = raf[2 * i + 1];
                 ra[i] = make_uint4(pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(b.x, b.y),
@@ -178,8 +282,8 @@ __global__ __launch_bounds__(256) void gemm_tile(GemmParams p) {
         }
 #pragma unroll
         for (int i = 0; i < B_PER; ++i) {
-            const int c = tid + 256 * i, r = c / CPR, kc = c % CPR;
-            *(uint4 *) (buf + (TR + r) * kPitch + kc * 8) = rb[i];
+            const int c = tid + NTH * i, r = c / CPR, kc = c % CPR;
+            *(uint4 *) (buf + (BM + r) * kPitch + kc * 8) = rb[i];
         }
     };
 
@@ -196,8 +300,8 @@ __global__ __launch_bounds__(256) void gemm_tile(GemmParams p) {
     sstore(buf0);
     __syncthreads();
 
-    const int arow = wr * (TR / 2) + (lane & 31);
-    const int brow = TR + wc * (TC / 2) + (lane & 31);
+    const int arow = wr * C::kWaveM + (lane & 31);
+    const int brow = BM + wc * C::kWaveN + (lane & 31);
     const int koff = 8 * (lane >> 5);
 
     for (int64_t kt = 0; kt < nk; ++kt) {
@@ -221,29 +325,186 @@ __global__ __launch_bounds__(256) void gemm_tile(GemmParams p) {
         __syncthreads();
     }
 
-    // Stage the fp32 tile through LDS (the K loop ended with a barrier, so
-    // both operand buffers are free), then write rows with consecutive threads
-    // on consecutive columns.  32x32 fragment: lane holds column (lane & 31);
-    // register v holds row 8*(v/4) + 4*(lane/32) + (v%4).
-    constexpr int kOutPitch = TC + 4;
-    static_assert(TR * kOutPitch * 4 <= 2 * (TR + TC) * kPitch * 2, "epilogue tile must fit the operand buffers");
-    float * otile = (float *) lds;
+    const uint16_t * resb = p.res ? p.res + (b2 * p.y_bs2 + b3 * p.y_bs3) : nullptr;
+    const int64_t nb = n0 + wr * C::kWaveM, mb = m0 + wc * C::kWaveN;
+    switch (epi_kind(p)) {
+        case kEpiF32: tile_store<kEpiF32>(p, y, resb, acc, nb, mb, lane); break;
+        case kEpiBf16: tile_store<kEpiBf16>(p, y, resb, acc, nb, mb, lane); break;
+        case kEpiBias: tile_store<kEpiBias>(p, y, resb, acc, nb, mb, lane); break;
+        case kEpiBiasGelu: tile_store<kEpiBiasGelu>(p, y, resb, acc, nb, mb, lane); break;
+        case kEpiBiasGated: tile_store<kEpiBiasGated>(p, y, resb, acc, nb, mb, lane); break;
+        default: tile_store<kEpiBiasResidual>(p, y, resb, acc, nb, mb, lane); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// gemm_dma: the bf16 x bf16 MFMA path for large products.  Operand tiles move
+// from global memory straight into LDS with global_load_lds_dwordx4 (no VGPR
+// staging), through a ring of S stages of BK columns, so S-1 stages are in
+// flight while one is multiplied: the L2/HBM latency is covered by the ring,
+// not by the registers of the wave.
+//
+// Each workgroup: BM tokens x BN features, WM x WN waves, 32x32x16 MFMA.
+// A stage holds BM activation rows then BN weight rows of BK bf16 each
+// (BK/8 chunks of 16 bytes).  One DMA instruction writes 64 consecutive
+// chunk slots (lane l -> slot base + l).  Slot p of row r holds chunk
+// p ^ swz(r): an XOR swizzle under which the 128-bit fragment reads of 32
+// consecutive rows are free of bank conflicts (chosen by measurement on
+// gfx950: (r>>2)&3 for 64-byte rows, (r>>1)&7 for 128-byte rows).  Rows past
+// N / M are clamped to the last row (their outputs are never stored).  The
+// stages are separate LDS objects and the K loop is unrolled by S, so the
+// compiler can tell a stage being read from the stages being filled and
+// waits only for the stage it needs.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+// s_waitcnt immediate: at most n vector-memory operations outstanding, other
+// counters untouched (vmcnt in bits [3:0] and [15:14]).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | (7 << 4) | (0xF << 8); }
+
+template <int BK>
+__host__ __device__ constexpr int dma_swz(int r) {
+    return BK == 32 ? (r >> 2) & 3 : (r >> 1) & 7;
+}
+
+__device__ __forceinline__ void cta_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int S>
+struct DmaCfg {
+    static constexpr int kThreads = 64 * WM * WN, kWaves = WM * WN;
+    static constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
+    static constexpr int FR = kWaveM / 32, FC = kWaveN / 32;
+    static constexpr int kRows = BM + BN, kChunks = BK / 8;
+    static constexpr int kStageElems = kRows * BK;
+    static constexpr int P = kRows * kChunks / kThreads;  // DMA instructions per thread per stage
+    static_assert(BK == 32 || BK == 64, "BK");
+    static_assert(S >= 2 && S <= 4, "ring of 2 to 4 stages");
+    static_assert(FR * 32 * WM == BM && FC * 32 * WN == BN, "wave tile must be whole 32x32 fragments");
+    static_assert(P * kThreads == kRows * kChunks, "stage/thread mismatch");
+    static_assert((size_t) S * kStageElems * 2 <= 160 * 1024, "LDS budget");
+};
+
+// Workgroups per CU that a configuration's LDS ring allows (at most 2).
+template <int BM, int BN, int WM, int WN, int BK, int S>
+constexpr int dma_occupancy() {
+    return (size_t) 2 * S * DmaCfg<BM, BN, WM, WN, BK, S>::kStageElems * 2 <= 160 * 1024 ? 2 : 1;
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int S, int OCC = 1>
+__global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_dma(GemmParams p, int nt_m, int nt_n) {
+    using C = DmaCfg<BM, BN, WM, WN, BK, S>;
+    constexpr int FR = C::FR, FC = C::FC, P = C::P, E = C::kStageElems, CH = C::kChunks;
+    __shared__ __align__(16) uint16_t st0[E];
+    __shared__ __align__(16) uint16_t st1[E];
+    __shared__ __align__(16) uint16_t st2[S > 2 ? E : 8];
+    __shared__ __align__(16) uint16_t st3[S > 3 ? E : 8];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave / WN, wc = wave % WN;
+    int tm, tn;
+    tile_coords((int) blockIdx.x, nt_m, nt_n, tm, tn);
+    const int64_t n0 = (int64_t) tn * BM, m0 = (int64_t) tm * BN;
+    const int64_t N = p.N, M = p.M;
+    const int nk = (int) (p.K / BK);
+
+    // Per-thread DMA sources: P chunk slots per stage, fixed rows and chunks,
+    // advanced by BK columns per k tile.
+    const char * src[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const int slot = (i * C::kWaves + wave) * 64 + lane;
+        const int r = slot / CH, c = (slot % CH) ^ dma_swz<BK>(slot / CH);
+        if (r < BM) {
+            const int64_t n = min(n0 + r, N - 1);
+            src[i] = (const char *) ((const uint16_t *) p.x + n * p.ldx + 8 * c);
+        } else {
+            const int64_t m = min(m0 + (r - BM), M - 1);
+            src[i] = (const char *) (p.w + m * p.ldw + 8 * c);
+        }
+    }
+    auto dma = [&](int kt, uint16_t * stage) {
+        const int64_t koff = (int64_t) min(kt, nk - 1) * BK * 2;
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+            __builtin_amdgcn_global_load_lds((glb_void_t *) (src[i] + koff),
+                                             (lds_void_t *) (stage + (i * C::kWaves + wave) * 64 * 8), 16, 0, 0);
+    };
+
+    f32x16_t acc[FR][FC];
 #pragma unroll
     for (int i = 0; i < FR; ++i)
 #pragma unroll
         for (int j = 0; j < FC; ++j)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int r = wr * (TR / 2) + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                const int c = wc * (TC / 2) + 32 * j + (lane & 31);
-                otile[r * kOutPitch + c] = acc[i][j][v];
-            }
-    __syncthreads();
-    const uint16_t * resb = p.res ? p.res + (b2 * p.y_bs2 + b3 * p.y_bs3) : nullptr;
-    for (int e = tid; e < TR * TC; e += 256) {
-        const int r = e / TC, c = e % TC;
-        const int64_t n = n0 + r, m = m0 + c;
-        if (n < N && m < M) store_out(p, y, resb, n, m, otile[r * kOutPitch + c]);
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    const int arow = wr * C::kWaveM + (lane & 31);
+    const int brow = BM + wc * C::kWaveN + (lane & 31);
+    const int sw = dma_swz<BK>(lane & 31);  // rows differ from lane & 31 by multiples of 32
+    int koff[BK / 16];
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) koff[s] = ((2 * s + (lane >> 5)) ^ sw) * 8;
+
+    auto mma = [&](const uint16_t * stage) {
+#pragma unroll
+        for (int s = 0; s < BK / 16; ++s) {
+            bf16x8_t a[FR], b[FC];
+#pragma unroll
+            for (int i = 0; i < FR; ++i) a[i] = *(const bf16x8_t *) (stage + (arow + 32 * i) * BK + koff[s]);
+#pragma unroll
+            for (int j = 0; j < FC; ++j) b[j] = *(const bf16x8_t *) (stage + (brow + 32 * j) * BK + koff[s]);
+#pragma unroll
+            for (int i = 0; i < FR; ++i)
+#pragma unroll
+                for (int j = 0; j < FC; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    };
+    // Step kt: wait for stage kt (S-2 younger stages may stay in flight),
+    // barrier, refill the stage freed by step kt-1 with tile kt+S-1, multiply.
+    auto step = [&](int kt, uint16_t * cur, uint16_t * refill) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * P));
+        cta_barrier();
+        dma(kt + S - 1, refill);
+        mma(cur);
+    };
+
+    dma(0, st0);
+    if constexpr (S > 2) dma(1, st1);
+    if constexpr (S > 3) dma(2, st2);
+    for (int kt = 0; kt < nk; kt += S) {
+        if constexpr (S == 2) {
+            step(kt, st0, st1);
+            if (kt + 1 < nk) step(kt + 1, st1, st0);
+        } else if constexpr (S == 3) {
+            step(kt, st0, st2);
+            if (kt + 1 < nk) step(kt + 1, st1, st0);
+            if (kt + 2 < nk) step(kt + 2, st2, st1);
+        } else {
+            step(kt, st0, st3);
+            if (kt + 1 < nk) step(kt + 1, st1, st0);
+            if (kt + 2 < nk) step(kt + 2, st2, st1);
+            if (kt + 3 < nk) step(kt + 3, st3, st2);
+        }
+    }
+    // Drain the ring's trailing (clamped, unused) refills before the
+    // workgroup's LDS can be reused.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+    const int64_t nb = n0 + wr * C::kWaveM, mb = m0 + wc * C::kWaveN;
+    char * y = (char *) p.y;
+    switch (epi_kind(p)) {
+        case kEpiF32: tile_store<kEpiF32>(p, y, p.res, acc, nb, mb, lane); break;
+        case kEpiBf16: tile_store<kEpiBf16>(p, y, p.res, acc, nb, mb, lane); break;
+        case kEpiBias: tile_store<kEpiBias>(p, y, p.res, acc, nb, mb, lane); break;
+        case kEpiBiasGelu: tile_store<kEpiBiasGelu>(p, y, p.res, acc, nb, mb, lane); break;
+        case kEpiBiasGated: tile_store<kEpiBiasGated>(p, y, p.res, acc, nb, mb, lane); break;
+        default: tile_store<kEpiBiasResidual>(p, y, p.res, acc, nb, mb, lane); break;
     }
 }
 
@@ -436,14 +697,47 @@ static void allow_lds(F kernel, size_t bytes) {
     if (bytes > 65536) (void) hipFuncSetAttribute((const void *) kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int) bytes);
 }
 
-template <int TR, int TC, bool XF32, bool VEC>
+template <int BM, int BN, int WM, int WN, bool XF32, bool VEC>
 static hipError_t run_tile(const GemmParams & p, int64_t batches, hipStream_t s) {
-    const size_t lds = 2 * (size_t) (TR + TC) * kPitch * sizeof(uint16_t);
-    static bool once = (allow_lds(gemm_tile<TR, TC, XF32, VEC>, lds), true);
+    using C = TileCfg<BM, BN, WM, WN>;
+    static bool once = (allow_lds(gemm_tile<BM, BN, WM, WN, XF32, VEC>, C::kLds), true);
     (void) once;
-    dim3 grid((unsigned) ((p.M + TC - 1) / TC), (unsigned) ((p.N + TR - 1) / TR), (unsigned) batches);
-    hipLaunchKernelGGL((gemm_tile<TR, TC, XF32, VEC>), grid, dim3(256), lds, s, p);
+    const int nt_m = (int) ((p.M + BN - 1) / BN), nt_n = (int) ((p.N + BM - 1) / BM);
+    dim3 grid((unsigned) (nt_m * nt_n), 1, (unsigned) batches);
+    hipLaunchKernelGGL((gemm_tile<BM, BN, WM, WN, XF32, VEC>), grid, dim3(C::kThreads), C::kLds, s, p, nt_m, nt_n);
     return hipGetLastError();
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int S>
+static hipError_t run_dma(const GemmParams & p, hipStream_t s) {
+    constexpr int occ = dma_occupancy<BM, BN, WM, WN, BK, S>();
+    const int nt_m = (int) ((p.M + BN - 1) / BN), nt_n = (int) ((p.N + BM - 1) / BM);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, BK, S, occ>), dim3((unsigned) (nt_m * nt_n)), dim3(64 * WM * WN), 0, s,
+                       p, nt_m, nt_n);
+    return hipGetLastError();
+}
+
+static int64_t tiles_of(const GemmParams & p, int bm, int bn) { return ((p.N + bm - 1) / bm) * ((p.M + bn - 1) / bn); }
+
+// Tile shape of the bf16 x bf16 DMA path, chosen so the grid fills the 256 CUs
+// (measured on the 3072-token products of the prefix pass):
+//  * 256 x 256, BK 32, 3 stages, 8 waves: when it gives at least one tile per
+//    CU (QKV 9216 x 3072, FFN-up 14336 x 3072);
+//  * 192 x 192, BK 64, 3 stages, 4 waves: 3072 x 3072 products, which it cuts
+//    into exactly 256 tiles (256 x 256 leaves 112 CUs idle);
+//  * 128 x 128, BK 64, 2 stages, 4 waves, two workgroups per CU: small grids
+//    (512-token prompt projections).
+// Returns false when the shape does not meet the path's preconditions.
+static bool dispatch_dma(const GemmParams & p, hipStream_t s, hipError_t & err) {
+    if (p.K % 32 != 0) return false;
+    if (tiles_of(p, 256, 256) >= 256) {
+        err = run_dma<256, 256, 4, 2, 32, 3>(p, s);
+        return true;
+    }
+    if (p.K % 64 != 0) return false;
+    if (tiles_of(p, 192, 192) >= 192) err = run_dma<192, 192, 2, 2, 64, 3>(p, s);
+    else err = run_dma<128, 128, 2, 2, 64, 2>(p, s);
+    return true;
 }
 
 hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
@@ -488,8 +782,12 @@ hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
         (void) once;
         return xf32 ? run_skinny<true>(p, a.ws, a.ws_bytes, s) : run_skinny<false>(p, a.ws, a.ws_bytes, s);
     }
-    if (vec) return xf32 ? run_tile<128, 128, true, true>(p, batches, s) : run_tile<128, 128, false, true>(p, batches, s);
-    return xf32 ? run_tile<128, 128, true, false>(p, batches, s) : run_tile<128, 128, false, false>(p, batches, s);
+    if (vec && !xf32 && batches == 1) {
+        hipError_t err = hipSuccess;
+        if (dispatch_dma(p, s, err)) return err;
+    }
+    if (vec) return xf32 ? run_tile<128, 128, 2, 2, true, true>(p, batches, s) : run_tile<128, 128, 2, 2, false, true>(p, batches, s);
+    return xf32 ? run_tile<128, 128, 2, 2, true, false>(p, batches, s) : run_tile<128, 128, 2, 2, false, false>(p, batches, s);
 }
 
 }  // namespace wamx
