@@ -21,7 +21,7 @@
 using namespace wamx;
 
 static constexpr size_t kAlign = 256;
-static constexpr size_t kWorkspaceBytes = 64ull << 20;  // K-split GEMM partials
+static constexpr size_t kWorkspaceBytes = 64ull << 20;  // K-split GEMM and key-split attention partials
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -237,6 +237,8 @@ static hipError_t run_joint_attn(wamx_backend * be, const wamx_tensor * node) {
     a.head_dim = q->ne[0];
     a.tq = q->ne[1];
     a.scale = param_f32(node, 1);
+    a.ws = be->workspace;
+    a.ws_bytes = kWorkspaceBytes;
     return launch_joint_attn(a, be->stream);
 }
 
@@ -960,6 +962,8 @@ wamx_status wamx_op_joint_attn(wamx_backend_t be, const void * q, const void * k
     a.head_dim = head_dim;
     a.tq = tq;
     a.scale = scale;
+    a.ws = be->workspace;
+    a.ws_bytes = kWorkspaceBytes;
     WAMX_LAUNCH(launch_joint_attn(a, be->stream));
 }
 

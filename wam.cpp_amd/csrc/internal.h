@@ -106,6 +106,8 @@ struct AttnArgs {
     void * out = nullptr;          // bf16 [Tq][H*dh]
     int64_t heads = 0, head_dim = 0, tq = 0;
     float scale = 1.0f;
+    void * ws = nullptr;           // fp32 partials of the key-split path
+    size_t ws_bytes = 0;
 };
 hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s);
 

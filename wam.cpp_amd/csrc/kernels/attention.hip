@@ -15,6 +15,8 @@
 #include "../internal.h"
 #include "device.h"
 
+#include <algorithm>
+
 namespace wamx {
 
 // ---------------------------------------------------------------------------
@@ -83,10 +85,103 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(const uint16_t
     }
 }
 
+// Vectorised qk_norm_rope for 16-byte aligned rows (width % 8 == 0, head_dim
+// % 8 == 0): thread i owns CPT chunks of 8 elements (4 rotation pairs of one
+// head); the row and weight chunks are loaded before the reduction, and each
+// chunk is stored as one 16-byte write.  theta = pos * 2^(i * log2(ts)).
+template <int CPT>
+__global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __restrict__ x, int64_t ldx,
+                                                          const uint16_t * __restrict__ w, uint16_t * __restrict__ dst,
+                                                          int heads, int head_dim, int64_t dst_tokens, int64_t tok0,
+                                                          int rope_mode, const int32_t * __restrict__ pos0,
+                                                          const int32_t * __restrict__ pos1,
+                                                          const int32_t * __restrict__ pos2, float eps, float l2ts128,
+                                                          float l2ts44, float l2ts42) {
+    __shared__ float red[16];
+    const int64_t t = blockIdx.x;
+    const int d = heads * head_dim;
+    const int nchunk = d >> 3;
+    uint4 xv[CPT], wv[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = min((int) threadIdx.x + i * (int) blockDim.x, nchunk - 1);
+        xv[i] = *(const uint4 *) (x + t * ldx + 8 * c);
+        wv[i] = *(const uint4 *) (w + 8 * c);
+    }
+    const float p0 = rope_mode == 2 ? 0.0f : (float) pos0[t];
+    const float p1 = rope_mode == 1 ? (float) pos1[t] : 0.0f;
+    const float p2 = rope_mode == 1 ? (float) pos2[t] : 0.0f;
+    float v[CPT][8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const bool ok = (int) threadIdx.x + i * (int) blockDim.x < nchunk;
+        const uint32_t u[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[i][2 * e] = ok ? bf16_to_f32((uint16_t) (u[e] & 0xffff)) : 0.0f;
+            v[i][2 * e + 1] = ok ? bf16_to_f32((uint16_t) (u[e] >> 16)) : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum = fmaf(v[i][e], v[i][e], sum);
+    }
+    const float inv_rms = rsqrtf(block_sum(sum, red) / (float) d + eps);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = (int) threadIdx.x + i * (int) blockDim.x;
+        if (c >= nchunk) continue;
+        const int e0 = 8 * c, h = e0 / head_dim, dd0 = e0 % head_dim;
+        const uint32_t wu[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+        uint32_t packed[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            // rms_norm_bf16_f32: y = x * inv_rms * w, f32.
+            float a = v[i][2 * j] * inv_rms * bf16_to_f32((uint16_t) (wu[j] & 0xffff));
+            float b = v[i][2 * j + 1] * inv_rms * bf16_to_f32((uint16_t) (wu[j] >> 16));
+            if (rope_mode != 2) {
+                const int dd = dd0 + 2 * j;
+                float theta;
+                if (rope_mode == 0) theta = p0 * exp2f((float) (dd >> 1) * l2ts128);
+                else if (dd < 44) theta = p0 * exp2f((float) (dd >> 1) * l2ts44);
+                else if (dd < 86) theta = p1 * exp2f((float) ((dd - 44) >> 1) * l2ts42);
+                else theta = p2 * exp2f((float) ((dd - 86) >> 1) * l2ts42);
+                float sn, cs;
+                sincosf(theta, &sn, &cs);
+                const float ra = a * cs - b * sn;
+                const float rb = a * sn + b * cs;
+                a = ra;
+                b = rb;
+            }
+            packed[j] = pack_bf16x2(a, b);
+        }
+        *(uint4 *) (dst + ((int64_t) h * dst_tokens + tok0 + t) * head_dim + dd0) =
+            make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    }
+}
+
 hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void * dst, int64_t heads, int64_t head_dim,
                                int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode, const int32_t * pos0,
                                const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s) {
     if (tokens <= 0) return hipSuccess;
+    const int64_t d = heads * head_dim;
+    if (d % 8 == 0 && head_dim % 8 == 0 && d / 8 <= 4096 && ldx % 8 == 0 && ((uintptr_t) x & 15) == 0 &&
+        ((uintptr_t) w & 15) == 0 && ((uintptr_t) dst & 15) == 0) {
+        const int64_t nchunk = d / 8;
+        const int cpt = nchunk <= 1024 ? 1 : nchunk <= 2048 ? 2 : 4;
+        const int threads = (int) std::min<int64_t>(1024, ((nchunk + cpt - 1) / cpt + 63) / 64 * 64);
+        const float l2ts128 = -2.0f / (float) head_dim * log2f(freq_base);
+        const float l2ts44 = -2.0f / 44.0f * log2f(freq_base);
+        const float l2ts42 = -2.0f / 42.0f * log2f(freq_base);
+#define WAMX_QK_VEC(CPT)                                                                                            \
+    hipLaunchKernelGGL(qk_norm_rope_vec<CPT>, dim3((unsigned) tokens), dim3((unsigned) threads), 0, s,            \
+                       (const uint16_t *) x, ldx, (const uint16_t *) w, (uint16_t *) dst, (int) heads, (int) head_dim, \
+                       dst_tokens, tok0, rope_mode, pos0, pos1, pos2, eps, l2ts128, l2ts44, l2ts42)
+        if (cpt == 1) WAMX_QK_VEC(1);
+        else if (cpt == 2) WAMX_QK_VEC(2);
+        else WAMX_QK_VEC(4);
+#undef WAMX_QK_VEC
+        return hipGetLastError();
+    }
     if ((heads * head_dim) / 2 > (int64_t) kQkThreads * kQkMaxPairs || (head_dim & 1) || (ldx & 1))
         return hipErrorInvalidValue;
     // theta_i = pos * theta_scale^i with theta_scale = base^(-2/n_dims) per rope section.
@@ -117,6 +212,12 @@ struct AttnParams {
     uint16_t * out;
     int64_t heads, tq;
     float scale_log2;
+    // Key-split mode: workgroup z of gridDim.z covers key blocks
+    // [z * split_blocks, (z + 1) * split_blocks) and writes fp32 partials.
+    int64_t split_blocks;
+    float * part_o;          // [split][head][query][kDh], unnormalised, scaled to part_m
+    float * part_m;          // [split][head][query] running max (log2 domain)
+    float * part_l;          // [split][head][query] running sum
 };
 
 // Zero the bf16 values of keys >= valid in 4 packed keys starting at first_key.
@@ -169,8 +270,10 @@ __device__ __forceinline__ void load_block(const AttnParams & p, int64_t b, int6
 
 // softmax(scale * Q K^T) V for one (head, group of 16*QT queries) per
 // workgroup; the NW waves take key blocks round-robin, each with one block of
-// prefetch, and merge their online-softmax states in LDS in wave order.
-template <int QT, int NW>
+// prefetch, and merge their online-softmax states in LDS in wave order.  With
+// SPLIT the workgroup covers one key range (blockIdx.z) and writes its merged
+// state as fp32 partials for joint_attn_merge instead of the output.
+template <int QT, int NW, bool SPLIT>
 __global__ __launch_bounds__(NW * 64) void joint_attn_kernel(AttnParams p) {
     constexpr int QG = 16 * QT;
     __shared__ float s_m[NW][QG];
@@ -206,11 +309,13 @@ __global__ __launch_bounds__(NW * 64) void joint_attn_kernel(AttnParams p) {
         l_run[t] = 0.0f;
     }
 
+    const int64_t b_begin = SPLIT ? (int64_t) blockIdx.z * p.split_blocks : 0;
+    const int64_t b_end = SPLIT ? min(p.nblocks, b_begin + p.split_blocks) : p.nblocks;
     KvBlock cur, nxt;
-    int64_t b = wave;
-    if (b < p.nblocks) load_block(p, b, h, g, c16, cur);
-    for (; b < p.nblocks; b += NW) {
-        if (b + NW < p.nblocks) load_block(p, b + NW, h, g, c16, nxt);
+    int64_t b = b_begin + wave;
+    if (b < b_end) load_block(p, b, h, g, c16, cur);
+    for (; b < b_end; b += NW) {
+        if (b + NW < b_end) load_block(p, b + NW, h, g, c16, nxt);
         const int valid = cur.valid;
         // S^T tiles: two 16-key tiles x QT query tiles.
         f32x4_t st[2][QT];
@@ -305,6 +410,7 @@ __global__ __launch_bounds__(NW * 64) void joint_attn_kernel(AttnParams p) {
         }
         __syncthreads();
     }
+    const int64_t nq = min((int64_t) QG, p.tq - q0);
     if (tid < QG) {
         float mstar = -INFINITY;
         for (int w = 0; w < NW; ++w) mstar = fmaxf(mstar, s_m[w][tid]);
@@ -312,14 +418,42 @@ __global__ __launch_bounds__(NW * 64) void joint_attn_kernel(AttnParams p) {
         for (int w = 0; w < NW; ++w)
             if (s_m[w][tid] != -INFINITY) l += s_l[w][tid] * exp2f(s_m[w][tid] - mstar);
         s_lstar[tid] = l;
+        if (SPLIT && tid < nq) {
+            const int64_t pi = ((int64_t) blockIdx.z * p.heads + h) * p.tq + q0 + tid;
+            p.part_m[pi] = mstar;
+            p.part_l[pi] = l;
+        }
     }
     __syncthreads();
-    const int64_t nq = min((int64_t) QG, p.tq - q0);
     for (int e = tid; e < nq * kDh; e += NW * 64) {
         const int q = e / kDh, d = e % kDh;
-        const float l = s_lstar[q];
-        p.out[(q0 + q) * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? s_o[q][d] / l : 0.0f);
+        if constexpr (SPLIT) {
+            p.part_o[(((int64_t) blockIdx.z * p.heads + h) * p.tq + q0 + q) * kDh + d] = s_o[q][d];
+        } else {
+            const float l = s_lstar[q];
+            p.out[(q0 + q) * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? s_o[q][d] / l : 0.0f);
+        }
     }
+}
+
+// Combines the key-split partials of one (head, query) per 128-thread
+// workgroup, splits in order: m* = max m_z, l* = sum l_z 2^(m_z - m*),
+// out = sum o_z 2^(m_z - m*) / l*.
+__global__ __launch_bounds__(kDh) void joint_attn_merge(AttnParams p, int nsplit) {
+    const int64_t hq = blockIdx.x, h = hq / p.tq, q = hq % p.tq;
+    const int d = threadIdx.x;
+    const int64_t stride = p.heads * p.tq;
+    float mstar = -INFINITY;
+    for (int z = 0; z < nsplit; ++z) mstar = fmaxf(mstar, p.part_m[z * stride + hq]);
+    float l = 0.0f, o = 0.0f;
+    for (int z = 0; z < nsplit; ++z) {
+        const float mz = p.part_m[z * stride + hq];
+        if (mz == -INFINITY) continue;
+        const float w = exp2f(mz - mstar);
+        l += p.part_l[z * stride + hq] * w;
+        o += p.part_o[(z * stride + hq) * kDh + d] * w;
+    }
+    p.out[q * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
 }
 
 // Softmax is order-free, so the keys are visited per source in 32-key blocks
@@ -327,8 +461,12 @@ __global__ __launch_bounds__(NW * 64) void joint_attn_kernel(AttnParams p) {
 // na keys) and source b (the current action tokens, nb keys).  The complete
 // MoT order [state, action, reference] (mot.cpp:402-403) only fixes the
 // reference's fp32 summation order, which the online softmax reassociates.
-// One workgroup per (head, query group): its waves split the key blocks and
-// merge in LDS, so no partial state crosses workgroups.
+// Within a workgroup the waves split the key blocks and merge in LDS; across
+// workgroups (key-split mode) the merge is a second kernel, so no partial
+// state crosses workgroups inside a kernel and no device-scope fence is used.
+constexpr int64_t kSplitBlocks = 8;   // key blocks (of 32) per split workgroup
+constexpr int64_t kMaxSplits = 32;
+constexpr int kSplitWaves = 4;
 hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     if (a.head_dim != kDh) return hipErrorInvalidValue;
     if (a.tq <= 0) return hipSuccess;
@@ -354,16 +492,35 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
         if (p.seg_len[i] > 0 &&
             (p.vt_ld[i] % 4 != 0 || p.vt_ld[i] < p.seg_len[i] || ((uintptr_t) p.vt[i] & 7) || ((uintptr_t) p.k[i] & 15)))
             return hipErrorInvalidValue;
-    // Few queries (the 48-token denoise step): 16-query groups and 8 waves per
-    // workgroup to spread the key stream over more CUs; many queries (the
-    // prefix pass): 48-query groups, 4 waves.
-    if (a.tq <= 64) {
-        const int64_t qgroups = (a.tq + 15) / 16;
-        hipLaunchKernelGGL((joint_attn_kernel<1, 8>), dim3((unsigned) a.heads, (unsigned) qgroups), dim3(512), 0, s, p);
-    } else {
+    // Many queries (the prefix pass): 48-query groups, 4 waves, one workgroup
+    // per (head, group).
+    if (a.tq > 64) {
         const int64_t qgroups = (a.tq + 47) / 48;
-        hipLaunchKernelGGL((joint_attn_kernel<3, 4>), dim3((unsigned) a.heads, (unsigned) qgroups), dim3(256), 0, s, p);
+        hipLaunchKernelGGL((joint_attn_kernel<3, 4, false>), dim3((unsigned) a.heads, (unsigned) qgroups), dim3(256), 0,
+                           s, p);
+        return hipGetLastError();
     }
+    // Few queries (the 48-token denoise step): heads x 16-query groups alone
+    // would occupy a fraction of the CUs, so the keys are also split into
+    // ranges of about kSplitBlocks blocks, each workgroup writing fp32
+    // partials that joint_attn_merge combines.
+    const int64_t qgroups = (a.tq + 15) / 16;
+    int64_t nsplit = (p.nblocks + kSplitBlocks - 1) / kSplitBlocks;
+    nsplit = std::min<int64_t>(nsplit, kMaxSplits);
+    const size_t part_bytes = (size_t) nsplit * a.heads * a.tq * (kDh + 2) * sizeof(float);
+    if (nsplit <= 1 || !a.ws || part_bytes > a.ws_bytes) {
+        hipLaunchKernelGGL((joint_attn_kernel<1, 8, false>), dim3((unsigned) a.heads, (unsigned) qgroups), dim3(512), 0,
+                           s, p);
+        return hipGetLastError();
+    }
+    p.split_blocks = (p.nblocks + nsplit - 1) / nsplit;
+    nsplit = (p.nblocks + p.split_blocks - 1) / p.split_blocks;
+    p.part_o = (float *) a.ws;
+    p.part_m = p.part_o + (size_t) nsplit * a.heads * a.tq * kDh;
+    p.part_l = p.part_m + (size_t) nsplit * a.heads * a.tq;
+    hipLaunchKernelGGL((joint_attn_kernel<1, kSplitWaves, true>),
+                       dim3((unsigned) a.heads, (unsigned) qgroups, (unsigned) nsplit), dim3(kSplitWaves * 64), 0, s, p);
+    hipLaunchKernelGGL(joint_attn_merge, dim3((unsigned) (a.heads * a.tq)), dim3(kDh), 0, s, p, (int) nsplit);
     return hipGetLastError();
 }
 

@@ -514,54 +514,63 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_dma(GemmParams p, int 
 //
 // gemm_skinny_part: grid = (feature blocks of 128) x (K splits).  The
 //   workgroup stages its K slice of the activations (all tokens, bf16) in LDS
-//   once; each of its 8 waves then streams 16 weight rows of the slice from
-//   HBM with a 4-step-deep branch-free prefetch and feeds MFMA 16x16x32 with
-//   activation fragments read from LDS.  Activation bytes per workgroup are
-//   48/128 of its weight bytes.  With one K split the epilogue is applied
-//   directly; otherwise fp32 partials go to a workspace.
+//   once, issuing every load of a batch before the first LDS store so the
+//   staging costs one memory latency, not one per chunk.  Each of its 8 waves
+//   then streams 16 weight rows of the slice from HBM with a 4-step-deep
+//   branch-free prefetch, and per 128-column step reads all activation
+//   fragments from LDS before feeding MFMA 16x16x32.  Activation bytes per
+//   workgroup are 48/128 of its weight bytes.  With one K split the epilogue
+//   is applied directly; otherwise fp32 partials go to a workspace.
 // gemm_skinny_reduce: sums the K-split partials in split order
-//   (deterministic) and applies the epilogue.  The kernel boundary orders the
-//   partial writes before the reads; no device-scope fences are needed.
-// Inside a 128-wide K step the k order is permuted so each lane reads 64
-// contiguous bytes of its weight row (a dot product is order-free as long as
-// the activation fragment uses the same permutation).
+//   (deterministic) and applies the epilogue, four outputs per thread with
+//   the split loads issued in batches of eight.  The kernel boundary orders
+//   the partial writes before the reads; no device-scope fences are needed.
+// Inside a 128-wide K step, MFMA chunk c of lane group g covers columns
+// 32c + 8g .. +8, so one load instruction reads 64 contiguous bytes of each
+// of its 16 weight rows (the activation fragments use the same order).
 // ---------------------------------------------------------------------------
 constexpr int kSkinnyWaves = 8;
-constexpr int kSkinnyFeat = 16 * kSkinnyWaves;  // features per workgroup
-constexpr int kSkinnyDepth = 4;                  // weight prefetch depth (128-wide steps)
+constexpr int kSkinnyRows = 32;                            // weight rows per wave (two MFMA groups)
+constexpr int kSkinnyFeat = kSkinnyRows * kSkinnyWaves;   // features per workgroup
+constexpr int kSkinnyDepth = 2;                            // weight prefetch depth (128-wide steps)
+constexpr int kSkinnyMaxKs = 1024;                         // longest K slice (LDS permitting)
+constexpr size_t kSkinnyLdsMax = 160 * 1024;
 
 template <bool XF32, int NT>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams p, float * part, int ks) {
-    extern __shared__ __align__(16) uint16_t xs[];  // [16*NT][ks + 8]
+    constexpr int RG = kSkinnyRows / 16;             // 16-row MFMA groups per wave
+    constexpr int LI = kSkinnyRows / 4;              // load instructions per step (4 rows x 256 B each)
+    extern __shared__ __align__(16) uint16_t xs[];  // [16*NT][ks + 8], then per-wave weight tiles
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r16 = lane & 15;
     const int64_t N = p.N, M = p.M, K = p.K;
     const int pitch = ks + 8;
-    const int64_t m0 = (int64_t) blockIdx.x * kSkinnyFeat;
+    const int64_t m0 = (int64_t) blockIdx.x * kSkinnyFeat + (int64_t) wave * kSkinnyRows;
     const int64_t kb = (int64_t) blockIdx.y * ks;
     const int64_t ke = min(K, kb + ks);
     const int klen = (int) (ke - kb);
+    // Wave-private weight tile: kSkinnyRows rows x 128 columns, 16-byte chunk j
+    // of row r stored at chunk position j ^ (r & 15) (conflict-free row writes
+    // and column reads).
+    uint16_t * wt = xs + 16 * NT * pitch + wave * (kSkinnyRows * 128);
 
-    // Stage x[0..N)[kb..ke) as bf16 (rows past N and columns past ke are zero).
-    const int cpr = ks / 8;
-    for (int c = tid; c < 16 * NT * cpr; c += kSkinnyWaves * 64) {
-        const int r = c / cpr, kc = c % cpr;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (r < N && kc * 8 < klen) v = load_x8<XF32>(p.x, r * p.ldx + kb + kc * 8);
-        *(uint4 *) (xs + r * pitch + kc * 8) = v;
-    }
-
-    const int64_t mrow = m0 + 16 * wave + r16;
-    const uint16_t * wrow = p.w + min(mrow, M - 1) * p.ldw + kb;
-    const int nsteps = (klen + 127) / 128;
-    uint4 wbuf[kSkinnyDepth][4];
-    auto wload = [&](int st, uint4 (&d)[4]) {
+    // Weight loads, row-coalesced: instruction c of a 128-column step reads
+    // rows 4c .. 4c+3 of the wave's rows, 256 contiguous bytes each (16 lanes
+    // per row).  Columns past the slice are clamped into it and masked to zero.
+    const int lrow = g, lchunk = r16;
+    const uint16_t * wbase[LI];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int k = st * 128 + 32 * g + 8 * c;
-            const bool kin = k < klen;
-            uint4 v = *(const uint4 *) (wrow + (kin ? k : klen - 8));
-            const uint32_t mask = kin ? 0xffffffffu : 0u;
+    for (int c = 0; c < LI; ++c) wbase[c] = p.w + min(m0 + 4 * c + lrow, M - 1) * p.ldw + kb;
+    const int nsteps = (klen + 127) / 128;
+    uint4 wbuf[kSkinnyDepth][LI];
+    auto wload = [&](int st, uint4 (&d)[LI]) {
+        const int k = st * 128 + 8 * lchunk;
+        const bool kin = k < klen;
+        const int kc = kin ? k : klen - 8;
+        const uint32_t mask = kin ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int c = 0; c < LI; ++c) {
+            uint4 v = *(const uint4 *) (wbase[c] + kc);
             v.x &= mask;
             v.y &= mask;
             v.z &= mask;
@@ -571,25 +580,63 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
     };
 #pragma unroll
     for (int i = 0; i < kSkinnyDepth; ++i) wload(min(i, nsteps - 1), wbuf[i]);
+
+    // Stage x[0..N)[kb..ke) as bf16 (rows past N and columns past ke are zero).
+    // Addresses are clamped into the tensor and the values masked, so every
+    // load of a batch is issued before the first LDS store.
+    const int cpr = ks / 8, total = 16 * NT * cpr;
+    constexpr int kStageBatch = 8;
+    for (int c0 = 0; c0 < total; c0 += kStageBatch * kSkinnyWaves * 64) {
+        uint4 v[kStageBatch];
+#pragma unroll
+        for (int u = 0; u < kStageBatch; ++u) {
+            const int c = min(c0 + u * kSkinnyWaves * 64 + tid, total - 1);
+            const int r = c / cpr, kc = c % cpr;
+            const bool ok = r < N && kc * 8 < klen;
+            const int64_t idx = (int64_t) min(r, (int) N - 1) * p.ldx + kb + min(kc * 8, klen - 8);
+            const uint4 x = load_x8<XF32>(p.x, idx);
+            v[u] = ok ? x : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < kStageBatch; ++u) {
+            const int c = c0 + u * kSkinnyWaves * 64 + tid;
+            if (c < total) *(uint4 *) (xs + (c / cpr) * pitch + (c % cpr) * 8) = v[u];
+        }
+    }
     __syncthreads();
 
-    f32x4_t acc[NT];
+    f32x4_t acc[RG][NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[rg][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint16_t * xrow = xs + r16 * pitch + 8 * g;
     for (int st0 = 0; st0 < nsteps; st0 += kSkinnyDepth) {
 #pragma unroll
         for (int i = 0; i < kSkinnyDepth; ++i) {
             const int st = st0 + i;
             if (st < nsteps) {
+                // registers -> wave tile (row 4c + lrow, chunk lchunk)
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int kk = st * 128 + 32 * g + 8 * c;
+                for (int c = 0; c < LI; ++c) {
+                    const int r = 4 * c + lrow;
+                    *(uint4 *) (wt + r * 128 + ((lchunk ^ (r & 15)) << 3)) = wbuf[i][c];
+                }
+                // MFMA chunk q: lane holds row r16 of group rg, columns 32q + 8g .. +8
 #pragma unroll
-                    for (int t = 0; t < NT; ++t) {
-                        const bf16x8_t a = *(const bf16x8_t *) (xs + (16 * t + r16) * pitch + kk);
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, wbuf[i][c]),
-                                                                         acc[t], 0, 0, 0);
-                    }
+                for (int q = 0; q < 4; ++q) {
+                    bf16x8_t wa[RG], xa[NT];
+#pragma unroll
+                    for (int rg = 0; rg < RG; ++rg)
+                        wa[rg] = *(const bf16x8_t *) (wt + (16 * rg + r16) * 128 + (((4 * q + g) ^ r16) << 3));
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+                        xa[t] = *(const bf16x8_t *) (xrow + 16 * t * pitch + st * 128 + 32 * q);
+#pragma unroll
+                    for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+                        for (int t = 0; t < NT; ++t)
+                            acc[rg][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[t], wa[rg], acc[rg][t], 0, 0, 0);
                 }
             }
             wload(min(st + kSkinnyDepth, nsteps - 1), wbuf[i]);
@@ -598,60 +645,95 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
 
     // 16x16 fragment: lane holds column (lane & 15) = feature, register r
     // holds row 4*(lane/16) + r = token within the tile.
-    if (mrow >= M) return;
-    if (gridDim.y == 1) {
+    float * pp = gridDim.y == 1 ? nullptr : part + (int64_t) blockIdx.y * N * M;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+        const int64_t mrow = m0 + 16 * rg + r16;
+        if (mrow >= M) continue;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t n = 16 * t + 4 * g + r;
-                if (n < N) store_out(p, p.y, p.res, n, mrow, acc[t][r]);
+                if (n >= N) continue;
+                if (pp) pp[n * M + mrow] = acc[rg][t][r];
+                else store_out(p, p.y, p.res, n, mrow, acc[rg][t][r]);
             }
-        return;
     }
-    float * pp = part + (int64_t) blockIdx.y * N * M;
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t n = 16 * t + 4 * g + r;
-            if (n < N) pp[n * M + mrow] = acc[t][r];
-        }
 }
 
-__global__ __launch_bounds__(256) void gemm_skinny_reduce(GemmParams p, const float * part, int splits) {
-    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+// LDS bytes of gemm_skinny_part: activation slice + the waves' weight tiles.
+static size_t skinny_lds_bytes(int nt, int ks) {
+    return (size_t) 16 * nt * (ks + 8) * sizeof(uint16_t) +
+           (size_t) kSkinnyWaves * kSkinnyRows * 128 * sizeof(uint16_t);
+}
+
+// V outputs per thread (V = 4 needs M % 4 == 0, so the four share a row).
+template <int V>
+__global__ __launch_bounds__(256) void gemm_skinny_reduce(GemmParams p, const float * __restrict__ part, int splits) {
+    typedef __attribute__((__vector_size__(V * sizeof(float)))) float fv_t;
     const int64_t total = p.N * p.M;
-    if (i >= total) return;
-    float s = part[i];
-    for (int sp = 1; sp < splits; ++sp) s += part[(int64_t) sp * total + i];
-    store_out(p, p.y, p.res, i / p.M, i % p.M, s);
+    const int64_t i0 = ((int64_t) blockIdx.x * 256 + threadIdx.x) * V;
+    if (i0 >= total) return;
+    fv_t s = *(const fv_t *) (part + i0);
+    constexpr int kBatch = 8;
+    for (int sp0 = 1; sp0 < splits; sp0 += kBatch) {
+        fv_t v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) v[u] = *(const fv_t *) (part + (int64_t) min(sp0 + u, splits - 1) * total + i0);
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (sp0 + u < splits) s += v[u];
+    }
+    const int64_t n = i0 / p.M, m = i0 % p.M;
+#pragma unroll
+    for (int e = 0; e < V; ++e) store_out(p, p.y, p.res, n, m + e, s[e]);
 }
 
-// K split of the skinny path: ~512 workgroups, slices of 256..1024 columns.
-static void skinny_plan(int64_t M, int64_t K, int & splits, int & ks) {
+// K split of the skinny path, from a small cost model (microseconds): the
+// slowest CU streams ceil(workgroups / 256) slices of kSkinnyFeat x ks
+// weights at its 1/256 share of 8 TB/s, plus a ramp per workgroup (one
+// workgroup per CU is resident: 8 waves of ~155 VGPRs); a split adds the fp32
+// partials (written and read once) and the reduce launch.  Measured on the
+// 48-token shapes this picks the fastest slice of the sweep for each.
+static void skinny_plan(int64_t M, int64_t N, int64_t K, int & splits, int & ks) {
     const int64_t nfb = (M + kSkinnyFeat - 1) / kSkinnyFeat;
-    int64_t s = (512 + nfb - 1) / nfb;                // aim at ~512 workgroups
-    s = std::max<int64_t>(1, std::min<int64_t>(s, K / 256));
-    int64_t k = ((K + s - 1) / s + 127) / 128 * 128;  // slice length, multiple of 128
-    k = std::min<int64_t>(k, 1024);
-    splits = (int) ((K + k - 1) / k);
-    ks = (int) k;
+    const int64_t nt = (N + 15) / 16;
+    double best = 1e30;
+    splits = (int) ((K + 127) / 128);
+    ks = 128;
+    for (int k = 128; k <= kSkinnyMaxKs; k += 128) {
+        const int64_t s = (K + k - 1) / k;
+        if (s > 1 && (int64_t) k * (s - 1) >= K) continue;
+        const size_t lds = skinny_lds_bytes((int) nt, k);
+        if (lds > kSkinnyLdsMax) break;
+        const int64_t wgs = nfb * s;
+        const int64_t per_cu = (wgs + 255) / 256;
+        double t = per_cu * ((double) kSkinnyFeat * std::min<int64_t>(k, K) * 2 / 31.25e3 + 1.5);
+        if (s > 1) t += (double) s * N * M * 4 * 2 / 8e6 + 3.0;
+        if (t < best) {
+            best = t;
+            splits = (int) s;
+            ks = k;
+        }
+        if (k >= K) break;
+    }
 }
 
 size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     int splits, ks;
-    skinny_plan(M, K, splits, ks);
+    skinny_plan(M, N, K, splits, ks);
     return splits > 1 ? (size_t) splits * N * M * sizeof(float) : 0;
 }
 
 template <bool XF32>
 static hipError_t run_skinny(const GemmParams & p, void * ws, size_t ws_bytes, hipStream_t s) {
     int splits, ks;
-    skinny_plan(p.M, p.K, splits, ks);
-    if (splits > 1 && (!ws || (size_t) splits * p.N * p.M * sizeof(float) > ws_bytes)) return hipErrorInvalidValue;
+    skinny_plan(p.M, p.N, p.K, splits, ks);
+    if (splits > 1 && (!ws || (size_t) splits * p.N * p.M * sizeof(float) > ws_bytes || ((uintptr_t) ws & 15)))
+        return hipErrorInvalidValue;
     const int nt = (int) ((p.N + 15) / 16);
-    const size_t lds = (size_t) 16 * nt * (ks + 8) * sizeof(uint16_t);
+    const size_t lds = skinny_lds_bytes(nt, ks);
     const dim3 grid((unsigned) ((p.M + kSkinnyFeat - 1) / kSkinnyFeat), (unsigned) splits);
     const dim3 block(kSkinnyWaves * 64);
     float * part = (float *) ws;
@@ -663,8 +745,12 @@ static hipError_t run_skinny(const GemmParams & p, void * ws, size_t ws_bytes, h
     }
     if (splits > 1) {
         const int64_t total = p.N * p.M;
-        hipLaunchKernelGGL(gemm_skinny_reduce, dim3((unsigned) ((total + 255) / 256)), dim3(256), 0, s, p,
-                           (const float *) part, splits);
+        if (p.M % 4 == 0)
+            hipLaunchKernelGGL(gemm_skinny_reduce<4>, dim3((unsigned) ((total / 4 + 255) / 256)), dim3(256), 0, s, p,
+                               (const float *) part, splits);
+        else
+            hipLaunchKernelGGL(gemm_skinny_reduce<1>, dim3((unsigned) ((total + 255) / 256)), dim3(256), 0, s, p,
+                               (const float *) part, splits);
     }
     return hipGetLastError();
 }
@@ -772,8 +858,8 @@ hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
                      a.w_bs2 % 8 == 0 && a.w_bs3 % 8 == 0 && a.x_bs2 % 8 == 0 && a.x_bs3 % 8 == 0;
 
     if (vec && batches == 1 && a.N <= 64) {
-        // K slices up to 1024 columns: 64 x 1032 bf16 = 132 KB of LDS.
-        constexpr size_t kMaxLds = 160 * 1024;
+        // The activation slice and the weight tiles may use all 160 KB of LDS.
+        constexpr size_t kMaxLds = kSkinnyLdsMax;
         static bool once = (allow_lds(gemm_skinny_part<true, 1>, kMaxLds), allow_lds(gemm_skinny_part<false, 1>, kMaxLds),
                             allow_lds(gemm_skinny_part<true, 2>, kMaxLds), allow_lds(gemm_skinny_part<false, 2>, kMaxLds),
                             allow_lds(gemm_skinny_part<true, 3>, kMaxLds), allow_lds(gemm_skinny_part<false, 3>, kMaxLds),

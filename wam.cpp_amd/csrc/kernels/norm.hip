@@ -14,6 +14,8 @@
 #include "../internal.h"
 #include "device.h"
 
+#include <algorithm>
+
 namespace wamx {
 
 constexpr int kNormThreads = 256;
@@ -193,12 +195,134 @@ __global__ void bias_gelu_bf16_kernel(const uint16_t * __restrict__ x, const uin
 }
 
 // ---------------------------------------------------------------------------
+// Vectorised form of norm_mod_bf16_kernel for 16-byte aligned rows with
+// cols % 8 == 0: thread i of the row owns CPT chunks of 8 elements, and the
+// row, scale and shift chunks are all loaded before the first reduction, so a
+// row costs one memory round trip.  The block is sized to the row (up to
+// 1024 threads), which spreads a short batch of rows over more waves.
+template <bool AFFINE, bool SS_BF16, int CPT>
+__global__ __launch_bounds__(1024) void norm_mod_bf16_vec(const uint16_t * __restrict__ x, int64_t ldx,
+                                                           const void * __restrict__ scale,
+                                                           const void * __restrict__ shift, int64_t ss,
+                                                           uint16_t * __restrict__ y, int64_t ldy, int cols, float eps) {
+    __shared__ float red[16];
+    const int64_t row = blockIdx.x;
+    const int nchunk = cols >> 3;
+    const int64_t so = row * ss;
+    uint4 xv[CPT], ha[CPT], hb[CPT];
+    float4 fa[CPT][2], fb[CPT][2];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = min((int) threadIdx.x + i * (int) blockDim.x, nchunk - 1);
+        xv[i] = *(const uint4 *) (x + row * ldx + 8 * c);
+        if constexpr (SS_BF16) {
+            ha[i] = *(const uint4 *) ((const uint16_t *) scale + so + 8 * c);
+            hb[i] = *(const uint4 *) ((const uint16_t *) shift + so + 8 * c);
+        } else {
+            fa[i][0] = *(const float4 *) ((const float *) scale + so + 8 * c);
+            fa[i][1] = *(const float4 *) ((const float *) scale + so + 8 * c + 4);
+            fb[i][0] = *(const float4 *) ((const float *) shift + so + 8 * c);
+            fb[i][1] = *(const float4 *) ((const float *) shift + so + 8 * c + 4);
+        }
+    }
+    float v[CPT][8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const bool ok = (int) threadIdx.x + i * (int) blockDim.x < nchunk;
+        const uint32_t u[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[i][2 * e] = ok ? bf16_to_f32((uint16_t) (u[e] & 0xffff)) : 0.0f;
+            v[i][2 * e + 1] = ok ? bf16_to_f32((uint16_t) (u[e] >> 16)) : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += v[i][e];
+    }
+    const float mean = block_sum(sum, red) / (float) cols;
+    float var = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        if ((int) threadIdx.x + i * (int) blockDim.x >= nchunk) continue;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float d = v[i][e] - mean;
+            var = fmaf(d, d, var);
+        }
+    }
+    var = block_sum(var, red) / (float) cols;
+    const float inv_std = rsqrtf(var + eps);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = (int) threadIdx.x + i * (int) blockDim.x;
+        if (c >= nchunk) continue;
+        float a[8], b[8];
+        if constexpr (SS_BF16) {
+            const uint32_t ua[4] = {ha[i].x, ha[i].y, ha[i].z, ha[i].w}, ub[4] = {hb[i].x, hb[i].y, hb[i].z, hb[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                a[2 * e] = bf16_to_f32((uint16_t) (ua[e] & 0xffff));
+                a[2 * e + 1] = bf16_to_f32((uint16_t) (ua[e] >> 16));
+                b[2 * e] = bf16_to_f32((uint16_t) (ub[e] & 0xffff));
+                b[2 * e + 1] = bf16_to_f32((uint16_t) (ub[e] >> 16));
+            }
+        } else {
+            const float af[8] = {fa[i][0].x, fa[i][0].y, fa[i][0].z, fa[i][0].w, fa[i][1].x, fa[i][1].y, fa[i][1].z, fa[i][1].w};
+            const float bf[8] = {fb[i][0].x, fb[i][0].y, fb[i][0].z, fb[i][0].w, fb[i][1].x, fb[i][1].y, fb[i][1].z, fb[i][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                a[e] = af[e];
+                b[e] = bf[e];
+            }
+        }
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float n = (v[i][e] - mean) * inv_std;
+            o[e] = AFFINE ? fmaf(n, a[e], b[e]) : fmaf(n, 1.0f + a[e], b[e]);
+        }
+        *(uint4 *) (y + row * ldy + 8 * c) =
+            make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7]));
+    }
+}
+
+template <bool AFFINE, bool SS_BF16>
+static hipError_t run_norm_mod_vec(const void * x, int64_t ldx, const void * scale, const void * shift, int64_t ss,
+                                   void * y, int64_t ldy, int64_t rows, int64_t cols, float eps, hipStream_t s) {
+    const int64_t nchunk = cols / 8;
+    const int cpt = nchunk <= 1024 ? 1 : nchunk <= 2048 ? 2 : 4;
+    const int threads = (int) std::min<int64_t>(1024, ((nchunk + cpt - 1) / cpt + 63) / 64 * 64);
+    const dim3 grid((unsigned) rows), block((unsigned) threads);
+    const uint16_t * xp = (const uint16_t *) x;
+    uint16_t * yp = (uint16_t *) y;
+    if (cpt == 1)
+        hipLaunchKernelGGL((norm_mod_bf16_vec<AFFINE, SS_BF16, 1>), grid, block, 0, s, xp, ldx, scale, shift, ss, yp, ldy,
+                           (int) cols, eps);
+    else if (cpt == 2)
+        hipLaunchKernelGGL((norm_mod_bf16_vec<AFFINE, SS_BF16, 2>), grid, block, 0, s, xp, ldx, scale, shift, ss, yp, ldy,
+                           (int) cols, eps);
+    else
+        hipLaunchKernelGGL((norm_mod_bf16_vec<AFFINE, SS_BF16, 4>), grid, block, 0, s, xp, ldx, scale, shift, ss, yp, ldy,
+                           (int) cols, eps);
+    return hipGetLastError();
+}
+
+static bool aligned16(const void * p) { return ((uintptr_t) p & 15) == 0; }
+
 hipError_t launch_norm_mod_bf16(const void * x, int64_t ldx, const void * scale, const void * shift, int32_t ss_type,
                                 int64_t ss, void * y, int64_t ldy, int64_t rows, int64_t cols, float eps, bool affine,
                                 hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    const dim3 grid((unsigned) rows), block(kNormThreads);
     const bool sb = ss_type == WAMX_TYPE_BF16;
+    const int ss_es = (affine || sb) ? 2 : 4;
+    const bool vec = cols % 8 == 0 && cols / 8 <= 4096 && ldx % 8 == 0 && ldy % 8 == 0 && (ss * ss_es) % 16 == 0 &&
+                     aligned16(x) && aligned16(y) && aligned16(scale) && aligned16(shift);
+    if (vec) {
+        if (affine) return run_norm_mod_vec<true, true>(x, ldx, scale, shift, ss, y, ldy, rows, cols, eps, s);
+        if (sb) return run_norm_mod_vec<false, true>(x, ldx, scale, shift, ss, y, ldy, rows, cols, eps, s);
+        return run_norm_mod_vec<false, false>(x, ldx, scale, shift, ss, y, ldy, rows, cols, eps, s);
+    }
+    const dim3 grid((unsigned) rows), block(kNormThreads);
     if (affine) {
         hipLaunchKernelGGL((norm_mod_bf16_kernel<true, true>), grid, block, 0, s, (const uint16_t *) x, ldx, scale, shift,
                            ss, (uint16_t *) y, ldy, (int) cols, eps);
