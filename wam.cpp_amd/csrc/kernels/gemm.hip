@@ -578,12 +578,11 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
             d[c] = v;
         }
     };
-#pragma unroll
-    for (int i = 0; i < kSkinnyDepth; ++i) wload(min(i, nsteps - 1), wbuf[i]);
-
     // Stage x[0..N)[kb..ke) as bf16 (rows past N and columns past ke are zero).
     // Addresses are clamped into the tensor and the values masked, so every
-    // load of a batch is issued before the first LDS store.
+    // load of a batch is issued before the first LDS store.  The first batch
+    // is issued before the weight prefetch: loads complete in order, so
+    // activations queued behind the weight stream would wait for it.
     const int cpr = ks / 8, total = 16 * NT * cpr;
     constexpr int kStageBatch = 8;
     for (int c0 = 0; c0 < total; c0 += kStageBatch * kSkinnyWaves * 64) {
@@ -596,6 +595,10 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
             const int64_t idx = (int64_t) min(r, (int) N - 1) * p.ldx + kb + min(kc * 8, klen - 8);
             const uint4 x = load_x8<XF32>(p.x, idx);
             v[u] = ok ? x : make_uint4(0, 0, 0, 0);
+        }
+        if (c0 == 0) {
+#pragma unroll
+            for (int i = 0; i < kSkinnyDepth; ++i) wload(min(i, nsteps - 1), wbuf[i]);
         }
 #pragma unroll
         for (int u = 0; u < kStageBatch; ++u) {
