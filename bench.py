@@ -4,6 +4,10 @@
 
 Workloads (synthetic, seeded, random-init weights; inputs resident in HBM
 before the timed region):
+  chunk  (default) one GWP-0.5-shaped MoT action chunk: prompt projection,
+         prefix pass over 1 state + 3x1024 visual tokens with 512 prompt
+         tokens, 10 flow-matching denoise steps of the 48-token action
+         expert; 30 layers, d=3072, 24x128 heads, FFN 14336, both experts.
   ffn    one dense FFN block at 2048 tokens: LayerNorm+adaLN modulation ->
          W_up [14336x3072] + bias + GELU-tanh -> W_down [3072x14336] + bias +
          gated residual (bf16 hidden state, fp32 accumulation).
@@ -82,7 +86,7 @@ def workload_gemm(be, args):
     ms = t.stop_ms() / args.steps
     roof = {"bound": "hbm", "achieved": bytes_ / (ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": bytes_ / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "traffic": None,
-            "kernel": "gemm_tile", "tflops": flops / (ms * 1e-3) / 1e12}
+            "kernel": "gemm_tile<128,128> (f32 activations)", "tflops": flops / (ms * 1e-3) / 1e12}
     # CPU baseline: the oracle's MUL_MAT on the full problem.
     t0 = time.perf_counter()
     oracle.mul_mat(w.reshape(M, K), x.reshape(N, K))
@@ -252,9 +256,9 @@ def workload_chunk(be, args):
     aup_bytes = Fa * Da * 2 + Ta * Da * 2 + Ta * Fa * 2 + Fa * 2
     roof = {"bound": "mfma", "achieved": flops / (up_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": flops / (up_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "traffic": None,
-            "kernel": "gemm_tile: prefix visual FFN-up 3072 tok x [14336 x 3072] + bias + GELU",
+            "kernel": "gemm_dma<256,256>: prefix visual FFN-up 3072 tok x [14336 x 3072] + bias + GELU",
             "kernel_ms": up_ms, "flops_per_launch": flops,
-            "skinny": {"kernel": "gemm_skinny: denoise FFN-up 48 tok x [14336 x 3072] + bias + GELU",
+            "skinny": {"kernel": "gemm_skinny_part + gemm_skinny_reduce: denoise FFN-up 48 tok x [14336 x 3072] + bias + GELU",
                        "kernel_ms": aup_ms, "achieved_gbs": aup_bytes / (aup_ms * 1e-3) / 1e9,
                        "frac_hbm": aup_bytes / (aup_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}}
 
