@@ -221,8 +221,13 @@ def test_qk_norm_rope(wx, be, orc, rng, mode):
 
 
 # --- attention ----------------------------------------------------------------------
+# Cases reach every kernel: key-split decode (tq <= 64 with many keys), the
+# single-workgroup decode (few keys), the LDS-tiled prefill (tq > 64, one key
+# source, ragged query and key blocks, prefix length 3073) and the generic
+# many-query kernel (two sources).
 @pytest.mark.parametrize("H,tq,na,nb,split", [(24, 48, 3076, 48, 1), (4, 48, 1028, 48, 1), (2, 5, 64, 0, 0),
-                                              (3, 200, 200, 0, 0), (2, 48, 512, 0, 0), (1, 1, 4, 4, 2)])
+                                              (3, 200, 200, 0, 0), (2, 48, 512, 0, 0), (1, 1, 4, 4, 2),
+                                              (2, 3073, 3072, 0, 0), (1, 130, 520, 0, 0), (2, 100, 96, 8, 1)])
 def test_joint_attention(wx, be, orc, H, tq, na, nb, split):
     print(f"joint_attn H={H} tq={tq} na={na} nb={nb}", flush=True)
     rng = np.random.default_rng(H * tq + na)

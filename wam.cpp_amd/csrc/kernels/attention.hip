@@ -197,6 +197,20 @@ hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void
 // ---------------------------------------------------------------------------
 // joint_attn
 // ---------------------------------------------------------------------------
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+// s_waitcnt immediate: at most n vector-memory operations outstanding, other
+// counters untouched (vmcnt in bits [3:0] and [15:14]).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | (7 << 4) | (0xF << 8); }
+
+__device__ __forceinline__ void cta_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 constexpr int kDh = 128;         // head_dim
 constexpr int kKB = 32;          // keys per block
 constexpr float kLog2e = 1.4426950408889634f;
@@ -456,6 +470,196 @@ __global__ __launch_bounds__(kDh) void joint_attn_merge(AttnParams p, int nsplit
     p.out[q * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
 }
 
+
+// ---------------------------------------------------------------------------
+// attn_prefill: softmax(scale * Q K^T) V for many queries over one key source
+// (the prefix self-attention, 3073 x 3073 keys per head, and the visual
+// cross-attention over the 512 prompt keys).
+//
+// Workgroup: 4 waves x 32 queries of one head.  Key blocks of 64: the K tile
+// [64 keys][128] and the V^T tile [128][64 keys] are copied into LDS with
+// global_load_lds_dwordx4 through a 2-stage ring (separate LDS objects, loop
+// unrolled by 2, so only the stage being read is waited for), shared by the
+// four waves.  Per block and wave: S^T = K Q^T with MFMA 32x32x16 (Q^T
+// fragments held in registers for the whole key loop), online softmax in the
+// log2 domain with P rounded to bf16, then O^T += V^T P^T with the P operand
+// taken straight from the S^T accumulators: the key slots of a PV k-step are
+// the keys that accumulator layout gives each lane half, and the V^T operand
+// reads the same keys as two 8-byte pieces.  Keys past the source length are
+// masked (scores to -inf, V^T values to zero).  The normalised O^T goes
+// through LDS so the output rows are written as 16-byte pieces.
+//
+// LDS rows are XOR-swizzled by 16-byte chunk: K chunk c of key r at
+// c ^ (r & 15), V^T chunk c of row d at c ^ ((d >> 1) & 7).
+// ---------------------------------------------------------------------------
+constexpr int kPfKeys = 64;
+constexpr int kPfWaves = 4;
+constexpr int kPfQueries = 32 * kPfWaves;
+constexpr int kPfStageElems = kPfKeys * kDh + kDh * kPfKeys;  // K tile + V^T tile
+
+__device__ __forceinline__ int pf_kswz(int key, int c) { return c ^ (key & 15); }
+__device__ __forceinline__ int pf_vswz(int d, int c) { return c ^ ((d >> 1) & 7); }
+
+__global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnParams p) {
+    __shared__ __align__(16) uint16_t st0[kPfStageElems];
+    __shared__ __align__(16) uint16_t st1[kPfStageElems];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, hl = lane >> 5;
+    const int64_t h = blockIdx.x, q0 = (int64_t) blockIdx.y * kPfQueries;
+    const int64_t nk = p.seg_len[0], vld = p.vt_ld[0];
+    const uint16_t * kbase = p.k[0] + h * nk * kDh;
+    const uint16_t * vbase = p.vt[0] + h * kDh * vld;
+    const int nblk = (int) ((nk + kPfKeys - 1) / kPfKeys);
+
+    // DMA slots: K tile 1024 chunks (key = s / 16), V^T tile 1024 chunks (row = s / 8).
+    auto dma = [&](int blk, uint16_t * stage) {
+        const int64_t k0 = (int64_t) min(blk, nblk - 1) * kPfKeys;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int slot = (i * kPfWaves + wave) * 64 + lane;
+            const int key = slot >> 4, c = pf_kswz(key, slot & 15);
+            const int64_t kr = min(k0 + key, nk - 1);
+            __builtin_amdgcn_global_load_lds((glb_void_t *) (kbase + kr * kDh + 8 * c),
+                                             (lds_void_t *) (stage + (i * kPfWaves + wave) * 512), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int slot = (i * kPfWaves + wave) * 64 + lane;
+            const int d = slot >> 3, c = pf_vswz(d, slot & 7);
+            const int64_t kc = min(k0 + 8 * c, vld - 8);
+            __builtin_amdgcn_global_load_lds((glb_void_t *) (vbase + (int64_t) d * vld + kc),
+                                             (lds_void_t *) (stage + kPfKeys * kDh + (i * kPfWaves + wave) * 512), 16,
+                                             0, 0);
+        }
+    };
+
+    // Q^T fragments (B operand of S^T = K Q^T): lane holds query l32 of the
+    // wave, dims 16s + 8hl .. +8 for k-step s.
+    bf16x8_t qf[8];
+    {
+        const int64_t qi = min(q0 + 32 * wave + l32, p.tq - 1);
+        const uint16_t * qrow = p.q + (h * p.tq + qi) * kDh + 8 * hl;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) qf[s] = *(const bf16x8_t *) (qrow + 16 * s);
+    }
+
+    f32x16_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    auto block = [&](int blk, const uint16_t * stage) {
+        const uint16_t * kt = stage;
+        const uint16_t * vt = stage + kPfKeys * kDh;
+        const int valid = (int) min((int64_t) kPfKeys, nk - (int64_t) blk * kPfKeys);
+        // S^T tiles: key tile t (32 keys) x the wave's 32 queries.
+        f32x16_t sacc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sacc[t][v] = 0.0f;
+            const int key = 32 * t + l32;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const bf16x8_t kf = *(const bf16x8_t *) (kt + key * kDh + 8 * pf_kswz(key, 2 * s + hl));
+                sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sacc[t], 0, 0, 0);
+            }
+        }
+        // Online softmax: lane holds query l32, keys 32t + 8(v/4) + 4hl + v%4;
+        // the other keys of its query are in lane ^ 32.
+        f32x16_t (&sv)[2] = sacc;  // scores are turned into probabilities in place
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int key = 32 * t + 8 * (v >> 2) + 4 * hl + (v & 3);
+                sv[t][v] = key < valid ? sacc[t][v] * p.scale_log2 : -INFINITY;
+                mx = fmaxf(mx, sv[t][v]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);
+        const float corr = exp2f(m_run - m_new);
+        float ps = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                sv[t][v] = round_bf16(exp2f(sv[t][v] - m_new));
+                ps += sv[t][v];
+            }
+        ps += __shfl_xor(ps, 32, 64);
+        l_run = l_run * corr + ps;
+        m_run = m_new;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[i][v] *= corr;
+        // O^T += V^T P^T, k-step (t, hh): key slots 0-3 = keys 32t+16hh+4hl+{0..3},
+        // slots 4-7 = keys 32t+16hh+8+4hl+{0..3}.
+        const bool partial = valid < kPfKeys;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const bf16x8_t pf = __builtin_bit_cast(
+                    bf16x8_t, make_uint4(pack_bf16x2(sv[t][8 * hh + 0], sv[t][8 * hh + 1]),
+                                         pack_bf16x2(sv[t][8 * hh + 2], sv[t][8 * hh + 3]),
+                                         pack_bf16x2(sv[t][8 * hh + 4], sv[t][8 * hh + 5]),
+                                         pack_bf16x2(sv[t][8 * hh + 6], sv[t][8 * hh + 7])));
+                const int ka = 32 * t + 16 * hh + 4 * hl;  // first key of each 8-byte piece: ka, ka + 8
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int d = 32 * i + l32;
+                    const uint16_t * row = vt + d * kPfKeys;
+                    uint2 a = *(const uint2 *) (row + 8 * pf_vswz(d, ka >> 3) + (ka & 7));
+                    uint2 b = *(const uint2 *) (row + 8 * pf_vswz(d, (ka + 8) >> 3) + ((ka + 8) & 7));
+                    if (partial) {
+                        a = mask4(a, ka, valid);
+                        b = mask4(b, ka + 8, valid);
+                    }
+                    const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, make_uint4(a.x, a.y, b.x, b.y));
+                    o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[i], 0, 0, 0);
+                }
+            }
+    };
+    auto step = [&](int blk, const uint16_t * cur, uint16_t * nxt) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        cta_barrier();
+        if (blk + 1 < nblk) dma(blk + 1, nxt);
+        block(blk, cur);
+    };
+
+    dma(0, st0);
+    for (int blk = 0; blk < nblk; blk += 2) {
+        step(blk, st0, st1);
+        if (blk + 1 < nblk) step(blk + 1, st1, st0);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    cta_barrier();
+
+    // Normalise and stage O (bf16, [query][dh]) in LDS, then write whole rows.
+    uint16_t * ot = st0;  // 128 queries x 128 dims = 32 KB <= one stage
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int d = 32 * i + 8 * (v >> 2) + 4 * hl + (v & 3);
+            ot[(32 * wave + l32) * kDh + d] = f32_to_bf16(o[i][v] * inv);
+        }
+    // A full workgroup fence: the LDS writes above must complete before other
+    // waves read them (a bare s_barrier does not wait for them).
+    __syncthreads();
+    const int64_t nq = min((int64_t) kPfQueries, p.tq - q0);
+    for (int c = tid; c < nq * (kDh / 8); c += kPfWaves * 64) {
+        const int q = c / (kDh / 8), dc = c % (kDh / 8);
+        *(uint4 *) (p.out + (q0 + q) * (p.heads * kDh) + h * kDh + 8 * dc) = *(const uint4 *) (ot + q * kDh + 8 * dc);
+    }
+}
+
 // Softmax is order-free, so the keys are visited per source in 32-key blocks
 // aligned to each source's start: source a ([state, reference] prefix cache,
 // na keys) and source b (the current action tokens, nb keys).  The complete
@@ -492,8 +696,17 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
         if (p.seg_len[i] > 0 &&
             (p.vt_ld[i] % 4 != 0 || p.vt_ld[i] < p.seg_len[i] || ((uintptr_t) p.vt[i] & 7) || ((uintptr_t) p.k[i] & 15)))
             return hipErrorInvalidValue;
-    // Many queries (the prefix pass): 48-query groups, 4 waves, one workgroup
-    // per (head, group).
+    // Many queries over one key source (the prefix self-attention, the
+    // visual cross-attention): the LDS-tiled flash kernel.
+    if (a.tq > 64 && p.seg_len[1] == 0 && p.seg_len[0] >= 8 && p.vt_ld[0] % 8 == 0 && ((uintptr_t) p.vt[0] & 15) == 0 &&
+        ((uintptr_t) p.q & 15) == 0 && ((uintptr_t) p.out & 15) == 0) {
+        const int64_t qblocks = (a.tq + kPfQueries - 1) / kPfQueries;
+        hipLaunchKernelGGL(attn_prefill_kernel, dim3((unsigned) a.heads, (unsigned) qblocks), dim3(kPfWaves * 64), 0, s,
+                           p);
+        return hipGetLastError();
+    }
+    // Other many-query cases: 48-query groups, 4 waves, one workgroup per
+    // (head, group).
     if (a.tq > 64) {
         const int64_t qgroups = (a.tq + 47) / 48;
         hipLaunchKernelGGL((joint_attn_kernel<3, 4, false>), dim3((unsigned) a.heads, (unsigned) qgroups), dim3(256), 0,
