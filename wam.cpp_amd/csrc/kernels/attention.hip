@@ -550,65 +550,76 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
         for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    auto block = [&](int blk, const uint16_t * stage) {
+    // Softmax state per lane (its query): m_run is the running max of
+    // scale*log2(e)*s used as the exponent offset.  It is raised lazily, only
+    // when a block's max exceeds it by more than kPfSlack, so most blocks skip
+    // rescaling O; probabilities stay <= 2^kPfSlack and O / l is unchanged.
+    constexpr float kPfSlack = 8.0f;
+    auto block = [&](int blk, const uint16_t * stage, bool partial) __attribute__((always_inline)) {
         const uint16_t * kt = stage;
         const uint16_t * vt = stage + kPfKeys * kDh;
-        const int valid = (int) min((int64_t) kPfKeys, nk - (int64_t) blk * kPfKeys);
+        const int valid = partial ? (int) (nk - (int64_t) blk * kPfKeys) : kPfKeys;
         // S^T tiles: key tile t (32 keys) x the wave's 32 queries.
         f32x16_t sacc[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) sacc[t][v] = 0.0f;
-            const int key = 32 * t + l32;
+            const uint16_t * krow = kt + (32 * t + l32) * kDh;
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const bf16x8_t kf = *(const bf16x8_t *) (kt + key * kDh + 8 * pf_kswz(key, 2 * s + hl));
+                const bf16x8_t kf = *(const bf16x8_t *) (krow + 8 * pf_kswz(l32, 2 * s + hl));
                 sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sacc[t], 0, 0, 0);
             }
         }
-        // Online softmax: lane holds query l32, keys 32t + 8(v/4) + 4hl + v%4;
-        // the other keys of its query are in lane ^ 32.
-        f32x16_t (&sv)[2] = sacc;  // scores are turned into probabilities in place
-        float mx = -INFINITY;
+        // Lane holds query l32, keys 32t + 8(v/4) + 4hl + v%4; the other keys
+        // of its query are in lane ^ 32.
+        if (partial) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    if (32 * t + 8 * (v >> 2) + 4 * hl + (v & 3) >= valid) sacc[t][v] = -INFINITY;
+        }
+        float mx = sacc[0][0];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int key = 32 * t + 8 * (v >> 2) + 4 * hl + (v & 3);
-                sv[t][v] = key < valid ? sacc[t][v] * p.scale_log2 : -INFINITY;
-                mx = fmaxf(mx, sv[t][v]);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx);
-        const float corr = exp2f(m_run - m_new);
+            for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sacc[t][v]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * p.scale_log2;
+        if (__builtin_amdgcn_read_exec() & __ballot(mx > m_run + kPfSlack)) {
+            const float m_new = mx > m_run + kPfSlack ? mx : m_run;
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= corr;
+            m_run = m_new;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[i][v] *= corr;
+        }
+        // P = bf16(2^(scale*log2e*s - m)), packed in pairs for the PV operand;
+        // the row sum adds the rounded values.
+        uint32_t pk[2][8];
         float ps = 0.0f;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                sv[t][v] = round_bf16(exp2f(sv[t][v] - m_new));
-                ps += sv[t][v];
+            for (int j = 0; j < 8; ++j) {
+                const float e0 = __builtin_amdgcn_exp2f(fmaf(sacc[t][2 * j], p.scale_log2, -m_run));
+                const float e1 = __builtin_amdgcn_exp2f(fmaf(sacc[t][2 * j + 1], p.scale_log2, -m_run));
+                pk[t][j] = pack_bf16x2(e0, e1);
+                ps += __uint_as_float(pk[t][j] << 16) + __uint_as_float(pk[t][j] & 0xffff0000u);
             }
         ps += __shfl_xor(ps, 32, 64);
-        l_run = l_run * corr + ps;
-        m_run = m_new;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) o[i][v] *= corr;
+        l_run += ps;
         // O^T += V^T P^T, k-step (t, hh): key slots 0-3 = keys 32t+16hh+4hl+{0..3},
         // slots 4-7 = keys 32t+16hh+8+4hl+{0..3}.
-        const bool partial = valid < kPfKeys;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const bf16x8_t pf = __builtin_bit_cast(
-                    bf16x8_t, make_uint4(pack_bf16x2(sv[t][8 * hh + 0], sv[t][8 * hh + 1]),
-                                         pack_bf16x2(sv[t][8 * hh + 2], sv[t][8 * hh + 3]),
-                                         pack_bf16x2(sv[t][8 * hh + 4], sv[t][8 * hh + 5]),
-                                         pack_bf16x2(sv[t][8 * hh + 6], sv[t][8 * hh + 7])));
+                    bf16x8_t, make_uint4(pk[t][4 * hh], pk[t][4 * hh + 1], pk[t][4 * hh + 2], pk[t][4 * hh + 3]));
                 const int ka = 32 * t + 16 * hh + 4 * hl;  // first key of each 8-byte piece: ka, ka + 8
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -625,11 +636,11 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
                 }
             }
     };
-    auto step = [&](int blk, const uint16_t * cur, uint16_t * nxt) {
+    auto step = [&](int blk, const uint16_t * cur, uint16_t * nxt) __attribute__((always_inline)) {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         cta_barrier();
         if (blk + 1 < nblk) dma(blk + 1, nxt);
-        block(blk, cur);
+        block(blk, cur, (int64_t) (blk + 1) * kPfKeys > nk);
     };
 
     dma(0, st0);
