@@ -221,13 +221,18 @@ def test_qk_norm_rope(wx, be, orc, rng, mode):
 
 
 # --- attention ----------------------------------------------------------------------
-# Cases reach every kernel: key-split decode (tq <= 64 with many keys), the
-# single-workgroup decode (few keys), the LDS-tiled prefill (tq > 64, one key
-# source, ragged query and key blocks, prefix length 3073) and the generic
-# many-query kernel (two sources).
+# Cases reach every kernel:
+#  * LDS-tiled flash kernel (key rows 16-byte aligned, V^T rows a multiple of 8
+#    keys): prefill (tq > 64, one source, ragged query and key blocks, 3073
+#    queries) and key-split decode over one or two sources (48 queries);
+#  * register-streamed key-split decode and its single-workgroup form (V^T rows
+#    a multiple of 4 keys only);
+#  * the generic many-query kernel (two sources, tq > 64).
 @pytest.mark.parametrize("H,tq,na,nb,split", [(24, 48, 3076, 48, 1), (4, 48, 1028, 48, 1), (2, 5, 64, 0, 0),
                                               (3, 200, 200, 0, 0), (2, 48, 512, 0, 0), (1, 1, 4, 4, 2),
-                                              (2, 3073, 3072, 0, 0), (1, 130, 520, 0, 0), (2, 100, 96, 8, 1)])
+                                              (2, 3073, 3072, 0, 0), (1, 130, 520, 0, 0), (2, 100, 96, 8, 1),
+                                              (8, 48, 3080, 48, 1), (3, 48, 520, 0, 0), (2, 17, 64, 8, 1),
+                                              (1, 64, 200, 16, 1)])
 def test_joint_attention(wx, be, orc, H, tq, na, nb, split):
     print(f"joint_attn H={H} tq={tq} na={na} nb={nb}", flush=True)
     rng = np.random.default_rng(H * tq + na)

@@ -453,19 +453,37 @@ __global__ __launch_bounds__(NW * 64) void joint_attn_kernel(AttnParams p) {
 // Combines the key-split partials of one (head, query) per 128-thread
 // workgroup, splits in order: m* = max m_z, l* = sum l_z 2^(m_z - m*),
 // out = sum o_z 2^(m_z - m*) / l*.
+// All loads of a batch of eight splits are issued before they are combined.
 __global__ __launch_bounds__(kDh) void joint_attn_merge(AttnParams p, int nsplit) {
     const int64_t hq = blockIdx.x, h = hq / p.tq, q = hq % p.tq;
     const int d = threadIdx.x;
     const int64_t stride = p.heads * p.tq;
+    constexpr int kB = 8;
     float mstar = -INFINITY;
-    for (int z = 0; z < nsplit; ++z) mstar = fmaxf(mstar, p.part_m[z * stride + hq]);
+    for (int z0 = 0; z0 < nsplit; z0 += kB) {
+        float m[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) m[u] = p.part_m[min(z0 + u, nsplit - 1) * stride + hq];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) mstar = fmaxf(mstar, m[u]);
+    }
     float l = 0.0f, o = 0.0f;
-    for (int z = 0; z < nsplit; ++z) {
-        const float mz = p.part_m[z * stride + hq];
-        if (mz == -INFINITY) continue;
-        const float w = exp2f(mz - mstar);
-        l += p.part_l[z * stride + hq] * w;
-        o += p.part_o[(z * stride + hq) * kDh + d] * w;
+    for (int z0 = 0; z0 < nsplit; z0 += kB) {
+        float m[kB], lz[kB], oz[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+            const int64_t z = min(z0 + u, nsplit - 1);
+            m[u] = p.part_m[z * stride + hq];
+            lz[u] = p.part_l[z * stride + hq];
+            oz[u] = p.part_o[(z * stride + hq) * kDh + d];
+        }
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+            if (z0 + u >= nsplit || m[u] == -INFINITY) continue;
+            const float w = exp2f(m[u] - mstar);
+            l += lz[u] * w;
+            o += oz[u] * w;
+        }
     }
     p.out[q * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
 }
@@ -500,34 +518,52 @@ constexpr int kPfStageElems = kPfKeys * kDh + kDh * kPfKeys;  // K tile + V^T ti
 __device__ __forceinline__ int pf_kswz(int key, int c) { return c ^ (key & 15); }
 __device__ __forceinline__ int pf_vswz(int d, int c) { return c ^ ((d >> 1) & 7); }
 
+template <bool SPLIT>
 __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnParams p) {
     __shared__ __align__(16) uint16_t st0[kPfStageElems];
     __shared__ __align__(16) uint16_t st1[kPfStageElems];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, hl = lane >> 5;
     const int64_t h = blockIdx.x, q0 = (int64_t) blockIdx.y * kPfQueries;
-    const int64_t nk = p.seg_len[0], vld = p.vt_ld[0];
-    const uint16_t * kbase = p.k[0] + h * nk * kDh;
-    const uint16_t * vbase = p.vt[0] + h * kDh * vld;
-    const int nblk = (int) ((nk + kPfKeys - 1) / kPfKeys);
+    // Key blocks of 64: source a's blocks, then source b's (each source's last
+    // block partial).
+    const int nblk_a = (int) ((p.seg_len[0] + kPfKeys - 1) / kPfKeys);
+    const int nblk = nblk_a + (int) ((p.seg_len[1] + kPfKeys - 1) / kPfKeys);
+    const int b_begin = SPLIT ? (int) blockIdx.z * (int) p.split_blocks : 0;
+    const int b_end = SPLIT ? min(nblk, b_begin + (int) p.split_blocks) : nblk;
+    struct Blk {
+        const uint16_t * kb;
+        const uint16_t * vb;
+        int64_t vld, k0, nk;
+    };
+    auto locate = [&](int blk) {
+        const int seg = blk < nblk_a ? 0 : 1;
+        Blk r;
+        r.nk = p.seg_len[seg];
+        r.vld = p.vt_ld[seg];
+        r.k0 = (int64_t) (blk - (seg ? nblk_a : 0)) * kPfKeys;
+        r.kb = p.k[seg] + h * r.nk * kDh;
+        r.vb = p.vt[seg] + h * kDh * r.vld;
+        return r;
+    };
 
     // DMA slots: K tile 1024 chunks (key = s / 16), V^T tile 1024 chunks (row = s / 8).
     auto dma = [&](int blk, uint16_t * stage) {
-        const int64_t k0 = (int64_t) min(blk, nblk - 1) * kPfKeys;
+        const Blk bl = locate(min(blk, b_end - 1));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int slot = (i * kPfWaves + wave) * 64 + lane;
             const int key = slot >> 4, c = pf_kswz(key, slot & 15);
-            const int64_t kr = min(k0 + key, nk - 1);
-            __builtin_amdgcn_global_load_lds((glb_void_t *) (kbase + kr * kDh + 8 * c),
+            const int64_t kr = min(bl.k0 + key, bl.nk - 1);
+            __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.kb + kr * kDh + 8 * c),
                                              (lds_void_t *) (stage + (i * kPfWaves + wave) * 512), 16, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int slot = (i * kPfWaves + wave) * 64 + lane;
             const int d = slot >> 3, c = pf_vswz(d, slot & 7);
-            const int64_t kc = min(k0 + 8 * c, vld - 8);
-            __builtin_amdgcn_global_load_lds((glb_void_t *) (vbase + (int64_t) d * vld + kc),
+            const int64_t kc = min(bl.k0 + 8 * c, bl.vld - 8);
+            __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.vb + (int64_t) d * bl.vld + kc),
                                              (lds_void_t *) (stage + kPfKeys * kDh + (i * kPfWaves + wave) * 512), 16,
                                              0, 0);
         }
@@ -558,7 +594,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
     auto block = [&](int blk, const uint16_t * stage, bool partial) __attribute__((always_inline)) {
         const uint16_t * kt = stage;
         const uint16_t * vt = stage + kPfKeys * kDh;
-        const int valid = partial ? (int) (nk - (int64_t) blk * kPfKeys) : kPfKeys;
+        const Blk bl = locate(blk);
+        const int valid = partial ? (int) (bl.nk - bl.k0) : kPfKeys;
         // S^T tiles: key tile t (32 keys) x the wave's 32 queries.
         f32x16_t sacc[2];
 #pragma unroll
@@ -639,17 +676,39 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
     auto step = [&](int blk, const uint16_t * cur, uint16_t * nxt) __attribute__((always_inline)) {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         cta_barrier();
-        if (blk + 1 < nblk) dma(blk + 1, nxt);
-        block(blk, cur, (int64_t) (blk + 1) * kPfKeys > nk);
+        if (blk + 1 < b_end) dma(blk + 1, nxt);
+        const Blk bl = locate(blk);
+        block(blk, cur, bl.k0 + kPfKeys > bl.nk);
     };
 
-    dma(0, st0);
-    for (int blk = 0; blk < nblk; blk += 2) {
+    dma(b_begin, st0);
+    for (int blk = b_begin; blk < b_end; blk += 2) {
         step(blk, st0, st1);
-        if (blk + 1 < nblk) step(blk + 1, st1, st0);
+        if (blk + 1 < b_end) step(blk + 1, st1, st0);
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     cta_barrier();
+
+    if constexpr (SPLIT) {
+        // Unnormalised O^T with its running max (log2 domain) and sum, for
+        // joint_attn_merge: part_o [split][head][query][dh].
+        const int64_t qi = q0 + 32 * wave + l32;
+        if (qi < p.tq) {
+            const int64_t pi = ((int64_t) blockIdx.z * p.heads + h) * p.tq + qi;
+            if (hl == 0) {
+                p.part_m[pi] = m_run;
+                p.part_l[pi] = l_run;
+            }
+            float * po = p.part_o + pi * kDh;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 16; v += 4)
+                    *(float4 *) (po + 32 * i + 8 * (v >> 2) + 4 * hl) =
+                        make_float4(o[i][v], o[i][v + 1], o[i][v + 2], o[i][v + 3]);
+        }
+        return;
+    }
 
     // Normalise and stage O (bf16, [query][dh]) in LDS, then write whole rows.
     uint16_t * ot = st0;  // 128 queries x 128 dims = 32 KB <= one stage
@@ -681,6 +740,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
 // state crosses workgroups inside a kernel and no device-scope fence is used.
 constexpr int64_t kSplitBlocks = 8;   // key blocks (of 32) per split workgroup
 constexpr int64_t kMaxSplits = 32;
+constexpr int64_t kFlashSplitBlocks = 4;  // 64-key blocks per split of the LDS-tiled decode
 constexpr int kSplitWaves = 4;
 hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     if (a.head_dim != kDh) return hipErrorInvalidValue;
@@ -709,12 +769,40 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
             return hipErrorInvalidValue;
     // Many queries over one key source (the prefix self-attention, the
     // visual cross-attention): the LDS-tiled flash kernel.
-    if (a.tq > 64 && p.seg_len[1] == 0 && p.seg_len[0] >= 8 && p.vt_ld[0] % 8 == 0 && ((uintptr_t) p.vt[0] & 15) == 0 &&
-        ((uintptr_t) p.q & 15) == 0 && ((uintptr_t) p.out & 15) == 0) {
+    auto flash_ok = [&](int i) {
+        return p.seg_len[i] == 0 || (p.seg_len[i] >= 8 && p.vt_ld[i] % 8 == 0 && ((uintptr_t) p.vt[i] & 15) == 0 &&
+                                     ((uintptr_t) p.k[i] & 15) == 0);
+    };
+    const bool flash = flash_ok(0) && flash_ok(1) && p.seg_len[0] > 0 && ((uintptr_t) p.q & 15) == 0 &&
+                       ((uintptr_t) p.out & 15) == 0;
+    if (flash && a.tq > 64 && p.seg_len[1] == 0) {
         const int64_t qblocks = (a.tq + kPfQueries - 1) / kPfQueries;
-        hipLaunchKernelGGL(attn_prefill_kernel, dim3((unsigned) a.heads, (unsigned) qblocks), dim3(kPfWaves * 64), 0, s,
-                           p);
+        hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3((unsigned) a.heads, (unsigned) qblocks),
+                           dim3(kPfWaves * 64), 0, s, p);
         return hipGetLastError();
+    }
+    // Few queries (the 48-token denoise step) over long key sources: the same
+    // LDS-tiled kernel, one workgroup per (head, key range), every key read
+    // once; fp32 partials merged by joint_attn_merge.
+    if (flash && a.tq <= kPfQueries) {
+        const int64_t nblk = (p.seg_len[0] + kPfKeys - 1) / kPfKeys + (p.seg_len[1] + kPfKeys - 1) / kPfKeys;
+        // About kFlashSplitBlocks blocks per split, but at least 8 splits (short
+        // sources such as the 512-key prompt would otherwise leave most CUs idle).
+        int64_t nsplit = std::min<int64_t>(
+            nblk, std::max<int64_t>((nblk + kFlashSplitBlocks - 1) / kFlashSplitBlocks, 8));
+        nsplit = std::min<int64_t>(nsplit, kMaxSplits);
+        p.split_blocks = (nblk + nsplit - 1) / nsplit;
+        nsplit = (nblk + p.split_blocks - 1) / p.split_blocks;
+        const size_t part_bytes = (size_t) nsplit * a.heads * a.tq * (kDh + 2) * sizeof(float);
+        if (a.ws && part_bytes <= a.ws_bytes) {
+            p.part_o = (float *) a.ws;
+            p.part_m = p.part_o + (size_t) nsplit * a.heads * a.tq * kDh;
+            p.part_l = p.part_m + (size_t) nsplit * a.heads * a.tq;
+            hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3((unsigned) a.heads, 1, (unsigned) nsplit),
+                               dim3(kPfWaves * 64), 0, s, p);
+            hipLaunchKernelGGL(joint_attn_merge, dim3((unsigned) (a.heads * a.tq)), dim3(kDh), 0, s, p, (int) nsplit);
+            return hipGetLastError();
+        }
     }
     // Other many-query cases: 48-query groups, 4 waves, one workgroup per
     // (head, group).
