@@ -28,11 +28,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 // GELU, tanh form of Hendrycks & Gimpel (arXiv:1606.08415):
-// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+// 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3).
+// Evaluated through the identity 0.5 (1 + tanh u) = 1 / (1 + e^(-2u)) with the
+// hardware base-2 exponential and reciprocal (1 ulp each): a few ulp of f32
+// from the tanh form, far inside one bf16 ulp.  Large |x| saturates to x (the
+// exponential underflows) or -0 (it overflows to +inf).
 __device__ __forceinline__ float gelu_tanh(float x) {
-    const float kSqrt2OverPi = 0.7978845608028654f;
+    const float kNeg2Sqrt2OverPiLog2e = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
     const float kCubic = 0.044715f;
-    return 0.5f * x * (1.0f + tanhf(kSqrt2OverPi * x * (1.0f + kCubic * x * x)));
+    const float t = kNeg2Sqrt2OverPiLog2e * x * fmaf(kCubic, x * x, 1.0f);
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
 // GELU with the exact Gaussian CDF: 0.5 x (1 + erf(x / sqrt 2)).

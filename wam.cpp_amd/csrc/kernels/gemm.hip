@@ -34,6 +34,7 @@ struct GemmParams {
     int64_t M, N, K;
     int64_t B2, r2, r3;
     int32_t y_type, epi;
+    int32_t vec_out;  // bf16 output written in 16-byte row chunks (see tile_store_lds)
 };
 
 // Epilogue for one output element (row n, col m) from the fp32 accumulator.
@@ -374,6 +375,127 @@ __device__ __forceinline__ void cta_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Orders a wave's own LDS writes before its later LDS reads (and the reads
+// before later writes): LDS executes one wave's instructions in order, so
+// only the compiler has to be kept from moving accesses across this point.
+__device__ __forceinline__ void wave_lds_fence() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), other counters untouched
+    asm volatile("" ::: "memory");
+}
+
+// Eight bf16 values (a 16-byte chunk) <-> f32.
+__device__ __forceinline__ void unpack8(const uint4 & u, float (&f)[8]) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f[2 * e] = __uint_as_float(w[e] << 16);
+        f[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+    }
+}
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                      pack_bf16x2(f[6], f[7]));
+}
+
+// Accumulator fragments -> global through a wave-private LDS region, for bf16
+// outputs with M, ldy (and ldres) multiples of 8 and 16-byte aligned rows.
+// Per 32-token fragment row the wave writes its GEMM outputs, rounded to bf16
+// (the value the unfused MUL_MAT stores), into `region` (32 rows of 32*FC
+// features, padded by 8 elements so the rows n and n+4 written by one
+// instruction fall in disjoint banks), then reads them back as 16-byte row
+// chunks and applies bias / GELU / gated residual on 8 features at a time with
+// 16-byte residual loads and stores.  Same rounding points as tile_store.
+template <int E, int FR, int FC>
+__device__ __forceinline__ void tile_store_lds(const GemmParams & p, uint16_t * __restrict__ y,
+                                               const uint16_t * __restrict__ resb, f32x16_t (&acc)[FR][FC],
+                                               int64_t nb, int64_t mb, int lane, uint16_t * __restrict__ region) {
+    constexpr bool kBias = E >= kEpiBias, kRes = E >= kEpiBiasGated;
+    constexpr int WN = 32 * FC, SP = WN + 8, CPR = WN / 8;
+    constexpr int PER = 32 * CPR / 64;            // 16-byte chunks per lane per fragment row
+    constexpr bool kFixedCol = 64 % CPR == 0;     // each lane keeps one chunk column
+    constexpr int G = PER % 4 == 0 ? 4 : PER % 3 == 0 ? 3 : PER;
+    static_assert(PER * 64 == 32 * CPR, "fragment row must split evenly over the wave");
+    const uint16_t * __restrict__ bias = p.bias;
+    const float * __restrict__ gate = p.gate;
+
+    // Per-chunk bias / gate, hoisted when the lane's chunk column is fixed.
+    float bfix[8] = {}, gfix[8] = {};
+    if constexpr (kFixedCol && kBias) {
+        const int64_t m = mb + 8 * (lane % CPR);
+        if (m < p.M) {
+            unpack8(*(const uint4 *) (bias + m), bfix);
+            if constexpr (E == kEpiBiasGated) {
+                const float4 g0 = *(const float4 *) (gate + m), g1 = *(const float4 *) (gate + m + 4);
+                gfix[0] = g0.x; gfix[1] = g0.y; gfix[2] = g0.z; gfix[3] = g0.w;
+                gfix[4] = g1.x; gfix[5] = g1.y; gfix[6] = g1.z; gfix[7] = g1.w;
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < FR; ++i) {
+#pragma unroll
+        for (int j = 0; j < FC; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int r = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                region[r * SP + 32 * j + (lane & 31)] = f32_to_bf16(acc[i][j][v]);
+            }
+        wave_lds_fence();
+
+        // G chunks at a time: their LDS and residual loads are issued together,
+        // and the live registers stay small beside the accumulators.
+#pragma unroll
+        for (int t0 = 0; t0 < PER; t0 += G) {
+            uint4 sv[G], hv[G];
+#pragma unroll
+            for (int u = 0; u < G; ++u) {
+                const int c = lane + 64 * (t0 + u), r = c / CPR, cc = c % CPR;
+                sv[u] = *(const uint4 *) (region + r * SP + 8 * cc);
+                if constexpr (kRes) {
+                    const int64_t n = min(nb + 32 * i + r, p.N - 1), m = min(mb + 8 * cc, p.M - 8);
+                    hv[u] = *(const uint4 *) (resb + n * p.ldres + m);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < G; ++u) {
+                const int c = lane + 64 * (t0 + u), r = c / CPR, cc = c % CPR;
+                const int64_t n = nb + 32 * i + r, m = mb + 8 * cc;
+                if (n >= p.N || m >= p.M) continue;
+                uint4 out = sv[u];
+                if constexpr (kBias) {
+                    float s[8], b[8], g[8] = {}, h[8] = {};
+                    unpack8(sv[u], s);
+                    if constexpr (kFixedCol) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) b[e] = bfix[e], g[e] = gfix[e];
+                    } else {
+                        unpack8(*(const uint4 *) (bias + m), b);
+                        if constexpr (E == kEpiBiasGated) {
+                            const float4 g0 = *(const float4 *) (gate + m), g1 = *(const float4 *) (gate + m + 4);
+                            g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
+                            g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
+                        }
+                    }
+                    if constexpr (kRes) unpack8(hv[u], h);
+                    float o[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        if constexpr (E == kEpiBias) o[e] = s[e] + b[e];
+                        else if constexpr (E == kEpiBiasGelu) o[e] = gelu_tanh(s[e] + b[e]);
+                        else if constexpr (E == kEpiBiasGated) o[e] = fmaf(round_bf16(s[e] + b[e]), g[e], h[e]);
+                        else o[e] = h[e] + round_bf16(s[e] + b[e]);
+                    }
+                    out = pack8(o);
+                }
+                *(uint4 *) (y + n * p.ldy + m) = out;
+            }
+        }
+        wave_lds_fence();  // the next fragment row overwrites the region
+    }
+}
+
 template <int BM, int BN, int WM, int WN, int BK, int S>
 struct DmaCfg {
     static constexpr int kThreads = 64 * WM * WN, kWaves = WM * WN;
@@ -497,6 +619,25 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_dma(GemmParams p, int 
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
     const int64_t nb = n0 + wr * C::kWaveM, mb = m0 + wc * C::kWaveN;
+    if (p.vec_out) {
+        // The ring is free once every wave has finished its last multiply and
+        // its trailing refills have landed: it becomes the wave-private
+        // staging regions of tile_store_lds, WPS regions per stage array.
+        constexpr int REG = 32 * (C::kWaveN + 8), WPS = E / REG;
+        static_assert(WPS >= 1 && WPS * S >= C::kWaves, "staging regions must fit in the ring");
+        __syncthreads();
+        const int sa = wave / WPS;
+        uint16_t * region = (sa == 0 ? st0 : sa == 1 ? st1 : sa == 2 ? st2 : st3) + (wave % WPS) * REG;
+        uint16_t * y = (uint16_t *) p.y;
+        switch (epi_kind(p)) {
+            case kEpiBias: tile_store_lds<kEpiBias>(p, y, p.res, acc, nb, mb, lane, region); break;
+            case kEpiBiasGelu: tile_store_lds<kEpiBiasGelu>(p, y, p.res, acc, nb, mb, lane, region); break;
+            case kEpiBiasGated: tile_store_lds<kEpiBiasGated>(p, y, p.res, acc, nb, mb, lane, region); break;
+            case kEpiBiasResidual: tile_store_lds<kEpiBiasResidual>(p, y, p.res, acc, nb, mb, lane, region); break;
+            default: tile_store_lds<kEpiBf16>(p, y, p.res, acc, nb, mb, lane, region); break;
+        }
+        return;
+    }
     char * y = (char *) p.y;
     switch (epi_kind(p)) {
         case kEpiF32: tile_store<kEpiF32>(p, y, p.res, acc, nb, mb, lane); break;
@@ -845,6 +986,8 @@ hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
     p.B2 = a.B2; p.r2 = a.r2; p.r3 = a.r3;
     p.y_type = a.y_type;
     p.epi = a.epi;
+    p.vec_out = epi_kind(p) != kEpiF32 && a.M % 8 == 0 && a.ldy % 8 == 0 && aligned16(a.y) && aligned16(a.bias) &&
+                aligned16(a.gate) && aligned16(a.res) && (a.res == nullptr || a.ldres % 8 == 0);
     const int64_t batches = a.B2 * a.B3;
     if (a.M <= 0 || a.N <= 0 || batches <= 0) return hipSuccess;
     if (a.K <= 0) return hipErrorInvalidValue;
