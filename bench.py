@@ -51,6 +51,30 @@ def cpu_info():
     return cores, model
 
 
+def _normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0, bf16: bool = False) -> np.ndarray:
+    """Seeded synthetic data (f32, or bf16 bit patterns when bf16=True)."""
+    v = np.random.default_rng(seed).standard_normal(n, dtype=np.float32) * np.float32(std) + np.float32(mean)
+    return wamx.f32_to_bf16(v) if bf16 else v
+
+
+# HBM bytes per launch of the roofline kernels, from the rocprofv3 FETCH_SIZE /
+# WRITE_SIZE passes of `bench.py --probe-traffic`, each scaled by the factor
+# the same counter gives for a streaming kernel of known size.  The summary in
+# profiles/ holds one "traffic_bytes <key> <bytes>" line per kernel.
+TRAFFIC_FILE = REPO / "profiles" / "traffic_roofline_kernels.md"
+
+
+def measured_traffic(key: str):
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            f = line.strip().strip("`").split()
+            if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == key:
+                return float(f[2])
+    except OSError:
+        pass
+    return None
+
+
 def time_op(be, fn, reps: int) -> float:
     """Average ms of fn() over reps launches, HIP events on the backend stream."""
     t = wamx.Timer(be)
@@ -64,10 +88,9 @@ def time_op(be, fn, reps: int) -> float:
 
 # ---------------------------------------------------------------------------
 def workload_gemm(be, args):
-    import oracle
     M, K, N = 3072, 3072, 256
-    w = oracle.fill_normal(M * K, 0x5EED0000 + 1, 0.0, 0.02, oracle.BF16)
-    x = oracle.fill_normal(N * K, 0x5EED0000 + 2)
+    w = _normal(M * K, 0x5EED0000 + 1, 0.0, 0.02, bf16=True)
+    x = _normal(N * K, 0x5EED0000 + 2)
     dw, dx, dy = be.array(w), be.array(x), be.empty(N * M * 4)
 
     def step():
@@ -88,6 +111,7 @@ def workload_gemm(be, args):
             "frac": bytes_ / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "traffic": None,
             "kernel": "gemm_tile<128,128> (f32 activations)", "tflops": flops / (ms * 1e-3) / 1e12}
     # CPU baseline: the oracle's MUL_MAT on the full problem.
+    import oracle
     t0 = time.perf_counter()
     oracle.mul_mat(w.reshape(M, K), x.reshape(N, K))
     cpu_ms = (time.perf_counter() - t0) * 1e3
@@ -101,17 +125,16 @@ def workload_gemm(be, args):
 
 
 def workload_ffn(be, args):
-    import oracle
     T, D, F = 2048, 3072, 14336
     seed = 0x5EED0000 + 2
-    x = oracle.fill_normal(T * D, seed + 1, 0.0, 1.0, oracle.BF16)
-    shift = oracle.fill_normal(D, seed + 2, 0.0, 0.1)
-    scale = oracle.fill_normal(D, seed + 3, 0.0, 0.1)
-    gate = oracle.fill_normal(D, seed + 4, 0.0, 0.1)
-    w_up = oracle.fill_normal(F * D, seed + 5, 0.0, 0.02, oracle.BF16)
-    b_up = oracle.fill_normal(F, seed + 6, 0.0, 0.02, oracle.BF16)
-    w_dn = oracle.fill_normal(D * F, seed + 7, 0.0, 0.02, oracle.BF16)
-    b_dn = oracle.fill_normal(D, seed + 8, 0.0, 0.02, oracle.BF16)
+    x = _normal(T * D, seed + 1, 0.0, 1.0, bf16=True)
+    shift = _normal(D, seed + 2, 0.0, 0.1)
+    scale = _normal(D, seed + 3, 0.0, 0.1)
+    gate = _normal(D, seed + 4, 0.0, 0.1)
+    w_up = _normal(F * D, seed + 5, 0.0, 0.02, bf16=True)
+    b_up = _normal(F, seed + 6, 0.0, 0.02, bf16=True)
+    w_dn = _normal(D * F, seed + 7, 0.0, 0.02, bf16=True)
+    b_dn = _normal(D, seed + 8, 0.0, 0.02, bf16=True)
     dx, dsh, dsc, dg = be.array(x), be.array(shift), be.array(scale), be.array(gate)
     dwu, dbu, dwd, dbd = be.array(w_up), be.array(b_up), be.array(w_dn), be.array(b_dn)
     dn, dh, dout = be.empty(T * D * 2), be.empty(T * F * 2), be.empty(T * D * 2)
@@ -145,14 +168,15 @@ def workload_ffn(be, args):
     up_ms = time_op(be, up, 10)
     down_ms = time_op(be, down, 10)
     norm_ms = time_op(be, norm, 20)
-    dom_ms, dom = (up_ms, "gemm_tile (FFN up + bias + GELU)") if up_ms >= down_ms else \
-        (down_ms, "gemm_tile (FFN down + bias + gated residual)")
+    dom_ms, dom = (up_ms, "gemm_dma<256,256> (FFN up + bias + GELU)") if up_ms >= down_ms else \
+        (down_ms, "gemm_dma<128,128> (FFN down + bias + gated residual)")
     roof = {"bound": "mfma", "achieved": gemm_flops / (dom_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": gemm_flops / (dom_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "traffic": None,
             "kernel": dom, "kernel_ms": dom_ms,
             "kernels_ms": {"norm_mod_bf16": norm_ms, "ffn_up": up_ms, "ffn_down": down_ms},
             "norm_gbs": (2 * T * D * 2) / (norm_ms * 1e-3) / 1e9}
     # CPU baseline: the oracle's FFN block on 256 of the 2048 tokens, scaled x8.
+    import oracle
     ts = 256
     xs = x.reshape(T, D)[:ts]
     t0 = time.perf_counter()
@@ -171,10 +195,9 @@ def workload_ffn(be, args):
 
 
 def _gwp_inputs(cfg, seed):
-    import oracle
     A, T = cfg["action_dim"], cfg["action_chunk"]
-    return (oracle.fill_normal(A, seed + 1), oracle.fill_normal(cfg["z_dim"] * 4 * cfg["grid_h"] * cfg["grid_w"], seed + 2),
-            oracle.fill_normal(cfg["n_lang"] * cfg["t5_hidden"], seed + 3), oracle.fill_normal(T * A, seed + 4))
+    return (_normal(A, seed + 1), _normal(cfg["z_dim"] * 4 * cfg["grid_h"] * cfg["grid_w"], seed + 2),
+            _normal(cfg["n_lang"] * cfg["t5_hidden"], seed + 3), _normal(T * A, seed + 4))
 
 
 def _read_weights(be, m, keep):
@@ -198,7 +221,6 @@ def workload_chunk(be, args):
     flow-matching denoise steps of the 48-token action expert, 30 layers at
     width 3072 (24x128 heads, FFN 14336) in both experts."""
     import ctypes as C
-    import oracle
     lib = be.lib
     c = lib.wamx_gwp_default_config()
     cfg = {k: getattr(c, k) for k, _ in wamx.GwpConfig._fields_}
@@ -234,7 +256,7 @@ def workload_chunk(be, args):
     T, D, F = cfg["grid_h"] * cfg["grid_w"], cfg["hidden"], cfg["ffn_dim"]
     w_up = lib.wamx_gwp_weight(m, b"gwp.blocks.0.visual_expert.ffn.net.0.proj.weight")
     b_up = lib.wamx_gwp_weight(m, b"gwp.blocks.0.visual_expert.ffn.net.0.proj.bias")
-    dx = be.array(oracle.fill_normal(T * D, 5, 0.0, 1.0, oracle.BF16))
+    dx = be.array(_normal(T * D, 5, 0.0, 1.0, bf16=True))
     dy = be.empty(T * F * 2)
 
     def up():
@@ -242,28 +264,37 @@ def workload_chunk(be, args):
                                       wamx.EPI_BIAS_GELU, None, None, dy.ptr, F, T, D), "linear")
     up_ms = time_op(be, up, 20)
     flops = 2.0 * T * D * F
-    # The 48-token FFN-up of the action expert (HBM-bound weight streaming).
-    w_aup = lib.wamx_gwp_weight(m, b"gwp.blocks.0.action_expert.ffn.net.0.proj.weight")
-    b_aup = lib.wamx_gwp_weight(m, b"gwp.blocks.0.action_expert.ffn.net.0.proj.bias")
+    # The 48-token FFN-up of the action expert (HBM-bound weight streaming),
+    # cycling through the 30 layers' weights as the denoise pass does, so the
+    # 88 MB weight is not resident in the 256 MB last-level cache.
     Ta, Da, Fa = cfg["action_chunk"], cfg["action_hidden"], cfg["action_ffn_dim"]
-    dxa = be.array(oracle.fill_normal(Ta * Da, 6, 0.0, 1.0, oracle.BF16))
+    aups = [(lib.wamx_gwp_weight(m, f"gwp.blocks.{l}.action_expert.ffn.net.0.proj.weight".encode()),
+             lib.wamx_gwp_weight(m, f"gwp.blocks.{l}.action_expert.ffn.net.0.proj.bias".encode()))
+            for l in range(cfg["n_layers"])]
+    dxa = be.array(_normal(Ta * Da, 6, 0.0, 1.0, bf16=True))
     dya = be.empty(Ta * Fa * 2)
+    nxt = [0]
 
     def aup():
+        w_aup, b_aup = aups[nxt[0] % len(aups)]
+        nxt[0] += 1
         wamx.check(lib.wamx_op_linear(be.ptr, w_aup.contents.data, dxa.ptr, wamx.TYPE_BF16, b_aup.contents.data,
                                       wamx.EPI_BIAS_GELU, None, None, dya.ptr, Fa, Ta, Da), "linear")
-    aup_ms = time_op(be, aup, 50)
+    aup_ms = time_op(be, aup, 60)
     aup_bytes = Fa * Da * 2 + Ta * Da * 2 + Ta * Fa * 2 + Fa * 2
     roof = {"bound": "mfma", "achieved": flops / (up_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": flops / (up_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "traffic": None,
+            "frac": flops / (up_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "traffic": measured_traffic("gemm_dma_ffn_up"),
             "kernel": "gemm_dma<256,256>: prefix visual FFN-up 3072 tok x [14336 x 3072] + bias + GELU",
             "kernel_ms": up_ms, "flops_per_launch": flops,
+            "algorithmic_bytes": T * D * 2 + F * D * 2 + F * 2 + T * F * 2,
             "skinny": {"kernel": "gemm_skinny_part + gemm_skinny_reduce: denoise FFN-up 48 tok x [14336 x 3072] + bias + GELU",
                        "kernel_ms": aup_ms, "achieved_gbs": aup_bytes / (aup_ms * 1e-3) / 1e9,
-                       "frac_hbm": aup_bytes / (aup_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}}
+                       "frac_hbm": aup_bytes / (aup_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": aup_bytes,
+                       "traffic": measured_traffic("gemm_skinny_ffn_up")}}
 
     # CPU baseline: the oracle on layer 0 (prompt K/V, prefix layer, one
     # denoise step) at full width, scaled by layers and steps.
+    import oracle
     L, S = cfg["n_layers"], cfg["num_steps"]
     w = _read_weights(be, m, lambda n: not n.startswith("gwp.blocks.") or n.startswith("gwp.blocks.0.")
                       or "scale_shift_table" in n)
@@ -296,18 +327,52 @@ def workload_chunk(be, args):
 WORKLOADS = {"chunk": workload_chunk, "ffn": workload_ffn, "gemm": workload_gemm}
 
 
+def probe_traffic(be, launches: int = 3):
+    """Launches for the rocprofv3 FETCH_SIZE / WRITE_SIZE passes: a streaming
+    kernel of known size (bias_gelu_bf16 over 64 Mi bf16 values: 128 MiB read,
+    128 MiB written) to scale the counters, then the roofline kernels at their
+    chunk shapes.  Prints the algorithmic bytes of each as one JSON line."""
+    lib = be.lib
+    n, width = 64 << 20, 14336
+    cx, cb, cy = be.array(_normal(n, 11, bf16=True)), be.array(_normal(width, 12, 0.0, 0.02, bf16=True)), be.empty(2 * n)
+    for _ in range(launches):
+        wamx.check(lib.wamx_op_bias_gelu_bf16(be.ptr, cx.ptr, cb.ptr, cy.ptr, n, width), "bias_gelu")
+    be.sync()
+    out = {"calibration": {"kernel": "bias_gelu_bf16_kernel", "read_bytes": 2 * n + 2 * width, "write_bytes": 2 * n}}
+    for key, T in (("gemm_dma_ffn_up", 3072), ("gemm_skinny_ffn_up", 48)):
+        D, F = 3072, 14336
+        w = be.array(_normal(F * D, 13, 0.0, 0.02, bf16=True))
+        b = be.array(_normal(F, 14, 0.0, 0.02, bf16=True))
+        x = be.array(_normal(T * D, 15, bf16=True))
+        y = be.empty(T * F * 2)
+        for _ in range(launches):
+            wamx.check(lib.wamx_op_linear(be.ptr, w.ptr, x.ptr, wamx.TYPE_BF16, b.ptr, wamx.EPI_BIAS_GELU, None, None,
+                                          y.ptr, F, T, D), "linear")
+        be.sync()
+        out[key] = {"tokens": T, "read_bytes": F * D * 2 + T * D * 2 + F * 2, "write_bytes": T * F * 2}
+        for a in (w, b, x, y):
+            a.free()
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="chunk", choices=sorted(WORKLOADS))
+    ap.add_argument("--probe-traffic", action="store_true",
+                    help="only launch the counter-calibration and roofline kernels (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the path would shard by heads / independent chunks, see the design notes)", file=sys.stderr)
         sys.exit(2)
     be = wamx.Backend(0)
+    if args.probe_traffic:
+        probe_traffic(be)
+        be.close()
+        return
     res = WORKLOADS[args.workload](be, args)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": res["higher_is_better"],
