@@ -1,0 +1,168 @@
+"""Row fusion in the graph executor: a LINEAR on a few tokens followed by the
+row ops that consume its output (LayerNorm / adaLN modulation of the residual
+stream; RMSNorm + RoPE of the Q and K column ranges and the V^T copy) runs as
+the skinny GEMM plus one reduce that applies the row ops.  The fused graph
+must produce the same bits as the standalone ops launched one at a time
+(wamx_op_linear, wamx_op_norm_modulation_bf16 / wamx_op_layer_norm_bf16,
+wamx_op_qk_norm_rope and a host transpose for V^T), which the per-op tests
+hold to the oracle.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+D, H, DH = 3072, 24, 128
+
+
+class Graph:
+    """A no-alloc context whose tensors are placed in one backend buffer."""
+
+    def __init__(self, wx, be):
+        self.wx, self.be, self.lib = wx, be, be.lib
+        self.ctx = self.lib.wamx_init(256)
+        self.buf = None
+
+    def t(self, typ, *ne):
+        return getattr(self.lib, f"wamx_new_tensor_{len(ne)}d")(self.ctx, typ, *ne)
+
+    def alloc(self):
+        self.buf = self.lib.wamx_backend_alloc_ctx_tensors(self.ctx, self.be.ptr)
+        assert self.buf, self.wx.last_error()
+
+    def set(self, t, a):
+        a = np.ascontiguousarray(a)
+        self.wx.check(self.lib.wamx_backend_tensor_set(t, a.ctypes.data, 0, a.nbytes), "tensor_set")
+
+    def get(self, t, dtype, shape):
+        a = np.empty(shape, dtype)
+        self.wx.check(self.lib.wamx_backend_tensor_get(t, a.ctypes.data, 0, a.nbytes), "tensor_get")
+        return a
+
+    def compute(self, *outs):
+        g = self.lib.wamx_new_graph(self.ctx, 256)
+        for o in outs:
+            self.lib.wamx_build_forward_expand(g, o)
+        self.wx.check(self.lib.wamx_backend_graph_compute(self.be.ptr, g), "graph_compute")
+        self.be.sync()
+
+    def close(self):
+        if self.buf:
+            self.lib.wamx_buffer_free(self.buf)
+        self.lib.wamx_free(self.ctx)
+
+
+def data(t):
+    return t.contents.data
+
+
+@pytest.mark.parametrize("T", [48, 17, 1])
+@pytest.mark.parametrize("kind", ["modulation", "layer_norm"])
+def test_linear_then_norm_is_bit_exact(wx, be, rng, T, kind):
+    print(f"fusion linear->norm {kind} T={T}", flush=True)
+    lib = be.lib
+    g = Graph(wx, be)
+    try:
+        w = g.t(wx.TYPE_BF16, D, D)
+        x = g.t(wx.TYPE_BF16, D, T)
+        b = g.t(wx.TYPE_BF16, D)
+        h = g.t(wx.TYPE_BF16, D, T)
+        gate = g.t(wx.TYPE_F32, D)
+        y = lib.wamx_linear(g.ctx, w, x, b, wx.EPI_BIAS_GATED, h, gate)
+        if kind == "modulation":
+            sc, sh = g.t(wx.TYPE_F32, D), g.t(wx.TYPE_F32, D)
+            n = lib.wamx_norm_modulation_bf16(g.ctx, y, sc, sh, 1e-6)
+        else:
+            sc, sh = g.t(wx.TYPE_BF16, D), g.t(wx.TYPE_BF16, D)
+            n = lib.wamx_layer_norm_bf16(g.ctx, y, sc, sh, 1e-6)
+        g.alloc()
+        hw = wx.f32_to_bf16(rng.standard_normal(D * D).astype(np.float32) * 0.02)
+        hx = wx.f32_to_bf16(rng.standard_normal(D * T).astype(np.float32))
+        hb = wx.f32_to_bf16(rng.standard_normal(D).astype(np.float32) * 0.02)
+        hh = wx.f32_to_bf16(rng.standard_normal(D * T).astype(np.float32))
+        hg = (rng.standard_normal(D) * 0.5).astype(np.float32)
+        if kind == "modulation":
+            hsc, hsh = (rng.standard_normal(D) * 0.1).astype(np.float32), (rng.standard_normal(D) * 0.1).astype(np.float32)
+        else:
+            hsc = wx.f32_to_bf16(1.0 + rng.standard_normal(D).astype(np.float32) * 0.1)
+            hsh = wx.f32_to_bf16(rng.standard_normal(D).astype(np.float32) * 0.1)
+        for t, a in ((w, hw), (x, hx), (b, hb), (h, hh), (gate, hg), (sc, hsc), (sh, hsh)):
+            g.set(t, a)
+        g.compute(n)
+        got_y = g.get(y, np.uint16, (T, D))
+        got_n = g.get(n, np.uint16, (T, D))
+
+        ref_y, ref_n = be.empty(T * D * 2), be.empty(T * D * 2)
+        wx.check(lib.wamx_op_linear(be.ptr, data(w), data(x), wx.TYPE_BF16, data(b), wx.EPI_BIAS_GATED, data(h),
+                                    C.cast(data(gate), C.POINTER(C.c_float)), ref_y.ptr, D, T, D))
+        if kind == "modulation":
+            wx.check(lib.wamx_op_norm_modulation_bf16(be.ptr, ref_y.ptr, D, C.cast(data(sc), C.POINTER(C.c_float)),
+                                                      C.cast(data(sh), C.POINTER(C.c_float)), 0, ref_n.ptr, T, D,
+                                                      1e-6))
+        else:
+            wx.check(lib.wamx_op_layer_norm_bf16(be.ptr, ref_y.ptr, D, data(sc), data(sh), ref_n.ptr, T, D, 1e-6))
+        be.sync()
+        assert np.array_equal(got_y, ref_y.download(np.uint16, (T, D)))
+        assert np.array_equal(got_n, ref_n.download(np.uint16, (T, D)))
+    finally:
+        g.close()
+
+
+@pytest.mark.parametrize("T", [48, 5])
+def test_qkv_split_is_bit_exact(wx, be, rng, T):
+    print(f"fusion qkv T={T}", flush=True)
+    lib = be.lib
+    g = Graph(wx, be)
+    try:
+        w = g.t(wx.TYPE_BF16, D, 3 * D)
+        x = g.t(wx.TYPE_BF16, D, T)
+        b = g.t(wx.TYPE_BF16, 3 * D)
+        nq, nk = g.t(wx.TYPE_BF16, D), g.t(wx.TYPE_BF16, D)
+        pos = g.t(wx.TYPE_I32, T)
+        tpad = (T + 3) // 4 * 4
+        vraw = g.t(wx.TYPE_BF16, tpad, DH, H)
+        qkv = lib.wamx_linear(g.ctx, w, x, b, wx.EPI_BIAS, None, None)
+        pitch = qkv.contents.nb[1]
+        q = lib.wamx_qk_norm_rope(g.ctx, lib.wamx_view_2d(g.ctx, qkv, D, T, pitch, 0), nq,
+                                  g.t(wx.TYPE_BF16, DH, T, H), 0, 0, pos, None, None, 1e-6, 10000.0)
+        k = lib.wamx_qk_norm_rope(g.ctx, lib.wamx_view_2d(g.ctx, qkv, D, T, pitch, 2 * D), nk,
+                                  g.t(wx.TYPE_BF16, DH, T, H), 0, 0, pos, None, None, 1e-6, 10000.0)
+        vsrc = lib.wamx_permute(g.ctx, lib.wamx_view_3d(g.ctx, qkv, DH, H, T, DH * 2, pitch, 4 * D), 1, 2, 0, 3)
+        vdst = lib.wamx_view_3d(g.ctx, vraw, T, DH, H, vraw.contents.nb[1], vraw.contents.nb[2], 0)
+        v = lib.wamx_cpy(g.ctx, vsrc, vdst)
+        g.alloc()
+        hw = wx.f32_to_bf16(rng.standard_normal(3 * D * D).astype(np.float32) * 0.02)
+        hx = wx.f32_to_bf16(rng.standard_normal(D * T).astype(np.float32))
+        hb = wx.f32_to_bf16(rng.standard_normal(3 * D).astype(np.float32) * 0.02)
+        hnq = wx.f32_to_bf16(1.0 + rng.standard_normal(D).astype(np.float32) * 0.1)
+        hnk = wx.f32_to_bf16(1.0 + rng.standard_normal(D).astype(np.float32) * 0.1)
+        hpos = np.arange(1, T + 1, dtype=np.int32)
+        for t, a in ((w, hw), (x, hx), (b, hb), (nq, hnq), (nk, hnk), (pos, hpos),
+                     (vraw, np.zeros(tpad * DH * H, np.uint16))):
+            g.set(t, a)
+        g.compute(q, k, v)
+        got_qkv = g.get(qkv, np.uint16, (T, 3 * D))
+        got_q = g.get(q, np.uint16, (H, T, DH))
+        got_k = g.get(k, np.uint16, (H, T, DH))
+        got_vt = g.get(vraw, np.uint16, (H, DH, tpad))[:, :, :T]
+
+        ref_qkv, ref_q, ref_k = be.empty(T * 3 * D * 2), be.empty(T * D * 2), be.empty(T * D * 2)
+        wx.check(lib.wamx_op_linear(be.ptr, data(w), data(x), wx.TYPE_BF16, data(b), wx.EPI_BIAS, None, None,
+                                    ref_qkv.ptr, 3 * D, T, D))
+        pp = C.cast(data(pos), C.POINTER(C.c_int32))
+        wx.check(lib.wamx_op_qk_norm_rope(be.ptr, ref_qkv.ptr, 3 * D, data(nq), ref_q.ptr, H, DH, T, T, 0, 0, pp,
+                                          None, None, 1e-6, 10000.0))
+        wx.check(lib.wamx_op_qk_norm_rope(be.ptr, ref_qkv.ptr + 2 * D, 3 * D, data(nk), ref_k.ptr, H, DH, T, T, 0,
+                                          0, pp, None, None, 1e-6, 10000.0))
+        be.sync()
+        rq = ref_qkv.download(np.uint16, (T, 3 * D))
+        assert np.array_equal(got_qkv, rq)
+        assert np.array_equal(got_q, ref_q.download(np.uint16, (H, T, DH)))
+        assert np.array_equal(got_k, ref_k.download(np.uint16, (H, T, DH)))
+        assert np.array_equal(got_vt, rq[:, 2 * D:].reshape(T, H, DH).transpose(1, 2, 0))
+    finally:
+        g.close()

@@ -54,6 +54,7 @@ struct wamx_backend {
     hipStream_t stream = nullptr;
     void * workspace = nullptr;  // K-split partials, reused by consecutive GEMMs on the stream
     bool use_graphs = true;
+    bool fuse_rows = true;       // split-K reduce + consuming row op in one launch
     std::unordered_map<uint64_t, GraphCacheEntry> graphs;
 };
 
@@ -185,7 +186,7 @@ static hipError_t run_mul_mat(wamx_backend * be, const wamx_tensor * node) {
     return launch_gemm(g, be->stream);
 }
 
-static hipError_t run_linear(wamx_backend * be, const wamx_tensor * node) {
+static GemmArgs linear_args(wamx_backend * be, const wamx_tensor * node) {
     const wamx_tensor * w = node->src[0];
     const wamx_tensor * x = node->src[1];
     GemmArgs g;
@@ -208,13 +209,146 @@ static hipError_t run_linear(wamx_backend * be, const wamx_tensor * node) {
     g.gate = node->src[4] ? (const float *) node->src[4]->data : nullptr;
     g.ws = be->workspace;
     g.ws_bytes = kWorkspaceBytes;
-    return launch_gemm(g, be->stream);
+    return g;
+}
+
+static hipError_t run_linear(wamx_backend * be, const wamx_tensor * node) {
+    return launch_gemm(linear_args(be, node), be->stream);
 }
 
 static float param_f32(const wamx_tensor * t, int i) {
     float v;
     memcpy(&v, &t->op_params[i], 4);
     return v;
+}
+
+// ---------------------------------------------------------------------------
+// Row fusion: a LINEAR on a few tokens (the split-K skinny path) followed
+// directly by the row ops that consume its output runs as the GEMM's part
+// kernel plus one reduce that applies those row ops (launch_gemm_rowpost):
+//   * LINEAR -> NORM of its output (LayerNorm / adaLN modulation), the
+//     residual-stream pattern h = lin(..., h); n = norm(h) of mot.cpp:130-145,
+//     284-346;
+//   * LINEAR -> up to three of QK_NORM_ROPE of a column range and the V^T
+//     copy (CPY of a permuted column range), the QKV split of mot.cpp:245-265,
+//     395-401.
+// The matched nodes are computed by the fused launch and skipped; anything
+// the fused path does not take runs node by node as before.
+// ---------------------------------------------------------------------------
+static bool is_noop(const wamx_tensor * t) {
+    switch (t->op) {
+        case WAMX_OP_NONE:
+        case WAMX_OP_VIEW:
+        case WAMX_OP_RESHAPE:
+        case WAMX_OP_PERMUTE:
+        case WAMX_OP_TRANSPOSE:
+            return true;
+        default:
+            return false;
+    }
+}
+
+static int next_compute(wamx_cgraph * g, int i, int n) {
+    for (int j = i + 1; j < n; ++j)
+        if (!is_noop(wamx_graph_node(g, j))) return j;
+    return n;
+}
+
+// Column offset of x inside the rows of `base` (x is base, or a view taking a
+// column range of each of its rows).
+static bool column_view(const wamx_tensor * x, const wamx_tensor * base, int64_t & col) {
+    if (x == base) {
+        col = 0;
+        return true;
+    }
+    if (x->op != WAMX_OP_VIEW || x->view_src != base || x->type != base->type || x->nb[0] != base->nb[0] ||
+        x->nb[1] != base->nb[1] || x->ne[1] != base->ne[1] || x->ne[2] != 1 || x->ne[3] != 1)
+        return false;
+    if (x->view_offs % base->nb[0] != 0 || x->view_offs + x->ne[0] * x->nb[0] > base->nb[1]) return false;
+    col = (int64_t) (x->view_offs / base->nb[0]);
+    return true;
+}
+
+// Matches the row ops after LINEAR node i; returns the index of the last node
+// they cover (> i), or -1.
+static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post) {
+    const wamx_tensor * lin = wamx_graph_node(g, i);
+    if (lin->type != WAMX_TYPE_BF16 || lin->ne[1] > 64 || lin->ne[2] != 1 || lin->ne[3] != 1 || lin->view_src)
+        return -1;
+    int j = next_compute(g, i, n);
+    if (j >= n) return -1;
+    const wamx_tensor * t = wamx_graph_node(g, j);
+    if (t->op == WAMX_OP_NORM) {
+        const wamx_tensor * sc = t->src[1];
+        const wamx_tensor * sh = t->src[2];
+        if (t->src[0] != lin || !sc || !sh || t->type != WAMX_TYPE_BF16 || !wamx_are_same_shape(t, lin) ||
+            t->nb[0] != 2)
+            return -1;
+        post.kind = kRowPostNorm;
+        post.scale = sc->data;
+        post.shift = sh->data;
+        post.ss_type = sc->type;
+        post.affine = sc->type == WAMX_TYPE_BF16;  // as compute_node: bf16 weights are the affine LayerNorm
+        post.ss = sc->ne[1] == 1 ? 0 : (int64_t) (sc->nb[1] / wamx_type_size(sc->type));
+        post.out = t->data;
+        post.ldo = (int64_t) t->nb[1] / 2;
+        post.eps = param_f32(t, 0);
+        return j;
+    }
+    post.kind = kRowPostSegs;
+    post.nseg = 0;
+    int last = -1;
+    const int64_t T = lin->ne[1];
+    while (j < n && post.nseg < 3) {
+        t = wamx_graph_node(g, j);
+        RowSeg seg;
+        int64_t width, head_dim;
+        if (t->op == WAMX_OP_QK_NORM_ROPE) {
+            const wamx_tensor * x = t->src[0];
+            if (!column_view(x, lin, seg.col) || !t->src[1] || t->type != WAMX_TYPE_BF16) break;
+            head_dim = t->ne[0];
+            width = x->ne[0];
+            if (width != head_dim * t->ne[2]) break;
+            seg.kind = kRowSegQk;
+            seg.w = t->src[1]->data;
+            seg.dst = t->data;
+            seg.dst_tokens = t->ne[1];
+            seg.tok0 = t->op_params[0];
+            seg.rope_mode = t->op_params[1];
+            seg.pos0 = t->src[3] ? (const int32_t *) t->src[3]->data : nullptr;
+            seg.pos1 = t->src[4] ? (const int32_t *) t->src[4]->data : nullptr;
+            seg.pos2 = t->src[5] ? (const int32_t *) t->src[5]->data : nullptr;
+            seg.eps = param_f32(t, 2);
+            seg.freq_base = param_f32(t, 3);
+        } else if (t->op == WAMX_OP_CPY) {
+            // V^T store: CPY(permute(view(lin) as [dh, H, T], 1, 2, 0), dst [T, dh, H]).
+            const wamx_tensor * p = t->src[0];
+            const wamx_tensor * v = p ? p->src[0] : nullptr;
+            if (!p || p->op != WAMX_OP_PERMUTE || !v || v->op != WAMX_OP_VIEW || v->view_src != lin ||
+                t->type != WAMX_TYPE_BF16 || p->type != WAMX_TYPE_BF16)
+                break;
+            head_dim = p->ne[1];
+            width = head_dim * p->ne[2];
+            if (p->ne[0] != T || p->ne[3] != 1 || p->nb[0] != lin->nb[1] || p->nb[1] != 2 ||
+                p->nb[2] != (size_t) head_dim * 2 || !wamx_are_same_shape(t, p) || t->nb[0] != 2)
+                break;
+            if (v->view_offs % 2 != 0 || v->view_offs + (size_t) width * 2 > lin->nb[1]) break;
+            seg.kind = kRowSegVt;
+            seg.col = (int64_t) (v->view_offs / 2);
+            seg.dst = t->data;
+            seg.vt_ld = (int64_t) t->nb[1] / 2;
+            seg.vt_hs = (int64_t) t->nb[2] / 2;
+        } else {
+            break;
+        }
+        if (post.nseg > 0 && (width != post.width || head_dim != post.head_dim)) break;
+        post.width = width;
+        post.head_dim = head_dim;
+        post.seg[post.nseg++] = seg;
+        last = j;
+        j = next_compute(g, j, n);
+    }
+    return post.nseg > 0 ? last : -1;
 }
 
 static hipError_t run_joint_attn(wamx_backend * be, const wamx_tensor * node) {
@@ -431,6 +565,22 @@ static wamx_status run_nodes(wamx_backend * be, wamx_cgraph * g) {
         if (!node->data && wamx_nelements(node) > 0) {
             set_errorf("graph_compute: node %d (%s '%s') is not allocated", i, wamx_op_name(node->op), node->name);
             return WAMX_STATUS_ALLOC_FAILED;
+        }
+        if (node->op == WAMX_OP_LINEAR && be->fuse_rows) {
+            RowPost post;
+            const int last = match_row_post(g, i, n, post);
+            if (last > i) {
+                const hipError_t ferr = launch_gemm_rowpost(linear_args(be, node), post, be->stream);
+                if (ferr == hipSuccess) {
+                    i = last;
+                    continue;
+                }
+                if (ferr != hipErrorNotSupported) {
+                    set_errorf("graph_compute: node %d (%s '%s') with its row ops failed: %s", i,
+                               wamx_op_name(node->op), node->name, hipGetErrorString(ferr));
+                    return WAMX_STATUS_FAILED;
+                }
+            }
         }
         const hipError_t err = compute_node(be, node);
         if (err != hipSuccess) {
@@ -707,6 +857,8 @@ wamx_backend_t wamx_backend_init(int device) {
     be->dev = &reg->devices[device];
     const char * env = getenv("WAMX_DISABLE_HIP_GRAPHS");
     be->use_graphs = !(env && env[0] && env[0] != '0');
+    env = getenv("WAMX_DISABLE_ROW_FUSION");
+    be->fuse_rows = !(env && env[0] && env[0] != '0');
     // A blocking stream, so synchronous tensor_set/get on the null stream are
     // ordered with the graph work (default priority).
     if (hipStreamCreate(&be->stream) != hipSuccess || hipMalloc(&be->workspace, kWorkspaceBytes) != hipSuccess) {

@@ -41,6 +41,48 @@ hipError_t launch_gemm(const GemmArgs & a, hipStream_t s);
 // Workspace the skinny path needs for an M x N x K product (0 when unsplit).
 size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
+// Row ops that consume a skinny GEMM's output, applied by its split-K reduce
+// in the same launch (one workgroup per token row).  The GEMM output itself
+// is still written.
+enum { kRowSegQk = 0, kRowSegVt = 1 };
+struct RowSeg {
+    int32_t kind = kRowSegQk;
+    int64_t col = 0;                 // first GEMM output column of the segment
+    // kRowSegQk: RMSNorm over the segment * w (bf16), RoPE, bf16 into
+    // dst[h][tok0 + t][dd] with dst_tokens rows per head (launch_qk_norm_rope).
+    const void * w = nullptr;
+    int64_t dst_tokens = 0, tok0 = 0;
+    int32_t rope_mode = 2;
+    const int32_t * pos0 = nullptr;
+    const int32_t * pos1 = nullptr;
+    const int32_t * pos2 = nullptr;
+    float eps = 0.0f, freq_base = 10000.0f;
+    // kRowSegVt: bf16 copy into dst[h * vt_hs + dd * vt_ld + t] (V^T storage).
+    int64_t vt_ld = 0, vt_hs = 0;
+    void * dst = nullptr;
+};
+enum { kRowPostNorm = 1, kRowPostSegs = 2 };
+struct RowPost {
+    int32_t kind = 0;
+    // kRowPostNorm: LayerNorm of the whole row into out (launch_norm_mod_bf16
+    // arguments: scale/shift of ss_type with row stride ss, affine).
+    const void * scale = nullptr;
+    const void * shift = nullptr;
+    int32_t ss_type = WAMX_TYPE_F32;
+    bool affine = false;
+    int64_t ss = 0;
+    void * out = nullptr;
+    int64_t ldo = 0;
+    float eps = 0.0f;
+    // kRowPostSegs: up to three segments of `width` columns, heads x head_dim.
+    int32_t nseg = 0;
+    int64_t width = 0, head_dim = 0;
+    RowSeg seg[3];
+};
+// The skinny GEMM whose reduce applies `post`.  Returns hipErrorNotSupported,
+// launching nothing, when the product or the row op does not fit that path.
+hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStream_t s);
+
 // ---------------------------------------------------------------------------
 // Row-wise norms (bf16 / f32), bias+GELU, gated residuals.
 // ---------------------------------------------------------------------------

@@ -14,6 +14,7 @@
 //   merge their states in LDS in wave order.
 #include "../internal.h"
 #include "device.h"
+#include "rowops.h"
 
 #include <algorithm>
 
@@ -108,54 +109,22 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
         xv[i] = *(const uint4 *) (x + t * ldx + 8 * c);
         wv[i] = *(const uint4 *) (w + 8 * c);
     }
-    const float p0 = rope_mode == 2 ? 0.0f : (float) pos0[t];
-    const float p1 = rope_mode == 1 ? (float) pos1[t] : 0.0f;
-    const float p2 = rope_mode == 1 ? (float) pos2[t] : 0.0f;
+    const RopeTok rt = rope_tok(rope_mode, pos0, pos1, pos2, t, l2ts128, l2ts44, l2ts42);
     float v[CPT][8];
-    float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-        const bool ok = (int) threadIdx.x + i * (int) blockDim.x < nchunk;
-        const uint32_t u[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+        unpack8(xv[i], v[i]);
+        if ((int) threadIdx.x + i * (int) blockDim.x >= nchunk)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[i][2 * e] = ok ? bf16_to_f32((uint16_t) (u[e] & 0xffff)) : 0.0f;
-            v[i][2 * e + 1] = ok ? bf16_to_f32((uint16_t) (u[e] >> 16)) : 0.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sum = fmaf(v[i][e], v[i][e], sum);
+            for (int e = 0; e < 8; ++e) v[i][e] = 0.0f;
     }
-    const float inv_rms = rsqrtf(block_sum(sum, red) / (float) d + eps);
+    const float inv_rms = row_inv_rms<CPT>(v, d, eps, red);
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
         const int c = (int) threadIdx.x + i * (int) blockDim.x;
         if (c >= nchunk) continue;
         const int e0 = 8 * c, h = e0 / head_dim, dd0 = e0 % head_dim;
-        const uint32_t wu[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
-        uint32_t packed[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            // rms_norm_bf16_f32: y = x * inv_rms * w, f32.
-            float a = v[i][2 * j] * inv_rms * bf16_to_f32((uint16_t) (wu[j] & 0xffff));
-            float b = v[i][2 * j + 1] * inv_rms * bf16_to_f32((uint16_t) (wu[j] >> 16));
-            if (rope_mode != 2) {
-                const int dd = dd0 + 2 * j;
-                float theta;
-                if (rope_mode == 0) theta = p0 * exp2f((float) (dd >> 1) * l2ts128);
-                else if (dd < 44) theta = p0 * exp2f((float) (dd >> 1) * l2ts44);
-                else if (dd < 86) theta = p1 * exp2f((float) ((dd - 44) >> 1) * l2ts42);
-                else theta = p2 * exp2f((float) ((dd - 86) >> 1) * l2ts42);
-                float sn, cs;
-                sincosf(theta, &sn, &cs);
-                const float ra = a * cs - b * sn;
-                const float rb = a * sn + b * cs;
-                a = ra;
-                b = rb;
-            }
-            packed[j] = pack_bf16x2(a, b);
-        }
-        *(uint4 *) (dst + ((int64_t) h * dst_tokens + tok0 + t) * head_dim + dd0) =
-            make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        *(uint4 *) (dst + ((int64_t) h * dst_tokens + tok0 + t) * head_dim + dd0) = qk_chunk(v[i], inv_rms, wv[i], dd0, rt);
     }
 }
 

@@ -15,6 +15,7 @@
 //  * gemm_simt   — f32 weights (generic MUL_MAT only), plain FMA.
 #include "../internal.h"
 #include "device.h"
+#include "rowops.h"
 
 #include <algorithm>
 
@@ -382,20 +383,6 @@ __device__ __forceinline__ void wave_lds_fence() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), other counters untouched
     asm volatile("" ::: "memory");
-}
-
-// Eight bf16 values (a 16-byte chunk) <-> f32.
-__device__ __forceinline__ void unpack8(const uint4 & u, float (&f)[8]) {
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        f[2 * e] = __uint_as_float(w[e] << 16);
-        f[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
-    }
-}
-__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
-    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
-                      pack_bf16x2(f[6], f[7]));
 }
 
 // Accumulator fragments -> global through a wave-private LDS region, for bf16
@@ -789,7 +776,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
 
     // 16x16 fragment: lane holds column (lane & 15) = feature, register r
     // holds row 4*(lane/16) + r = token within the tile.
-    float * pp = gridDim.y == 1 ? nullptr : part + (int64_t) blockIdx.y * N * M;
+    // part == nullptr: a single K slice applies the epilogue directly.
+    float * pp = part ? part + (int64_t) blockIdx.y * N * M : nullptr;
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
         const int64_t mrow = m0 + 16 * rg + r16;
@@ -834,6 +822,132 @@ __global__ __launch_bounds__(256) void gemm_skinny_reduce(GemmParams p, const fl
     for (int e = 0; e < V; ++e) store_out(p, p.y, p.res, n, m + e, s[e]);
 }
 
+// ---------------------------------------------------------------------------
+// skinny_reduce_row: the split-K reduce of one token row fused with the row op
+// that consumes the GEMM output, so a denoise-step projection costs two
+// launches (part + this) instead of three.  One workgroup per token; thread c
+// owns 8-column chunk c of each segment, which is the chunk layout of the
+// standalone row kernels (norm_mod_bf16_vec / qk_norm_rope_vec with one chunk
+// per thread), and the row arithmetic is shared with them (rowops.h), so the
+// fused and unfused paths give the same bits.  The GEMM output row is written
+// as well (16-byte chunks).
+//   POST kPostNormAffine / kPostNormModF32 / kPostNormModBf16: LayerNorm of
+//     the row (weights, or adaLN modulation in f32 / bf16) into rp.out;
+//   POST kPostSegs: NSEG segments of rp.width columns, each either RMSNorm +
+//     RoPE into a head-major Q/K tensor or a copy into V^T storage.
+// ---------------------------------------------------------------------------
+enum { kPostNormAffine = 1, kPostNormModF32, kPostNormModBf16, kPostSegs };
+
+// The value store_out_t<E> writes (same rounding points), as f32, for the 8
+// outputs m .. m+7 of token row n.
+template <int E>
+__device__ __forceinline__ void epi_vals(const GemmParams & p, int64_t n, int64_t m, const float (&acc)[8],
+                                         float (&o)[8]) {
+    if constexpr (E == kEpiBf16) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = round_bf16(acc[e]);
+    } else {
+        float b[8], h[8] = {}, g[8] = {};
+        unpack8(*(const uint4 *) (p.bias + m), b);
+        if constexpr (E >= kEpiBiasGated) unpack8(*(const uint4 *) (p.res + n * p.ldres + m), h);
+        if constexpr (E == kEpiBiasGated) load8_f32(p.gate + m, g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float a = round_bf16(acc[e]) + b[e];
+            if constexpr (E == kEpiBias) o[e] = round_bf16(a);
+            else if constexpr (E == kEpiBiasGelu) o[e] = round_bf16(gelu_tanh(a));
+            else if constexpr (E == kEpiBiasGated) o[e] = round_bf16(fmaf(round_bf16(a), g[e], h[e]));
+            else o[e] = round_bf16(h[e] + round_bf16(a));
+        }
+    }
+}
+
+// Device copy of the row op (RowPost with the RoPE scales precomputed).
+struct RowSegDev {
+    int32_t kind, rope_mode;
+    int64_t col, dst_tokens, tok0, vt_ld, vt_hs;
+    const uint16_t * w;
+    uint16_t * dst;
+    const int32_t *pos0, *pos1, *pos2;
+    float eps, l2ts128, l2ts44, l2ts42;
+};
+struct RowPostDev {
+    const void * scale;
+    const void * shift;
+    int64_t ss, ldo;
+    uint16_t * out;
+    float eps;
+    int32_t width, head_dim;
+    RowSegDev seg[3];
+};
+
+template <int E, int POST, int NSEG>
+__global__ __launch_bounds__(512) void skinny_reduce_row(GemmParams p, const float * __restrict__ part, int splits,
+                                                         RowPostDev rp) {
+    __shared__ float red[16];
+    const int64_t n = blockIdx.x;
+    const int c = threadIdx.x;
+    const int64_t NM = p.N * p.M;
+    float v[NSEG][8];
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+        const int64_t m = (POST == kPostSegs ? rp.seg[s].col : 0) + 8 * c;
+        const float * src = part + n * p.M + m;
+        float acc[8];
+        load8_f32(src, acc);
+        constexpr int kB = 4;
+        for (int sp0 = 1; sp0 < splits; sp0 += kB) {
+            float t[kB][8];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) load8_f32(src + (int64_t) min(sp0 + u, splits - 1) * NM, t[u]);
+#pragma unroll
+            for (int u = 0; u < kB; ++u)
+                if (sp0 + u < splits)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[e] += t[u][e];
+        }
+        epi_vals<E>(p, n, m, acc, v[s]);
+        *(uint4 *) ((uint16_t *) p.y + n * p.ldy + m) = pack8(v[s]);
+    }
+
+    if constexpr (POST != kPostSegs) {
+        constexpr bool kAffine = POST == kPostNormAffine, kSsBf16 = POST != kPostNormModF32;
+        float a[8], b[8];
+        const int64_t so = n * rp.ss + 8 * c;
+        if constexpr (kSsBf16) {
+            unpack8(*(const uint4 *) ((const uint16_t *) rp.scale + so), a);
+            unpack8(*(const uint4 *) ((const uint16_t *) rp.shift + so), b);
+        } else {
+            load8_f32((const float *) rp.scale + so, a);
+            load8_f32((const float *) rp.shift + so, b);
+        }
+        float mean, inv_std;
+        row_mean_istd<1>(v, (int) blockDim.x, (int) p.M, rp.eps, red, mean, inv_std);
+        *(uint4 *) (rp.out + n * rp.ldo + 8 * c) = norm_chunk<kAffine>(v[0], mean, inv_std, a, b);
+    } else {
+        const int hd = rp.head_dim, e0 = 8 * c, h = e0 / hd, dd0 = e0 % hd;
+#pragma unroll
+        for (int s = 0; s < NSEG; ++s) {
+            const RowSegDev & sg = rp.seg[s];
+            if (sg.kind == kRowSegQk) {
+                const uint4 wv = *(const uint4 *) (sg.w + 8 * c);
+                const RopeTok rt = rope_tok(sg.rope_mode, sg.pos0, sg.pos1, sg.pos2, n, sg.l2ts128, sg.l2ts44,
+                                            sg.l2ts42);
+                float t[1][8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) t[0][e] = v[s][e];
+                const float inv_rms = row_inv_rms<1>(t, rp.width, sg.eps, red);
+                *(uint4 *) (sg.dst + ((int64_t) h * sg.dst_tokens + sg.tok0 + n) * hd + dd0) =
+                    qk_chunk(v[s], inv_rms, wv, dd0, rt);
+            } else {
+                uint16_t * d = sg.dst + (int64_t) h * sg.vt_hs + sg.tok0 + n;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d[(int64_t) (dd0 + e) * sg.vt_ld] = f32_to_bf16(v[s][e]);
+            }
+        }
+    }
+}
+
 // K split of the skinny path, from a small cost model (microseconds): the
 // slowest CU streams ceil(workgroups / 256) slices of kSkinnyFeat x ks
 // weights at its 1/256 share of 8 TB/s, plus a ramp per workgroup (one
@@ -870,23 +984,31 @@ size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     return splits > 1 ? (size_t) splits * N * M * sizeof(float) : 0;
 }
 
+// gemm_skinny_part over `splits` K slices of ks columns; part == nullptr
+// (single slice only) applies the epilogue in the part kernel.
+static void launch_skinny_part(const GemmParams & p, bool xf32, float * part, int splits, int ks, hipStream_t s) {
+    const int nt = (int) ((p.N + 15) / 16);
+    const size_t lds = skinny_lds_bytes(nt, ks);
+    const dim3 grid((unsigned) ((p.M + kSkinnyFeat - 1) / kSkinnyFeat), (unsigned) splits);
+    const dim3 block(kSkinnyWaves * 64);
+#define WAMX_SKINNY(XF, NT) hipLaunchKernelGGL((gemm_skinny_part<XF, NT>), grid, block, lds, s, p, part, ks)
+    switch (nt) {
+        case 1: if (xf32) WAMX_SKINNY(true, 1); else WAMX_SKINNY(false, 1); break;
+        case 2: if (xf32) WAMX_SKINNY(true, 2); else WAMX_SKINNY(false, 2); break;
+        case 3: if (xf32) WAMX_SKINNY(true, 3); else WAMX_SKINNY(false, 3); break;
+        default: if (xf32) WAMX_SKINNY(true, 4); else WAMX_SKINNY(false, 4); break;
+    }
+#undef WAMX_SKINNY
+}
+
 template <bool XF32>
 static hipError_t run_skinny(const GemmParams & p, void * ws, size_t ws_bytes, hipStream_t s) {
     int splits, ks;
     skinny_plan(p.M, p.N, p.K, splits, ks);
     if (splits > 1 && (!ws || (size_t) splits * p.N * p.M * sizeof(float) > ws_bytes || ((uintptr_t) ws & 15)))
         return hipErrorInvalidValue;
-    const int nt = (int) ((p.N + 15) / 16);
-    const size_t lds = skinny_lds_bytes(nt, ks);
-    const dim3 grid((unsigned) ((p.M + kSkinnyFeat - 1) / kSkinnyFeat), (unsigned) splits);
-    const dim3 block(kSkinnyWaves * 64);
-    float * part = (float *) ws;
-    switch (nt) {
-        case 1: hipLaunchKernelGGL((gemm_skinny_part<XF32, 1>), grid, block, lds, s, p, part, ks); break;
-        case 2: hipLaunchKernelGGL((gemm_skinny_part<XF32, 2>), grid, block, lds, s, p, part, ks); break;
-        case 3: hipLaunchKernelGGL((gemm_skinny_part<XF32, 3>), grid, block, lds, s, p, part, ks); break;
-        default: hipLaunchKernelGGL((gemm_skinny_part<XF32, 4>), grid, block, lds, s, p, part, ks); break;
-    }
+    float * part = splits > 1 ? (float *) ws : nullptr;
+    launch_skinny_part(p, XF32, part, splits, ks, s);
     if (splits > 1) {
         const int64_t total = p.N * p.M;
         if (p.M % 4 == 0)
@@ -970,7 +1092,7 @@ static bool dispatch_dma(const GemmParams & p, hipStream_t s, hipError_t & err) 
     return true;
 }
 
-hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
+static GemmParams make_params(const GemmArgs & a) {
     GemmParams p{};
     p.w = (const uint16_t *) a.w;
     p.x = a.x;
@@ -988,6 +1110,138 @@ hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
     p.epi = a.epi;
     p.vec_out = epi_kind(p) != kEpiF32 && a.M % 8 == 0 && a.ldy % 8 == 0 && aligned16(a.y) && aligned16(a.bias) &&
                 aligned16(a.gate) && aligned16(a.res) && (a.res == nullptr || a.ldres % 8 == 0);
+    return p;
+}
+
+static bool vec_operands(const GemmArgs & a) {
+    return a.K % 8 == 0 && a.ldw % 8 == 0 && a.ldx % 8 == 0 && aligned16(a.w) && aligned16(a.x) && a.w_bs2 % 8 == 0 &&
+           a.w_bs3 % 8 == 0 && a.x_bs2 % 8 == 0 && a.x_bs3 % 8 == 0;
+}
+
+static void allow_skinny_lds() {
+    // The activation slice and the weight tiles may use all 160 KB of LDS.
+    constexpr size_t kMaxLds = kSkinnyLdsMax;
+    static bool once = (allow_lds(gemm_skinny_part<true, 1>, kMaxLds), allow_lds(gemm_skinny_part<false, 1>, kMaxLds),
+                        allow_lds(gemm_skinny_part<true, 2>, kMaxLds), allow_lds(gemm_skinny_part<false, 2>, kMaxLds),
+                        allow_lds(gemm_skinny_part<true, 3>, kMaxLds), allow_lds(gemm_skinny_part<false, 3>, kMaxLds),
+                        allow_lds(gemm_skinny_part<true, 4>, kMaxLds), allow_lds(gemm_skinny_part<false, 4>, kMaxLds),
+                        true);
+    (void) once;
+}
+
+// RoPE section scales as launch_qk_norm_rope computes them (host log2f).
+static void rope_scales(int64_t head_dim, float base, float & l128, float & l44, float & l42) {
+    l128 = -2.0f / (float) head_dim * log2f(base);
+    l44 = -2.0f / 44.0f * log2f(base);
+    l42 = -2.0f / 42.0f * log2f(base);
+}
+
+hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStream_t s) {
+    const GemmParams p = make_params(a);
+    const int E = epi_kind(p);
+    if (a.w_type != WAMX_TYPE_BF16 || (a.x_type != WAMX_TYPE_BF16 && a.x_type != WAMX_TYPE_F32) ||
+        a.y_type != WAMX_TYPE_BF16 || a.B2 * a.B3 != 1 || a.N <= 0 || a.N > 64 || a.M <= 0 || a.K <= 0 ||
+        !vec_operands(a) || !p.vec_out || E == kEpiF32 || !a.ws || !aligned16(a.ws))
+        return hipErrorNotSupported;
+    int splits, ks;
+    skinny_plan(p.M, p.N, p.K, splits, ks);
+    if ((size_t) splits * p.N * p.M * sizeof(float) > a.ws_bytes) return hipErrorNotSupported;
+
+    // The row op: one thread per 8-column chunk, the whole row (or segment)
+    // in one workgroup whose size is a multiple of the wave.
+    RowPostDev d{};
+    int post_kind, nseg = 1;
+    int64_t nchunk;
+    if (post.kind == kRowPostNorm) {
+        const int es = (post.affine || post.ss_type == WAMX_TYPE_BF16) ? 2 : 4;
+        if (!post.out || post.ldo % 8 != 0 || !aligned16(post.out) || !aligned16(post.scale) || !aligned16(post.shift) ||
+            (post.ss * es) % 16 != 0)
+            return hipErrorNotSupported;
+        post_kind = post.affine ? kPostNormAffine : post.ss_type == WAMX_TYPE_BF16 ? kPostNormModBf16 : kPostNormModF32;
+        nchunk = p.M / 8;
+        d.scale = post.scale;
+        d.shift = post.shift;
+        d.ss = post.ss;
+        d.out = (uint16_t *) post.out;
+        d.ldo = post.ldo;
+        d.eps = post.eps;
+    } else if (post.kind == kRowPostSegs) {
+        if (post.nseg < 1 || post.nseg > 3 || post.head_dim <= 0 || post.head_dim % 8 != 0 || post.width <= 0 ||
+            post.width % post.head_dim != 0)
+            return hipErrorNotSupported;
+        if (E != kEpiBf16 && E != kEpiBias) return hipErrorNotSupported;
+        post_kind = kPostSegs;
+        nseg = post.nseg;
+        nchunk = post.width / 8;
+        d.width = (int32_t) post.width;
+        d.head_dim = (int32_t) post.head_dim;
+        for (int i = 0; i < nseg; ++i) {
+            const RowSeg & g = post.seg[i];
+            RowSegDev & o = d.seg[i];
+            if (g.col < 0 || g.col % 8 != 0 || g.col + post.width > p.M || !g.dst) return hipErrorNotSupported;
+            if (g.kind == kRowSegQk) {
+                if (!aligned16(g.w) || !aligned16(g.dst) || !g.w || (g.rope_mode != 2 && !g.pos0) ||
+                    (g.rope_mode == 1 && (!g.pos1 || !g.pos2)))
+                    return hipErrorNotSupported;
+            } else if (g.kind != kRowSegVt) {
+                return hipErrorNotSupported;
+            }
+            o.kind = g.kind;
+            o.rope_mode = g.rope_mode;
+            o.col = g.col;
+            o.dst_tokens = g.dst_tokens;
+            o.tok0 = g.tok0;
+            o.vt_ld = g.vt_ld;
+            o.vt_hs = g.vt_hs;
+            o.w = (const uint16_t *) g.w;
+            o.dst = (uint16_t *) g.dst;
+            o.pos0 = g.pos0;
+            o.pos1 = g.pos1;
+            o.pos2 = g.pos2;
+            o.eps = g.eps;
+            rope_scales(post.head_dim, g.freq_base, o.l2ts128, o.l2ts44, o.l2ts42);
+        }
+    } else {
+        return hipErrorNotSupported;
+    }
+    if (nchunk <= 0 || nchunk > 512 || nchunk % 64 != 0) return hipErrorNotSupported;
+
+    allow_skinny_lds();
+    const float * part = (const float *) a.ws;
+    launch_skinny_part(p, a.x_type == WAMX_TYPE_F32, (float *) a.ws, splits, ks, s);
+    const dim3 grid((unsigned) p.N), block((unsigned) nchunk);
+#define WAMX_ROW(EK, PK, NS) hipLaunchKernelGGL((skinny_reduce_row<EK, PK, NS>), grid, block, 0, s, p, part, splits, d)
+#define WAMX_ROW_NORM(EK)                                                   \
+    switch (post_kind) {                                                    \
+        case kPostNormAffine: WAMX_ROW(EK, kPostNormAffine, 1); break;      \
+        case kPostNormModBf16: WAMX_ROW(EK, kPostNormModBf16, 1); break;    \
+        default: WAMX_ROW(EK, kPostNormModF32, 1); break;                   \
+    }
+#define WAMX_ROW_SEGS(EK)                                                   \
+    switch (nseg) {                                                         \
+        case 1: WAMX_ROW(EK, kPostSegs, 1); break;                          \
+        case 2: WAMX_ROW(EK, kPostSegs, 2); break;                          \
+        default: WAMX_ROW(EK, kPostSegs, 3); break;                         \
+    }
+    if (post_kind == kPostSegs) {
+        if (E == kEpiBf16) WAMX_ROW_SEGS(kEpiBf16) else WAMX_ROW_SEGS(kEpiBias)
+    } else {
+        switch (E) {
+            case kEpiBf16: WAMX_ROW_NORM(kEpiBf16) break;
+            case kEpiBias: WAMX_ROW_NORM(kEpiBias) break;
+            case kEpiBiasGelu: WAMX_ROW_NORM(kEpiBiasGelu) break;
+            case kEpiBiasGated: WAMX_ROW_NORM(kEpiBiasGated) break;
+            default: WAMX_ROW_NORM(kEpiBiasResidual) break;
+        }
+    }
+#undef WAMX_ROW_SEGS
+#undef WAMX_ROW_NORM
+#undef WAMX_ROW
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
+    const GemmParams p = make_params(a);
     const int64_t batches = a.B2 * a.B3;
     if (a.M <= 0 || a.N <= 0 || batches <= 0) return hipSuccess;
     if (a.K <= 0) return hipErrorInvalidValue;
@@ -1000,18 +1254,10 @@ hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
     if (a.w_type != WAMX_TYPE_BF16 || (a.x_type != WAMX_TYPE_BF16 && a.x_type != WAMX_TYPE_F32))
         return hipErrorInvalidValue;
     const bool xf32 = a.x_type == WAMX_TYPE_F32;
-    const bool vec = a.K % 8 == 0 && a.ldw % 8 == 0 && a.ldx % 8 == 0 && aligned16(a.w) && aligned16(a.x) &&
-                     a.w_bs2 % 8 == 0 && a.w_bs3 % 8 == 0 && a.x_bs2 % 8 == 0 && a.x_bs3 % 8 == 0;
+    const bool vec = vec_operands(a);
 
     if (vec && batches == 1 && a.N <= 64) {
-        // The activation slice and the weight tiles may use all 160 KB of LDS.
-        constexpr size_t kMaxLds = kSkinnyLdsMax;
-        static bool once = (allow_lds(gemm_skinny_part<true, 1>, kMaxLds), allow_lds(gemm_skinny_part<false, 1>, kMaxLds),
-                            allow_lds(gemm_skinny_part<true, 2>, kMaxLds), allow_lds(gemm_skinny_part<false, 2>, kMaxLds),
-                            allow_lds(gemm_skinny_part<true, 3>, kMaxLds), allow_lds(gemm_skinny_part<false, 3>, kMaxLds),
-                            allow_lds(gemm_skinny_part<true, 4>, kMaxLds), allow_lds(gemm_skinny_part<false, 4>, kMaxLds),
-                            true);
-        (void) once;
+        allow_skinny_lds();
         return xf32 ? run_skinny<true>(p, a.ws, a.ws_bytes, s) : run_skinny<false>(p, a.ws, a.ws_bytes, s);
     }
     if (vec && !xf32 && batches == 1) {

@@ -13,6 +13,7 @@
 // normalised and written once: bytes = row in + row out.
 #include "../internal.h"
 #include "device.h"
+#include "rowops.h"
 
 #include <algorithm>
 
@@ -226,46 +227,23 @@ __global__ __launch_bounds__(1024) void norm_mod_bf16_vec(const uint16_t * __res
         }
     }
     float v[CPT][8];
-    float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-        const bool ok = (int) threadIdx.x + i * (int) blockDim.x < nchunk;
-        const uint32_t u[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+        unpack8(xv[i], v[i]);
+        if ((int) threadIdx.x + i * (int) blockDim.x >= nchunk)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[i][2 * e] = ok ? bf16_to_f32((uint16_t) (u[e] & 0xffff)) : 0.0f;
-            v[i][2 * e + 1] = ok ? bf16_to_f32((uint16_t) (u[e] >> 16)) : 0.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sum += v[i][e];
+            for (int e = 0; e < 8; ++e) v[i][e] = 0.0f;
     }
-    const float mean = block_sum(sum, red) / (float) cols;
-    float var = 0.0f;
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-        if ((int) threadIdx.x + i * (int) blockDim.x >= nchunk) continue;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float d = v[i][e] - mean;
-            var = fmaf(d, d, var);
-        }
-    }
-    var = block_sum(var, red) / (float) cols;
-    const float inv_std = rsqrtf(var + eps);
+    float mean, inv_std;
+    row_mean_istd<CPT>(v, nchunk, cols, eps, red, mean, inv_std);
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
         const int c = (int) threadIdx.x + i * (int) blockDim.x;
         if (c >= nchunk) continue;
         float a[8], b[8];
         if constexpr (SS_BF16) {
-            const uint32_t ua[4] = {ha[i].x, ha[i].y, ha[i].z, ha[i].w}, ub[4] = {hb[i].x, hb[i].y, hb[i].z, hb[i].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                a[2 * e] = bf16_to_f32((uint16_t) (ua[e] & 0xffff));
-                a[2 * e + 1] = bf16_to_f32((uint16_t) (ua[e] >> 16));
-                b[2 * e] = bf16_to_f32((uint16_t) (ub[e] & 0xffff));
-                b[2 * e + 1] = bf16_to_f32((uint16_t) (ub[e] >> 16));
-            }
+            unpack8(ha[i], a);
+            unpack8(hb[i], b);
         } else {
             const float af[8] = {fa[i][0].x, fa[i][0].y, fa[i][0].z, fa[i][0].w, fa[i][1].x, fa[i][1].y, fa[i][1].z, fa[i][1].w};
             const float bf[8] = {fb[i][0].x, fb[i][0].y, fb[i][0].z, fb[i][0].w, fb[i][1].x, fb[i][1].y, fb[i][1].z, fb[i][1].w};
@@ -275,14 +253,7 @@ __global__ __launch_bounds__(1024) void norm_mod_bf16_vec(const uint16_t * __res
                 b[e] = bf[e];
             }
         }
-        float o[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float n = (v[i][e] - mean) * inv_std;
-            o[e] = AFFINE ? fmaf(n, a[e], b[e]) : fmaf(n, 1.0f + a[e], b[e]);
-        }
-        *(uint4 *) (y + row * ldy + 8 * c) =
-            make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7]));
+        *(uint4 *) (y + row * ldy + 8 * c) = norm_chunk<AFFINE>(v[i], mean, inv_std, a, b);
     }
 }
 
