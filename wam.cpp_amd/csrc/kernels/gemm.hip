@@ -664,7 +664,7 @@ constexpr int kSkinnyDepth = 2;                            // weight prefetch de
 constexpr int kSkinnyMaxKs = 1024;                         // longest K slice (LDS permitting)
 constexpr size_t kSkinnyLdsMax = 160 * 1024;
 
-template <bool XF32, int NT>
+template <bool XF32, int NT, int DEPTH = kSkinnyDepth>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams p, float * part, int ks) {
     constexpr int RG = kSkinnyRows / 16;             // 16-row MFMA groups per wave
     constexpr int LI = kSkinnyRows / 4;              // load instructions per step (4 rows x 256 B each)
@@ -690,7 +690,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
 #pragma unroll
     for (int c = 0; c < LI; ++c) wbase[c] = p.w + min(m0 + 4 * c + lrow, M - 1) * p.ldw + kb;
     const int nsteps = (klen + 127) / 128;
-    uint4 wbuf[kSkinnyDepth][LI];
+    uint4 wbuf[DEPTH][LI];
     auto wload = [&](int st, uint4 (&d)[LI]) {
         const int k = st * 128 + 8 * lchunk;
         const bool kin = k < klen;
@@ -726,7 +726,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
         }
         if (c0 == 0) {
 #pragma unroll
-            for (int i = 0; i < kSkinnyDepth; ++i) wload(min(i, nsteps - 1), wbuf[i]);
+            for (int i = 0; i < DEPTH; ++i) wload(min(i, nsteps - 1), wbuf[i]);
         }
 #pragma unroll
         for (int u = 0; u < kStageBatch; ++u) {
@@ -742,9 +742,9 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[rg][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const uint16_t * xrow = xs + r16 * pitch + 8 * g;
-    for (int st0 = 0; st0 < nsteps; st0 += kSkinnyDepth) {
+    for (int st0 = 0; st0 < nsteps; st0 += DEPTH) {
 #pragma unroll
-        for (int i = 0; i < kSkinnyDepth; ++i) {
+        for (int i = 0; i < DEPTH; ++i) {
             const int st = st0 + i;
             if (st < nsteps) {
                 // registers -> wave tile (row 4c + lrow, chunk lchunk)
@@ -770,7 +770,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
                             acc[rg][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[t], wa[rg], acc[rg][t], 0, 0, 0);
                 }
             }
-            wload(min(st + kSkinnyDepth, nsteps - 1), wbuf[i]);
+            if (st + DEPTH < nsteps) wload(st + DEPTH, wbuf[i]);
         }
     }
 
@@ -825,16 +825,17 @@ __global__ __launch_bounds__(256) void gemm_skinny_reduce(GemmParams p, const fl
 // ---------------------------------------------------------------------------
 // skinny_reduce_row: the split-K reduce of one token row fused with the row op
 // that consumes the GEMM output, so a denoise-step projection costs two
-// launches (part + this) instead of three.  One workgroup per token; thread c
-// owns 8-column chunk c of each segment, which is the chunk layout of the
+// launches (part + this) instead of three.  One workgroup per token (and
+// segment); thread c owns 8-column chunk c, which is the chunk layout of the
 // standalone row kernels (norm_mod_bf16_vec / qk_norm_rope_vec with one chunk
 // per thread), and the row arithmetic is shared with them (rowops.h), so the
 // fused and unfused paths give the same bits.  The GEMM output row is written
 // as well (16-byte chunks).
 //   POST kPostNormAffine / kPostNormModF32 / kPostNormModBf16: LayerNorm of
 //     the row (weights, or adaLN modulation in f32 / bf16) into rp.out;
-//   POST kPostSegs: NSEG segments of rp.width columns, each either RMSNorm +
-//     RoPE into a head-major Q/K tensor or a copy into V^T storage.
+//   POST kPostSegs: up to three segments of rp.width columns, one per
+//     workgroup row of the grid, each either RMSNorm + RoPE into a head-major
+//     Q/K tensor or a copy into V^T storage.
 // ---------------------------------------------------------------------------
 enum { kPostNormAffine = 1, kPostNormModF32, kPostNormModBf16, kPostSegs };
 
@@ -881,34 +882,34 @@ struct RowPostDev {
     RowSegDev seg[3];
 };
 
-template <int E, int POST, int NSEG>
+template <int E, int POST>
 __global__ __launch_bounds__(512) void skinny_reduce_row(GemmParams p, const float * __restrict__ part, int splits,
                                                          RowPostDev rp) {
     __shared__ float red[16];
     const int64_t n = blockIdx.x;
     const int c = threadIdx.x;
     const int64_t NM = p.N * p.M;
-    float v[NSEG][8];
+    const RowSegDev & sg = rp.seg[POST == kPostSegs ? blockIdx.y : 0];
+    const int64_t m = (POST == kPostSegs ? sg.col : 0) + 8 * c;
+    const float * src = part + n * p.M + m;
+    // Every split is requested before the first sum (in batches of kB), so
+    // the row costs one memory round trip per batch; the sums run in split
+    // order, as in gemm_skinny_reduce.
+    constexpr int kB = 20;
+    float acc[8];
+    for (int sp0 = 0; sp0 < splits; sp0 += kB) {
+        float t[kB][8];
 #pragma unroll
-    for (int s = 0; s < NSEG; ++s) {
-        const int64_t m = (POST == kPostSegs ? rp.seg[s].col : 0) + 8 * c;
-        const float * src = part + n * p.M + m;
-        float acc[8];
-        load8_f32(src, acc);
-        constexpr int kB = 4;
-        for (int sp0 = 1; sp0 < splits; sp0 += kB) {
-            float t[kB][8];
+        for (int u = 0; u < kB; ++u) load8_f32(src + (int64_t) min(sp0 + u, splits - 1) * NM, t[u]);
 #pragma unroll
-            for (int u = 0; u < kB; ++u) load8_f32(src + (int64_t) min(sp0 + u, splits - 1) * NM, t[u]);
+        for (int u = 0; u < kB; ++u)
+            if (sp0 + u < splits)
 #pragma unroll
-            for (int u = 0; u < kB; ++u)
-                if (sp0 + u < splits)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[e] += t[u][e];
-        }
-        epi_vals<E>(p, n, m, acc, v[s]);
-        *(uint4 *) ((uint16_t *) p.y + n * p.ldy + m) = pack8(v[s]);
+                for (int e = 0; e < 8; ++e) acc[e] = sp0 + u == 0 ? t[u][e] : acc[e] + t[u][e];
     }
+    float v[1][8];
+    epi_vals<E>(p, n, m, acc, v[0]);
+    *(uint4 *) ((uint16_t *) p.y + n * p.ldy + m) = pack8(v[0]);
 
     if constexpr (POST != kPostSegs) {
         constexpr bool kAffine = POST == kPostNormAffine, kSsBf16 = POST != kPostNormModF32;
@@ -926,24 +927,16 @@ __global__ __launch_bounds__(512) void skinny_reduce_row(GemmParams p, const flo
         *(uint4 *) (rp.out + n * rp.ldo + 8 * c) = norm_chunk<kAffine>(v[0], mean, inv_std, a, b);
     } else {
         const int hd = rp.head_dim, e0 = 8 * c, h = e0 / hd, dd0 = e0 % hd;
+        if (sg.kind == kRowSegQk) {
+            const uint4 wv = *(const uint4 *) (sg.w + 8 * c);
+            const RopeTok rt = rope_tok(sg.rope_mode, sg.pos0, sg.pos1, sg.pos2, n, sg.l2ts128, sg.l2ts44, sg.l2ts42);
+            const float inv_rms = row_inv_rms<1>(v, rp.width, sg.eps, red);
+            *(uint4 *) (sg.dst + ((int64_t) h * sg.dst_tokens + sg.tok0 + n) * hd + dd0) =
+                qk_chunk(v[0], inv_rms, wv, dd0, rt);
+        } else {
+            uint16_t * d = sg.dst + (int64_t) h * sg.vt_hs + sg.tok0 + n;
 #pragma unroll
-        for (int s = 0; s < NSEG; ++s) {
-            const RowSegDev & sg = rp.seg[s];
-            if (sg.kind == kRowSegQk) {
-                const uint4 wv = *(const uint4 *) (sg.w + 8 * c);
-                const RopeTok rt = rope_tok(sg.rope_mode, sg.pos0, sg.pos1, sg.pos2, n, sg.l2ts128, sg.l2ts44,
-                                            sg.l2ts42);
-                float t[1][8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) t[0][e] = v[s][e];
-                const float inv_rms = row_inv_rms<1>(t, rp.width, sg.eps, red);
-                *(uint4 *) (sg.dst + ((int64_t) h * sg.dst_tokens + sg.tok0 + n) * hd + dd0) =
-                    qk_chunk(v[s], inv_rms, wv, dd0, rt);
-            } else {
-                uint16_t * d = sg.dst + (int64_t) h * sg.vt_hs + sg.tok0 + n;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) d[(int64_t) (dd0 + e) * sg.vt_ld] = f32_to_bf16(v[s][e]);
-            }
+            for (int e = 0; e < 8; ++e) d[(int64_t) (dd0 + e) * sg.vt_ld] = f32_to_bf16(v[0][e]);
         }
     }
 }
@@ -1209,22 +1202,17 @@ hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStre
     allow_skinny_lds();
     const float * part = (const float *) a.ws;
     launch_skinny_part(p, a.x_type == WAMX_TYPE_F32, (float *) a.ws, splits, ks, s);
-    const dim3 grid((unsigned) p.N), block((unsigned) nchunk);
-#define WAMX_ROW(EK, PK, NS) hipLaunchKernelGGL((skinny_reduce_row<EK, PK, NS>), grid, block, 0, s, p, part, splits, d)
+    const dim3 grid((unsigned) p.N, (unsigned) nseg), block((unsigned) nchunk);
+#define WAMX_ROW(EK, PK) hipLaunchKernelGGL((skinny_reduce_row<EK, PK>), grid, block, 0, s, p, part, splits, d)
 #define WAMX_ROW_NORM(EK)                                                   \
     switch (post_kind) {                                                    \
-        case kPostNormAffine: WAMX_ROW(EK, kPostNormAffine, 1); break;      \
-        case kPostNormModBf16: WAMX_ROW(EK, kPostNormModBf16, 1); break;    \
-        default: WAMX_ROW(EK, kPostNormModF32, 1); break;                   \
-    }
-#define WAMX_ROW_SEGS(EK)                                                   \
-    switch (nseg) {                                                         \
-        case 1: WAMX_ROW(EK, kPostSegs, 1); break;                          \
-        case 2: WAMX_ROW(EK, kPostSegs, 2); break;                          \
-        default: WAMX_ROW(EK, kPostSegs, 3); break;                         \
+        case kPostNormAffine: WAMX_ROW(EK, kPostNormAffine); break;         \
+        case kPostNormModBf16: WAMX_ROW(EK, kPostNormModBf16); break;       \
+        default: WAMX_ROW(EK, kPostNormModF32); break;                      \
     }
     if (post_kind == kPostSegs) {
-        if (E == kEpiBf16) WAMX_ROW_SEGS(kEpiBf16) else WAMX_ROW_SEGS(kEpiBias)
+        if (E == kEpiBf16) WAMX_ROW(kEpiBf16, kPostSegs);
+        else WAMX_ROW(kEpiBias, kPostSegs);
     } else {
         switch (E) {
             case kEpiBf16: WAMX_ROW_NORM(kEpiBf16) break;
@@ -1234,7 +1222,6 @@ hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStre
             default: WAMX_ROW_NORM(kEpiBiasResidual) break;
         }
     }
-#undef WAMX_ROW_SEGS
 #undef WAMX_ROW_NORM
 #undef WAMX_ROW
     return hipGetLastError();
