@@ -278,8 +278,9 @@ def workload_chunk(be, args):
     def aup():
         w_aup, b_aup = aups[nxt[0] % len(aups)]
         nxt[0] += 1
-        wamx.check(lib.wamx_op_linear(be.ptr, w_aup.contents.data, dxa.ptr, wamx.TYPE_BF16, b_aup.contents.data,
-                                      wamx.EPI_BIAS_GELU, None, None, dya.ptr, Fa, Ta, Da), "linear")
+        wamx.check(lib.wamx_op_linear_tiled(be.ptr, w_aup.contents.data, dxa.ptr, wamx.TYPE_BF16,
+                                            b_aup.contents.data, wamx.EPI_BIAS_GELU, None, None, dya.ptr, Fa, Ta, Da),
+                   "linear_tiled")
     aup_ms = time_op(be, aup, 60)
     aup_bytes = Fa * Da * 2 + Ta * Da * 2 + Ta * Fa * 2 + Fa * 2
     roof = {"bound": "mfma", "achieved": flops / (up_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
@@ -287,7 +288,8 @@ def workload_chunk(be, args):
             "kernel": "gemm_dma<256,256>: prefix visual FFN-up 3072 tok x [14336 x 3072] + bias + GELU",
             "kernel_ms": up_ms, "flops_per_launch": flops,
             "algorithmic_bytes": T * D * 2 + F * D * 2 + F * 2 + T * F * 2,
-            "skinny": {"kernel": "gemm_skinny_part + gemm_skinny_reduce: denoise FFN-up 48 tok x [14336 x 3072] + bias + GELU",
+            "skinny": {"kernel": "gemm_skinny_tiled + gemm_skinny_reduce: denoise FFN-up 48 tok x [14336 x 3072] (tiled) "
+                                 "+ bias + GELU",
                        "kernel_ms": aup_ms, "achieved_gbs": aup_bytes / (aup_ms * 1e-3) / 1e9,
                        "frac_hbm": aup_bytes / (aup_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": aup_bytes,
                        "traffic": measured_traffic("gemm_skinny_ffn_up")}}
@@ -339,19 +341,36 @@ def probe_traffic(be, launches: int = 3):
         wamx.check(lib.wamx_op_bias_gelu_bf16(be.ptr, cx.ptr, cb.ptr, cy.ptr, n, width), "bias_gelu")
     be.sync()
     out = {"calibration": {"kernel": "bias_gelu_bf16_kernel", "read_bytes": 2 * n + 2 * width, "write_bytes": 2 * n}}
+    D, F = 3072, 14336
+    hw = _normal(F * D, 13, 0.0, 0.02, bf16=True)
     for key, T in (("gemm_dma_ffn_up", 3072), ("gemm_skinny_ffn_up", 48)):
-        D, F = 3072, 14336
-        w = be.array(_normal(F * D, 13, 0.0, 0.02, bf16=True))
         b = be.array(_normal(F, 14, 0.0, 0.02, bf16=True))
         x = be.array(_normal(T * D, 15, bf16=True))
         y = be.empty(T * F * 2)
-        for _ in range(launches):
-            wamx.check(lib.wamx_op_linear(be.ptr, w.ptr, x.ptr, wamx.TYPE_BF16, b.ptr, wamx.EPI_BIAS_GELU, None, None,
-                                          y.ptr, F, T, D), "linear")
+        if T > 64:   # row-major weight, many-token GEMM
+            w = be.array(hw)
+            for _ in range(launches):
+                wamx.check(lib.wamx_op_linear(be.ptr, w.ptr, x.ptr, wamx.TYPE_BF16, b.ptr, wamx.EPI_BIAS_GELU, None,
+                                              None, y.ptr, F, T, D), "linear")
+        else:        # the action expert's weights live in the tiled buffer type
+            ctx = lib.wamx_init(4)
+            wt = lib.wamx_new_tensor_2d(ctx, wamx.TYPE_BF16, D, F)
+            buf = lib.wamx_backend_alloc_ctx_tensors_from_buft(ctx, lib.wamx_backend_tiled_buffer_type(0))
+            if not buf:
+                raise RuntimeError(wamx.last_error())
+            wamx.check(lib.wamx_backend_tensor_set(wt, hw.ctypes.data, 0, hw.nbytes), "tensor_set")
+            for _ in range(launches):
+                wamx.check(lib.wamx_op_linear_tiled(be.ptr, wt.contents.data, x.ptr, wamx.TYPE_BF16, b.ptr,
+                                                    wamx.EPI_BIAS_GELU, None, None, y.ptr, F, T, D), "linear_tiled")
         be.sync()
         out[key] = {"tokens": T, "read_bytes": F * D * 2 + T * D * 2 + F * 2, "write_bytes": T * F * 2}
-        for a in (w, b, x, y):
+        for a in (b, x, y):
             a.free()
+        if T > 64:
+            w.free()
+        else:
+            lib.wamx_buffer_free(buf)
+            lib.wamx_free(ctx)
     print(json.dumps(out), flush=True)
 
 

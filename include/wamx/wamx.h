@@ -332,6 +332,14 @@ WAMX_API const char *    wamx_backend_name(wamx_backend_t backend);
 WAMX_API void *          wamx_backend_stream(wamx_backend_t backend);   /* hipStream_t */
 WAMX_API wamx_buffer_type_t wamx_backend_get_default_buffer_type(wamx_backend_t backend);
 WAMX_API wamx_buffer_type_t wamx_backend_buffer_type(int device);
+/* The tiled weight buffer type of a device, in the role of ggml's repacking
+ * "extra" buffer types (ggml_backend_dev_get_extra_bufts / the CPU backend's
+ * weight repack, ggml b9866): a 2-D bf16 weight [K][M] with M % 16 == 0 and
+ * K % 32 == 0 allocated here is stored MFMA-tiled and is read by the few-token
+ * (<= 64) MUL_MAT/LINEAR path only (supports_op says so); tensor set/get/copy
+ * convert to and from the row-major layout, and a set writes the whole tensor.
+ * wam.cpp would place the action expert's projection weights here. */
+WAMX_API wamx_buffer_type_t wamx_backend_tiled_buffer_type(int device);
 
 /* Buffers (ggml_backend_buft_alloc_buffer, ggml_backend_alloc_ctx_tensors). */
 WAMX_API wamx_buffer_t wamx_buft_alloc_buffer(wamx_buffer_type_t buft, size_t size);
@@ -343,6 +351,8 @@ WAMX_API void *        wamx_buffer_get_base(wamx_buffer_t buf);
 WAMX_API size_t        wamx_buffer_get_size(wamx_buffer_t buf);
 WAMX_API wamx_status   wamx_tensor_alloc(wamx_buffer_t buf, wamx_tensor * t, void * addr);
 WAMX_API wamx_buffer_t wamx_backend_alloc_ctx_tensors(wamx_context * ctx, wamx_backend_t backend);
+/* ggml_backend_alloc_ctx_tensors_from_buft (ggml-alloc.h, b9866). */
+WAMX_API wamx_buffer_t wamx_backend_alloc_ctx_tensors_from_buft(wamx_context * ctx, wamx_buffer_type_t buft);
 
 /* Tensor data movement (ggml_backend_tensor_set/get/copy). */
 WAMX_API wamx_status wamx_backend_tensor_set(wamx_tensor * t, const void * data, size_t offset, size_t size);
@@ -382,6 +392,13 @@ WAMX_API wamx_status wamx_op_mul_mat(wamx_backend_t be, const void * w, int64_t 
 WAMX_API wamx_status wamx_op_linear(wamx_backend_t be, const void * w, const void * x, int32_t x_type,
                                     const void * bias, int32_t epilogue, const void * residual,
                                     const float * gate, void * y, int64_t M, int64_t N, int64_t K);
+/* wamx_op_linear with w in the MFMA-tiled layout of the tiled buffer type
+ * (the data pointer of a tensor placed by wamx_backend_tiled_buffer_type);
+ * M % 16 == 0, K % 32 == 0, N <= 64.  Plays the part of the matmul over a
+ * repacked weight in ggml's CPU extra buffer types (ggml-cpu repack). */
+WAMX_API wamx_status wamx_op_linear_tiled(wamx_backend_t be, const void * w, const void * x, int32_t x_type,
+                                          const void * bias, int32_t epilogue, const void * residual,
+                                          const float * gate, void * y, int64_t M, int64_t N, int64_t K);
 /* norm_bf16_fused<bs,false> (native-bf16.patch:368-409): y = bf16(n*(1+scale)+shift).
  * scale/shift f32, row stride ss (0 = broadcast). */
 WAMX_API wamx_status wamx_op_norm_modulation_bf16(wamx_backend_t be, const void * x, int64_t ldx,

@@ -34,6 +34,7 @@ struct wamx_device {
 struct wamx_buffer_type {
     wamx_device * dev = nullptr;
     char name[32] = {0};
+    bool tiled = false;  // weights placed here are stored MFMA-tiled (see tensor_is_tiled)
 };
 
 struct wamx_buffer {
@@ -61,6 +62,7 @@ struct wamx_backend {
 struct wamx_backend_reg {
     std::vector<wamx_device> devices;
     std::vector<wamx_buffer_type> bufts;
+    std::vector<wamx_buffer_type> tiled_bufts;
 };
 
 // ---------------------------------------------------------------------------
@@ -73,6 +75,7 @@ static struct wamx_backend_reg * registry() {
         if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
         r->devices.resize(n);
         r->bufts.resize(n);
+        r->tiled_bufts.resize(n);
         for (int i = 0; i < n; ++i) {
             r->devices[i].index = i;
             snprintf(r->devices[i].name, sizeof r->devices[i].name, "ROCm%d", i);
@@ -82,6 +85,9 @@ static struct wamx_backend_reg * registry() {
                          prop.multiProcessorCount);
             r->bufts[i].dev = &r->devices[i];
             snprintf(r->bufts[i].name, sizeof r->bufts[i].name, "ROCm%d", i);
+            r->tiled_bufts[i].dev = &r->devices[i];
+            r->tiled_bufts[i].tiled = true;
+            snprintf(r->tiled_bufts[i].name, sizeof r->tiled_bufts[i].name, "ROCm%d_Tiled", i);
         }
         return r;
     }();
@@ -112,28 +118,85 @@ static wamx_buffer_t buft_alloc_buffer(wamx_buffer_type_t buft, size_t size) {
     return b;
 }
 
+// ---------------------------------------------------------------------------
+// Tiled weights.  A 2-D bf16 tensor [K][M] (ggml ne = {K, M}) with M % 16 == 0
+// and K % 32 == 0 placed in a tiled buffer is stored in the MFMA-tiled layout
+// of launch_tile_weights and marked by t->extra; set/get/copy convert from and
+// to the row-major ggml layout, so callers always see row-major data.  The
+// skinny GEMM reads such weights with one 1 KB load per MFMA fragment.  This
+// plays the part of ggml's repacking "extra" buffer types (the CPU backend's
+// weight repack), for the few-token projections.
+// ---------------------------------------------------------------------------
+static int k_tiled_tag;
+
+static bool tileable(const wamx_tensor * t) {
+    return t->type == WAMX_TYPE_BF16 && !t->view_src && t->ne[2] == 1 && t->ne[3] == 1 && t->ne[1] % 16 == 0 &&
+           t->ne[0] % 32 == 0 && t->nb[0] == 2 && t->nb[1] == (size_t) t->ne[0] * 2;
+}
+
+namespace wamx {
+bool tensor_is_tiled(const wamx_tensor * t) { return t && t->extra == &k_tiled_tag; }
+
+hipError_t tensor_set_from_device(wamx_tensor * t, const void * src, hipStream_t s) {
+    if (!tensor_is_tiled(t)) return hipMemcpyAsync(t->data, src, wamx_nbytes(t), hipMemcpyDeviceToDevice, s);
+    return launch_tile_weights(src, t->data, t->ne[1], t->ne[0], false, s);
+}
+}  // namespace wamx
+
+// Whole-tensor conversions through a temporary device buffer.
+static hipError_t tiled_set(wamx_tensor * t, const void * host) {
+    void * tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, wamx_nbytes(t));
+    if (e != hipSuccess) return e;
+    e = hipMemcpy(tmp, host, wamx_nbytes(t), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_tile_weights(tmp, t->data, t->ne[1], t->ne[0], false, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    hipFree(tmp);
+    return e;
+}
+static hipError_t tiled_get(const wamx_tensor * t, void * host, size_t off, size_t size) {
+    void * tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, wamx_nbytes(t));
+    if (e != hipSuccess) return e;
+    e = launch_tile_weights(t->data, tmp, t->ne[1], t->ne[0], true, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(host, (const char *) tmp + off, size, hipMemcpyDeviceToHost);
+    hipFree(tmp);
+    return e;
+}
+static hipError_t tensor_copy_impl(const wamx_tensor * src, wamx_tensor * dst) {
+    const bool ts = tensor_is_tiled(src), td = tensor_is_tiled(dst);
+    if (ts == td) return hipMemcpy(dst->data, src->data, wamx_nbytes(src), hipMemcpyDeviceToDevice);
+    const wamx_tensor * t = ts ? src : dst;  // the tiled side fixes M and K
+    hipError_t e = launch_tile_weights(src->data, dst->data, t->ne[1], t->ne[0], ts, nullptr);
+    return e == hipSuccess ? hipDeviceSynchronize() : e;
+}
+
 static void buffer_free(wamx_buffer_t b) {
     if (!b) return;
     if (b->base) hipFree(b->base);
     delete b;
 }
 static void * buffer_get_base(wamx_buffer_t b) { return b ? b->base : nullptr; }
-static wamx_status buffer_init_tensor(wamx_buffer_t, wamx_tensor * t) {
+static wamx_status buffer_init_tensor(wamx_buffer_t b, wamx_tensor * t) {
     if (t->view_src && t->view_src->data) t->data = (char *) t->view_src->data + t->view_offs;
+    if (b && b->buft && b->buft->tiled && tileable(t)) t->extra = &k_tiled_tag;
     return WAMX_STATUS_SUCCESS;
 }
 static void buffer_memset_tensor(wamx_buffer_t, wamx_tensor * t, uint8_t v, size_t off, size_t size) {
     hipMemset((char *) t->data + off, v, size);
 }
 static void buffer_set_tensor(wamx_buffer_t, wamx_tensor * t, const void * data, size_t off, size_t size) {
-    hipMemcpy((char *) t->data + off, data, size, hipMemcpyHostToDevice);
+    if (tensor_is_tiled(t) && off == 0 && size == wamx_nbytes(t)) tiled_set(t, data);
+    else if (!tensor_is_tiled(t)) hipMemcpy((char *) t->data + off, data, size, hipMemcpyHostToDevice);
 }
 static void buffer_get_tensor(wamx_buffer_t, const wamx_tensor * t, void * data, size_t off, size_t size) {
-    hipMemcpy(data, (const char *) t->data + off, size, hipMemcpyDeviceToHost);
+    if (tensor_is_tiled(t)) tiled_get(t, data, off, size);
+    else hipMemcpy(data, (const char *) t->data + off, size, hipMemcpyDeviceToHost);
 }
 static bool buffer_cpy_tensor(wamx_buffer_t, const wamx_tensor * src, wamx_tensor * dst) {
     if (!src->data || !dst->data || wamx_nbytes(src) != wamx_nbytes(dst)) return false;
-    return hipMemcpy(dst->data, src->data, wamx_nbytes(src), hipMemcpyDeviceToDevice) == hipSuccess;
+    if ((tensor_is_tiled(src) || tensor_is_tiled(dst)) && !wamx_are_same_shape(src, dst)) return false;
+    return tensor_copy_impl(src, dst) == hipSuccess;
 }
 static void buffer_clear(wamx_buffer_t b, uint8_t v) {
     if (b && b->base) hipMemset(b->base, v, b->size);
@@ -183,6 +246,7 @@ static hipError_t run_mul_mat(wamx_backend * be, const wamx_tensor * node) {
     g.r3 = b->ne[3] / a->ne[3];
     g.ws = be->workspace;
     g.ws_bytes = kWorkspaceBytes;
+    g.w_tiled = tensor_is_tiled(a);
     return launch_gemm(g, be->stream);
 }
 
@@ -209,6 +273,7 @@ static GemmArgs linear_args(wamx_backend * be, const wamx_tensor * node) {
     g.gate = node->src[4] ? (const float *) node->src[4]->data : nullptr;
     g.ws = be->workspace;
     g.ws_bytes = kWorkspaceBytes;
+    g.w_tiled = tensor_is_tiled(w);
     return g;
 }
 
@@ -469,6 +534,12 @@ static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
     }
 }
 
+// A tiled weight multiplies only the few-token activations of the skinny path.
+static bool tiled_product_ok(const wamx_tensor * x) {
+    return (x->type == WAMX_TYPE_BF16 || x->type == WAMX_TYPE_F32) && x->ne[1] <= 64 && x->ne[2] == 1 && x->ne[3] == 1 &&
+           rows_contig(x);
+}
+
 static bool supports(const wamx_tensor * t) {
     auto ok_type = [](const wamx_tensor * x) {
         return x && (x->type == WAMX_TYPE_F32 || x->type == WAMX_TYPE_BF16 || x->type == WAMX_TYPE_F16 ||
@@ -476,6 +547,16 @@ static bool supports(const wamx_tensor * t) {
     };
     const wamx_tensor * s0 = t->src[0];
     const wamx_tensor * s1 = t->src[1];
+    const bool view_op = t->op == WAMX_OP_NONE || t->op == WAMX_OP_VIEW || t->op == WAMX_OP_RESHAPE ||
+                         t->op == WAMX_OP_PERMUTE || t->op == WAMX_OP_TRANSPOSE;
+    // A tiled weight is read only whole, as the weight of MUL_MAT / LINEAR:
+    // any other reader, or a reader of a view of it, would see the tiled order.
+    for (int i = 0; i < WAMX_MAX_SRC && !view_op; ++i) {
+        const wamx_tensor * x = t->src[i];
+        if (!x) continue;
+        if (x->view_src && tensor_is_tiled(x->view_src)) return false;
+        if (tensor_is_tiled(x) && !(i == 0 && (t->op == WAMX_OP_MUL_MAT || t->op == WAMX_OP_LINEAR))) return false;
+    }
     switch (t->op) {
         case WAMX_OP_NONE:
         case WAMX_OP_VIEW:
@@ -508,6 +589,7 @@ static bool supports(const wamx_tensor * t) {
         case WAMX_OP_RMS_NORM:
             return rows_contig(s0) && (t->src[1] ? s0->type == WAMX_TYPE_BF16 : s0->type == WAMX_TYPE_F32);
         case WAMX_OP_MUL_MAT:
+            if (tensor_is_tiled(s0)) return tiled_product_ok(s1);
             return (s0->type == WAMX_TYPE_BF16 || s0->type == WAMX_TYPE_F32) &&
                    (s1->type == WAMX_TYPE_BF16 || s1->type == WAMX_TYPE_F32) && rows_contig(s0) && rows_contig(s1) &&
                    wamx_is_contiguous(t);
@@ -518,8 +600,9 @@ static bool supports(const wamx_tensor * t) {
         case WAMX_OP_UNARY:
             if (t->src[1]) return s0->type == WAMX_TYPE_BF16 && wamx_is_contiguous(s0);
             return ok_type(s0) && t->op_params[0] >= 0 && t->op_params[0] <= 2;
-        case WAMX_OP_IM2COL:
         case WAMX_OP_LINEAR:
+            return !tensor_is_tiled(s0) || tiled_product_ok(s1);  // otherwise validated by the constructor
+        case WAMX_OP_IM2COL:
         case WAMX_OP_QK_NORM_ROPE:
         case WAMX_OP_JOINT_ATTN:
         case WAMX_OP_MODULATION:
@@ -891,6 +974,11 @@ wamx_buffer_type_t wamx_backend_buffer_type(int device) {
 wamx_buffer_type_t wamx_backend_get_default_buffer_type(wamx_backend_t be) {
     return be ? wamx_backend_buffer_type(be->dev->index) : nullptr;
 }
+wamx_buffer_type_t wamx_backend_tiled_buffer_type(int device) {
+    struct wamx_backend_reg * reg = registry();
+    if (device < 0 || device >= (int) reg->tiled_bufts.size()) return nullptr;
+    return &reg->tiled_bufts[device];
+}
 
 wamx_buffer_t wamx_buft_alloc_buffer(wamx_buffer_type_t buft, size_t size) { return buft_alloc_buffer(buft, size); }
 size_t wamx_buft_get_alignment(wamx_buffer_type_t buft) { return buft_get_alignment(buft); }
@@ -915,23 +1003,37 @@ wamx_status wamx_tensor_alloc(wamx_buffer_t buf, wamx_tensor * t, void * addr) {
 wamx_status wamx_backend_tensor_set(wamx_tensor * t, const void * data, size_t offset, size_t size) {
     WAMX_REQUIRE(t && t->data, "tensor_set: tensor not allocated");
     WAMX_REQUIRE(offset + size <= wamx_nbytes(t), "tensor_set: out of range");
+    if (tensor_is_tiled(t)) {
+        WAMX_REQUIRE(offset == 0 && size == wamx_nbytes(t), "tensor_set: a tiled weight is set whole");
+        WAMX_HIP_TRY(tiled_set(t, data));
+        return WAMX_STATUS_SUCCESS;
+    }
     WAMX_HIP_TRY(hipMemcpy((char *) t->data + offset, data, size, hipMemcpyHostToDevice));
     return WAMX_STATUS_SUCCESS;
 }
 wamx_status wamx_backend_tensor_get(const wamx_tensor * t, void * data, size_t offset, size_t size) {
     WAMX_REQUIRE(t && t->data, "tensor_get: tensor not allocated");
     WAMX_REQUIRE(offset + size <= wamx_nbytes(t), "tensor_get: out of range");
+    if (tensor_is_tiled(t)) {
+        WAMX_HIP_TRY(tiled_get(t, data, offset, size));
+        return WAMX_STATUS_SUCCESS;
+    }
     WAMX_HIP_TRY(hipMemcpy(data, (const char *) t->data + offset, size, hipMemcpyDeviceToHost));
     return WAMX_STATUS_SUCCESS;
 }
 wamx_status wamx_backend_tensor_copy(const wamx_tensor * src, wamx_tensor * dst) {
     WAMX_REQUIRE(src && dst && src->data && dst->data, "tensor_copy: unallocated tensor");
     WAMX_REQUIRE(wamx_nbytes(src) == wamx_nbytes(dst), "tensor_copy: size mismatch");
-    WAMX_HIP_TRY(hipMemcpy(dst->data, src->data, wamx_nbytes(src), hipMemcpyDeviceToDevice));
+    WAMX_REQUIRE((!tensor_is_tiled(src) && !tensor_is_tiled(dst)) || wamx_are_same_shape(src, dst),
+                 "tensor_copy: a tiled weight copies to or from a tensor of its shape");
+    WAMX_HIP_TRY(tensor_copy_impl(src, dst));
     return WAMX_STATUS_SUCCESS;
 }
 wamx_status wamx_backend_tensor_memset(wamx_tensor * t, uint8_t value, size_t offset, size_t size) {
     WAMX_REQUIRE(t && t->data && offset + size <= wamx_nbytes(t), "tensor_memset: bad range");
+    // A byte fill is layout-independent only over the whole tiled tensor.
+    WAMX_REQUIRE(!tensor_is_tiled(t) || (offset == 0 && size == wamx_nbytes(t)),
+                 "tensor_memset: a tiled weight is filled whole");
     WAMX_HIP_TRY(hipMemset((char *) t->data + offset, value, size));
     return WAMX_STATUS_SUCCESS;
 }
@@ -991,9 +1093,9 @@ wamx_status wamx_op_mul_mat(wamx_backend_t be, const void * w, int64_t ldw, cons
     WAMX_LAUNCH(launch_gemm(g, be->stream));
 }
 
-wamx_status wamx_op_linear(wamx_backend_t be, const void * w, const void * x, int32_t x_type, const void * bias,
-                           int32_t epilogue, const void * residual, const float * gate, void * y, int64_t M, int64_t N,
-                           int64_t K) {
+static wamx_status op_linear(wamx_backend_t be, const void * w, bool w_tiled, const void * x, int32_t x_type,
+                             const void * bias, int32_t epilogue, const void * residual, const float * gate, void * y,
+                             int64_t M, int64_t N, int64_t K) {
     WAMX_REQUIRE(be && w && x && y && M > 0 && N > 0 && K > 0, "wamx_op_linear: bad arguments");
     WAMX_REQUIRE(epilogue >= WAMX_EPI_NONE && epilogue <= WAMX_EPI_BIAS_RESIDUAL, "wamx_op_linear: epilogue");
     WAMX_REQUIRE(epilogue == WAMX_EPI_NONE || bias, "wamx_op_linear: bias required");
@@ -1017,9 +1119,23 @@ wamx_status wamx_op_linear(wamx_backend_t be, const void * w, const void * x, in
     g.res = residual;
     g.ldres = M;
     g.gate = gate;
+    g.w_tiled = w_tiled;
     g.ws = be->workspace;
     g.ws_bytes = kWorkspaceBytes;
     WAMX_LAUNCH(launch_gemm(g, be->stream));
+}
+
+wamx_status wamx_op_linear(wamx_backend_t be, const void * w, const void * x, int32_t x_type, const void * bias,
+                           int32_t epilogue, const void * residual, const float * gate, void * y, int64_t M, int64_t N,
+                           int64_t K) {
+    return op_linear(be, w, false, x, x_type, bias, epilogue, residual, gate, y, M, N, K);
+}
+
+wamx_status wamx_op_linear_tiled(wamx_backend_t be, const void * w, const void * x, int32_t x_type, const void * bias,
+                                 int32_t epilogue, const void * residual, const float * gate, void * y, int64_t M,
+                                 int64_t N, int64_t K) {
+    WAMX_REQUIRE(M % 16 == 0 && K % 32 == 0 && N <= 64, "wamx_op_linear_tiled: needs M %% 16 == 0, K %% 32 == 0, N <= 64");
+    return op_linear(be, w, true, x, x_type, bias, epilogue, residual, gate, y, M, N, K);
 }
 
 wamx_status wamx_op_norm_modulation_bf16(wamx_backend_t be, const void * x, int64_t ldx, const float * scale,

@@ -16,12 +16,14 @@
 #include <math.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <map>
 #include <memory>
 #include <string>
 #include <vector>
 
 #include "common.h"
+#include "internal.h"
 
 using namespace wamx;
 
@@ -62,6 +64,9 @@ struct wamx_gwp_model {
 
     wamx_context * wctx = nullptr;
     wamx_buffer_t wbuf = nullptr;
+    // The action expert's few-token projections, in the tiled buffer type.
+    wamx_context * tctx = nullptr;
+    wamx_buffer_t tbuf = nullptr;
     std::vector<std::pair<std::string, wamx_tensor *>> weights;
     std::map<std::string, wamx_tensor *> by_name;
 
@@ -98,19 +103,24 @@ struct wamx_gwp_model {
         wamx_free(sctx);
         wamx_buffer_free(wbuf);
         wamx_free(wctx);
+        wamx_buffer_free(tbuf);
+        wamx_free(tctx);
     }
 
-    wamx_tensor * add_weight(const std::string & name, int64_t ne0, int64_t ne1 = 1, int64_t ne2 = 1, int64_t ne3 = 1) {
-        wamx_tensor * t = wamx_new_tensor_4d(wctx, WAMX_TYPE_BF16, ne0, ne1, ne2, ne3);
+    wamx_tensor * add_weight(const std::string & name, int64_t ne0, int64_t ne1 = 1, int64_t ne2 = 1, int64_t ne3 = 1,
+                             bool tiled = false) {
+        wamx_tensor * t = wamx_new_tensor_4d(tiled ? tctx : wctx, WAMX_TYPE_BF16, ne0, ne1, ne2, ne3);
         if (!t) return nullptr;
         wamx_set_name(t, name.c_str());
         weights.push_back({name, t});
         by_name[name] = t;
         return t;
     }
-    // Linear layer [out][in]: ggml ne = {in, out}.
-    void add_linear(const std::string & prefix, int64_t in, int64_t out, wamx_tensor ** w, wamx_tensor ** b) {
-        *w = add_weight(prefix + ".weight", in, out);
+    // Linear layer [out][in]: ggml ne = {in, out}; `tiled` places the weight
+    // in the tiled buffer (products of at most 64 tokens only).
+    void add_linear(const std::string & prefix, int64_t in, int64_t out, wamx_tensor ** w, wamx_tensor ** b,
+                    bool tiled = false) {
+        *w = add_weight(prefix + ".weight", in, out, 1, 1, tiled);
         *b = add_weight(prefix + ".bias", out);
     }
 };
@@ -238,7 +248,8 @@ static bool create_weights(wamx_gwp_model * m) {
     const int64_t d = (int64_t) c.n_heads * c.head_dim, da = c.action_hidden, E = c.enc_hidden, A = c.action_dim;
     const int64_t L = c.n_layers;
     m->wctx = wamx_init(64 * L + 256);
-    if (!m->wctx) return false;
+    m->tctx = wamx_init(8 * L + 16);
+    if (!m->wctx || !m->tctx) return false;
     m->patch_w = m->add_weight("gwp.patch_embedding.weight", 2, 2, c.z_dim, d);
     m->patch_b = m->add_weight("gwp.patch_embedding.bias", d);
     auto mlp = [&](const std::string & p, int64_t in, int64_t out, Mlp3 & r) {
@@ -262,33 +273,41 @@ static bool create_weights(wamx_gwp_model * m) {
     // Per-layer scale_shift_table [6][width] of each expert, packed [width, 6, L].
     m->a_tables = m->add_weight("gwp.blocks.action_expert.scale_shift_table", da, 6, L);
     m->v_tables = m->add_weight("gwp.blocks.visual_expert.scale_shift_table", d, 6, L);
-    auto expert = [&](const std::string & p, int64_t w, int64_t ffn, ExpertLayer & e) {
-        m->add_linear(p + ".attn1.to_qkv", w, 3 * d, &e.qkv_w, &e.qkv_b);
+    // The action expert's projections run on 48 denoise tokens (and the 1
+    // state token of the prefix) and use the tiled layout; its cross-attention
+    // K/V projections run on the 512 prompt tokens and stay row-major.
+    auto expert = [&](const std::string & p, int64_t w, int64_t ffn, ExpertLayer & e, bool t) {
+        m->add_linear(p + ".attn1.to_qkv", w, 3 * d, &e.qkv_w, &e.qkv_b, t);
         e.norm_q = m->add_weight(p + ".attn1.norm_q.weight", d);
         e.norm_k = m->add_weight(p + ".attn1.norm_k.weight", d);
-        m->add_linear(p + ".attn1.to_out.0", d, w, &e.o_w, &e.o_b);
+        m->add_linear(p + ".attn1.to_out.0", d, w, &e.o_w, &e.o_b, t);
         e.n2_w = m->add_weight(p + ".norm2.weight", w);
         e.n2_b = m->add_weight(p + ".norm2.bias", w);
-        m->add_linear(p + ".attn2.to_q", w, d, &e.cq_w, &e.cq_b);
+        m->add_linear(p + ".attn2.to_q", w, d, &e.cq_w, &e.cq_b, t);
         m->add_linear(p + ".attn2.to_k", w, d, &e.ck_w, &e.ck_b);
         m->add_linear(p + ".attn2.to_v", w, d, &e.cv_w, &e.cv_b);
         e.cnq = m->add_weight(p + ".attn2.norm_q.weight", d);
         e.cnk = m->add_weight(p + ".attn2.norm_k.weight", d);
-        m->add_linear(p + ".attn2.to_out.0", d, w, &e.co_w, &e.co_b);
-        m->add_linear(p + ".ffn.net.0.proj", w, ffn, &e.up_w, &e.up_b);
-        m->add_linear(p + ".ffn.net.2", ffn, w, &e.dn_w, &e.dn_b);
+        m->add_linear(p + ".attn2.to_out.0", d, w, &e.co_w, &e.co_b, t);
+        m->add_linear(p + ".ffn.net.0.proj", w, ffn, &e.up_w, &e.up_b, t);
+        m->add_linear(p + ".ffn.net.2", ffn, w, &e.dn_w, &e.dn_b, t);
     };
     m->act.resize(L);
     m->vis.resize(L);
     for (int64_t l = 0; l < L; ++l) {
         const std::string b = "gwp.blocks." + std::to_string(l);
-        expert(b + ".action_expert", da, c.action_ffn_dim, m->act[l]);
-        expert(b + ".visual_expert", d, c.ffn_dim, m->vis[l]);
+        expert(b + ".action_expert", da, c.action_ffn_dim, m->act[l], true);
+        expert(b + ".visual_expert", d, c.ffn_dim, m->vis[l], false);
     }
     for (auto & kv : m->weights)
         if (!kv.second) return false;
     m->wbuf = wamx_backend_alloc_ctx_tensors(m->wctx, m->be);
-    return m->wbuf != nullptr;
+    // The tiled buffer type of the backend's device.
+    wamx_buffer_type_t tb = nullptr;
+    for (int i = 0; i < wamx_get_device_count(); ++i)
+        if (wamx_backend_buffer_type(i) == wamx_backend_get_default_buffer_type(m->be)) tb = wamx_backend_tiled_buffer_type(i);
+    m->tbuf = tb ? wamx_backend_alloc_ctx_tensors_from_buft(m->tctx, tb) : nullptr;
+    return m->wbuf != nullptr && m->tbuf != nullptr;
 }
 
 static bool create_storage(wamx_gwp_model * m) {
@@ -602,6 +621,14 @@ uint64_t wamx_gwp_param_count(wamx_gwp_t m) {
 
 wamx_status wamx_gwp_init_synthetic(wamx_gwp_t m, uint64_t seed, float wstd) {
     WAMX_REQUIRE(m, "wamx_gwp_init_synthetic: null model");
+    // Tiled weights are generated row-major into a staging buffer and then
+    // written in their layout, so every weight holds the same values as the
+    // row-major fill of the same seed.
+    size_t stage_bytes = 0;
+    for (auto & kv : m->weights)
+        if (tensor_is_tiled(kv.second)) stage_bytes = std::max(stage_bytes, wamx_nbytes(kv.second));
+    void * stage = stage_bytes ? wamx_device_malloc(m->be, stage_bytes) : nullptr;
+    WAMX_REQUIRE(!stage_bytes || stage, "wamx_gwp_init_synthetic: staging allocation failed");
     for (auto & kv : m->weights) {
         const std::string & n = kv.first;
         float mean = 0.0f, sd = wstd;
@@ -617,11 +644,22 @@ wamx_status wamx_gwp_init_synthetic(wamx_gwp_t m, uint64_t seed, float wstd) {
         } else if (n.find("scale_shift_table") != std::string::npos) {
             sd = 0.1f;
         }
-        const wamx_status st = wamx_fill_normal(m->be, kv.second->data, WAMX_TYPE_BF16, wamx_nelements(kv.second),
-                                                seed ^ fnv1a(n), mean, sd);
-        if (st != WAMX_STATUS_SUCCESS) return st;
+        const bool tiled = tensor_is_tiled(kv.second);
+        wamx_status st = wamx_fill_normal(m->be, tiled ? stage : kv.second->data, WAMX_TYPE_BF16,
+                                          wamx_nelements(kv.second), seed ^ fnv1a(n), mean, sd);
+        if (st == WAMX_STATUS_SUCCESS && tiled &&
+            tensor_set_from_device(kv.second, stage, (hipStream_t) wamx_backend_stream(m->be)) != hipSuccess) {
+            set_errorf("wamx_gwp_init_synthetic: tiling %s failed", n.c_str());
+            st = WAMX_STATUS_FAILED;
+        }
+        if (st != WAMX_STATUS_SUCCESS) {
+            wamx_backend_synchronize(m->be);
+            if (stage) wamx_device_free(m->be, stage);
+            return st;
+        }
     }
     wamx_backend_synchronize(m->be);
+    if (stage) wamx_device_free(m->be, stage);
     return WAMX_STATUS_SUCCESS;
 }
 

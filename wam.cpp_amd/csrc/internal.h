@@ -35,9 +35,17 @@ struct GemmArgs {
     const float * gate = nullptr;            // f32 [M]
     void * ws = nullptr;                     // K-split partials of the skinny path
     size_t ws_bytes = 0;
+    bool w_tiled = false;                    // w in the MFMA-tiled layout (launch_tile_weights)
 };
 
 hipError_t launch_gemm(const GemmArgs & a, hipStream_t s);
+// Row-major bf16 [M][K] <-> the MFMA-tiled weight layout of the tiled buffer
+// type ([M/16][K/32] tiles of 1 KB; M % 16 == 0, K % 32 == 0).
+hipError_t launch_tile_weights(const void * src, void * dst, int64_t M, int64_t K, bool untile, hipStream_t s);
+// Whether t is a weight stored in the tiled layout (placed in a tiled buffer).
+bool tensor_is_tiled(const wamx_tensor * t);
+// Writes the row-major device array src into t, tiling it when t is tiled.
+hipError_t tensor_set_from_device(wamx_tensor * t, const void * src, hipStream_t s);
 // Workspace the skinny path needs for an M x N x K product (0 when unsplit).
 size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K);
 

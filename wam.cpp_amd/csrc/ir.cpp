@@ -743,7 +743,13 @@ static const struct {
 // non-view tensor of the context; views then alias their sources.
 wamx_buffer_t wamx_backend_alloc_ctx_tensors(wamx_context * ctx, wamx_backend_t be) {
     if (!ctx || !be) return nullptr;
-    wamx_buffer_type_t buft = wamx_backend_get_default_buffer_type(be);
+    return wamx_backend_alloc_ctx_tensors_from_buft(ctx, wamx_backend_get_default_buffer_type(be));
+}
+
+// ggml_backend_alloc_ctx_tensors_from_buft; every placed tensor goes through
+// the buffer's init_tensor (which marks weights of a tiled buffer).
+wamx_buffer_t wamx_backend_alloc_ctx_tensors_from_buft(wamx_context * ctx, wamx_buffer_type_t buft) {
+    if (!ctx || !buft) return nullptr;
     const size_t align = wamx_buft_get_alignment(buft);
     size_t total = 0;
     for (auto & t : ctx->tensors)
@@ -753,10 +759,12 @@ wamx_buffer_t wamx_backend_alloc_ctx_tensors(wamx_context * ctx, wamx_backend_t 
     if (!buf) return nullptr;
     char * base = (char *) wamx_buffer_get_base(buf);
     size_t off = 0;
+    const wamx_buffer_i * bi = wamx_buffer_iface();
     for (auto & t : ctx->tensors) {
         if (t->data || t->view_src) continue;
         t->data = base + off;
         t->buffer = buf;
+        bi->init_tensor(buf, t.get());
         off += (wamx_nbytes(t.get()) + align - 1) / align * align;
     }
     for (auto & t : ctx->tensors) {

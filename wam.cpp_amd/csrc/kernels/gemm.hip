@@ -664,6 +664,62 @@ constexpr int kSkinnyDepth = 2;                            // weight prefetch de
 constexpr int kSkinnyMaxKs = 1024;                         // longest K slice (LDS permitting)
 constexpr size_t kSkinnyLdsMax = 160 * 1024;
 
+// Stages x[0..N)[kb..kb+klen) as bf16 in LDS rows of ks + 8 elements (rows
+// past N and columns past klen are zero).  Addresses are clamped into the
+// tensor and the values masked, so every load of a batch is issued before the
+// first LDS store.  `prologue` (the weight prefetch) runs after the first
+// batch is issued: loads complete in order, so activations queued behind the
+// weight stream would wait for it.
+template <bool XF32, typename Prologue>
+__device__ __forceinline__ void skinny_stage_x(const GemmParams & p, uint16_t * xs, int rows, int ks, int64_t kb,
+                                               int klen, Prologue && prologue) {
+    const int tid = threadIdx.x, pitch = ks + 8;
+    const int cpr = ks / 8, total = rows * cpr;
+    constexpr int kStageBatch = 8, kThreads = kSkinnyWaves * 64;
+    for (int c0 = 0; c0 < total; c0 += kStageBatch * kThreads) {
+        uint4 v[kStageBatch];
+#pragma unroll
+        for (int u = 0; u < kStageBatch; ++u) {
+            const int c = min(c0 + u * kThreads + tid, total - 1);
+            const int r = c / cpr, kc = c % cpr;
+            const bool ok = r < p.N && kc * 8 < klen;
+            const int64_t idx = (int64_t) min(r, (int) p.N - 1) * p.ldx + kb + min(kc * 8, klen - 8);
+            const uint4 x = load_x8<XF32>(p.x, idx);
+            v[u] = ok ? x : make_uint4(0, 0, 0, 0);
+        }
+        if (c0 == 0) prologue();
+#pragma unroll
+        for (int u = 0; u < kStageBatch; ++u) {
+            const int c = c0 + u * kThreads + tid;
+            if (c < total) *(uint4 *) (xs + (c / cpr) * pitch + (c % cpr) * 8) = v[u];
+        }
+    }
+    __syncthreads();
+}
+
+// 16x16 fragments -> fp32 partials of K slice blockIdx.y, or (part ==
+// nullptr, a single slice) the epilogue.  Lane holds feature mrow[rg] (column
+// lane & 15), register r holds token 16t + 4*(lane/16) + r.
+template <int RG, int NT>
+__device__ __forceinline__ void skinny_store(const GemmParams & p, float * part, const f32x4_t (&acc)[RG][NT],
+                                             const int64_t (&mrow)[RG], const bool (&mok)[RG], int lane) {
+    const int64_t N = p.N, M = p.M;
+    float * pp = part ? part + (int64_t) blockIdx.y * N * M : nullptr;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+        if (!mok[rg]) continue;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t n = 16 * t + 4 * (lane >> 4) + r;
+                if (n >= N) continue;
+                if (pp) pp[n * M + mrow[rg]] = acc[rg][t][r];
+                else store_out(p, p.y, p.res, n, mrow[rg], acc[rg][t][r]);
+            }
+    }
+}
+
 template <bool XF32, int NT, int DEPTH = kSkinnyDepth>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams p, float * part, int ks) {
     constexpr int RG = kSkinnyRows / 16;             // 16-row MFMA groups per wave
@@ -671,7 +727,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
     extern __shared__ __align__(16) uint16_t xs[];  // [16*NT][ks + 8], then per-wave weight tiles
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r16 = lane & 15;
-    const int64_t N = p.N, M = p.M, K = p.K;
+    const int64_t M = p.M, K = p.K;
     const int pitch = ks + 8;
     const int64_t m0 = (int64_t) blockIdx.x * kSkinnyFeat + (int64_t) wave * kSkinnyRows;
     const int64_t kb = (int64_t) blockIdx.y * ks;
@@ -691,50 +747,19 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
     for (int c = 0; c < LI; ++c) wbase[c] = p.w + min(m0 + 4 * c + lrow, M - 1) * p.ldw + kb;
     const int nsteps = (klen + 127) / 128;
     uint4 wbuf[DEPTH][LI];
+    // The loads only fill registers; the K-tail mask is applied where the
+    // values are consumed (any use of a loaded register right after the load
+    // would make the wave wait for it and serialise the prefetch).
     auto wload = [&](int st, uint4 (&d)[LI]) {
         const int k = st * 128 + 8 * lchunk;
-        const bool kin = k < klen;
-        const int kc = kin ? k : klen - 8;
-        const uint32_t mask = kin ? 0xffffffffu : 0u;
+        const int kc = k < klen ? k : klen - 8;
 #pragma unroll
-        for (int c = 0; c < LI; ++c) {
-            uint4 v = *(const uint4 *) (wbase[c] + kc);
-            v.x &= mask;
-            v.y &= mask;
-            v.z &= mask;
-            v.w &= mask;
-            d[c] = v;
-        }
+        for (int c = 0; c < LI; ++c) d[c] = *(const uint4 *) (wbase[c] + kc);
     };
-    // Stage x[0..N)[kb..ke) as bf16 (rows past N and columns past ke are zero).
-    // Addresses are clamped into the tensor and the values masked, so every
-    // load of a batch is issued before the first LDS store.  The first batch
-    // is issued before the weight prefetch: loads complete in order, so
-    // activations queued behind the weight stream would wait for it.
-    const int cpr = ks / 8, total = 16 * NT * cpr;
-    constexpr int kStageBatch = 8;
-    for (int c0 = 0; c0 < total; c0 += kStageBatch * kSkinnyWaves * 64) {
-        uint4 v[kStageBatch];
+    skinny_stage_x<XF32>(p, xs, 16 * NT, ks, kb, klen, [&]() {
 #pragma unroll
-        for (int u = 0; u < kStageBatch; ++u) {
-            const int c = min(c0 + u * kSkinnyWaves * 64 + tid, total - 1);
-            const int r = c / cpr, kc = c % cpr;
-            const bool ok = r < N && kc * 8 < klen;
-            const int64_t idx = (int64_t) min(r, (int) N - 1) * p.ldx + kb + min(kc * 8, klen - 8);
-            const uint4 x = load_x8<XF32>(p.x, idx);
-            v[u] = ok ? x : make_uint4(0, 0, 0, 0);
-        }
-        if (c0 == 0) {
-#pragma unroll
-            for (int i = 0; i < DEPTH; ++i) wload(min(i, nsteps - 1), wbuf[i]);
-        }
-#pragma unroll
-        for (int u = 0; u < kStageBatch; ++u) {
-            const int c = c0 + u * kSkinnyWaves * 64 + tid;
-            if (c < total) *(uint4 *) (xs + (c / cpr) * pitch + (c % cpr) * 8) = v[u];
-        }
-    }
-    __syncthreads();
+        for (int i = 0; i < DEPTH; ++i) wload(min(i, nsteps - 1), wbuf[i]);
+    });
 
     f32x4_t acc[RG][NT];
 #pragma unroll
@@ -747,11 +772,15 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
         for (int i = 0; i < DEPTH; ++i) {
             const int st = st0 + i;
             if (st < nsteps) {
-                // registers -> wave tile (row 4c + lrow, chunk lchunk)
+                // registers -> wave tile (row 4c + lrow, chunk lchunk); columns
+                // past the slice are zeroed here.
+                const uint32_t mask = st * 128 + 8 * lchunk < klen ? 0xffffffffu : 0u;
 #pragma unroll
                 for (int c = 0; c < LI; ++c) {
                     const int r = 4 * c + lrow;
-                    *(uint4 *) (wt + r * 128 + ((lchunk ^ (r & 15)) << 3)) = wbuf[i][c];
+                    const uint4 v = wbuf[i][c];
+                    *(uint4 *) (wt + r * 128 + ((lchunk ^ (r & 15)) << 3)) =
+                        make_uint4(v.x & mask, v.y & mask, v.z & mask, v.w & mask);
                 }
                 // MFMA chunk q: lane holds row r16 of group rg, columns 32q + 8g .. +8
 #pragma unroll
@@ -770,28 +799,107 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_part(GemmParams
                             acc[rg][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[t], wa[rg], acc[rg][t], 0, 0, 0);
                 }
             }
-            if (st + DEPTH < nsteps) wload(st + DEPTH, wbuf[i]);
+            // Refilled on every pass (past the end with the last step again, an
+            // L2 hit), so every path issues the same loads and the wait before
+            // a slot's use counts only the younger slots' loads.
+            wload(min(st + DEPTH, nsteps - 1), wbuf[i]);
         }
     }
-
-    // 16x16 fragment: lane holds column (lane & 15) = feature, register r
-    // holds row 4*(lane/16) + r = token within the tile.
-    // part == nullptr: a single K slice applies the epilogue directly.
-    float * pp = part ? part + (int64_t) blockIdx.y * N * M : nullptr;
+    int64_t mrow[RG];
+    bool mok[RG];
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
-        const int64_t mrow = m0 + 16 * rg + r16;
-        if (mrow >= M) continue;
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t n = 16 * t + 4 * g + r;
-                if (n >= N) continue;
-                if (pp) pp[n * M + mrow] = acc[rg][t][r];
-                else store_out(p, p.y, p.res, n, mrow, acc[rg][t][r]);
-            }
+        mrow[rg] = m0 + 16 * rg + r16;
+        mok[rg] = mrow[rg] < M;
     }
+    skinny_store<RG, NT>(p, part, acc, mrow, mok, lane);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA-tiled weights (the tiled buffer type): [M/16][K/32] tiles of 1 KB; in
+// tile (gr, q) lane l's 16 bytes are w[16 gr + (l & 15)][32 q + 8 (l >> 4) ..
+// +8], which is the B-operand fragment of MFMA 16x16x32 for 16 features and
+// 32 k.  One wave load instruction reads one tile (1 KB contiguous) straight
+// into MFMA registers; a 16-row group streams along K contiguously.
+// ---------------------------------------------------------------------------
+__global__ void tile_weights_kernel(const uint16_t * __restrict__ src, uint16_t * __restrict__ dst, int64_t M,
+                                    int64_t K, int untile) {
+    const int64_t chunk = (int64_t) blockIdx.x * 256 + threadIdx.x;  // 16-byte chunk of the tiled layout
+    if (chunk >= M * K / 8) return;
+    const int64_t tile = chunk >> 6, kt = K / 32;
+    const int l = (int) (chunk & 63);
+    const int64_t row = 16 * (tile / kt) + (l & 15), k = 32 * (tile % kt) + 8 * (l >> 4);
+    if (untile) *(uint4 *) (dst + row * K + k) = *(const uint4 *) (src + chunk * 8);
+    else *(uint4 *) (dst + chunk * 8) = *(const uint4 *) (src + row * K + k);
+}
+
+hipError_t launch_tile_weights(const void * src, void * dst, int64_t M, int64_t K, bool untile, hipStream_t s) {
+    if (M <= 0 || K <= 0) return hipSuccess;
+    if (M % 16 != 0 || K % 32 != 0 || (((uintptr_t) src | (uintptr_t) dst) & 15)) return hipErrorInvalidValue;
+    const int64_t chunks = M * K / 8;
+    hipLaunchKernelGGL(tile_weights_kernel, dim3((unsigned) ((chunks + 255) / 256)), dim3(256), 0, s,
+                       (const uint16_t *) src, (uint16_t *) dst, M, K, untile ? 1 : 0);
+    return hipGetLastError();
+}
+
+// gemm_skinny_part on tiled weights: each of the 8 waves owns one 16-row
+// group (a workgroup covers 128 features), streams its tiles DEPTH steps ahead
+// and feeds them to the MFMAs as loaded, with no LDS on the weight path.  The
+// accumulation order over K is that of gemm_skinny_part, so both give the same
+// bits.  K % 32 == 0 and M % 16 == 0 (the tiled layout's conditions).
+constexpr int kTiledFeat = 16 * kSkinnyWaves;
+
+template <bool XF32, int NT, int DEPTH = kSkinnyDepth>
+__global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_tiled(GemmParams p, float * part, int ks) {
+    extern __shared__ __align__(16) uint16_t xs[];  // [16*NT][ks + 8]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int64_t M = p.M, K = p.K;
+    const int pitch = ks + 8;
+    const int64_t ngrp = M / 16, kt = K / 32;
+    const int64_t grp = (int64_t) blockIdx.x * kSkinnyWaves + wave;
+    const int64_t kb = (int64_t) blockIdx.y * ks;
+    const int klen = (int) (min(K, kb + ks) - kb);
+    const int nsteps = (klen + 127) / 128, ntiles = klen / 32;
+    const uint16_t * wrow = p.w + (min(grp, ngrp - 1) * kt + kb / 32) * 512 + lane * 8;
+    uint4 wbuf[DEPTH][4];
+    auto wload = [&](int st, uint4 (&d)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) d[q] = *(const uint4 *) (wrow + (int64_t) min(st * 4 + q, ntiles - 1) * 512);
+    };
+    skinny_stage_x<XF32>(p, xs, 16 * NT, ks, kb, klen, [&]() {
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) wload(min(i, nsteps - 1), wbuf[i]);
+    });
+
+    f32x4_t acc[1][NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[0][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint16_t * xrow = xs + r16 * pitch + 8 * g;
+    for (int st0 = 0; st0 < nsteps; st0 += DEPTH) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) {
+            const int st = st0 + i;
+            if (st < nsteps) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (st * 4 + q >= ntiles) continue;  // K tail: the 32-column chunk is past the slice
+                    bf16x8_t xa[NT];
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+                        xa[t] = *(const bf16x8_t *) (xrow + 16 * t * pitch + st * 128 + 32 * q);
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+                        acc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            xa[t], __builtin_bit_cast(bf16x8_t, wbuf[i][q]), acc[0][t], 0, 0, 0);
+                }
+            }
+            wload(min(st + DEPTH, nsteps - 1), wbuf[i]);
+        }
+    }
+    const int64_t mrow[1] = {16 * grp + r16};
+    const bool mok[1] = {grp < ngrp};
+    skinny_store<1, NT>(p, part, acc, mrow, mok, lane);
 }
 
 // LDS bytes of gemm_skinny_part: activation slice + the waves' weight tiles.
@@ -979,11 +1087,50 @@ size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K) {
 
 // gemm_skinny_part over `splits` K slices of ks columns; part == nullptr
 // (single slice only) applies the epilogue in the part kernel.
-static void launch_skinny_part(const GemmParams & p, bool xf32, float * part, int splits, int ks, hipStream_t s) {
+// K slices of the tiled kernel (128 features per workgroup): the shortest of
+// 384..1536 that keeps the grid within about two workgroups per CU (measured
+// on the 48-token shapes: 384 for 3072 x 3072, 512 for QKV, 768 for the FFN).
+static void skinny_tiled_plan(int64_t M, int64_t N, int64_t K, int & splits, int & ks) {
+    const int64_t nfb = (M / 16 + kSkinnyWaves - 1) / kSkinnyWaves;
+    const int nt = (int) ((N + 15) / 16);
+    static const int kSlices[] = {384, 512, 768, 1024, 1536};
+    splits = (int) ((K + 383) / 384);
+    ks = 384;
+    for (int c : kSlices) {
+        if ((size_t) 16 * nt * (c + 8) * sizeof(uint16_t) > kSkinnyLdsMax) break;
+        ks = c;
+        splits = (int) ((K + c - 1) / c);
+        if (nfb * splits <= 480 || c >= K) break;
+    }
+}
+
+static void skinny_plan_for(const GemmParams & p, bool tiled, int & splits, int & ks) {
+    if (tiled) skinny_tiled_plan(p.M, p.N, p.K, splits, ks);
+    else skinny_plan(p.M, p.N, p.K, splits, ks);
+}
+
+// gemm_skinny_part (or gemm_skinny_tiled) over `splits` K slices of ks
+// columns; part == nullptr (single slice only) applies the epilogue in the
+// part kernel.
+static void launch_skinny_part(const GemmParams & p, bool xf32, bool tiled, float * part, int splits, int ks,
+                               hipStream_t s) {
     const int nt = (int) ((p.N + 15) / 16);
+    const dim3 block(kSkinnyWaves * 64);
+    if (tiled) {
+        const size_t lds = (size_t) 16 * nt * (ks + 8) * sizeof(uint16_t);
+        const dim3 grid((unsigned) ((p.M / 16 + kSkinnyWaves - 1) / kSkinnyWaves), (unsigned) splits);
+#define WAMX_TILED(XF, NT) hipLaunchKernelGGL((gemm_skinny_tiled<XF, NT>), grid, block, lds, s, p, part, ks)
+        switch (nt) {
+            case 1: if (xf32) WAMX_TILED(true, 1); else WAMX_TILED(false, 1); break;
+            case 2: if (xf32) WAMX_TILED(true, 2); else WAMX_TILED(false, 2); break;
+            case 3: if (xf32) WAMX_TILED(true, 3); else WAMX_TILED(false, 3); break;
+            default: if (xf32) WAMX_TILED(true, 4); else WAMX_TILED(false, 4); break;
+        }
+#undef WAMX_TILED
+        return;
+    }
     const size_t lds = skinny_lds_bytes(nt, ks);
     const dim3 grid((unsigned) ((p.M + kSkinnyFeat - 1) / kSkinnyFeat), (unsigned) splits);
-    const dim3 block(kSkinnyWaves * 64);
 #define WAMX_SKINNY(XF, NT) hipLaunchKernelGGL((gemm_skinny_part<XF, NT>), grid, block, lds, s, p, part, ks)
     switch (nt) {
         case 1: if (xf32) WAMX_SKINNY(true, 1); else WAMX_SKINNY(false, 1); break;
@@ -994,14 +1141,13 @@ static void launch_skinny_part(const GemmParams & p, bool xf32, float * part, in
 #undef WAMX_SKINNY
 }
 
-template <bool XF32>
-static hipError_t run_skinny(const GemmParams & p, void * ws, size_t ws_bytes, hipStream_t s) {
+static hipError_t run_skinny(const GemmParams & p, bool xf32, bool tiled, void * ws, size_t ws_bytes, hipStream_t s) {
     int splits, ks;
-    skinny_plan(p.M, p.N, p.K, splits, ks);
+    skinny_plan_for(p, tiled, splits, ks);
     if (splits > 1 && (!ws || (size_t) splits * p.N * p.M * sizeof(float) > ws_bytes || ((uintptr_t) ws & 15)))
         return hipErrorInvalidValue;
     float * part = splits > 1 ? (float *) ws : nullptr;
-    launch_skinny_part(p, XF32, part, splits, ks, s);
+    launch_skinny_part(p, xf32, tiled, part, splits, ks, s);
     if (splits > 1) {
         const int64_t total = p.N * p.M;
         if (p.M % 4 == 0)
@@ -1118,6 +1264,10 @@ static void allow_skinny_lds() {
                         allow_lds(gemm_skinny_part<true, 2>, kMaxLds), allow_lds(gemm_skinny_part<false, 2>, kMaxLds),
                         allow_lds(gemm_skinny_part<true, 3>, kMaxLds), allow_lds(gemm_skinny_part<false, 3>, kMaxLds),
                         allow_lds(gemm_skinny_part<true, 4>, kMaxLds), allow_lds(gemm_skinny_part<false, 4>, kMaxLds),
+                        allow_lds(gemm_skinny_tiled<true, 1>, kMaxLds), allow_lds(gemm_skinny_tiled<false, 1>, kMaxLds),
+                        allow_lds(gemm_skinny_tiled<true, 2>, kMaxLds), allow_lds(gemm_skinny_tiled<false, 2>, kMaxLds),
+                        allow_lds(gemm_skinny_tiled<true, 3>, kMaxLds), allow_lds(gemm_skinny_tiled<false, 3>, kMaxLds),
+                        allow_lds(gemm_skinny_tiled<true, 4>, kMaxLds), allow_lds(gemm_skinny_tiled<false, 4>, kMaxLds),
                         true);
     (void) once;
 }
@@ -1136,8 +1286,9 @@ hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStre
         a.y_type != WAMX_TYPE_BF16 || a.B2 * a.B3 != 1 || a.N <= 0 || a.N > 64 || a.M <= 0 || a.K <= 0 ||
         !vec_operands(a) || !p.vec_out || E == kEpiF32 || !a.ws || !aligned16(a.ws))
         return hipErrorNotSupported;
+    if (a.w_tiled && (p.M % 16 != 0 || p.K % 32 != 0)) return hipErrorNotSupported;
     int splits, ks;
-    skinny_plan(p.M, p.N, p.K, splits, ks);
+    skinny_plan_for(p, a.w_tiled, splits, ks);
     if ((size_t) splits * p.N * p.M * sizeof(float) > a.ws_bytes) return hipErrorNotSupported;
 
     // The row op: one thread per 8-column chunk, the whole row (or segment)
@@ -1201,7 +1352,7 @@ hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStre
 
     allow_skinny_lds();
     const float * part = (const float *) a.ws;
-    launch_skinny_part(p, a.x_type == WAMX_TYPE_F32, (float *) a.ws, splits, ks, s);
+    launch_skinny_part(p, a.x_type == WAMX_TYPE_F32, a.w_tiled, (float *) a.ws, splits, ks, s);
     const dim3 grid((unsigned) p.N, (unsigned) nseg), block((unsigned) nchunk);
 #define WAMX_ROW(EK, PK) hipLaunchKernelGGL((skinny_reduce_row<EK, PK>), grid, block, 0, s, p, part, splits, d)
 #define WAMX_ROW_NORM(EK)                                                   \
@@ -1243,9 +1394,12 @@ hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
     const bool xf32 = a.x_type == WAMX_TYPE_F32;
     const bool vec = vec_operands(a);
 
+    // Tiled weights exist for the few-token products only.
+    if (a.w_tiled && (!vec || batches != 1 || a.N > 64 || a.M % 16 != 0 || a.K % 32 != 0))
+        return hipErrorNotSupported;
     if (vec && batches == 1 && a.N <= 64) {
         allow_skinny_lds();
-        return xf32 ? run_skinny<true>(p, a.ws, a.ws_bytes, s) : run_skinny<false>(p, a.ws, a.ws_bytes, s);
+        return run_skinny(p, xf32, a.w_tiled, a.ws, a.ws_bytes, s);
     }
     if (vec && !xf32 && batches == 1) {
         hipError_t err = hipSuccess;

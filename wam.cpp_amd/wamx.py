@@ -95,6 +95,7 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_memcpy_d2h": (C.c_int, [vp, vp, vp, sz]),
         "wamx_op_mul_mat": (C.c_int, [vp, vp, i64, vp, i32, i64, vp, i32, i64, i64, i64, i64]),
         "wamx_op_linear": (C.c_int, [vp, vp, vp, i32, vp, i32, vp, vp, vp, i64, i64, i64]),
+        "wamx_op_linear_tiled": (C.c_int, [vp, vp, vp, i32, vp, i32, vp, vp, vp, i64, i64, i64]),
         "wamx_op_norm_modulation_bf16": (C.c_int, [vp, vp, i64, vp, vp, i64, vp, i64, i64, f32]),
         "wamx_op_layer_norm_bf16": (C.c_int, [vp, vp, i64, vp, vp, vp, i64, i64, f32]),
         "wamx_op_rms_norm_bf16_f32": (C.c_int, [vp, vp, i64, vp, vp, i64, i64, f32]),
@@ -172,6 +173,9 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_backend_supports_op": (C.c_bool, [vp, TensorP]),
         "wamx_backend_graph_compute": (C.c_int, [vp, vp]),
         "wamx_backend_alloc_ctx_tensors": (vp, [vp, vp]),
+        "wamx_backend_alloc_ctx_tensors_from_buft": (vp, [vp, vp]),
+        "wamx_backend_tiled_buffer_type": (vp, [C.c_int]),
+        "wamx_backend_buffer_type": (vp, [C.c_int]),
         "wamx_buffer_free": (None, [vp]),
         "wamx_gallocr_new": (vp, [vp]),
         "wamx_gallocr_alloc_graph": (C.c_bool, [vp, vp]),
@@ -179,6 +183,8 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_gallocr_free": (None, [vp]),
         "wamx_backend_tensor_set": (C.c_int, [TensorP, vp, sz, sz]),
         "wamx_backend_tensor_get": (C.c_int, [TensorP, vp, sz, sz]),
+        "wamx_backend_tensor_copy": (C.c_int, [TensorP, TensorP]),
+        "wamx_backend_tensor_memset": (C.c_int, [TensorP, C.c_uint8, sz, sz]),
         "wamx_ggml_op_count": (C.c_int, []),
         "wamx_ggml_op_name": (C.c_char_p, [C.c_int]),
         "wamx_ggml_op_to_wamx": (i32, [C.c_int]),
