@@ -72,6 +72,10 @@ struct wamx_gwp_model {
 
     wamx_tensor *patch_w = nullptr, *patch_b = nullptr, *action_sst = nullptr;
     wamx_tensor *a_tables = nullptr, *v_tables = nullptr;  // [d, 6, L] bf16
+    // Cross-attention K/V projections of every layer, per expert (0 action,
+    // 1 visual): weight [w, 2·L·d] and bias [2·L·d]; layer l's to_k rows start
+    // at 2l·d and its to_v rows at (2l+1)·d.  The per-layer weights are views.
+    wamx_tensor *kv_w[2] = {nullptr, nullptr}, *kv_b[2] = {nullptr, nullptr};
     Mlp3 state_enc{}, action_enc{}, action_dec{};
     Cond acond{}, vcond{};
     std::vector<ExpertLayer> act, vis;
@@ -122,6 +126,18 @@ struct wamx_gwp_model {
                     bool tiled = false) {
         *w = add_weight(prefix + ".weight", in, out, 1, 1, tiled);
         *b = add_weight(prefix + ".bias", out);
+    }
+    // A linear layer whose weight rows [row0, row0+out) and bias entries live
+    // inside the packed tensors `pw` [in, R] and `pb` [R].
+    void add_linear_view(const std::string & prefix, wamx_tensor * pw, wamx_tensor * pb, int64_t row0, int64_t out,
+                         wamx_tensor ** w, wamx_tensor ** b) {
+        *w = wamx_view_2d(wctx, pw, pw->ne[0], out, pw->nb[1], (size_t) row0 * pw->nb[1]);
+        *b = wamx_view_1d(wctx, pb, out, (size_t) row0 * pb->nb[0]);
+        for (auto & [name, t] : {std::pair<std::string, wamx_tensor *>{prefix + ".weight", *w}, {prefix + ".bias", *b}}) {
+            if (t) wamx_set_name(t, name.c_str());
+            weights.push_back({name, t});
+            by_name[name] = t;
+        }
     }
 };
 
@@ -204,19 +220,20 @@ struct Builder {
     }
 
     // expert_cross_ffn against uncached text (build_attention, text_encoder.cpp:26-73).
-    wamx_tensor * cross_ffn_uncached(const ExpertLayer & e, wamx_tensor * h, wamx_tensor * txt, wamx_tensor * cshift,
-                                     wamx_tensor * cscale, wamx_tensor * cgate) {
-        const int64_t T = h->ne[1], NL = txt->ne[1];
+    // `kv` is the packed K/V projection of the text for every layer
+    // [2·L·d, NL]; layer l's K columns start at 2l·d, its V columns at (2l+1)·d.
+    wamx_tensor * cross_ffn_uncached(const ExpertLayer & e, wamx_tensor * h, wamx_tensor * kv, int64_t l,
+                                     wamx_tensor * cshift, wamx_tensor * cscale, wamx_tensor * cgate) {
+        const int64_t T = h->ne[1], NL = kv->ne[1], d = (int64_t) c.n_heads * c.head_dim;
         wamx_tensor * n = wamx_layer_norm_bf16(ctx, h, e.n2_w, e.n2_b, c.eps);
         wamx_tensor * q = lin(e.cq_w, e.cq_b, n);
-        wamx_tensor * k = lin(e.ck_w, e.ck_b, txt);
-        wamx_tensor * v = lin(e.cv_w, e.cv_b, txt);
+        wamx_tensor * k = cols(kv, d, 2 * l * d);
         wamx_tensor * Q = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, c.head_dim, T, c.n_heads);
         Q = wamx_qk_norm_rope(ctx, q, e.cnq, Q, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
         wamx_tensor * K = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, c.head_dim, NL, c.n_heads);
         K = wamx_qk_norm_rope(ctx, k, e.cnk, K, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
         wamx_tensor * vraw = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, round_up(NL, 4), c.head_dim, c.n_heads);
-        wamx_tensor * V = store_v(v, 0, vt_view(vraw, 0, NL));
+        wamx_tensor * V = store_v(kv, (2 * l + 1) * d, vt_view(vraw, 0, NL));
         wamx_tensor * att = wamx_joint_attn(ctx, Q, K, V, nullptr, nullptr, 0, scale);
         h = lin(e.co_w, e.co_b, att, WAMX_EPI_BIAS_RESIDUAL, h);
         return ffn(e, h, cshift, cscale, cgate);
@@ -276,7 +293,15 @@ static bool create_weights(wamx_gwp_model * m) {
     // The action expert's projections run on 48 denoise tokens (and the 1
     // state token of the prefix) and use the tiled layout; its cross-attention
     // K/V projections run on the 512 prompt tokens and stay row-major.
-    auto expert = [&](const std::string & p, int64_t w, int64_t ffn, ExpertLayer & e, bool t) {
+    // The prompt-token K/V projections of all layers are packed per expert, so
+    // the prompt's K and V for every layer come out of one GEMM (one launch of
+    // 2·L·d features instead of 2·L launches of d).
+    for (int x = 0; x < 2; ++x) {
+        m->kv_w[x] = wamx_new_tensor_2d(m->wctx, WAMX_TYPE_BF16, x == 0 ? da : d, 2 * L * d);
+        m->kv_b[x] = wamx_new_tensor_1d(m->wctx, WAMX_TYPE_BF16, 2 * L * d);
+        if (!m->kv_w[x] || !m->kv_b[x]) return false;
+    }
+    auto expert = [&](const std::string & p, int64_t w, int64_t ffn, ExpertLayer & e, bool t, int64_t l) {
         m->add_linear(p + ".attn1.to_qkv", w, 3 * d, &e.qkv_w, &e.qkv_b, t);
         e.norm_q = m->add_weight(p + ".attn1.norm_q.weight", d);
         e.norm_k = m->add_weight(p + ".attn1.norm_k.weight", d);
@@ -284,8 +309,9 @@ static bool create_weights(wamx_gwp_model * m) {
         e.n2_w = m->add_weight(p + ".norm2.weight", w);
         e.n2_b = m->add_weight(p + ".norm2.bias", w);
         m->add_linear(p + ".attn2.to_q", w, d, &e.cq_w, &e.cq_b, t);
-        m->add_linear(p + ".attn2.to_k", w, d, &e.ck_w, &e.ck_b);
-        m->add_linear(p + ".attn2.to_v", w, d, &e.cv_w, &e.cv_b);
+        m->add_linear_view(p + ".attn2.to_k", m->kv_w[t ? 0 : 1], m->kv_b[t ? 0 : 1], 2 * l * d, d, &e.ck_w, &e.ck_b);
+        m->add_linear_view(p + ".attn2.to_v", m->kv_w[t ? 0 : 1], m->kv_b[t ? 0 : 1], (2 * l + 1) * d, d, &e.cv_w,
+                           &e.cv_b);
         e.cnq = m->add_weight(p + ".attn2.norm_q.weight", d);
         e.cnk = m->add_weight(p + ".attn2.norm_k.weight", d);
         m->add_linear(p + ".attn2.to_out.0", d, w, &e.co_w, &e.co_b, t);
@@ -296,8 +322,8 @@ static bool create_weights(wamx_gwp_model * m) {
     m->vis.resize(L);
     for (int64_t l = 0; l < L; ++l) {
         const std::string b = "gwp.blocks." + std::to_string(l);
-        expert(b + ".action_expert", da, c.action_ffn_dim, m->act[l], true);
-        expert(b + ".visual_expert", d, c.ffn_dim, m->vis[l], false);
+        expert(b + ".action_expert", da, c.action_ffn_dim, m->act[l], true, l);
+        expert(b + ".visual_expert", d, c.ffn_dim, m->vis[l], false, l);
     }
     for (auto & kv : m->weights)
         if (!kv.second) return false;
@@ -403,14 +429,13 @@ static bool build_prompt_graph(wamx_gwp_model * m) {
     wamx_tensor * txt = b.text(m->acond, m->in_prompt);
     wamx_build_forward_expand(g, wamx_cpy(ctx, txt, m->action_prompt));
     const int64_t d = (int64_t) c.n_heads * c.head_dim;
+    wamx_tensor * kv = b.lin(m->kv_w[0], m->kv_b[0], txt);  // every layer's prompt K/V [2·L·d, NL]
     for (int l = 0; l < c.n_layers; ++l) {
         const ExpertLayer & e = m->act[l];
-        wamx_tensor * k = b.lin(e.ck_w, e.ck_b, txt);
-        wamx_tensor * v = b.lin(e.cv_w, e.cv_b, txt);
+        wamx_tensor * k = b.cols(kv, d, 2 * (int64_t) l * d);
         wamx_build_forward_expand(
             g, wamx_qk_norm_rope(ctx, k, e.cnk, m->lk[l], 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f));
-        (void) d;
-        wamx_build_forward_expand(g, b.store_v(v, 0, b.vt_view(m->lv_raw[l], 0, c.n_lang)));
+        wamx_build_forward_expand(g, b.store_v(kv, (2 * (int64_t) l + 1) * d, b.vt_view(m->lv_raw[l], 0, c.n_lang)));
     }
     wamx_graph_assign_uid(g);
     m->galloc[0] = wamx_gallocr_new(m->be);
@@ -439,6 +464,7 @@ static bool build_prefix_graph(wamx_gwp_model * m) {
     // identical, so one row is computed and broadcast (bit-identical).
     b.condition(m->vcond, m->in_freq0, &vtemb, &vmod);
     wamx_tensor * vtext = b.text(m->vcond, m->in_prompt);
+    wamx_tensor * vkv = b.lin(m->kv_w[1], m->kv_b[1], vtext);  // every layer's text K/V [2·L·d, NL]
     wamx_tensor * amods = wamx_modulation(ctx, smod, m->a_tables);  // [da, 6, L] f32
     wamx_tensor * vmods = wamx_modulation(ctx, vmod, m->v_tables);  // [d, 6, L] f32
 
@@ -474,7 +500,7 @@ static bool build_prefix_graph(wamx_gwp_model * m) {
         vh = b.lin(ev.o_w, ev.o_b, vatt, WAMX_EPI_BIAS_GATED, vh, b.part(vmods, d, l, 2));
         sh = b.cross_ffn_cached(ea, sh, m->lk[l], m->lv[l], b.part(amods, da, l, 3), b.part(amods, da, l, 4),
                                 b.part(amods, da, l, 5));
-        vh = b.cross_ffn_uncached(ev, vh, vtext, b.part(vmods, d, l, 3), b.part(vmods, d, l, 4),
+        vh = b.cross_ffn_uncached(ev, vh, vkv, l, b.part(vmods, d, l, 3), b.part(vmods, d, l, 4),
                                   b.part(vmods, d, l, 5));
     }
     wamx_graph_assign_uid(g);
