@@ -609,9 +609,11 @@ wamx_gwp_t wamx_gwp_create(wamx_backend_t be, const wamx_gwp_config * cfg) {
     m->cfg = c;
     m->nimg = (int64_t) c.grid_h * c.grid_w;
     m->P = 1 + m->nimg;
-    m->Ppad = round_up(m->P, 8);
-    m->NLpad = round_up(c.n_lang, 8);
-    m->Tpad = round_up(c.action_chunk, 8);
+    // V^T rows padded to 64 keys (128 bytes), so every 64-key block of a row
+    // the attention kernels copy is one aligned 128-byte segment.
+    m->Ppad = round_up(m->P, 64);
+    m->NLpad = round_up(c.n_lang, 64);
+    m->Tpad = round_up(c.action_chunk, 64);
     if (!create_weights(m.get())) {
         set_errorf("wamx_gwp_create: weight allocation failed: %s", wamx_last_error());
         return nullptr;

@@ -487,6 +487,49 @@ constexpr int kPfStageElems = kPfKeys * kDh + kDh * kPfKeys;  // K tile + V^T ti
 __device__ __forceinline__ int pf_kswz(int key, int c) { return c ^ (key & 15); }
 __device__ __forceinline__ int pf_vswz(int d, int c) { return c ^ ((d >> 1) & 7); }
 
+// Key block `blk` of head h: source a's 64-key blocks come first, then
+// source b's (each source's last block partial).
+struct PfBlk {
+    const uint16_t * kb;
+    const uint16_t * vb;
+    int64_t vld, k0, nk;
+};
+__device__ __forceinline__ PfBlk pf_locate(const AttnParams & p, int64_t h, int nblk_a, int blk) {
+    const int seg = blk < nblk_a ? 0 : 1;
+    PfBlk r;
+    r.nk = p.seg_len[seg];
+    r.vld = p.vt_ld[seg];
+    r.k0 = (int64_t) (blk - (seg ? nblk_a : 0)) * kPfKeys;
+    r.kb = p.k[seg] + h * r.nk * kDh;
+    r.vb = p.vt[seg] + h * kDh * r.vld;
+    return r;
+}
+
+// One block's K tile and V^T tile into an LDS stage by a workgroup of
+// kPfWaves waves: 8 global_load_lds_dwordx4 per thread.  DMA slots: K tile
+// 1024 chunks (key = s / 16), V^T tile 1024 chunks (row = s / 8).  Rows past
+// the source end are clamped to its last key (the consumer masks them).
+__device__ __forceinline__ void pf_dma(const PfBlk & bl, uint16_t * stage, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int slot = (i * kPfWaves + wave) * 64 + lane;
+        const int key = slot >> 4, c = pf_kswz(key, slot & 15);
+        const int64_t kr = min(bl.k0 + key, bl.nk - 1);
+        __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.kb + kr * kDh + 8 * c),
+                                         (lds_void_t *) (stage + (i * kPfWaves + wave) * 512), 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int slot = (i * kPfWaves + wave) * 64 + lane;
+        const int d = slot >> 3, c = pf_vswz(d, slot & 7);
+        const int64_t kc = min(bl.k0 + 8 * c, bl.vld - 8);
+        __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.vb + (int64_t) d * bl.vld + kc),
+                                         (lds_void_t *) (stage + kPfKeys * kDh + (i * kPfWaves + wave) * 512), 16, 0,
+                                         0);
+    }
+}
+constexpr int kPfDmaPerBlock = 8;  // global_load_lds per thread per block
+
 template <bool SPLIT>
 __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnParams p) {
     __shared__ __align__(16) uint16_t st0[kPfStageElems];
@@ -494,49 +537,12 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, hl = lane >> 5;
     const int64_t h = blockIdx.x, q0 = (int64_t) blockIdx.y * kPfQueries;
-    // Key blocks of 64: source a's blocks, then source b's (each source's last
-    // block partial).
     const int nblk_a = (int) ((p.seg_len[0] + kPfKeys - 1) / kPfKeys);
     const int nblk = nblk_a + (int) ((p.seg_len[1] + kPfKeys - 1) / kPfKeys);
     const int b_begin = SPLIT ? (int) blockIdx.z * (int) p.split_blocks : 0;
     const int b_end = SPLIT ? min(nblk, b_begin + (int) p.split_blocks) : nblk;
-    struct Blk {
-        const uint16_t * kb;
-        const uint16_t * vb;
-        int64_t vld, k0, nk;
-    };
-    auto locate = [&](int blk) {
-        const int seg = blk < nblk_a ? 0 : 1;
-        Blk r;
-        r.nk = p.seg_len[seg];
-        r.vld = p.vt_ld[seg];
-        r.k0 = (int64_t) (blk - (seg ? nblk_a : 0)) * kPfKeys;
-        r.kb = p.k[seg] + h * r.nk * kDh;
-        r.vb = p.vt[seg] + h * kDh * r.vld;
-        return r;
-    };
-
-    // DMA slots: K tile 1024 chunks (key = s / 16), V^T tile 1024 chunks (row = s / 8).
-    auto dma = [&](int blk, uint16_t * stage) {
-        const Blk bl = locate(min(blk, b_end - 1));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int slot = (i * kPfWaves + wave) * 64 + lane;
-            const int key = slot >> 4, c = pf_kswz(key, slot & 15);
-            const int64_t kr = min(bl.k0 + key, bl.nk - 1);
-            __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.kb + kr * kDh + 8 * c),
-                                             (lds_void_t *) (stage + (i * kPfWaves + wave) * 512), 16, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int slot = (i * kPfWaves + wave) * 64 + lane;
-            const int d = slot >> 3, c = pf_vswz(d, slot & 7);
-            const int64_t kc = min(bl.k0 + 8 * c, bl.vld - 8);
-            __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.vb + (int64_t) d * bl.vld + kc),
-                                             (lds_void_t *) (stage + kPfKeys * kDh + (i * kPfWaves + wave) * 512), 16,
-                                             0, 0);
-        }
-    };
+    auto locate = [&](int blk) { return pf_locate(p, h, nblk_a, blk); };
+    auto dma = [&](int blk, uint16_t * stage) { pf_dma(locate(min(blk, b_end - 1)), stage, wave, lane); };
 
     // Q^T fragments (B operand of S^T = K Q^T): lane holds query l32 of the
     // wave, dims 16s + 8hl .. +8 for k-step s.
@@ -563,7 +569,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
     auto block = [&](int blk, const uint16_t * stage, bool partial) __attribute__((always_inline)) {
         const uint16_t * kt = stage;
         const uint16_t * vt = stage + kPfKeys * kDh;
-        const Blk bl = locate(blk);
+        const PfBlk bl = locate(blk);
         const int valid = partial ? (int) (bl.nk - bl.k0) : kPfKeys;
         // S^T tiles: key tile t (32 keys) x the wave's 32 queries.
         f32x16_t sacc[2];
@@ -592,7 +598,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sacc[t][v]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * p.scale_log2;
+        mx = max_xor32(mx) * p.scale_log2;
         if (__builtin_amdgcn_read_exec() & __ballot(mx > m_run + kPfSlack)) {
             const float m_new = mx > m_run + kPfSlack ? mx : m_run;
             const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -616,8 +622,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
                 pk[t][j] = pack_bf16x2(e0, e1);
                 ps += __uint_as_float(pk[t][j] << 16) + __uint_as_float(pk[t][j] & 0xffff0000u);
             }
-        ps += __shfl_xor(ps, 32, 64);
-        l_run += ps;
+        l_run += sum_xor32(ps);
         // O^T += V^T P^T, k-step (t, hh): key slots 0-3 = keys 32t+16hh+4hl+{0..3},
         // slots 4-7 = keys 32t+16hh+8+4hl+{0..3}.
 #pragma unroll
@@ -646,7 +651,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         cta_barrier();
         if (blk + 1 < b_end) dma(blk + 1, nxt);
-        const Blk bl = locate(blk);
+        const PfBlk bl = locate(blk);
         block(blk, cur, bl.k0 + kPfKeys > bl.nk);
     };
 
@@ -699,6 +704,269 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
     }
 }
 
+// ---------------------------------------------------------------------------
+// attn_decode: softmax(scale * Q K^T) V for at most 64 queries (the 48-token
+// denoise step) over long key sources, one workgroup per (head, key range).
+//
+// All four waves work on real queries: in every 64-key block (the attn_prefill
+// K / V^T tiles, same LDS layout and swizzle) wave w takes keys 16w..16w+15
+// for all 16*QT queries.  S^T = K Q^T with MFMA 16x16x32 (one 16-key x
+// 16-query tile per query tile, Q^T fragments in registers), online softmax
+// per (wave, query) in the log2 domain with P rounded to bf16, then O^T +=
+// V^T P^T with MFMA 16x16x16, whose P operand is the S^T accumulator as it
+// stands (lane: query l%16, keys 4(l/16)..+4) and whose V^T operand is one
+// 8-byte LDS read of the same four keys.  Blocks stream through a 4-stage
+// ring, three in flight.  At the end the waves' states merge in LDS in wave
+// order, and the workgroup writes its key range's partial (unnormalised O,
+// max, sum) for attn_merge_kernel, or the output when the range is all keys.
+// ---------------------------------------------------------------------------
+constexpr int kDecStages = 4;
+constexpr int kDecPitch = kDh;  // fp32 merge rows, 16-byte chunks XOR-swizzled by query
+
+__device__ __forceinline__ uint32_t lds_addr(const void * ptr) {
+    return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) void *) ptr;
+}
+
+template <int QT>
+__global__ __launch_bounds__(kPfWaves * 64, 1) void attn_decode_kernel(AttnParams p) {
+    static_assert(QT >= 1 && 16 * QT * kDh * 4 <= kPfStageElems * 2, "a wave's merge rows fit in one stage");
+    __shared__ __align__(16) uint16_t ring[kDecStages][kPfStageElems];
+    __shared__ float s_m[kPfWaves][16 * QT];
+    __shared__ float s_l[kPfWaves][16 * QT];
+    __shared__ float s_mstar[16 * QT], s_lstar[16 * QT];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, c16 = lane & 15;
+    const int64_t h = blockIdx.x;
+    const int nblk_a = (int) ((p.seg_len[0] + kPfKeys - 1) / kPfKeys);
+    const int nblk = nblk_a + (int) ((p.seg_len[1] + kPfKeys - 1) / kPfKeys);
+    const int b_begin = (int) blockIdx.z * (int) p.split_blocks;
+    const int b_end = min(nblk, b_begin + (int) p.split_blocks);
+    // Only the range's own blocks are loaded (no clamped repeats past its end).
+    auto dma = [&](int blk, int stage) {
+        if (blk < b_end) pf_dma(pf_locate(p, h, nblk_a, blk), &ring[stage][0], wave, lane);
+    };
+
+    // Q^T fragments (B operand of S^T = K Q^T): lane holds query 16t + c16,
+    // dims 32c + 8g .. +8 for k-step c.
+    bf16x8_t qf[QT][4];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        const int64_t qi = min((int64_t) (16 * t + c16), p.tq - 1);
+        const uint16_t * qrow = p.q + (h * p.tq + qi) * kDh + 8 * g;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qf[t][c] = *(const bf16x8_t *) (qrow + 32 * c);
+    }
+    f32x4_t o[QT][8];
+    float m_run[QT], l_run[QT];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        m_run[t] = -INFINITY;
+        l_run[t] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[t][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // LDS byte offsets of this lane's operands within a stage: K row `key`
+    // (16-byte chunk 4c + g) and V^T rows 16dt + c16 (keys k4 .. k4+3).
+    const int key = 16 * wave + c16, k4 = 16 * wave + 4 * g;
+    uint32_t koff[4], voff[8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) koff[c] = (uint32_t) (key * kDh + 8 * pf_kswz(key, 4 * c + g)) * 2;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+        const int d = 16 * dt + c16;
+        voff[dt] = (uint32_t) (kPfKeys * kDh + d * kPfKeys + 8 * pf_vswz(d, k4 >> 3) + (k4 & 7)) * 2;
+    }
+
+    // Lazy rescaling as in attn_prefill: the exponent offset is raised only
+    // when a block's max exceeds it by more than kSlack.
+    constexpr float kSlack = 8.0f;
+    auto block = [&](int stage, int valid) __attribute__((always_inline)) {
+        // The operand reads are issued as LDS instructions the compiler's
+        // wait insertion does not track against the ring's in-flight DMA
+        // (which it would otherwise drain); the explicit wait below covers
+        // them, and the barrier before this block covers the DMA.
+        const uint32_t base = lds_addr(&ring[stage][0]);
+        bf16x8_t kf[4];
+        uint2 va[8];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) asm volatile("ds_read_b128 %0, %1" : "=v"(kf[c]) : "v"(base + koff[c]));
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) asm volatile("ds_read_b64 %0, %1" : "=v"(va[dt]) : "v"(base + voff[dt]));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(kf[c]));
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            asm volatile("" : "+v"(va[dt]));
+            if (valid < kPfKeys) va[dt] = mask4(va[dt], k4, valid);
+        }
+        // S^T for every query tile first: QT independent MFMA chains.
+        f32x4_t sacc[QT];
+#pragma unroll
+        for (int t = 0; t < QT; ++t) sacc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < QT; ++t) sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[c], qf[t][c], sacc[t], 0, 0, 0);
+        // Online softmax: lane holds query 16t + c16, keys k4 + r; the wave's
+        // other keys of the query are in lanes ^16, ^32.
+        bf16x4_t pf[QT];
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+            bool ok[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                ok[r] = k4 + r < valid;
+                if (ok[r]) mx = fmaxf(mx, sacc[t][r]);
+            }
+            mx = max_xor32(max_xor16(mx)) * p.scale_log2;
+            if (__builtin_amdgcn_read_exec() & __ballot(mx > m_run[t] + kSlack)) {
+                const float m_new = mx > m_run[t] + kSlack ? mx : m_run[t];
+                const float corr = __builtin_amdgcn_exp2f(m_run[t] - m_new);
+                l_run[t] *= corr;
+                m_run[t] = m_new;
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) o[t][dt][r] *= corr;
+            }
+            float e[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                e[r] = ok[r] ? __builtin_amdgcn_exp2f(fmaf(sacc[t][r], p.scale_log2, -m_run[t])) : 0.0f;
+            const uint32_t p01 = pack_bf16x2(e[0], e[1]), p23 = pack_bf16x2(e[2], e[3]);
+            const float ps = __uint_as_float(p01 << 16) + __uint_as_float(p01 & 0xffff0000u) +
+                             __uint_as_float(p23 << 16) + __uint_as_float(p23 & 0xffff0000u);
+            l_run[t] += sum_xor32(sum_xor16(ps));
+            pf[t] = __builtin_bit_cast(bf16x4_t, make_uint2(p01, p23));
+        }
+        // O^T += V^T P^T: 8 x QT independent MFMAs.
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int t = 0; t < QT; ++t)
+                o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va[dt]), pf[t], o[t][dt],
+                                                                     0, 0, 0);
+    };
+    // Block i: wait for it (blocks i+1, i+2 may stay in flight), barrier
+    // (every wave is past block i-1), refill block i-1's stage with block i+3.
+    dma(b_begin, 0);
+    dma(b_begin + 1, 1);
+    dma(b_begin + 2, 2);
+    for (int blk = b_begin; blk < b_end; ++blk) {
+        const int stage = (blk - b_begin) & (kDecStages - 1);
+        // Blocks issued after this one: min(2, b_end - 1 - blk).
+        const int younger = min(kDecStages - 2, b_end - 1 - blk);
+        if (younger == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kPfDmaPerBlock));
+        else if (younger == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kPfDmaPerBlock));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        cta_barrier();
+        dma(blk + kDecStages - 1, (stage + kDecStages - 1) & (kDecStages - 1));
+        const PfBlk bl = pf_locate(p, h, nblk_a, blk);
+        block(stage, (int) min((int64_t) kPfKeys, bl.nk - bl.k0));
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+
+    // Merge the waves in LDS: wave w's O^T (scaled to the common max) goes to
+    // stage w as fp32 rows [query][dh], 16-byte chunk j of query q at j ^ (q & 15).
+#pragma unroll
+    for (int t = 0; t < QT; ++t)
+        if (g == 0) {
+            s_m[wave][16 * t + c16] = m_run[t];
+            s_l[wave][16 * t + c16] = l_run[t];
+        }
+    __syncthreads();
+    if (tid < 16 * QT) {
+        float mstar = -INFINITY, l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kPfWaves; ++w) mstar = fmaxf(mstar, s_m[w][tid]);
+#pragma unroll
+        for (int w = 0; w < kPfWaves; ++w)
+            if (s_m[w][tid] != -INFINITY) l += s_l[w][tid] * __builtin_amdgcn_exp2f(s_m[w][tid] - mstar);
+        s_mstar[tid] = mstar;
+        s_lstar[tid] = l;
+    }
+    float * mine = (float *) &ring[wave][0];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        const int q = 16 * t + c16;
+        float mstar = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kPfWaves; ++w) mstar = fmaxf(mstar, s_m[w][q]);
+        const float fac = m_run[t] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[t] - mstar);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+            *(float4 *) (mine + q * kDecPitch + 4 * ((4 * dt + g) ^ c16)) =
+                make_float4(o[t][dt][0] * fac, o[t][dt][1] * fac, o[t][dt][2] * fac, o[t][dt][3] * fac);
+    }
+    __syncthreads();
+    // Four dims per thread and step: the waves' rows summed in wave order.
+    const int nq = (int) min((int64_t) (16 * QT), p.tq);
+    const bool split = gridDim.z > 1;
+    for (int e = tid; e < nq * (kDh / 4); e += kPfWaves * 64) {
+        const int q = e / (kDh / 4), j = e % (kDh / 4);
+        const int off = q * kDecPitch + 4 * (j ^ (q & 15));
+        float4 acc = *(const float4 *) ((const float *) &ring[0][0] + off);
+#pragma unroll
+        for (int w = 1; w < kPfWaves; ++w) {
+            const float4 v = *(const float4 *) ((const float *) &ring[w][0] + off);
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        if (split) {
+            const int64_t pi = ((int64_t) blockIdx.z * p.heads + h) * p.tq + q;
+            *(float4 *) (p.part_o + pi * kDh + 4 * j) = acc;
+            if (j == 0) {
+                p.part_m[pi] = s_mstar[q];
+                p.part_l[pi] = s_lstar[q];
+            }
+        } else {
+            const float l = s_lstar[q], inv = l > 0.0f ? 1.0f / l : 0.0f;
+            *(uint2 *) (p.out + (int64_t) q * (p.heads * kDh) + h * kDh + 4 * j) =
+                make_uint2(pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv));
+        }
+    }
+}
+
+// Combines the key-range partials of one (head, query) per 128-thread
+// workgroup, ranges in order: m* = max m_z, l* = sum l_z 2^(m_z - m*),
+// out = sum o_z 2^(m_z - m*) / l*.  Every partial is requested before the
+// first is combined (nsplit <= MAXS), so the merge costs one memory latency.
+template <int MAXS>
+__global__ __launch_bounds__(kDh) void attn_merge_kernel(AttnParams p, int nsplit) {
+    const int64_t hq = blockIdx.x;
+    const int d = threadIdx.x;
+    const int64_t h = hq / p.tq, q = hq % p.tq, stride = p.heads * p.tq;
+    float m[MAXS], lz[MAXS], oz[MAXS];
+#pragma unroll
+    for (int u = 0; u < MAXS; ++u) {
+        const int64_t z = min(u, nsplit - 1);
+        m[u] = p.part_m[z * stride + hq];
+        lz[u] = p.part_l[z * stride + hq];
+        oz[u] = p.part_o[(z * stride + hq) * kDh + d];
+    }
+    float mstar = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < MAXS; ++u)
+        if (u < nsplit) mstar = fmaxf(mstar, m[u]);
+    float l = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int u = 0; u < MAXS; ++u) {
+        if (u >= nsplit || m[u] == -INFINITY) continue;
+        const float w = __builtin_amdgcn_exp2f(m[u] - mstar);
+        l += lz[u] * w;
+        o += oz[u] * w;
+    }
+    p.out[q * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
+}
+constexpr int kDecMaxSplits = 16;
+constexpr int kDecTargetWgs = 256;
+
 // Softmax is order-free, so the keys are visited per source in 32-key blocks
 // aligned to each source's start: source a ([state, reference] prefix cache,
 // na keys) and source b (the current action tokens, nb keys).  The complete
@@ -750,9 +1018,40 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
                            dim3(kPfWaves * 64), 0, s, p);
         return hipGetLastError();
     }
-    // Few queries (the 48-token denoise step) over long key sources: the same
-    // LDS-tiled kernel, one workgroup per (head, key range), every key read
-    // once; fp32 partials merged by joint_attn_merge.
+    // At most 64 queries (the 48-token denoise step) over long key sources:
+    // attn_decode, one workgroup per (head, key range) with about one
+    // workgroup per CU in all, every key read once; the ranges' fp32 partials
+    // are merged by attn_merge_kernel.
+    if (flash && a.tq <= 16 * 4) {
+        const int64_t nblk = (p.seg_len[0] + kPfKeys - 1) / kPfKeys + (p.seg_len[1] + kPfKeys - 1) / kPfKeys;
+        int64_t nsplit = std::min<int64_t>({(kDecTargetWgs + a.heads - 1) / a.heads, nblk, (int64_t) kDecMaxSplits});
+        p.split_blocks = (nblk + nsplit - 1) / nsplit;
+        nsplit = (nblk + p.split_blocks - 1) / p.split_blocks;
+        const size_t part_bytes = (size_t) nsplit * a.heads * a.tq * (kDh + 2) * sizeof(float);
+        if (nsplit > 1 && (!a.ws || part_bytes > a.ws_bytes)) {
+            nsplit = 1;
+            p.split_blocks = nblk;
+        }
+        if (nsplit > 1) {
+            p.part_o = (float *) a.ws;
+            p.part_m = p.part_o + (size_t) nsplit * a.heads * a.tq * kDh;
+            p.part_l = p.part_m + (size_t) nsplit * a.heads * a.tq;
+        }
+        const dim3 grid((unsigned) a.heads, 1, (unsigned) nsplit), block(kPfWaves * 64);
+        switch ((a.tq + 15) / 16) {
+            case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, block, 0, s, p); break;
+            case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, block, 0, s, p); break;
+            case 3: hipLaunchKernelGGL(attn_decode_kernel<3>, grid, block, 0, s, p); break;
+            default: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, block, 0, s, p); break;
+        }
+        if (nsplit > 1)
+            hipLaunchKernelGGL(attn_merge_kernel<kDecMaxSplits>, dim3((unsigned) (a.heads * a.tq)), dim3(kDh), 0, s, p,
+                               (int) nsplit);
+        return hipGetLastError();
+    }
+    // Up to 128 queries over long key sources: the LDS-tiled prefill kernel,
+    // one workgroup per (head, key range), every key read once; fp32 partials
+    // merged by joint_attn_merge.
     if (flash && a.tq <= kPfQueries) {
         const int64_t nblk = (p.seg_len[0] + kPfKeys - 1) / kPfKeys + (p.seg_len[1] + kPfKeys - 1) / kPfKeys;
         // About kFlashSplitBlocks blocks per split, but at least 8 splits (short

@@ -9,8 +9,32 @@ namespace wamx {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+// Four bf16 bit patterns: the operand type of MFMA 16x16x16 bf16 (_1k).
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short bf16x4_t;
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t) h << 16); }
+
+// Pairwise combines across lanes l and l ^ 16 (or l ^ 32) with gfx950's VALU
+// lane swaps (v_permlane16_swap / v_permlane32_swap of a value with itself
+// leave the lower and the upper lane's value in the two results in every
+// lane), instead of an LDS-routed shuffle.  max and + are commutative, so
+// both lanes of a pair get the same bits.
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // Round-to-nearest-even f32 -> bf16 with gfx950's v_cvt_pk_bf16_f32.  Checked
 // on the device against the integer RNE rule of the host helper over all 2^32

@@ -492,7 +492,7 @@ struct DmaCfg {
     static constexpr int kStageElems = kRows * BK;
     static constexpr int P = kRows * kChunks / kThreads;  // DMA instructions per thread per stage
     static_assert(BK == 32 || BK == 64, "BK");
-    static_assert(S >= 2 && S <= 4, "ring of 2 to 4 stages");
+    static_assert(S >= 2 && S <= 5, "ring of 2 to 5 stages");
     static_assert(FR * 32 * WM == BM && FC * 32 * WN == BN, "wave tile must be whole 32x32 fragments");
     static_assert(P * kThreads == kRows * kChunks, "stage/thread mismatch");
     static_assert((size_t) S * kStageElems * 2 <= 160 * 1024, "LDS budget");
