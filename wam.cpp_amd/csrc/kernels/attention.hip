@@ -715,22 +715,25 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
 // per (wave, query) in the log2 domain with P rounded to bf16, then O^T +=
 // V^T P^T with MFMA 16x16x16, whose P operand is the S^T accumulator as it
 // stands (lane: query l%16, keys 4(l/16)..+4) and whose V^T operand is one
-// 8-byte LDS read of the same four keys.  Blocks stream through a 4-stage
-// ring, three in flight.  At the end the waves' states merge in LDS in wave
-// order, and the workgroup writes its key range's partial (unnormalised O,
-// max, sum) for attn_merge_kernel, or the output when the range is all keys.
+// 8-byte LDS read of the same four keys.  Blocks stream through an S-stage
+// LDS ring with S-1 in flight: S = 2 (64 KB) runs two workgroups per CU, so
+// one workgroup's softmax and waits overlap the other's copies and MFMAs.  At
+// the end the waves' states merge in LDS in wave order, one half of the head
+// dims at a time, and the workgroup writes its key range's partial
+// (unnormalised O, max, sum) for attn_merge_kernel, or the output when the
+// range is all keys.
 // ---------------------------------------------------------------------------
-constexpr int kDecStages = 4;
-constexpr int kDecPitch = kDh;  // fp32 merge rows, 16-byte chunks XOR-swizzled by query
+constexpr int kDecHalf = kDh / 2;  // fp32 merge rows of 64 dims, 16-byte chunks XOR-swizzled by query
 
 __device__ __forceinline__ uint32_t lds_addr(const void * ptr) {
     return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) void *) ptr;
 }
 
-template <int QT>
-__global__ __launch_bounds__(kPfWaves * 64, 1) void attn_decode_kernel(AttnParams p) {
-    static_assert(QT >= 1 && 16 * QT * kDh * 4 <= kPfStageElems * 2, "a wave's merge rows fit in one stage");
-    __shared__ __align__(16) uint16_t ring[kDecStages][kPfStageElems];
+template <int QT, int S>
+__global__ __launch_bounds__(kPfWaves * 64, S == 2 ? 2 : 1) void attn_decode_kernel(AttnParams p) {
+    static_assert(QT >= 1 && QT <= 4 && (S == 2 || S == 4), "query tiles / ring stages");
+    static_assert(kPfWaves * 16 * QT * kDecHalf * 4 <= S * kPfStageElems * 2, "the merge rows fit in the ring");
+    __shared__ __align__(16) uint16_t ring[S][kPfStageElems];
     __shared__ float s_m[kPfWaves][16 * QT];
     __shared__ float s_l[kPfWaves][16 * QT];
     __shared__ float s_mstar[16 * QT], s_lstar[16 * QT];
@@ -850,28 +853,29 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void attn_decode_kernel(AttnParam
                 o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va[dt]), pf[t], o[t][dt],
                                                                      0, 0, 0);
     };
-    // Block i: wait for it (blocks i+1, i+2 may stay in flight), barrier
-    // (every wave is past block i-1), refill block i-1's stage with block i+3.
-    dma(b_begin, 0);
-    dma(b_begin + 1, 1);
-    dma(b_begin + 2, 2);
+    // Block i: wait for it (blocks i+1 .. i+S-2 may stay in flight), barrier
+    // (every wave is past block i-1), refill block i-1's stage with block i+S-1.
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i) dma(b_begin + i, i);
     for (int blk = b_begin; blk < b_end; ++blk) {
-        const int stage = (blk - b_begin) & (kDecStages - 1);
-        // Blocks issued after this one: min(2, b_end - 1 - blk).
-        const int younger = min(kDecStages - 2, b_end - 1 - blk);
-        if (younger == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kPfDmaPerBlock));
+        const int stage = (blk - b_begin) & (S - 1);
+        // Blocks issued after this one: min(S - 2, b_end - 1 - blk).
+        const int younger = min(S - 2, b_end - 1 - blk);
+        if (younger >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kPfDmaPerBlock));
         else if (younger == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kPfDmaPerBlock));
         else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         cta_barrier();
-        dma(blk + kDecStages - 1, (stage + kDecStages - 1) & (kDecStages - 1));
+        dma(blk + S - 1, (stage + S - 1) & (S - 1));
         const PfBlk bl = pf_locate(p, h, nblk_a, blk);
         block(stage, (int) min((int64_t) kPfKeys, bl.nk - bl.k0));
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
 
-    // Merge the waves in LDS: wave w's O^T (scaled to the common max) goes to
-    // stage w as fp32 rows [query][dh], 16-byte chunk j of query q at j ^ (q & 15).
+    // Merge the waves in LDS, one half of the head dims at a time: wave w's
+    // O^T (scaled to the common max) goes to region w as fp32 rows [query][64
+    // dims], 16-byte chunk j of query q at j ^ (q & 15); every thread then sums
+    // four dims of one query over the waves in wave order.
 #pragma unroll
     for (int t = 0; t < QT; ++t)
         if (g == 0) {
@@ -889,46 +893,57 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void attn_decode_kernel(AttnParam
         s_mstar[tid] = mstar;
         s_lstar[tid] = l;
     }
-    float * mine = (float *) &ring[wave][0];
+    float fac[QT];
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-        const int q = 16 * t + c16;
         float mstar = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kPfWaves; ++w) mstar = fmaxf(mstar, s_m[w][q]);
-        const float fac = m_run[t] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[t] - mstar);
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            *(float4 *) (mine + q * kDecPitch + 4 * ((4 * dt + g) ^ c16)) =
-                make_float4(o[t][dt][0] * fac, o[t][dt][1] * fac, o[t][dt][2] * fac, o[t][dt][3] * fac);
+        for (int w = 0; w < kPfWaves; ++w) mstar = fmaxf(mstar, s_m[w][16 * t + c16]);
+        fac[t] = m_run[t] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[t] - mstar);
     }
-    __syncthreads();
-    // Four dims per thread and step: the waves' rows summed in wave order.
+    constexpr int kRegion = 16 * QT * kDecHalf;  // floats per wave
+    float * const rows = (float *) &ring[0][0];
     const int nq = (int) min((int64_t) (16 * QT), p.tq);
     const bool split = gridDim.z > 1;
-    for (int e = tid; e < nq * (kDh / 4); e += kPfWaves * 64) {
-        const int q = e / (kDh / 4), j = e % (kDh / 4);
-        const int off = q * kDecPitch + 4 * (j ^ (q & 15));
-        float4 acc = *(const float4 *) ((const float *) &ring[0][0] + off);
 #pragma unroll
-        for (int w = 1; w < kPfWaves; ++w) {
-            const float4 v = *(const float4 *) ((const float *) &ring[w][0] + off);
-            acc.x += v.x;
-            acc.y += v.y;
-            acc.z += v.z;
-            acc.w += v.w;
-        }
-        if (split) {
-            const int64_t pi = ((int64_t) blockIdx.z * p.heads + h) * p.tq + q;
-            *(float4 *) (p.part_o + pi * kDh + 4 * j) = acc;
-            if (j == 0) {
-                p.part_m[pi] = s_mstar[q];
-                p.part_l[pi] = s_lstar[q];
+    for (int half = 0; half < 2; ++half) {
+        if (half) __syncthreads();  // the previous half's rows have been read
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+            const int q = 16 * t + c16;
+#pragma unroll
+            for (int dd = 0; dd < 4; ++dd) {
+                const int dt = 4 * half + dd;
+                *(float4 *) (rows + wave * kRegion + q * kDecHalf + 4 * ((4 * dd + g) ^ c16)) =
+                    make_float4(o[t][dt][0] * fac[t], o[t][dt][1] * fac[t], o[t][dt][2] * fac[t], o[t][dt][3] * fac[t]);
             }
-        } else {
-            const float l = s_lstar[q], inv = l > 0.0f ? 1.0f / l : 0.0f;
-            *(uint2 *) (p.out + (int64_t) q * (p.heads * kDh) + h * kDh + 4 * j) =
-                make_uint2(pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv));
+        }
+        __syncthreads();
+        for (int e = tid; e < nq * (kDecHalf / 4); e += kPfWaves * 64) {
+            const int q = e / (kDecHalf / 4), j = e % (kDecHalf / 4);
+            const int off = q * kDecHalf + 4 * (j ^ (q & 15));
+            const int d = kDecHalf * half + 4 * j;
+            float4 acc = *(const float4 *) (rows + off);
+#pragma unroll
+            for (int w = 1; w < kPfWaves; ++w) {
+                const float4 v = *(const float4 *) (rows + w * kRegion + off);
+                acc.x += v.x;
+                acc.y += v.y;
+                acc.z += v.z;
+                acc.w += v.w;
+            }
+            if (split) {
+                const int64_t pi = ((int64_t) blockIdx.z * p.heads + h) * p.tq + q;
+                *(float4 *) (p.part_o + pi * kDh + d) = acc;
+                if (d == 0) {
+                    p.part_m[pi] = s_mstar[q];
+                    p.part_l[pi] = s_lstar[q];
+                }
+            } else {
+                const float l = s_lstar[q], inv = l > 0.0f ? 1.0f / l : 0.0f;
+                *(uint2 *) (p.out + (int64_t) q * (p.heads * kDh) + h * kDh + d) =
+                    make_uint2(pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv));
+            }
         }
     }
 }
@@ -964,7 +979,10 @@ __global__ __launch_bounds__(kDh) void attn_merge_kernel(AttnParams p, int nspli
     }
     p.out[q * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
 }
-constexpr int kDecMaxSplits = 16;
+constexpr int kDecMaxSplits = 32;
+// About one workgroup per CU in all: more ranges shorten each workgroup's
+// stream but add partial traffic and merge work (measured best on the
+// 24-head, 3121-key denoise shape at 10 ranges).
 constexpr int kDecTargetWgs = 256;
 
 // Softmax is order-free, so the keys are visited per source in 32-key blocks
@@ -1024,6 +1042,7 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     // are merged by attn_merge_kernel.
     if (flash && a.tq <= 16 * 4) {
         const int64_t nblk = (p.seg_len[0] + kPfKeys - 1) / kPfKeys + (p.seg_len[1] + kPfKeys - 1) / kPfKeys;
+        const int qt = (int) ((a.tq + 15) / 16);  // <= 3: 2-stage ring at two workgroups per CU
         int64_t nsplit = std::min<int64_t>({(kDecTargetWgs + a.heads - 1) / a.heads, nblk, (int64_t) kDecMaxSplits});
         p.split_blocks = (nblk + nsplit - 1) / nsplit;
         nsplit = (nblk + p.split_blocks - 1) / p.split_blocks;
@@ -1038,15 +1057,16 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
             p.part_l = p.part_m + (size_t) nsplit * a.heads * a.tq;
         }
         const dim3 grid((unsigned) a.heads, 1, (unsigned) nsplit), block(kPfWaves * 64);
-        switch ((a.tq + 15) / 16) {
-            case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, block, 0, s, p); break;
-            case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, block, 0, s, p); break;
-            case 3: hipLaunchKernelGGL(attn_decode_kernel<3>, grid, block, 0, s, p); break;
-            default: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, block, 0, s, p); break;
+        switch (qt) {
+            case 1: hipLaunchKernelGGL((attn_decode_kernel<1, 2>), grid, block, 0, s, p); break;
+            case 2: hipLaunchKernelGGL((attn_decode_kernel<2, 2>), grid, block, 0, s, p); break;
+            case 3: hipLaunchKernelGGL((attn_decode_kernel<3, 2>), grid, block, 0, s, p); break;
+            default: hipLaunchKernelGGL((attn_decode_kernel<4, 4>), grid, block, 0, s, p); break;
         }
-        if (nsplit > 1)
-            hipLaunchKernelGGL(attn_merge_kernel<kDecMaxSplits>, dim3((unsigned) (a.heads * a.tq)), dim3(kDh), 0, s, p,
-                               (int) nsplit);
+        const dim3 mgrid((unsigned) (a.heads * a.tq)), mblock(kDh);
+        if (nsplit > 16) hipLaunchKernelGGL(attn_merge_kernel<kDecMaxSplits>, mgrid, mblock, 0, s, p, (int) nsplit);
+        else if (nsplit > 8) hipLaunchKernelGGL(attn_merge_kernel<16>, mgrid, mblock, 0, s, p, (int) nsplit);
+        else if (nsplit > 1) hipLaunchKernelGGL(attn_merge_kernel<8>, mgrid, mblock, 0, s, p, (int) nsplit);
         return hipGetLastError();
     }
     // Up to 128 queries over long key sources: the LDS-tiled prefill kernel,
