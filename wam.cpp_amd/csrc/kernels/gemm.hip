@@ -949,17 +949,27 @@ enum { kPostNormAffine = 1, kPostNormModF32, kPostNormModBf16, kPostSegs };
 
 // The value store_out_t<E> writes (same rounding points), as f32, for the 8
 // outputs m .. m+7 of token row n.
+// The epilogue inputs of 8 outputs (bias, residual, gate), loaded ahead of
+// the values they combine with.
 template <int E>
-__device__ __forceinline__ void epi_vals(const GemmParams & p, int64_t n, int64_t m, const float (&acc)[8],
-                                         float (&o)[8]) {
+struct EpiIn {
+    float b[8], h[8], g[8];
+};
+template <int E>
+__device__ __forceinline__ void epi_load(const GemmParams & p, int64_t n, int64_t m, EpiIn<E> & in) {
+    if constexpr (E != kEpiBf16) unpack8(*(const uint4 *) (p.bias + m), in.b);
+    if constexpr (E >= kEpiBiasGated) unpack8(*(const uint4 *) (p.res + n * p.ldres + m), in.h);
+    if constexpr (E == kEpiBiasGated) load8_f32(p.gate + m, in.g);
+}
+template <int E>
+__device__ __forceinline__ void epi_apply(const EpiIn<E> & in, const float (&acc)[8], float (&o)[8]) {
     if constexpr (E == kEpiBf16) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = round_bf16(acc[e]);
     } else {
-        float b[8], h[8] = {}, g[8] = {};
-        unpack8(*(const uint4 *) (p.bias + m), b);
-        if constexpr (E >= kEpiBiasGated) unpack8(*(const uint4 *) (p.res + n * p.ldres + m), h);
-        if constexpr (E == kEpiBiasGated) load8_f32(p.gate + m, g);
+        const float(&b)[8] = in.b;
+        const float(&h)[8] = in.h;
+        const float(&g)[8] = in.g;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const float a = round_bf16(acc[e]) + b[e];
@@ -1000,9 +1010,29 @@ __global__ __launch_bounds__(512) void skinny_reduce_row(GemmParams p, const flo
     const RowSegDev & sg = rp.seg[POST == kPostSegs ? blockIdx.y : 0];
     const int64_t m = (POST == kPostSegs ? sg.col : 0) + 8 * c;
     const float * src = part + n * p.M + m;
-    // Every split is requested before the first sum (in batches of kB), so
-    // the row costs one memory round trip per batch; the sums run in split
-    // order, as in gemm_skinny_reduce.
+    // The row op's and the epilogue's inputs are requested first, then every
+    // split (in batches of kB), so the row costs one memory round trip; the
+    // sums run in split order, as in gemm_skinny_reduce.
+    EpiIn<E> ein;
+    epi_load<E>(p, n, m, ein);
+    constexpr bool kNorm = POST != kPostSegs;
+    constexpr bool kAffine = POST == kPostNormAffine, kSsBf16 = POST != kPostNormModF32;
+    float a[8], b[8];
+    uint4 wv = make_uint4(0, 0, 0, 0);
+    RopeTok rt{};
+    if constexpr (kNorm) {
+        const int64_t so = n * rp.ss + 8 * c;
+        if constexpr (kSsBf16) {
+            unpack8(*(const uint4 *) ((const uint16_t *) rp.scale + so), a);
+            unpack8(*(const uint4 *) ((const uint16_t *) rp.shift + so), b);
+        } else {
+            load8_f32((const float *) rp.scale + so, a);
+            load8_f32((const float *) rp.shift + so, b);
+        }
+    } else if (sg.kind == kRowSegQk) {
+        wv = *(const uint4 *) (sg.w + 8 * c);
+        rt = rope_tok(sg.rope_mode, sg.pos0, sg.pos1, sg.pos2, n, sg.l2ts128, sg.l2ts44, sg.l2ts42);
+    }
     constexpr int kB = 20;
     float acc[8];
     for (int sp0 = 0; sp0 < splits; sp0 += kB) {
@@ -1016,28 +1046,16 @@ __global__ __launch_bounds__(512) void skinny_reduce_row(GemmParams p, const flo
                 for (int e = 0; e < 8; ++e) acc[e] = sp0 + u == 0 ? t[u][e] : acc[e] + t[u][e];
     }
     float v[1][8];
-    epi_vals<E>(p, n, m, acc, v[0]);
+    epi_apply<E>(ein, acc, v[0]);
     *(uint4 *) ((uint16_t *) p.y + n * p.ldy + m) = pack8(v[0]);
 
-    if constexpr (POST != kPostSegs) {
-        constexpr bool kAffine = POST == kPostNormAffine, kSsBf16 = POST != kPostNormModF32;
-        float a[8], b[8];
-        const int64_t so = n * rp.ss + 8 * c;
-        if constexpr (kSsBf16) {
-            unpack8(*(const uint4 *) ((const uint16_t *) rp.scale + so), a);
-            unpack8(*(const uint4 *) ((const uint16_t *) rp.shift + so), b);
-        } else {
-            load8_f32((const float *) rp.scale + so, a);
-            load8_f32((const float *) rp.shift + so, b);
-        }
+    if constexpr (kNorm) {
         float mean, inv_std;
         row_mean_istd<1>(v, (int) blockDim.x, (int) p.M, rp.eps, red, mean, inv_std);
         *(uint4 *) (rp.out + n * rp.ldo + 8 * c) = norm_chunk<kAffine>(v[0], mean, inv_std, a, b);
     } else {
         const int hd = rp.head_dim, e0 = 8 * c, h = e0 / hd, dd0 = e0 % hd;
         if (sg.kind == kRowSegQk) {
-            const uint4 wv = *(const uint4 *) (sg.w + 8 * c);
-            const RopeTok rt = rope_tok(sg.rope_mode, sg.pos0, sg.pos1, sg.pos2, n, sg.l2ts128, sg.l2ts44, sg.l2ts42);
             const float inv_rms = row_inv_rms<1>(v, rp.width, sg.eps, red);
             *(uint4 *) (sg.dst + ((int64_t) h * sg.dst_tokens + sg.tok0 + n) * hd + dd0) =
                 qk_chunk(v[0], inv_rms, wv, dd0, rt);
