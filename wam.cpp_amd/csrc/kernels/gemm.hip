@@ -92,6 +92,22 @@ __device__ __forceinline__ void store_out(const GemmParams & p, void * yb, const
     }
 }
 
+// store_out with the bias, residual and gate values already loaded.
+__device__ __forceinline__ void store_pre(const GemmParams & p, void * yb, int64_t n, int64_t m, float acc, float bias,
+                                          float res, float gate) {
+    const int64_t yi = n * p.ldy + m;
+    switch (epi_kind(p)) {
+        case kEpiF32: ((float *) yb)[yi] = acc; return;
+        case kEpiBf16: ((uint16_t *) yb)[yi] = f32_to_bf16(acc); return;
+        case kEpiBias: ((uint16_t *) yb)[yi] = f32_to_bf16(round_bf16(acc) + bias); return;
+        case kEpiBiasGelu: ((uint16_t *) yb)[yi] = f32_to_bf16(gelu_tanh(round_bf16(acc) + bias)); return;
+        case kEpiBiasGated:
+            ((uint16_t *) yb)[yi] = f32_to_bf16(fmaf(round_bf16(round_bf16(acc) + bias), gate, res));
+            return;
+        default: ((uint16_t *) yb)[yi] = f32_to_bf16(res + round_bf16(round_bf16(acc) + bias)); return;
+    }
+}
+
 // 8 consecutive activations as packed bf16 (f32 sources rounded RNE).
 template <bool XF32>
 __device__ __forceinline__ uint4 load_x8(const void * x, int64_t idx) {
@@ -915,6 +931,16 @@ __global__ __launch_bounds__(256) void gemm_skinny_reduce(GemmParams p, const fl
     const int64_t total = p.N * p.M;
     const int64_t i0 = ((int64_t) blockIdx.x * 256 + threadIdx.x) * V;
     if (i0 >= total) return;
+    const int64_t n = i0 / p.M, m = i0 % p.M;
+    // Epilogue inputs first, so the outputs cost one memory round trip.
+    const int ek = epi_kind(p);
+    float bias[V] = {}, res[V] = {}, gate[V] = {};
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        if (ek >= kEpiBias) bias[e] = bf16_to_f32(p.bias[m + e]);
+        if (ek >= kEpiBiasGated) res[e] = bf16_to_f32(p.res[n * p.ldres + m + e]);
+        if (ek == kEpiBiasGated) gate[e] = p.gate[m + e];
+    }
     fv_t s = *(const fv_t *) (part + i0);
     constexpr int kBatch = 8;
     for (int sp0 = 1; sp0 < splits; sp0 += kBatch) {
@@ -925,9 +951,8 @@ __global__ __launch_bounds__(256) void gemm_skinny_reduce(GemmParams p, const fl
         for (int u = 0; u < kBatch; ++u)
             if (sp0 + u < splits) s += v[u];
     }
-    const int64_t n = i0 / p.M, m = i0 % p.M;
 #pragma unroll
-    for (int e = 0; e < V; ++e) store_out(p, p.y, p.res, n, m + e, s[e]);
+    for (int e = 0; e < V; ++e) store_pre(p, p.y, n, m + e, s[e], bias[e], res[e], gate[e]);
 }
 
 // ---------------------------------------------------------------------------
