@@ -653,6 +653,174 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_dma(GemmParams p, int 
 }
 
 // ---------------------------------------------------------------------------
+// gemm_dma_pipe: gemm_dma's LDS-DMA ring (BK = 32, S >= 3 stages) with a
+// software-pipelined step.  The compiler's wait insertion cannot tell the
+// ring's LDS stages apart and drains every in-flight copy before the first
+// fragment read after a barrier; here the fragment reads are explicit
+// ds_read_b128 instructions with explicit lgkmcnt waits, so only the wait
+// this schedule asks for is taken:
+//   step kt: issue the reads of k-step 1 of tile kt; wait for k-step 0's
+//   reads; MFMAs of k-step 0; wait for tile kt+1's copies and barrier (every
+//   wave is past tile kt-1); refill tile kt-1's stage with tile kt+S-1; wait
+//   for k-step 1's reads; issue k-step 0's reads of tile kt+1; MFMAs of
+//   k-step 1.
+// Scheduling barriers keep the MFMA groups on their side of the waits.  Same
+// tiles, swizzle, accumulation order and epilogue as gemm_dma: same bits.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t lds_addr(const void * ptr) {
+    return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) void *) ptr;
+}
+template <int OFF>
+__device__ __forceinline__ bf16x8_t ds_read128(uint32_t addr) {
+    bf16x8_t v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+    return v;
+}
+// At most N LDS operations of this wave outstanding; the fragments are tied
+// to the wait so no use of them is scheduled above it.
+template <int N, int FR, int FC>
+__device__ __forceinline__ void lgkm_wait(bf16x8_t (&a)[FR], bf16x8_t (&b)[FC]) {
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
+#pragma unroll
+    for (int i = 0; i < FR; ++i) asm volatile("" : "+v"(a[i]));
+#pragma unroll
+    for (int j = 0; j < FC; ++j) asm volatile("" : "+v"(b[j]));
+}
+
+template <int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_dma_pipe(GemmParams p, int nt_m, int nt_n) {
+    constexpr int BK = 32;
+    using C = DmaCfg<BM, BN, WM, WN, BK, S>;
+    constexpr int FR = C::FR, FC = C::FC, P = C::P, E = C::kStageElems, CH = C::kChunks;
+    static_assert(S >= 3, "the mid-step barrier needs three or more stages");
+    static_assert(FR <= 4 && FC <= 4, "fragment count");
+    __shared__ __align__(16) uint16_t st0[E];
+    __shared__ __align__(16) uint16_t st1[E];
+    __shared__ __align__(16) uint16_t st2[E];
+    __shared__ __align__(16) uint16_t st3[S > 3 ? E : 8];
+    __shared__ __align__(16) uint16_t st4[S > 4 ? E : 8];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave / WN, wc = wave % WN;
+    int tm, tn;
+    tile_coords((int) blockIdx.x, nt_m, nt_n, tm, tn);
+    const int64_t n0 = (int64_t) tn * BM, m0 = (int64_t) tm * BN;
+    const int64_t N = p.N, M = p.M;
+    const int nk = (int) (p.K / BK);
+    const char * src[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const int slot = (i * C::kWaves + wave) * 64 + lane;
+        const int r = slot / CH, c = (slot % CH) ^ dma_swz<BK>(slot / CH);
+        if (r < BM) {
+            const int64_t n = min(n0 + r, N - 1);
+            src[i] = (const char *) ((const uint16_t *) p.x + n * p.ldx + 8 * c);
+        } else {
+            const int64_t m = min(m0 + (r - BM), M - 1);
+            src[i] = (const char *) (p.w + m * p.ldw + 8 * c);
+        }
+    }
+    uint16_t * const stp[5] = {st0, st1, st2, S > 3 ? st3 : st0, S > 4 ? st4 : st0};
+    auto dma = [&](int kt, int stage) {
+        const int64_t koff = (int64_t) min(kt, nk - 1) * BK * 2;
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+            __builtin_amdgcn_global_load_lds((glb_void_t *) (src[i] + koff),
+                                             (lds_void_t *) (stp[stage] + (i * C::kWaves + wave) * 64 * 8), 16, 0, 0);
+    };
+
+    f32x16_t acc[FR][FC];
+#pragma unroll
+    for (int i = 0; i < FR; ++i)
+#pragma unroll
+        for (int j = 0; j < FC; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    // Byte offsets of this lane's fragments in a stage, per 16-wide k-step.
+    const int arow = wr * C::kWaveM + (lane & 31);
+    const int brow = BM + wc * C::kWaveN + (lane & 31);
+    const int sw = dma_swz<BK>(lane & 31);
+    uint32_t aoff[2], boff[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int ko = ((2 * ks + (lane >> 5)) ^ sw) * 8;
+        aoff[ks] = (uint32_t) (arow * BK + ko) * 2;
+        boff[ks] = (uint32_t) (brow * BK + ko) * 2;
+    }
+    const uint32_t sbase[5] = {lds_addr(st0), lds_addr(st1), lds_addr(st2), lds_addr(stp[3]), lds_addr(stp[4])};
+
+    constexpr int RS = 32 * BK * 2;  // bytes between fragment rows 32 apart
+    bf16x8_t a0[FR], b0[FC], a1[FR], b1[FC];
+    auto read = [&](bf16x8_t (&a)[FR], bf16x8_t (&b)[FC], int stage, int ks) {
+        const uint32_t ab = sbase[stage] + aoff[ks], bb = sbase[stage] + boff[ks];
+        a[0] = ds_read128<0>(ab);
+        if constexpr (FR > 1) a[1] = ds_read128<RS>(ab);
+        if constexpr (FR > 2) a[2] = ds_read128<2 * RS>(ab);
+        if constexpr (FR > 3) a[3] = ds_read128<3 * RS>(ab);
+        b[0] = ds_read128<0>(bb);
+        if constexpr (FC > 1) b[1] = ds_read128<RS>(bb);
+        if constexpr (FC > 2) b[2] = ds_read128<2 * RS>(bb);
+        if constexpr (FC > 3) b[3] = ds_read128<3 * RS>(bb);
+    };
+    auto mma = [&](bf16x8_t (&a)[FR], bf16x8_t (&b)[FC]) {
+#pragma unroll
+        for (int i = 0; i < FR; ++i)
+#pragma unroll
+            for (int j = 0; j < FC; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    };
+    auto step = [&](int kt, int cur) {
+        const int nxt = cur + 1 == S ? 0 : cur + 1, prv = cur == 0 ? S - 1 : cur - 1;
+        read(a1, b1, cur, 1);
+        lgkm_wait<FR + FC>(a0, b0);
+        mma(a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 3) * P));  // tile kt+1 landed
+        cta_barrier();
+        dma(kt + S - 1, prv);
+        lgkm_wait<0>(a1, b1);
+        if (kt + 1 < nk) read(a0, b0, nxt, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i) dma(i, i);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * P));
+    cta_barrier();
+    read(a0, b0, 0, 0);
+    for (int kt = 0; kt < nk; kt += S) {
+        step(kt, 0);
+        if (kt + 1 < nk) step(kt + 1, 1);
+        if (kt + 2 < nk) step(kt + 2, 2);
+        if constexpr (S > 3)
+            if (kt + 3 < nk) step(kt + 3, 3);
+        if constexpr (S > 4)
+            if (kt + 4 < nk) step(kt + 4, 4);
+    }
+    // Drain the ring's trailing (clamped, unused) refills before the LDS is
+    // reused by the epilogue.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+    const int64_t nb = n0 + wr * C::kWaveM, mb = m0 + wc * C::kWaveN;
+    constexpr int REG = 32 * (C::kWaveN + 8), WPS = E / REG;
+    static_assert(WPS >= 1 && WPS * S >= C::kWaves, "staging regions must fit in the ring");
+    __syncthreads();
+    const int sa = wave / WPS;
+    uint16_t * region = (sa == 0 ? st0 : sa == 1 ? st1 : sa == 2 ? st2 : sa == 3 ? stp[3] : stp[4]) + (wave % WPS) * REG;
+    uint16_t * y = (uint16_t *) p.y;
+    switch (epi_kind(p)) {
+        case kEpiBias: tile_store_lds<kEpiBias>(p, y, p.res, acc, nb, mb, lane, region); break;
+        case kEpiBiasGelu: tile_store_lds<kEpiBiasGelu>(p, y, p.res, acc, nb, mb, lane, region); break;
+        case kEpiBiasGated: tile_store_lds<kEpiBiasGated>(p, y, p.res, acc, nb, mb, lane, region); break;
+        case kEpiBiasResidual: tile_store_lds<kEpiBiasResidual>(p, y, p.res, acc, nb, mb, lane, region); break;
+        default: tile_store_lds<kEpiBf16>(p, y, p.res, acc, nb, mb, lane, region); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // gemm_skinny: N <= 64 tokens (the 48-token action expert), HBM-bound weight
 // streaming in two kernels.
 //
@@ -1250,26 +1418,36 @@ static hipError_t run_dma(const GemmParams & p, hipStream_t s) {
                        p, nt_m, nt_n);
     return hipGetLastError();
 }
+// The pipelined form (BK 32) for vector-stored bf16 outputs, else gemm_dma.
+template <int BM, int BN, int WM, int WN, int S, int BKF, int SF>
+static hipError_t run_dma_pipe(const GemmParams & p, hipStream_t s) {
+    if (!p.vec_out) return run_dma<BM, BN, WM, WN, BKF, SF>(p, s);
+    const int nt_m = (int) ((p.M + BN - 1) / BN), nt_n = (int) ((p.N + BM - 1) / BM);
+    hipLaunchKernelGGL((gemm_dma_pipe<BM, BN, WM, WN, S>), dim3((unsigned) (nt_m * nt_n)), dim3(64 * WM * WN), 0, s,
+                       p, nt_m, nt_n);
+    return hipGetLastError();
+}
 
 static int64_t tiles_of(const GemmParams & p, int bm, int bn) { return ((p.N + bm - 1) / bm) * ((p.M + bn - 1) / bn); }
 
 // Tile shape of the bf16 x bf16 DMA path, chosen so the grid fills the 256 CUs
 // (measured on the 3072-token products of the prefix pass):
-//  * 256 x 256, BK 32, 3 stages, 8 waves: when it gives at least one tile per
-//    CU (QKV 9216 x 3072, FFN-up 14336 x 3072);
-//  * 192 x 192, BK 64, 3 stages, 4 waves: 3072 x 3072 products, which it cuts
-//    into exactly 256 tiles (256 x 256 leaves 112 CUs idle);
+//  * 256 x 256, 8 waves: when it gives at least one tile per CU (QKV 9216 x
+//    3072, FFN-up 14336 x 3072), pipelined with BK 32 and 4 stages;
+//  * 192 x 192, 4 waves: 3072 x 3072 products, which it cuts into exactly 256
+//    tiles (256 x 256 leaves 112 CUs idle), pipelined with BK 32 and 4 stages;
+//  (f32 or unaligned outputs take gemm_dma with BK 32 / 64 and 3 stages);
 //  * 128 x 128, BK 64, 2 stages, 4 waves, two workgroups per CU: small grids
 //    (512-token prompt projections).
 // Returns false when the shape does not meet the path's preconditions.
 static bool dispatch_dma(const GemmParams & p, hipStream_t s, hipError_t & err) {
     if (p.K % 32 != 0) return false;
     if (tiles_of(p, 256, 256) >= 256) {
-        err = run_dma<256, 256, 4, 2, 32, 3>(p, s);
+        err = run_dma_pipe<256, 256, 4, 2, 4, 32, 3>(p, s);
         return true;
     }
     if (p.K % 64 != 0) return false;
-    if (tiles_of(p, 192, 192) >= 192) err = run_dma<192, 192, 2, 2, 64, 3>(p, s);
+    if (tiles_of(p, 192, 192) >= 192) err = run_dma_pipe<192, 192, 2, 2, 4, 64, 3>(p, s);
     else err = run_dma<128, 128, 2, 2, 64, 2>(p, s);
     return true;
 }
