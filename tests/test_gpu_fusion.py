@@ -166,3 +166,34 @@ def test_qkv_split_is_bit_exact(wx, be, rng, T):
         assert np.array_equal(got_vt, rq[:, 2 * D:].reshape(T, H, DH).transpose(1, 2, 0))
     finally:
         g.close()
+
+
+@pytest.mark.parametrize("T,k0", [(3072, 1), (512, 0), (100, 3), (40, 0)])
+def test_v_transpose_store_is_exact(wx, be, rng, T, k0):
+    """The V^T store of the attention caches (CPY of a permuted token-major
+    view into [head][dim][token] at token offset k0): the tiled transposing
+    copy (T >= 64) and the generic strided copy give the transposed bits."""
+    print(f"V^T store T={T} k0={k0}", flush=True)
+    lib = be.lib
+    g = Graph(wx, be)
+    try:
+        width = 3 * D
+        src = g.t(wx.TYPE_BF16, width, T)
+        ld = (k0 + T + 63) // 64 * 64
+        vraw = g.t(wx.TYPE_BF16, ld, DH, H)
+        pitch = src.contents.nb[1]
+        vsrc = lib.wamx_permute(g.ctx, lib.wamx_view_3d(g.ctx, src, DH, H, T, DH * 2, pitch, 4 * D), 1, 2, 0, 3)
+        vdst = lib.wamx_view_3d(g.ctx, vraw, T, DH, H, vraw.contents.nb[1], vraw.contents.nb[2], 2 * k0)
+        v = lib.wamx_cpy(g.ctx, vsrc, vdst)
+        g.alloc()
+        hs = wx.f32_to_bf16(rng.standard_normal(width * T).astype(np.float32)).reshape(T, width)
+        fill = np.full(ld * DH * H, 0x7777, np.uint16)
+        g.set(src, hs)
+        g.set(vraw, fill)
+        g.compute(v)
+        got = g.get(vraw, np.uint16, (H, DH, ld))
+        want = fill.reshape(H, DH, ld).copy()
+        want[:, :, k0:k0 + T] = hs[:, 2 * D:].reshape(T, H, DH).transpose(1, 2, 0)
+        assert np.array_equal(got, want)
+    finally:
+        g.close()

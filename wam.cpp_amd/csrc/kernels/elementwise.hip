@@ -70,6 +70,29 @@ __global__ void copy_kernel(Ref4 src, Ref4 dst, int64_t n) {
     }
 }
 
+// A copy between two same-shape views of 2-byte elements that transposes
+// dims 0 and 1 in memory: dst's dim 0 and src's dim 1 are contiguous (the
+// V^T store of the attention caches: token-major V -> [head][dim][token]).
+// 64 x 64 tiles through LDS, so both the reads (along dim 1) and the writes
+// (along dim 0) are consecutive addresses across consecutive threads.
+__global__ __launch_bounds__(256) void transpose01_kernel(Ref4 src, Ref4 dst) {
+    __shared__ uint16_t tile[64][66];
+    const int64_t b0 = (int64_t) blockIdx.x * 64, b1 = (int64_t) blockIdx.y * 64;
+    const int64_t i2 = blockIdx.z % src.ne2, i3 = blockIdx.z / src.ne2;
+    const int t = threadIdx.x;
+#pragma unroll 4
+    for (int k = 0; k < 16; ++k) {
+        const int idx = k * 256 + t, r = idx >> 6, c = idx & 63;  // r: dim 0, c: dim 1
+        if (b0 + r < src.ne0 && b1 + c < src.ne1) tile[r][c] = *(const uint16_t *) at(src, b0 + r, b1 + c, i2, i3);
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int k = 0; k < 16; ++k) {
+        const int idx = k * 256 + t, r = idx >> 6, c = idx & 63;  // r: dim 1, c: dim 0
+        if (b0 + c < dst.ne0 && b1 + r < dst.ne1) *(uint16_t *) at(dst, b0 + c, b1 + r, i2, i3) = tile[c][r];
+    }
+}
+
 __global__ void binary_kernel(int op, Ref4 a, Ref4 b, Ref4 dst, int64_t n) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -245,6 +268,16 @@ hipError_t launch_copy(const TensorRef & src, const TensorRef & dst, hipStream_t
     const int64_t n = nel(dst);
     if (n <= 0) return hipSuccess;
     if (nel(src) != n) return hipErrorInvalidValue;
+    const bool two_byte = src.type == dst.type && (src.type == WAMX_TYPE_BF16 || src.type == WAMX_TYPE_F16);
+    const bool same_shape =
+        src.ne[0] == dst.ne[0] && src.ne[1] == dst.ne[1] && src.ne[2] == dst.ne[2] && src.ne[3] == dst.ne[3];
+    if (two_byte && same_shape && dst.nb[0] == 2 && src.nb[1] == 2 && src.nb[0] != 2 && src.ne[0] >= 64 &&
+        src.ne[1] >= 16) {
+        const dim3 grid((unsigned) ((src.ne[0] + 63) / 64), (unsigned) ((src.ne[1] + 63) / 64),
+                        (unsigned) (src.ne[2] * src.ne[3]));
+        hipLaunchKernelGGL(transpose01_kernel, grid, dim3(256), 0, s, to_ref4(src), to_ref4(dst));
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(copy_kernel, grid1d(n), dim3(256), 0, s, to_ref4(src), to_ref4(dst), n);
     return hipGetLastError();
 }
