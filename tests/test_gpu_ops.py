@@ -224,7 +224,8 @@ def test_qk_norm_rope(wx, be, orc, rng, mode):
 # Cases reach every kernel:
 #  * LDS-tiled flash kernel (key rows 16-byte aligned, V^T rows a multiple of 8
 #    keys): prefill (tq > 64, one source, ragged query and key blocks, 3073
-#    queries) and key-split decode over one or two sources (48 queries);
+#    queries) and key-split decode over one or two sources (48 queries), with
+#    16-query groups over short sources (ragged last group);
 #  * register-streamed key-split decode and its single-workgroup form (V^T rows
 #    a multiple of 4 keys only);
 #  * the generic many-query kernel (two sources, tq > 64).
@@ -232,7 +233,7 @@ def test_qk_norm_rope(wx, be, orc, rng, mode):
                                               (3, 200, 200, 0, 0), (2, 48, 512, 0, 0), (1, 1, 4, 4, 2),
                                               (2, 3073, 3072, 0, 0), (1, 130, 520, 0, 0), (2, 100, 96, 8, 1),
                                               (8, 48, 3080, 48, 1), (3, 48, 520, 0, 0), (2, 17, 64, 8, 1),
-                                              (1, 64, 200, 16, 1)])
+                                              (1, 64, 200, 16, 1), (5, 40, 700, 24, 1)])
 def test_joint_attention(wx, be, orc, H, tq, na, nb, split):
     print(f"joint_attn H={H} tq={tq} na={na} nb={nb}", flush=True)
     rng = np.random.default_rng(H * tq + na)

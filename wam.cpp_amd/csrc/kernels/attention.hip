@@ -706,7 +706,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
 
 // ---------------------------------------------------------------------------
 // attn_decode: softmax(scale * Q K^T) V for at most 64 queries (the 48-token
-// denoise step) over long key sources, one workgroup per (head, key range).
+// denoise step) over long key sources, one workgroup per (head, group of
+// 16*QT queries, key range).
 //
 // All four waves work on real queries: in every 64-key block (the attn_prefill
 // K / V^T tiles, same LDS layout and swizzle) wave w takes keys 16w..16w+15
@@ -740,6 +741,7 @@ __global__ __launch_bounds__(kPfWaves * 64, S == 2 ? 2 : 1) void attn_decode_ker
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c16 = lane & 15;
     const int64_t h = blockIdx.x;
+    const int64_t q0 = (int64_t) blockIdx.y * 16 * QT;  // first query of this workgroup's group
     const int nblk_a = (int) ((p.seg_len[0] + kPfKeys - 1) / kPfKeys);
     const int nblk = nblk_a + (int) ((p.seg_len[1] + kPfKeys - 1) / kPfKeys);
     const int b_begin = (int) blockIdx.z * (int) p.split_blocks;
@@ -754,7 +756,7 @@ __global__ __launch_bounds__(kPfWaves * 64, S == 2 ? 2 : 1) void attn_decode_ker
     bf16x8_t qf[QT][4];
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-        const int64_t qi = min((int64_t) (16 * t + c16), p.tq - 1);
+        const int64_t qi = min(q0 + 16 * t + c16, p.tq - 1);
         const uint16_t * qrow = p.q + (h * p.tq + qi) * kDh + 8 * g;
 #pragma unroll
         for (int c = 0; c < 4; ++c) qf[t][c] = *(const bf16x8_t *) (qrow + 32 * c);
@@ -903,7 +905,7 @@ __global__ __launch_bounds__(kPfWaves * 64, S == 2 ? 2 : 1) void attn_decode_ker
     }
     constexpr int kRegion = 16 * QT * kDecHalf;  // floats per wave
     float * const rows = (float *) &ring[0][0];
-    const int nq = (int) min((int64_t) (16 * QT), p.tq);
+    const int nq = (int) min((int64_t) (16 * QT), p.tq - q0);
     const bool split = gridDim.z > 1;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -933,7 +935,7 @@ __global__ __launch_bounds__(kPfWaves * 64, S == 2 ? 2 : 1) void attn_decode_ker
                 acc.w += v.w;
             }
             if (split) {
-                const int64_t pi = ((int64_t) blockIdx.z * p.heads + h) * p.tq + q;
+                const int64_t pi = ((int64_t) blockIdx.z * p.heads + h) * p.tq + q0 + q;
                 *(float4 *) (p.part_o + pi * kDh + d) = acc;
                 if (d == 0) {
                     p.part_m[pi] = s_mstar[q];
@@ -941,7 +943,7 @@ __global__ __launch_bounds__(kPfWaves * 64, S == 2 ? 2 : 1) void attn_decode_ker
                 }
             } else {
                 const float l = s_lstar[q], inv = l > 0.0f ? 1.0f / l : 0.0f;
-                *(uint2 *) (p.out + (int64_t) q * (p.heads * kDh) + h * kDh + d) =
+                *(uint2 *) (p.out + (q0 + q) * (p.heads * kDh) + h * kDh + d) =
                     make_uint2(pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv));
             }
         }
@@ -984,6 +986,11 @@ constexpr int kDecMaxSplits = 32;
 // stream but add partial traffic and merge work (measured best on the
 // 24-head, 3121-key denoise shape at 10 ranges).
 constexpr int kDecTargetWgs = 256;
+// Sources of at most this many 64-key blocks (the 512-key prompt) are split
+// by query tile as well: measured on 24 heads x 48 queries x 512 keys, 16-query
+// workgroups in 4 key ranges take 10.3 us against 12.3 us for 48-query
+// workgroups in 8 ranges (decode + merge).
+constexpr int64_t kDecShortBlocks = 16;
 
 // Softmax is order-free, so the keys are visited per source in 32-key blocks
 // aligned to each source's start: source a ([state, reference] prefix cache,
@@ -1042,8 +1049,14 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     // are merged by attn_merge_kernel.
     if (flash && a.tq <= 16 * 4) {
         const int64_t nblk = (p.seg_len[0] + kPfKeys - 1) / kPfKeys + (p.seg_len[1] + kPfKeys - 1) / kPfKeys;
-        const int qt = (int) ((a.tq + 15) / 16);  // <= 3: 2-stage ring at two workgroups per CU
-        int64_t nsplit = std::min<int64_t>({(kDecTargetWgs + a.heads - 1) / a.heads, nblk, (int64_t) kDecMaxSplits});
+        // Query tiles of 16 per workgroup: all queries (<= 3: 2-stage ring at
+        // two workgroups per CU), or one tile per workgroup when the source is
+        // short (few key ranges per head would leave most CUs idle, and the
+        // per-block cost falls with the query count).
+        const int qt = nblk <= kDecShortBlocks ? 1 : (int) ((a.tq + 15) / 16);
+        const int64_t qg = (a.tq + 16 * qt - 1) / (16 * qt);
+        int64_t nsplit =
+            std::min<int64_t>({(kDecTargetWgs + a.heads * qg - 1) / (a.heads * qg), nblk, (int64_t) kDecMaxSplits});
         p.split_blocks = (nblk + nsplit - 1) / nsplit;
         nsplit = (nblk + p.split_blocks - 1) / p.split_blocks;
         const size_t part_bytes = (size_t) nsplit * a.heads * a.tq * (kDh + 2) * sizeof(float);
@@ -1056,7 +1069,7 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
             p.part_m = p.part_o + (size_t) nsplit * a.heads * a.tq * kDh;
             p.part_l = p.part_m + (size_t) nsplit * a.heads * a.tq;
         }
-        const dim3 grid((unsigned) a.heads, 1, (unsigned) nsplit), block(kPfWaves * 64);
+        const dim3 grid((unsigned) a.heads, (unsigned) qg, (unsigned) nsplit), block(kPfWaves * 64);
         switch (qt) {
             case 1: hipLaunchKernelGGL((attn_decode_kernel<1, 2>), grid, block, 0, s, p); break;
             case 2: hipLaunchKernelGGL((attn_decode_kernel<2, 2>), grid, block, 0, s, p); break;
