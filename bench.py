@@ -168,8 +168,8 @@ def workload_ffn(be, args):
     up_ms = time_op(be, up, 10)
     down_ms = time_op(be, down, 10)
     norm_ms = time_op(be, norm, 20)
-    dom_ms, dom = (up_ms, "gemm_dma<256,256> (FFN up + bias + GELU)") if up_ms >= down_ms else \
-        (down_ms, "gemm_dma<128,128> (FFN down + bias + gated residual)")
+    dom_ms, dom = (up_ms, "gemm_dma_pipe (FFN up + bias + GELU)") if up_ms >= down_ms else \
+        (down_ms, "gemm_dma_pipe (FFN down + bias + gated residual)")
     roof = {"bound": "mfma", "achieved": gemm_flops / (dom_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": gemm_flops / (dom_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "traffic": None,
             "kernel": dom, "kernel_ms": dom_ms,
@@ -285,7 +285,7 @@ def workload_chunk(be, args):
     aup_bytes = Fa * Da * 2 + Ta * Da * 2 + Ta * Fa * 2 + Fa * 2
     roof = {"bound": "mfma", "achieved": flops / (up_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": flops / (up_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "traffic": measured_traffic("gemm_dma_ffn_up"),
-            "kernel": "gemm_dma<256,256>: prefix visual FFN-up 3072 tok x [14336 x 3072] + bias + GELU",
+            "kernel": "gemm_dma_pipe<256,256>: prefix visual FFN-up 3072 tok x [14336 x 3072] + bias + GELU",
             "kernel_ms": up_ms, "flops_per_launch": flops,
             "algorithmic_bytes": T * D * 2 + F * D * 2 + F * 2 + T * F * 2,
             "skinny": {"kernel": "gemm_skinny_tiled + gemm_skinny_reduce: denoise FFN-up 48 tok x [14336 x 3072] (tiled) "
