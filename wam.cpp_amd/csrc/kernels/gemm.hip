@@ -668,14 +668,23 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_dma(GemmParams p, int 
 // Scheduling barriers keep the MFMA groups on their side of the waits.  Same
 // tiles, swizzle, accumulation order and epilogue as gemm_dma: same bits.
 //
-// PP (ping-pong, 8 waves): waves 0-3 and 4-7 (one of each per SIMD) run the
-// same sequence of K steps, [memory phase: both k-steps' fragment reads of
-// tile kt + this wave's copies of tile kt+S-1; barrier; MFMA phase; barrier],
-// with waves 4-7 one barrier behind.  At every barrier interval one wave of
-// each SIMD reads LDS and issues copies while the other issues MFMAs, so the
-// two never compete for the same phase.  Waits: tile kt+1's copies must have
-// landed by the barrier before either group's memory phase of kt+1.
+// SCHED selects how the waves share the step:
+//  kSchedSingle: every wave runs the step above.
+//  kSchedPingPong (8 waves): waves 0-3 and 4-7 (one of each per SIMD) run the
+//    same sequence of K steps, [memory phase: both k-steps' fragment reads of
+//    tile kt + this wave's copies of tile kt+S-1; barrier; MFMA phase;
+//    barrier], with waves 4-7 one barrier behind.  At every barrier interval
+//    one wave of each SIMD reads LDS and issues copies while the other issues
+//    MFMAs.  Tile kt+1's copies must have landed by the barrier before either
+//    group's memory phase of kt+1.
+//  kSchedProducer: WM*WN consumer waves run the step without copies, and as
+//    many producer waves (launched after them, a second wave per SIMD) issue
+//    every copy, wait for tile kt+1 and meet the consumers at the step's
+//    barrier.  The producers' registers are the consumers' allocation, so the
+//    consumers must fit in 256.
 // ---------------------------------------------------------------------------
+enum { kSchedSingle = 0, kSchedPingPong, kSchedProducer };
+
 __device__ __forceinline__ uint32_t lds_addr(const void * ptr) {
     return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) void *) ptr;
 }
@@ -696,13 +705,16 @@ __device__ __forceinline__ void lgkm_wait(bf16x8_t (&a)[FR], bf16x8_t (&b)[FC]) 
     for (int j = 0; j < FC; ++j) asm volatile("" : "+v"(b[j]));
 }
 
-template <int BM, int BN, int WM, int WN, int S, bool PP = false>
-__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_dma_pipe(GemmParams p, int nt_m, int nt_n) {
+template <int BM, int BN, int WM, int WN, int S, int SCHED = kSchedSingle>
+__global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1) void gemm_dma_pipe(
+    GemmParams p, int nt_m, int nt_n) {
     constexpr int BK = 32;
     using C = DmaCfg<BM, BN, WM, WN, BK, S>;
     constexpr int FR = C::FR, FC = C::FC, P = C::P, E = C::kStageElems, CH = C::kChunks;
+    constexpr bool PP = SCHED == kSchedPingPong, kProd = SCHED == kSchedProducer;
     static_assert(S >= 3, "the mid-step barrier needs three or more stages");
     static_assert(!PP || WM * WN == 8, "ping-pong pairs two waves per SIMD");
+    static_assert(!kProd || WM * WN == 4, "producers take the second wave of each SIMD");
     static_assert(FR <= 4 && FC <= 4, "fragment count");
     __shared__ __align__(16) uint16_t st0[E];
     __shared__ __align__(16) uint16_t st1[E];
@@ -711,6 +723,10 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_dma_pipe(GemmParams p, i
     __shared__ __align__(16) uint16_t st4[S > 4 ? E : 8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // Producer waves (kSchedProducer) follow the consumers; `cw` is the wave's
+    // index within its role, which fixes its share of each stage's copies.
+    const bool producer = kProd && wave >= C::kWaves;
+    const int cw = producer ? wave - C::kWaves : wave;
     const int wr = wave / WN, wc = wave % WN;
     int tm, tn;
     tile_coords((int) blockIdx.x, nt_m, nt_n, tm, tn);
@@ -720,7 +736,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_dma_pipe(GemmParams p, i
     const char * src[P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-        const int slot = (i * C::kWaves + wave) * 64 + lane;
+        const int slot = (i * C::kWaves + cw) * 64 + lane;
         const int r = slot / CH, c = (slot % CH) ^ dma_swz<BK>(slot / CH);
         if (r < BM) {
             const int64_t n = min(n0 + r, N - 1);
@@ -736,8 +752,36 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_dma_pipe(GemmParams p, i
 #pragma unroll
         for (int i = 0; i < P; ++i)
             __builtin_amdgcn_global_load_lds((glb_void_t *) (src[i] + koff),
-                                             (lds_void_t *) (stp[stage] + (i * C::kWaves + wave) * 64 * 8), 16, 0, 0);
+                                             (lds_void_t *) (stp[stage] + (i * C::kWaves + cw) * 64 * 8), 16, 0, 0);
     };
+
+    if constexpr (kProd) {
+        if (producer) {
+            // Step kt: tile kt+1 lands before the step's barrier; after it the
+            // stage of tile kt-1 (every consumer is past it) takes tile kt+S-1.
+            auto pstep = [&](int kt, int cur) {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 3) * P));
+                cta_barrier();
+                dma(kt + S - 1, cur == 0 ? S - 1 : cur - 1);
+            };
+#pragma unroll
+            for (int i = 0; i < S - 1; ++i) dma(i, i);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * P));
+            cta_barrier();
+            for (int kt = 0; kt < nk; kt += S) {
+                pstep(kt, 0);
+                if (kt + 1 < nk) pstep(kt + 1, 1);
+                if (kt + 2 < nk) pstep(kt + 2, 2);
+                if constexpr (S > 3)
+                    if (kt + 3 < nk) pstep(kt + 3, 3);
+                if constexpr (S > 4)
+                    if (kt + 4 < nk) pstep(kt + 4, 4);
+            }
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            __syncthreads();  // the consumers' barrier before the epilogue
+            return;
+        }
+    }
 
     f32x16_t acc[FR][FC];
 #pragma unroll
@@ -786,9 +830,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_dma_pipe(GemmParams p, i
         lgkm_wait<FR + FC>(a0, b0);
         mma(a0, b0);
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 3) * P));  // tile kt+1 landed
+        if constexpr (!kProd) __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 3) * P));  // tile kt+1 landed
         cta_barrier();
-        dma(kt + S - 1, prv);
+        if constexpr (!kProd) dma(kt + S - 1, prv);
         lgkm_wait<0>(a1, b1);
         if (kt + 1 < nk) read(a0, b0, nxt, 0);
         __builtin_amdgcn_sched_barrier(0);
@@ -820,9 +864,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_dma_pipe(GemmParams p, i
         cta_barrier();
     };
 
+    if constexpr (!kProd) {
 #pragma unroll
-    for (int i = 0; i < S - 1; ++i) dma(i, i);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * P));
+        for (int i = 0; i < S - 1; ++i) dma(i, i);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * P));
+    }
     cta_barrier();
     if constexpr (PP) {
         using I0 = std::integral_constant<int, 0>;
@@ -1477,12 +1523,13 @@ static hipError_t run_dma(const GemmParams & p, hipStream_t s) {
     return hipGetLastError();
 }
 // The pipelined form (BK 32) for vector-stored bf16 outputs, else gemm_dma.
-template <int BM, int BN, int WM, int WN, int S, int BKF, int SF, bool PP = false>
+template <int BM, int BN, int WM, int WN, int S, int BKF, int SF, int SCHED = kSchedSingle>
 static hipError_t run_dma_pipe(const GemmParams & p, hipStream_t s) {
     if (!p.vec_out) return run_dma<BM, BN, WM, WN, BKF, SF>(p, s);
     const int nt_m = (int) ((p.M + BN - 1) / BN), nt_n = (int) ((p.N + BM - 1) / BM);
-    hipLaunchKernelGGL((gemm_dma_pipe<BM, BN, WM, WN, S, PP>), dim3((unsigned) (nt_m * nt_n)), dim3(64 * WM * WN), 0,
-                       s, p, nt_m, nt_n);
+    const int threads = 64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1);
+    hipLaunchKernelGGL((gemm_dma_pipe<BM, BN, WM, WN, S, SCHED>), dim3((unsigned) (nt_m * nt_n)), dim3(threads), 0, s,
+                       p, nt_m, nt_n);
     return hipGetLastError();
 }
 
@@ -1494,7 +1541,8 @@ static int64_t tiles_of(const GemmParams & p, int bm, int bn) { return ((p.N + b
 //    3072, FFN-up 14336 x 3072), ping-pong with BK 32 and 4 stages (6-9%
 //    faster than the single-group schedule on both);
 //  * 192 x 192, 4 waves: 3072 x 3072 products, which it cuts into exactly 256
-//    tiles (256 x 256 leaves 112 CUs idle), pipelined with BK 32 and 4 stages;
+//    tiles (256 x 256 leaves 112 CUs idle), pipelined with BK 32 and 4 stages,
+//    copies issued by 4 producer waves (2-4% faster on O and FFN-down);
 //  (f32 or unaligned outputs take gemm_dma with BK 32 / 64 and 3 stages);
 //  * 128 x 128, BK 64, 2 stages, 4 waves, two workgroups per CU: small grids
 //    (512-token prompt projections).
@@ -1502,11 +1550,11 @@ static int64_t tiles_of(const GemmParams & p, int bm, int bn) { return ((p.N + b
 static bool dispatch_dma(const GemmParams & p, hipStream_t s, hipError_t & err) {
     if (p.K % 32 != 0) return false;
     if (tiles_of(p, 256, 256) >= 256) {
-        err = run_dma_pipe<256, 256, 4, 2, 4, 32, 3, true>(p, s);
+        err = run_dma_pipe<256, 256, 4, 2, 4, 32, 3, kSchedPingPong>(p, s);
         return true;
     }
     if (p.K % 64 != 0) return false;
-    if (tiles_of(p, 192, 192) >= 192) err = run_dma_pipe<192, 192, 2, 2, 4, 64, 3>(p, s);
+    if (tiles_of(p, 192, 192) >= 192) err = run_dma_pipe<192, 192, 2, 2, 4, 64, 3, kSchedProducer>(p, s);
     else err = run_dma<128, 128, 2, 2, 64, 2>(p, s);
     return true;
 }
