@@ -75,6 +75,52 @@ __global__ void copy_kernel(Ref4 src, Ref4 dst, int64_t n) {
 // V^T store of the attention caches: token-major V -> [head][dim][token]).
 // 64 x 64 tiles through LDS, so both the reads (along dim 1) and the writes
 // (along dim 0) are consecutive addresses across consecutive threads.
+// transpose01_kernel with 16-byte global accesses: src dim 1 and dst dim 0
+// contiguous, 16-byte aligned rows, ne1 % 8 == 0 (every source chunk is whole;
+// destination chunks past ne0 are written element by element).  A 64 x 64
+// tile per workgroup: 512 source chunks of 8 elements are loaded (two per
+// thread, both issued before the LDS stores), transposed through LDS and
+// stored as 512 destination chunks.
+__global__ __launch_bounds__(256) void transpose01_vec_kernel(Ref4 src, Ref4 dst) {
+    __shared__ uint32_t tile[64][33];  // tile[r][j]: elements 2j, 2j+1 of source row r
+    const int64_t b0 = (int64_t) blockIdx.x * 64, b1 = (int64_t) blockIdx.y * 64;
+    const int64_t i2 = blockIdx.z % src.ne2, i3 = blockIdx.z / src.ne2;
+    const int t = threadIdx.x;
+    uint4 v[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int q = k * 256 + t, r = q >> 3, c8 = q & 7;
+        const bool ok = b0 + r < src.ne0 && b1 + 8 * c8 < src.ne1;
+        v[k] = ok ? *(const uint4 *) at(src, b0 + r, b1 + 8 * c8, i2, i3) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int q = k * 256 + t, r = q >> 3, c8 = q & 7;
+        tile[r][4 * c8] = v[k].x;
+        tile[r][4 * c8 + 1] = v[k].y;
+        tile[r][4 * c8 + 2] = v[k].z;
+        tile[r][4 * c8 + 3] = v[k].w;
+    }
+    __syncthreads();
+    const uint16_t * tl = (const uint16_t *) &tile[0][0];  // element (r, c) at r * 66 + c
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int q = k * 256 + t, d = q >> 3, c8 = q & 7;  // destination row b1 + d, elements b0 + 8 c8 ..
+        if (b1 + d >= dst.ne1) continue;
+        uint16_t e[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = tl[(8 * c8 + i) * 66 + d];
+        const int64_t j0 = b0 + 8 * c8;
+        if (j0 + 8 <= dst.ne0) {
+            *(uint4 *) at(dst, j0, b1 + d, i2, i3) =
+                make_uint4(e[0] | (uint32_t) e[1] << 16, e[2] | (uint32_t) e[3] << 16, e[4] | (uint32_t) e[5] << 16,
+                           e[6] | (uint32_t) e[7] << 16);
+        } else {
+            for (int i = 0; i < 8 && j0 + i < dst.ne0; ++i) *(uint16_t *) at(dst, j0 + i, b1 + d, i2, i3) = e[i];
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void transpose01_kernel(Ref4 src, Ref4 dst) {
     __shared__ uint16_t tile[64][66];
     const int64_t b0 = (int64_t) blockIdx.x * 64, b1 = (int64_t) blockIdx.y * 64;
@@ -275,7 +321,14 @@ hipError_t launch_copy(const TensorRef & src, const TensorRef & dst, hipStream_t
         src.ne[1] >= 16) {
         const dim3 grid((unsigned) ((src.ne[0] + 63) / 64), (unsigned) ((src.ne[1] + 63) / 64),
                         (unsigned) (src.ne[2] * src.ne[3]));
-        hipLaunchKernelGGL(transpose01_kernel, grid, dim3(256), 0, s, to_ref4(src), to_ref4(dst));
+        auto a16 = [](const void * p, int64_t a, int64_t b, int64_t c) {
+            return (((uintptr_t) p | (uintptr_t) a | (uintptr_t) b | (uintptr_t) c) & 15) == 0;
+        };
+        if (src.ne[1] % 8 == 0 && a16(src.data, src.nb[0], src.nb[2], src.nb[3]) &&
+            a16(dst.data, dst.nb[1], dst.nb[2], dst.nb[3]))
+            hipLaunchKernelGGL(transpose01_vec_kernel, grid, dim3(256), 0, s, to_ref4(src), to_ref4(dst));
+        else
+            hipLaunchKernelGGL(transpose01_kernel, grid, dim3(256), 0, s, to_ref4(src), to_ref4(dst));
         return hipGetLastError();
     }
     hipLaunchKernelGGL(copy_kernel, grid1d(n), dim3(256), 0, s, to_ref4(src), to_ref4(dst), n);
