@@ -168,13 +168,13 @@ def test_qkv_split_is_bit_exact(wx, be, rng, T):
         g.close()
 
 
-@pytest.mark.parametrize("T,k0", [(3072, 1), (512, 0), (3073, 0), (130, 0), (100, 3), (40, 0)])
+@pytest.mark.parametrize("T,k0", [(3072, 1), (512, 0), (3073, 0), (130, 0), (130, 7), (100, 3), (40, 0)])
 def test_v_transpose_store_is_exact(wx, be, rng, T, k0):
     """The V^T store of the attention caches (CPY of a permuted token-major
     view into [head][dim][token] at token offset k0): the tiled transposing
-    copy (T >= 64; 16-byte accesses when the destination offset is aligned,
-    with a ragged last tile at T = 3073 and 130) and the generic strided copy
-    give the transposed bits."""
+    copy (T >= 64; 16-byte accesses, the destination offset k0 taken as a
+    shift of the 16-byte grid, ragged first and last tiles) and the generic
+    strided copy give the transposed bits."""
     print(f"V^T store T={T} k0={k0}", flush=True)
     lib = be.lib
     g = Graph(wx, be)

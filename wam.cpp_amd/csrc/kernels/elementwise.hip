@@ -76,13 +76,16 @@ __global__ void copy_kernel(Ref4 src, Ref4 dst, int64_t n) {
 // 64 x 64 tiles through LDS, so both the reads (along dim 1) and the writes
 // (along dim 0) are consecutive addresses across consecutive threads.
 // transpose01_kernel with 16-byte global accesses: src dim 1 and dst dim 0
-// contiguous, 16-byte aligned rows, ne1 % 8 == 0 (every source chunk is whole;
-// destination chunks past ne0 are written element by element).  A 64 x 64
-// tile per workgroup: 512 source chunks of 8 elements are loaded (two per
-// thread, both issued before the LDS stores), transposed through LDS and
-// stored as 512 destination chunks.
-__global__ __launch_bounds__(256) void transpose01_vec_kernel(Ref4 src, Ref4 dst) {
-    __shared__ uint32_t tile[64][33];  // tile[r][j]: elements 2j, 2j+1 of source row r
+// contiguous, ne1 % 8 == 0 and 16-byte aligned row strides.  The destination
+// may start `mis` elements past a 16-byte boundary (a cache written from token
+// 1): `dst` is then the aligned view `mis` elements earlier, and destination
+// element j holds source row j - mis.  A 64 x 64 tile of the destination's
+// 16-byte grid per workgroup: 512 source chunks of 8 elements are loaded (two
+// per thread, both issued before the LDS stores), transposed through LDS and
+// stored as 512 destination chunks; chunks that are not whole inside
+// [mis, ne0 of dst) are written element by element.
+__global__ __launch_bounds__(256) void transpose01_vec_kernel(Ref4 src, Ref4 dst, int mis) {
+    __shared__ uint32_t tile[64][33];  // tile[r][j]: elements 2j, 2j+1 of source row b0 + r - mis
     const int64_t b0 = (int64_t) blockIdx.x * 64, b1 = (int64_t) blockIdx.y * 64;
     const int64_t i2 = blockIdx.z % src.ne2, i3 = blockIdx.z / src.ne2;
     const int t = threadIdx.x;
@@ -90,8 +93,9 @@ __global__ __launch_bounds__(256) void transpose01_vec_kernel(Ref4 src, Ref4 dst
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int q = k * 256 + t, r = q >> 3, c8 = q & 7;
-        const bool ok = b0 + r < src.ne0 && b1 + 8 * c8 < src.ne1;
-        v[k] = ok ? *(const uint4 *) at(src, b0 + r, b1 + 8 * c8, i2, i3) : make_uint4(0, 0, 0, 0);
+        const int64_t sr = b0 + r - mis;
+        const bool ok = sr >= 0 && sr < src.ne0 && b1 + 8 * c8 < src.ne1;
+        v[k] = ok ? *(const uint4 *) at(src, sr, b1 + 8 * c8, i2, i3) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -111,12 +115,13 @@ __global__ __launch_bounds__(256) void transpose01_vec_kernel(Ref4 src, Ref4 dst
 #pragma unroll
         for (int i = 0; i < 8; ++i) e[i] = tl[(8 * c8 + i) * 66 + d];
         const int64_t j0 = b0 + 8 * c8;
-        if (j0 + 8 <= dst.ne0) {
+        if (j0 >= mis && j0 + 8 <= dst.ne0) {
             *(uint4 *) at(dst, j0, b1 + d, i2, i3) =
                 make_uint4(e[0] | (uint32_t) e[1] << 16, e[2] | (uint32_t) e[3] << 16, e[4] | (uint32_t) e[5] << 16,
                            e[6] | (uint32_t) e[7] << 16);
         } else {
-            for (int i = 0; i < 8 && j0 + i < dst.ne0; ++i) *(uint16_t *) at(dst, j0 + i, b1 + d, i2, i3) = e[i];
+            for (int i = 0; i < 8; ++i)
+                if (j0 + i >= mis && j0 + i < dst.ne0) *(uint16_t *) at(dst, j0 + i, b1 + d, i2, i3) = e[i];
         }
     }
 }
@@ -324,10 +329,15 @@ hipError_t launch_copy(const TensorRef & src, const TensorRef & dst, hipStream_t
         auto a16 = [](const void * p, int64_t a, int64_t b, int64_t c) {
             return (((uintptr_t) p | (uintptr_t) a | (uintptr_t) b | (uintptr_t) c) & 15) == 0;
         };
-        if (src.ne[1] % 8 == 0 && a16(src.data, src.nb[0], src.nb[2], src.nb[3]) &&
-            a16(dst.data, dst.nb[1], dst.nb[2], dst.nb[3]))
-            hipLaunchKernelGGL(transpose01_vec_kernel, grid, dim3(256), 0, s, to_ref4(src), to_ref4(dst));
-        else
+        const int mis = (int) (((uintptr_t) dst.data & 15) / 2);  // elements past the 16-byte boundary
+        if (src.ne[1] % 8 == 0 && ((uintptr_t) dst.data & 1) == 0 && a16(src.data, src.nb[0], src.nb[2], src.nb[3]) &&
+            a16(nullptr, dst.nb[1], dst.nb[2], dst.nb[3])) {
+            Ref4 dv = to_ref4(dst);
+            dv.data -= 2 * mis;
+            dv.ne0 += mis;
+            const dim3 vgrid((unsigned) ((dv.ne0 + 63) / 64), grid.y, grid.z);
+            hipLaunchKernelGGL(transpose01_vec_kernel, vgrid, dim3(256), 0, s, to_ref4(src), dv, mis);
+        } else
             hipLaunchKernelGGL(transpose01_kernel, grid, dim3(256), 0, s, to_ref4(src), to_ref4(dst));
         return hipGetLastError();
     }
