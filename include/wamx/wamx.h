@@ -141,6 +141,7 @@ typedef struct wamx_tensor {
     void *   data;                         /* device address once allocated */
     char     name[WAMX_MAX_NAME];
     void *   extra;
+    int32_t  lane;                         /* execution lane (0 or 1), set by wamx_set_lane */
 } wamx_tensor;
 
 typedef struct wamx_context wamx_context;
@@ -258,6 +259,13 @@ WAMX_API int           wamx_graph_n_nodes(const wamx_cgraph * g);
 WAMX_API wamx_tensor * wamx_graph_node(wamx_cgraph * g, int i);
 WAMX_API void          wamx_graph_assign_uid(wamx_cgraph * g);   /* native-bf16.patch:700-703 */
 WAMX_API uint64_t      wamx_graph_uid(const wamx_cgraph * g);
+/* Execution lane of the tensors `ctx` creates from now on (0 or 1).  No
+ * counterpart in the reference (ggml schedules a graph on one stream): a
+ * graph whose nodes use both lanes runs lane 1 on a second stream, ordered
+ * against lane 0 only where one lane's node reads or writes memory the other
+ * lane's earlier nodes wrote or read.  Intermediates touched by both lanes are
+ * not recycled by the graph allocator. */
+WAMX_API void          wamx_set_lane(wamx_context * ctx, int lane);
 
 /* ---------------------------------------------------------------------------
  * Backend plugin interface (restating ggml-backend-impl.h, b9866).

@@ -54,6 +54,14 @@ struct wamx_backend {
     wamx_device * dev = nullptr;
     hipStream_t stream = nullptr;
     void * workspace = nullptr;  // K-split partials, reused by consecutive GEMMs on the stream
+    // Lane 1 of two-lane graphs: its own stream and partials workspace, made
+    // on first use.  cs / cws are the stream and workspace of the node being
+    // launched (lane 0's outside a two-lane graph).
+    hipStream_t stream2 = nullptr;
+    void * workspace2 = nullptr;
+    hipStream_t cs = nullptr;
+    void * cws = nullptr;
+    std::vector<hipEvent_t> events;  // cross-lane ordering, reused from graph to graph
     bool use_graphs = true;
     bool fuse_rows = true;       // split-K reduce + consuming row op in one launch
     std::unordered_map<uint64_t, GraphCacheEntry> graphs;
@@ -244,10 +252,10 @@ static hipError_t run_mul_mat(wamx_backend * be, const wamx_tensor * node) {
     g.B3 = b->ne[3];
     g.r2 = b->ne[2] / a->ne[2];
     g.r3 = b->ne[3] / a->ne[3];
-    g.ws = be->workspace;
+    g.ws = be->cws;
     g.ws_bytes = kWorkspaceBytes;
     g.w_tiled = tensor_is_tiled(a);
-    return launch_gemm(g, be->stream);
+    return launch_gemm(g, be->cs);
 }
 
 static GemmArgs linear_args(wamx_backend * be, const wamx_tensor * node) {
@@ -271,14 +279,14 @@ static GemmArgs linear_args(wamx_backend * be, const wamx_tensor * node) {
     g.res = node->src[3] ? node->src[3]->data : nullptr;
     g.ldres = node->src[3] ? (int64_t) node->src[3]->nb[1] / 2 : 0;
     g.gate = node->src[4] ? (const float *) node->src[4]->data : nullptr;
-    g.ws = be->workspace;
+    g.ws = be->cws;
     g.ws_bytes = kWorkspaceBytes;
     g.w_tiled = tensor_is_tiled(w);
     return g;
 }
 
 static hipError_t run_linear(wamx_backend * be, const wamx_tensor * node) {
-    return launch_gemm(linear_args(be, node), be->stream);
+    return launch_gemm(linear_args(be, node), be->cs);
 }
 
 static float param_f32(const wamx_tensor * t, int i) {
@@ -313,9 +321,14 @@ static bool is_noop(const wamx_tensor * t) {
     }
 }
 
-static int next_compute(wamx_cgraph * g, int i, int n) {
-    for (int j = i + 1; j < n; ++j)
-        if (!is_noop(wamx_graph_node(g, j))) return j;
+// Next node after i that launches work; in a two-lane graph (`lanes`) only
+// nodes of node i's lane count, so a LINEAR fuses with its own lane's row ops.
+static int next_compute(wamx_cgraph * g, int i, int n, bool lanes) {
+    const int lane = wamx_graph_node(g, i)->lane;
+    for (int j = i + 1; j < n; ++j) {
+        const wamx_tensor * t = wamx_graph_node(g, j);
+        if (!is_noop(t) && (!lanes || t->lane == lane)) return j;
+    }
     return n;
 }
 
@@ -336,11 +349,11 @@ static bool column_view(const wamx_tensor * x, const wamx_tensor * base, int64_t
 
 // Matches the row ops after LINEAR node i; returns the index of the last node
 // they cover (> i), or -1.
-static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post) {
+static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post, bool lanes) {
     const wamx_tensor * lin = wamx_graph_node(g, i);
     if (lin->type != WAMX_TYPE_BF16 || lin->ne[1] > 64 || lin->ne[2] != 1 || lin->ne[3] != 1 || lin->view_src)
         return -1;
-    int j = next_compute(g, i, n);
+    int j = next_compute(g, i, n, lanes);
     if (j >= n) return -1;
     const wamx_tensor * t = wamx_graph_node(g, j);
     if (t->op == WAMX_OP_NORM) {
@@ -411,7 +424,7 @@ static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post) {
         post.head_dim = head_dim;
         post.seg[post.nseg++] = seg;
         last = j;
-        j = next_compute(g, j, n);
+        j = next_compute(g, j, n, lanes);
     }
     return post.nseg > 0 ? last : -1;
 }
@@ -436,13 +449,13 @@ static hipError_t run_joint_attn(wamx_backend * be, const wamx_tensor * node) {
     a.head_dim = q->ne[0];
     a.tq = q->ne[1];
     a.scale = param_f32(node, 1);
-    a.ws = be->workspace;
+    a.ws = be->cws;
     a.ws_bytes = kWorkspaceBytes;
-    return launch_joint_attn(a, be->stream);
+    return launch_joint_attn(a, be->cs);
 }
 
 static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
-    hipStream_t s = be->stream;
+    hipStream_t s = be->cs;
     wamx_tensor * s0 = node->src[0];
     wamx_tensor * s1 = node->src[1];
     switch (node->op) {
@@ -633,46 +646,171 @@ static uint64_t graph_signature(wamx_cgraph * g) {
     return h;
 }
 
+static const wamx_tensor * root_of_c(const wamx_tensor * t) { return t->view_src ? t->view_src : t; }
+
+// Cross-lane order of a two-lane graph.  Memory is tracked per root tensor
+// (views resolve to their root): a node of lane A follows the latest node of
+// lane B that wrote a root it reads (RAW), wrote or read a root it writes
+// (WAW, WAR).  Within a lane the stream keeps node order, so waiting for the
+// latest such node of the other lane covers every earlier one.  wait_for[i] is
+// that node (-1: none); signal[j] marks the nodes whose completion is waited
+// for.  Returns false when every node is on lane 0.
+static bool plan_lanes(wamx_cgraph * g, std::vector<int> & wait_for, std::vector<char> & signal) {
+    const int n = wamx_graph_n_nodes(g);
+    wait_for.assign(n, -1);
+    signal.assign(n, 0);
+    bool two = false;
+    for (int i = 0; i < n && !two; ++i) two = wamx_graph_node(g, i)->lane != 0;
+    if (!two) return false;
+    struct Use {
+        int write[2] = {-1, -1};
+        int read[2] = {-1, -1};
+    };
+    std::unordered_map<const wamx_tensor *, Use> use;
+    for (int i = 0; i < n; ++i) {
+        const wamx_tensor * node = wamx_graph_node(g, i);
+        if (is_noop(node)) continue;
+        const int a = node->lane ? 1 : 0, b = 1 - a;
+        const wamx_tensor * w = root_of_c(node);
+        int dep = -1;
+        Use & uw = use[w];
+        dep = std::max({dep, uw.write[b], uw.read[b]});
+        for (int k = 0; k < WAMX_MAX_SRC; ++k) {
+            if (!node->src[k]) continue;
+            const wamx_tensor * r = root_of_c(node->src[k]);
+            if (r != w) dep = std::max(dep, use[r].write[b]);
+        }
+        for (int k = 0; k < WAMX_MAX_SRC; ++k) {
+            if (!node->src[k]) continue;
+            const wamx_tensor * r = root_of_c(node->src[k]);
+            if (r != w) use[r].read[a] = i;
+        }
+        use[w].write[a] = i;
+        if (dep >= 0) {
+            wait_for[i] = dep;
+            signal[dep] = 1;
+        }
+    }
+    return true;
+}
+
+static hipError_t ensure_lane1(wamx_backend * be, size_t nevents) {
+    if (!be->stream2 && hipStreamCreate(&be->stream2) != hipSuccess) return hipErrorOutOfMemory;
+    if (!be->workspace2 && hipMalloc(&be->workspace2, kWorkspaceBytes) != hipSuccess) return hipErrorOutOfMemory;
+    while (be->events.size() < nevents) {
+        hipEvent_t e = nullptr;
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return hipErrorOutOfMemory;
+        be->events.push_back(e);
+    }
+    return hipSuccess;
+}
+
+// Launches every node.  In a two-lane graph lane-1 nodes go to the second
+// stream, each node first waits for the other lane's node it must follow
+// (plan_lanes), and nodes the other lane waits for record an event (events 0
+// and 1 fork and join the lanes, signalling nodes use 2, 3, ... in node order).
+// A LINEAR fused with its row ops takes its members' waits and records their
+// events.
 static wamx_status run_nodes(wamx_backend * be, wamx_cgraph * g) {
     const int n = wamx_graph_n_nodes(g);
-    for (int i = 0; i < n; ++i) {
+    std::vector<int> wait_for;
+    std::vector<char> signal;
+    const bool two = plan_lanes(g, wait_for, signal);
+    std::vector<int> slot(n, -1);
+    int nsig = 0;
+    if (two)
+        for (int i = 0; i < n; ++i)
+            if (signal[i]) slot[i] = 2 + nsig++;
+    if (two) {
+        const hipError_t e = ensure_lane1(be, (size_t) nsig + 2);
+        if (e != hipSuccess) {
+            set_error("graph_compute: second lane stream, workspace or events unavailable");
+            return WAMX_STATUS_ALLOC_FAILED;
+        }
+        // Fork: lane 1 starts after everything queued on lane 0 so far.
+        hipEventRecord(be->events[0], be->stream);
+        hipStreamWaitEvent(be->stream2, be->events[0], 0);
+    }
+    std::vector<char> done(n, 0);
+    wamx_status status = WAMX_STATUS_SUCCESS;
+    for (int i = 0; i < n && status == WAMX_STATUS_SUCCESS; ++i) {
+        if (done[i]) continue;
         wamx_tensor * node = wamx_graph_node(g, i);
         for (int k = 0; k < WAMX_MAX_SRC; ++k) {
             const wamx_tensor * s = node->src[k];
             if (s && !s->data && wamx_nelements(s) > 0) {
                 set_errorf("graph_compute: node %d (%s '%s') source %d '%s' has no data", i, wamx_op_name(node->op),
                            node->name, k, s->name);
-                return WAMX_STATUS_FAILED;
+                status = WAMX_STATUS_FAILED;
+                break;
             }
         }
+        if (status != WAMX_STATUS_SUCCESS) break;
         if (!node->data && wamx_nelements(node) > 0) {
             set_errorf("graph_compute: node %d (%s '%s') is not allocated", i, wamx_op_name(node->op), node->name);
-            return WAMX_STATUS_ALLOC_FAILED;
+            status = WAMX_STATUS_ALLOC_FAILED;
+            break;
         }
+        const int lane = two && node->lane ? 1 : 0;
+        be->cs = lane ? be->stream2 : be->stream;
+        be->cws = lane ? be->workspace2 : be->workspace;
+        // Members of this launch: the node, or the LINEAR and its fused row ops.
+        int members[8] = {i};
+        int nm = 1;
+        bool fused = false;
         if (node->op == WAMX_OP_LINEAR && be->fuse_rows) {
             RowPost post;
-            const int last = match_row_post(g, i, n, post);
+            const int last = match_row_post(g, i, n, post, two);
             if (last > i) {
-                const hipError_t ferr = launch_gemm_rowpost(linear_args(be, node), post, be->stream);
-                if (ferr == hipSuccess) {
-                    i = last;
-                    continue;
+                for (int j = i + 1; j <= last && nm < 8; ++j) {
+                    const wamx_tensor * t = wamx_graph_node(g, j);
+                    if (!is_noop(t) && (!two || (t->lane ? 1 : 0) == lane)) members[nm++] = j;
                 }
-                if (ferr != hipErrorNotSupported) {
+                int dep = -1;
+                for (int m = 0; m < nm; ++m) dep = std::max(dep, two ? wait_for[members[m]] : -1);
+                // A member that must follow an other-lane node launched after
+                // this LINEAR cannot run in this launch: run them one by one.
+                hipError_t ferr = hipErrorNotSupported;
+                if (dep <= i) {
+                    if (dep >= 0) hipStreamWaitEvent(be->cs, be->events[slot[dep]], 0);
+                    ferr = launch_gemm_rowpost(linear_args(be, node), post, be->cs);
+                }
+                if (ferr == hipSuccess) {
+                    fused = true;
+                    for (int m = 0; m < nm; ++m) done[members[m]] = 1;
+                } else if (ferr != hipErrorNotSupported) {
                     set_errorf("graph_compute: node %d (%s '%s') with its row ops failed: %s", i,
                                wamx_op_name(node->op), node->name, hipGetErrorString(ferr));
-                    return WAMX_STATUS_FAILED;
+                    status = WAMX_STATUS_FAILED;
+                    break;
+                } else {
+                    nm = 1;
                 }
             }
         }
-        const hipError_t err = compute_node(be, node);
-        if (err != hipSuccess) {
-            set_errorf("graph_compute: node %d (%s '%s') failed: %s", i, wamx_op_name(node->op), node->name,
-                       hipGetErrorString(err));
-            return WAMX_STATUS_FAILED;
+        if (!fused) {
+            if (two && wait_for[i] >= 0) hipStreamWaitEvent(be->cs, be->events[slot[wait_for[i]]], 0);
+            const hipError_t err = compute_node(be, node);
+            if (err != hipSuccess) {
+                set_errorf("graph_compute: node %d (%s '%s') failed: %s", i, wamx_op_name(node->op), node->name,
+                           hipGetErrorString(err));
+                status = WAMX_STATUS_FAILED;
+                break;
+            }
+            done[i] = 1;
         }
+        if (two)
+            for (int m = 0; m < nm; ++m)
+                if (signal[members[m]]) hipEventRecord(be->events[slot[members[m]]], be->cs);
     }
-    return WAMX_STATUS_SUCCESS;
+    if (two) {
+        // Join: lane 0 ends after lane 1's last launch.
+        hipEventRecord(be->events[1], be->stream2);
+        hipStreamWaitEvent(be->stream, be->events[1], 0);
+    }
+    be->cs = be->stream;
+    be->cws = be->workspace;
+    return status;
 }
 
 static void release_graph(GraphCacheEntry & e) {
@@ -839,20 +977,28 @@ struct FreeList {
 
 static wamx_tensor * root_of(wamx_tensor * t) { return t->view_src ? t->view_src : t; }
 
+// Memory plan in node order: a root tensor is placed at its first use and its
+// block recycled after its last use.  In a two-lane graph each lane has its own
+// arena (a lane's nodes run in order on its stream, so reuse inside a lane is
+// safe), and tensors touched by nodes of both lanes are never recycled, since
+// the other lane may still be reading them when a later node of the first
+// lane would take their memory.
 static bool gallocr_alloc(wamx_gallocr * ga, wamx_cgraph * g) {
     const int n = wamx_graph_n_nodes(g);
     std::vector<wamx_tensor *> order;  // tensors that need memory, in first-use order
     std::unordered_map<wamx_tensor *, int> last_use;
     std::unordered_map<wamx_tensor *, int> first_def;
+    std::unordered_map<wamx_tensor *, int> lanes;  // bit l: touched by a lane-l node
     const int kForever = 1 << 30;
     auto needs = [](wamx_tensor * t) { return t && !t->data && !t->view_src && wamx_nelements(t) > 0; };
-    auto touch = [&](wamx_tensor * t, int i) {
+    auto touch = [&](wamx_tensor * t, int i, int lane) {
         wamx_tensor * r = root_of(t);
         if (!needs(r)) return;
         if (!first_def.count(r)) {
             first_def[r] = i;
             order.push_back(r);
         }
+        lanes[r] |= 1 << lane;
         int & lu = last_use[r];
         lu = std::max(lu, i);
         // Graph inputs and outputs stay put; unallocated leaves without the
@@ -863,30 +1009,40 @@ static bool gallocr_alloc(wamx_gallocr * ga, wamx_cgraph * g) {
     };
     for (int i = 0; i < n; ++i) {
         wamx_tensor * node = wamx_graph_node(g, i);
+        const int lane = node->lane ? 1 : 0;
         for (int k = 0; k < WAMX_MAX_SRC; ++k)
-            if (node->src[k]) touch(node->src[k], i);
-        touch(node, i);
+            if (node->src[k]) touch(node->src[k], i, lane);
+        touch(node, i, lane);
     }
+    for (auto * t : order)
+        if (lanes[t] == 3) last_use[t] = kForever;
     // Leaf inputs and tensors first touched as sources are live from the start.
-    FreeList fl;
+    FreeList fl[2];
+    auto arena = [&](wamx_tensor * t) { return lanes[t] == 2 ? 1 : 0; };
     std::unordered_map<wamx_tensor *, size_t> offset;
     std::vector<std::vector<wamx_tensor *>> frees(n);
     for (auto * t : order)
         if (last_use[t] < n) frees[last_use[t]].push_back(t);
     auto size_of = [](wamx_tensor * t) { return align_up(wamx_nbytes(t), kAlign); };
+    auto place = [&](wamx_tensor * t) { offset[t] = fl[arena(t)].alloc(size_of(t)); };
     for (auto * t : order)
-        if (first_def[t] == 0 || (t->flags & WAMX_TENSOR_FLAG_INPUT)) offset[t] = fl.alloc(size_of(t));
+        if (first_def[t] == 0 || (t->flags & WAMX_TENSOR_FLAG_INPUT)) place(t);
     for (int i = 0; i < n; ++i) {
         wamx_tensor * node = wamx_graph_node(g, i);
         for (int k = 0; k < WAMX_MAX_SRC; ++k) {
             wamx_tensor * r = node->src[k] ? root_of(node->src[k]) : nullptr;
-            if (r && needs(r) && !offset.count(r)) offset[r] = fl.alloc(size_of(r));
+            if (r && needs(r) && !offset.count(r)) place(r);
         }
         wamx_tensor * r = root_of(node);
-        if (needs(r) && !offset.count(r)) offset[r] = fl.alloc(size_of(r));
-        for (auto * t : frees[i]) fl.release(offset[t], size_of(t));
+        if (needs(r) && !offset.count(r)) place(r);
+        for (auto * t : frees[i]) fl[arena(t)].release(offset[t], size_of(t));
     }
-    const size_t total = std::max<size_t>(fl.high, kAlign);
+    // Lane 1's arena follows lane 0's.
+    const size_t base1 = align_up(fl[0].high, kAlign);
+    for (auto & kv : offset)
+        if (arena(kv.first) == 1) kv.second += base1;
+    const size_t high = base1 + fl[1].high;
+    const size_t total = std::max<size_t>(high, kAlign);
     if (!ga->buffer || ga->buffer->size < total) {
         if (ga->buffer) buffer_free(ga->buffer);
         ga->buffer = buft_alloc_buffer(wamx_backend_get_default_buffer_type(ga->be), total);
@@ -949,6 +1105,8 @@ wamx_backend_t wamx_backend_init(int device) {
         be_free(be);
         return nullptr;
     }
+    be->cs = be->stream;
+    be->cws = be->workspace;
     return be;
 }
 
@@ -956,7 +1114,11 @@ static void be_free(wamx_backend_t be) {
     if (!be) return;
     hipSetDevice(be->dev->index);
     if (be->stream) hipStreamSynchronize(be->stream);
+    if (be->stream2) hipStreamSynchronize(be->stream2);
     for (auto & kv : be->graphs) release_graph(kv.second);
+    for (hipEvent_t e : be->events) hipEventDestroy(e);
+    if (be->workspace2) hipFree(be->workspace2);
+    if (be->stream2) hipStreamDestroy(be->stream2);
     if (be->workspace) hipFree(be->workspace);
     if (be->stream) hipStreamDestroy(be->stream);
     delete be;

@@ -451,41 +451,53 @@ static bool build_prefix_graph(wamx_gwp_model * m) {
     Builder b(m, ctx);
     wamx_cgraph * g = m->graph[1] = wamx_new_graph(ctx, 160 * c.n_layers + 512);
 
+    // The state token's chain (its expert projections, row ops and attention
+    // query) runs on lane 1, concurrently with the visual tokens' on lane 0;
+    // the two meet only through the prefix K/V cache of each layer.
+    wamx_set_lane(ctx, 1);
     wamx_tensor * sh = b.mlp3(m->state_enc, m->in_state);  // [da, 1]
+    wamx_tensor *stemb, *smod;
+    b.condition(m->acond, m->in_freq0, &stemb, &smod);
+    wamx_tensor * amods = wamx_modulation(ctx, smod, m->a_tables);  // [da, 6, L] f32
+    wamx_set_lane(ctx, 0);
     // Patch embedding: conv 2x2 stride 2 as im2col + bf16 MUL_MAT + bias (cache.cpp:203-218).
     wamx_tensor * cols = wamx_im2col(ctx, m->patch_w, m->in_latent, 2, 2, 0, 0, 1, 1, WAMX_TYPE_BF16);
     cols = wamx_reshape_2d(ctx, cols, cols->ne[0], nimg);
     wamx_tensor * pw = wamx_reshape_2d(ctx, m->patch_w, 4 * (int64_t) c.z_dim, d);
     wamx_tensor * vh = b.lin(pw, m->patch_b, cols);  // [d, nimg]
 
-    wamx_tensor *stemb, *smod, *vtemb, *vmod;
-    b.condition(m->acond, m->in_freq0, &stemb, &smod);
+    wamx_tensor *vtemb, *vmod;
     // Every visual token has the timestep-0 embedding; its condition rows are
     // identical, so one row is computed and broadcast (bit-identical).
     b.condition(m->vcond, m->in_freq0, &vtemb, &vmod);
     wamx_tensor * vtext = b.text(m->vcond, m->in_prompt);
     wamx_tensor * vkv = b.lin(m->kv_w[1], m->kv_b[1], vtext);  // every layer's text K/V [2·L·d, NL]
-    wamx_tensor * amods = wamx_modulation(ctx, smod, m->a_tables);  // [da, 6, L] f32
     wamx_tensor * vmods = wamx_modulation(ctx, vmod, m->v_tables);  // [d, 6, L] f32
 
     for (int l = 0; l < c.n_layers; ++l) {
         const ExpertLayer & ea = m->act[l];
         const ExpertLayer & ev = m->vis[l];
+        // State token (lane 1): its Q, and row 0 of the layer's K / V^T cache
+        // (1-D rope at position 0).
+        wamx_set_lane(ctx, 1);
         wamx_tensor * sn = wamx_norm_modulation_bf16(ctx, sh, b.part(amods, da, l, 1), b.part(amods, da, l, 0), c.eps);
         wamx_tensor * sqkv = b.lin(ea.qkv_w, ea.qkv_b, sn);
-        wamx_tensor * vn = wamx_norm_modulation_bf16(ctx, vh, b.part(vmods, d, l, 1), b.part(vmods, d, l, 0), c.eps);
-        wamx_tensor * vqkv = b.lin(ev.qkv_w, ev.qkv_b, vn);
-        // Q [dh, P, H] and K (prefix storage) in [state, visual] order: 1-D rope at
-        // position 0 for the state, 3-D {44,42,42} rope for the visual tokens.
-        wamx_tensor * Q = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, dh, P, H);
-        Q = wamx_qk_norm_rope(ctx, b.cols(sqkv, d, 0), ea.norm_q, Q, 0, 0, m->in_spos, nullptr, nullptr, c.eps, 10000.0f);
-        Q = wamx_qk_norm_rope(ctx, b.cols(vqkv, d, 0), ev.norm_q, Q, 1, 1, m->in_vt, m->in_vh, m->in_vw, c.eps,
-                              10000.0f);
+        wamx_tensor * Qs = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, dh, 1, H);
+        Qs = wamx_qk_norm_rope(ctx, b.cols(sqkv, d, 0), ea.norm_q, Qs, 0, 0, m->in_spos, nullptr, nullptr, c.eps,
+                               10000.0f);
         wamx_tensor * K = wamx_qk_norm_rope(ctx, b.cols(sqkv, d, d), ea.norm_k, m->pk[l], 0, 0, m->in_spos, nullptr,
                                             nullptr, c.eps, 10000.0f);
+        wamx_tensor * v0 = b.store_v(sqkv, 2 * d, b.vt_view(m->pv_raw[l], 0, 1));
+        // Visual tokens (lane 0): their Q, and rows 1..P of the cache (3-D
+        // {44,42,42} rope).
+        wamx_set_lane(ctx, 0);
+        wamx_tensor * vn = wamx_norm_modulation_bf16(ctx, vh, b.part(vmods, d, l, 1), b.part(vmods, d, l, 0), c.eps);
+        wamx_tensor * vqkv = b.lin(ev.qkv_w, ev.qkv_b, vn);
+        wamx_tensor * Qv = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, dh, nimg, H);
+        Qv = wamx_qk_norm_rope(ctx, b.cols(vqkv, d, 0), ev.norm_q, Qv, 0, 1, m->in_vt, m->in_vh, m->in_vw, c.eps,
+                               10000.0f);
         K = wamx_qk_norm_rope(ctx, b.cols(vqkv, d, d), ev.norm_k, K, 1, 1, m->in_vt, m->in_vh, m->in_vw, c.eps,
                               10000.0f);
-        wamx_tensor * v0 = b.store_v(sqkv, 2 * d, b.vt_view(m->pv_raw[l], 0, 1));
         wamx_tensor * v1 = b.store_v(vqkv, 2 * d, after(b.vt_view(m->pv_raw[l], 1, nimg), v0));
         wamx_tensor * V = after(b.vt_view(m->pv_raw[l], 0, P), v1);
         wamx_set_output(K);
@@ -493,16 +505,20 @@ static bool build_prefix_graph(wamx_gwp_model * m) {
         wamx_build_forward_expand(g, K);
         wamx_build_forward_expand(g, V);
         if (l + 1 == c.n_layers) break;  // the last layer's K/V are the outputs
-        wamx_tensor * att = wamx_joint_attn(ctx, Q, K, V, nullptr, nullptr, 0, b.scale);  // [d, P]
-        wamx_tensor * satt = wamx_view_2d(ctx, att, d, 1, att->nb[1], 0);
-        wamx_tensor * vatt = wamx_view_2d(ctx, att, d, nimg, att->nb[1], att->nb[1]);
-        sh = b.lin(ea.o_w, ea.o_b, satt, WAMX_EPI_BIAS_GATED, sh, b.part(amods, da, l, 2));
+        // Joint attention over [state, visual] keys, per query set: a query's
+        // output does not depend on the other queries.
+        wamx_tensor * vatt = wamx_joint_attn(ctx, Qv, K, V, nullptr, nullptr, 0, b.scale);  // [d, nimg]
         vh = b.lin(ev.o_w, ev.o_b, vatt, WAMX_EPI_BIAS_GATED, vh, b.part(vmods, d, l, 2));
-        sh = b.cross_ffn_cached(ea, sh, m->lk[l], m->lv[l], b.part(amods, da, l, 3), b.part(amods, da, l, 4),
-                                b.part(amods, da, l, 5));
         vh = b.cross_ffn_uncached(ev, vh, vkv, l, b.part(vmods, d, l, 3), b.part(vmods, d, l, 4),
                                   b.part(vmods, d, l, 5));
+        wamx_set_lane(ctx, 1);
+        wamx_tensor * satt = wamx_joint_attn(ctx, Qs, K, V, nullptr, nullptr, 0, b.scale);  // [d, 1]
+        sh = b.lin(ea.o_w, ea.o_b, satt, WAMX_EPI_BIAS_GATED, sh, b.part(amods, da, l, 2));
+        sh = b.cross_ffn_cached(ea, sh, m->lk[l], m->lv[l], b.part(amods, da, l, 3), b.part(amods, da, l, 4),
+                                b.part(amods, da, l, 5));
+        wamx_set_lane(ctx, 0);
     }
+    wamx_set_lane(ctx, 0);
     wamx_graph_assign_uid(g);
     m->galloc[1] = wamx_gallocr_new(m->be);
     return m->galloc[1] && wamx_gallocr_alloc_graph(m->galloc[1], g);

@@ -38,6 +38,7 @@ struct wamx_context {
     std::vector<std::unique_ptr<wamx_tensor>> tensors;
     std::vector<std::unique_ptr<wamx_cgraph>> graphs;
     size_t max_tensors = 0;
+    int32_t lane = 0;  // lane of the tensors created from now on
 };
 
 struct wamx_cgraph {
@@ -70,6 +71,7 @@ static wamx_tensor * new_tensor_impl(wamx_context * ctx, int32_t type, int n_dim
     t->nb[0] = wamx_type_size(type);
     for (int i = 1; i < WAMX_MAX_DIMS; ++i) t->nb[i] = t->nb[i - 1] * (size_t)t->ne[i - 1];
     t->op = WAMX_OP_NONE;
+    t->lane = ctx->lane;
     wamx_tensor * raw = t.get();
     ctx->tensors.push_back(std::move(t));
     return raw;
@@ -174,6 +176,10 @@ void wamx_set_name(wamx_tensor * t, const char * name) {
 }
 void wamx_set_input(wamx_tensor * t) { if (t) t->flags |= WAMX_TENSOR_FLAG_INPUT; }
 void wamx_set_output(wamx_tensor * t) { if (t) t->flags |= WAMX_TENSOR_FLAG_OUTPUT; }
+
+void wamx_set_lane(wamx_context * ctx, int lane) {
+    if (ctx) ctx->lane = lane ? 1 : 0;
+}
 
 wamx_tensor * wamx_new_tensor(wamx_context * ctx, int32_t type, int n_dims, const int64_t * ne) {
     if (n_dims < 1 || n_dims > WAMX_MAX_DIMS) return fail("wamx_new_tensor");

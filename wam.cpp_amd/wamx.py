@@ -47,6 +47,7 @@ Tensor._fields_ = [
     ("data", C.c_void_p),
     ("name", C.c_char * 64),
     ("extra", C.c_void_p),
+    ("lane", C.c_int32),
 ]
 TensorP = C.POINTER(Tensor)
 
@@ -123,6 +124,7 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_set_name": (None, [TensorP, C.c_char_p]),
         "wamx_set_input": (None, [TensorP]),
         "wamx_set_output": (None, [TensorP]),
+        "wamx_set_lane": (None, [vp, C.c_int]),
         "wamx_new_tensor_1d": (TensorP, [vp, i32, i64]),
         "wamx_new_tensor_2d": (TensorP, [vp, i32, i64, i64]),
         "wamx_new_tensor_3d": (TensorP, [vp, i32, i64, i64, i64]),
