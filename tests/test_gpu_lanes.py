@@ -111,3 +111,43 @@ def test_two_lanes_match_one_lane(wx, be, rng, capture):
     finally:
         one.close()
         two.close()
+
+
+def test_allocator_keeps_lanes_apart(wx, be):
+    """A tensor that lane 1 writes first and lane 0 reads later must not take
+    memory lane 0 has recycled: lane 0 may still be running the nodes that
+    used it.  It goes to lane 1's arena, away from every lane-0 intermediate."""
+    lib = be.lib
+    ctx = lib.wamx_init(64)
+    pctx = lib.wamx_init(16)
+    bf = wx.TYPE_BF16
+    try:
+        w = lib.wamx_new_tensor_2d(pctx, bf, D, D)
+        b = lib.wamx_new_tensor_1d(pctx, bf, D)
+        x = lib.wamx_new_tensor_2d(pctx, bf, D, T)
+        pbuf = lib.wamx_backend_alloc_ctx_tensors(pctx, be.ptr)
+        assert pbuf, wx.last_error()
+        lin = lambda a: lib.wamx_linear(ctx, w, a, b, wx.EPI_BIAS, None, None)
+        lib.wamx_set_lane(ctx, 0)
+        p1 = lin(x)
+        p2 = lin(p1)          # p1 is recycled after this node
+        lib.wamx_set_lane(ctx, 1)
+        z = lin(x)            # first touched on lane 1, read by lane 0 below
+        lib.wamx_set_lane(ctx, 0)
+        out = lib.wamx_linear(ctx, w, z, b, wx.EPI_BIAS_RESIDUAL, p2, None)
+        lib.wamx_set_output(out)
+        g = lib.wamx_new_graph(ctx, 64)
+        lib.wamx_build_forward_expand(g, p2)  # node order: p1, p2, z, out
+        lib.wamx_build_forward_expand(g, out)
+        ga = lib.wamx_gallocr_new(be.ptr)
+        try:
+            assert lib.wamx_gallocr_alloc_graph(ga, g), wx.last_error()
+            nbytes = D * T * 2
+            zs, ps = z.contents.data, p1.contents.data
+            assert zs + nbytes <= ps or ps + nbytes <= zs, "lane-1 tensor placed in recycled lane-0 memory"
+        finally:
+            lib.wamx_gallocr_free(ga)
+        lib.wamx_buffer_free(pbuf)
+    finally:
+        lib.wamx_free(ctx)
+        lib.wamx_free(pctx)

@@ -979,16 +979,18 @@ static wamx_tensor * root_of(wamx_tensor * t) { return t->view_src ? t->view_src
 
 // Memory plan in node order: a root tensor is placed at its first use and its
 // block recycled after its last use.  In a two-lane graph each lane has its own
-// arena (a lane's nodes run in order on its stream, so reuse inside a lane is
-// safe), and tensors touched by nodes of both lanes are never recycled, since
-// the other lane may still be reading them when a later node of the first
-// lane would take their memory.
+// arena, and a tensor is placed in the arena of the lane that touches it first
+// (a lane's nodes run in order on its stream, so reuse inside a lane is safe;
+// memory the other lane freed may still be in use there).  Tensors touched by
+// nodes of both lanes are never recycled, since the other lane may still be
+// reading them when a later node of the first lane would take their memory.
 static bool gallocr_alloc(wamx_gallocr * ga, wamx_cgraph * g) {
     const int n = wamx_graph_n_nodes(g);
     std::vector<wamx_tensor *> order;  // tensors that need memory, in first-use order
     std::unordered_map<wamx_tensor *, int> last_use;
     std::unordered_map<wamx_tensor *, int> first_def;
-    std::unordered_map<wamx_tensor *, int> lanes;  // bit l: touched by a lane-l node
+    std::unordered_map<wamx_tensor *, int> lanes;       // bit l: touched by a lane-l node
+    std::unordered_map<wamx_tensor *, int> first_lane;  // lane of the first node touching it
     const int kForever = 1 << 30;
     auto needs = [](wamx_tensor * t) { return t && !t->data && !t->view_src && wamx_nelements(t) > 0; };
     auto touch = [&](wamx_tensor * t, int i, int lane) {
@@ -996,6 +998,7 @@ static bool gallocr_alloc(wamx_gallocr * ga, wamx_cgraph * g) {
         if (!needs(r)) return;
         if (!first_def.count(r)) {
             first_def[r] = i;
+            first_lane[r] = lane;
             order.push_back(r);
         }
         lanes[r] |= 1 << lane;
@@ -1018,7 +1021,7 @@ static bool gallocr_alloc(wamx_gallocr * ga, wamx_cgraph * g) {
         if (lanes[t] == 3) last_use[t] = kForever;
     // Leaf inputs and tensors first touched as sources are live from the start.
     FreeList fl[2];
-    auto arena = [&](wamx_tensor * t) { return lanes[t] == 2 ? 1 : 0; };
+    auto arena = [&](wamx_tensor * t) { return first_lane[t]; };
     std::unordered_map<wamx_tensor *, size_t> offset;
     std::vector<std::vector<wamx_tensor *>> frees(n);
     for (auto * t : order)
