@@ -236,15 +236,23 @@ def workload_chunk(be, args):
         wamx.check(lib.wamx_gwp_predict(m, None), "predict")
     be.sync()
     phases = np.zeros(3)
+    action = np.empty(noise.size, np.float32)
+    # One request at a time, as the reference's predict serves them: submit
+    # the three graphs, then read the action chunk back (which waits for it).
     t = wamx.Timer(be)
     t.start()
     for _ in range(args.steps):
         wamx.check(lib.wamx_gwp_predict(m, None), "predict")
+        wamx.check(lib.wamx_gwp_get_action(m, action.ctypes.data), "get_action")
     ms = t.stop_ms() / args.steps
+    # Back-to-back chunks with no read-back between them, for comparison.
+    t.start()
+    for _ in range(args.steps):
+        wamx.check(lib.wamx_gwp_predict(m, None), "predict")
+    ms_pipelined = t.stop_ms() / args.steps
     for _ in range(3):
         wamx.check(lib.wamx_gwp_predict(m, C.byref(tm)), "predict")
         phases += np.array([tm.prompt_ms, tm.prefix_ms, tm.denoise_ms]) / 3
-    action = np.empty(noise.size, np.float32)
     wamx.check(lib.wamx_gwp_get_action(m, action.ctypes.data), "get_action")
     if not np.all(np.isfinite(action)):
         raise RuntimeError("non-finite action chunk")
@@ -322,6 +330,7 @@ def workload_chunk(be, args):
                                    "a 48x32 action chunk, batch 1",
                        "params": params, "graph_nodes": nodes,
                        "phase_ms": {"prompt": phases[0], "prefix": phases[1], "denoise": phases[2]},
+                       "ms_per_chunk_back_to_back": ms_pipelined,
                        "gemm_mfma_frac": roof["frac"]},
             "roofline": roof, "cpu_baseline": cpu}
 

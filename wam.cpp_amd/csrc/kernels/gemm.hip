@@ -1218,7 +1218,8 @@ __global__ __launch_bounds__(256) void gemm_skinny_reduce(GemmParams p, const fl
     for (int sp0 = 1; sp0 < splits; sp0 += kBatch) {
         fv_t v[kBatch];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) v[u] = *(const fv_t *) (part + (int64_t) min(sp0 + u, splits - 1) * total + i0);
+        for (int u = 0; u < kBatch; ++u)
+            if (sp0 + u < splits) v[u] = *(const fv_t *) (part + (int64_t) (sp0 + u) * total + i0);
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
             if (sp0 + u < splits) s += v[u];
@@ -1335,7 +1336,8 @@ __global__ __launch_bounds__(512) void skinny_reduce_row(GemmParams p, const flo
     for (int sp0 = 0; sp0 < splits; sp0 += kB) {
         float t[kB][8];
 #pragma unroll
-        for (int u = 0; u < kB; ++u) load8_f32(src + (int64_t) min(sp0 + u, splits - 1) * NM, t[u]);
+        for (int u = 0; u < kB; ++u)
+            if (sp0 + u < splits) load8_f32(src + (int64_t) (sp0 + u) * NM, t[u]);
 #pragma unroll
         for (int u = 0; u < kB; ++u)
             if (sp0 + u < splits)
