@@ -128,8 +128,8 @@ def test_graph_replay_is_deterministic(wx, be):
 
 
 def test_full_width_one_layer_matches_oracle(wx, be, orc):
-    """BASELINE widths (d = 3072, 24 heads, FFN 14336, 48 action tokens, 512
-    prompt tokens) on two layers and 2 denoise steps with 256 visual tokens."""
+    """Full GWP-0.5 widths (d = 3072, 24 heads, FFN 14336, 48 action tokens,
+    512 prompt tokens) on two layers and 2 denoise steps with 256 visual tokens."""
     cfg = dict(n_layers=2, hidden=3072, n_heads=24, head_dim=128, ffn_dim=14336, action_hidden=3072,
                action_ffn_dim=14336, action_chunk=48, action_dim=32, grid_h=8, grid_w=32, n_lang=512,
                t5_hidden=4096, z_dim=48, num_steps=2, enc_hidden=128, shift=5.0, eps=1e-6)
