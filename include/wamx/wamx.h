@@ -97,10 +97,15 @@ typedef enum wamx_op {
     WAMX_OP_COUNT
 } wamx_op;
 
+/* UNARY sub-op in op_params[0].  The values restate enum ggml_unary_op of
+ * ggml b9866 (GELU 8, SILU 10, GELU_ERF 14; not verified against its header),
+ * so the codes ggml writes (native-bf16.patch:626) read the same here; every
+ * other code is refused by supports_op.  wamx_graph_from_ggml translates by
+ * name (ggml_unary_op_name) and does not depend on these values. */
 typedef enum wamx_unary_op {
-    WAMX_UNARY_GELU     = 0,  /* tanh approximation, ggml_gelu */
-    WAMX_UNARY_GELU_ERF = 1,
-    WAMX_UNARY_SILU     = 2,
+    WAMX_UNARY_GELU     = 8,   /* tanh approximation, ggml_gelu */
+    WAMX_UNARY_SILU     = 10,
+    WAMX_UNARY_GELU_ERF = 14,
 } wamx_unary_op;
 
 typedef enum wamx_prec {
@@ -198,6 +203,10 @@ WAMX_API wamx_tensor * wamx_rms_norm(wamx_context * ctx, wamx_tensor * a, float 
 WAMX_API wamx_tensor * wamx_mul_mat(wamx_context * ctx, wamx_tensor * a, wamx_tensor * b);
 WAMX_API wamx_tensor * wamx_mul_mat_out_type(wamx_context * ctx, wamx_tensor * a, wamx_tensor * b, int32_t type);
 WAMX_API void          wamx_mul_mat_set_prec(wamx_tensor * a, int32_t prec);
+/* ggml_soft_max_ext: y = softmax(a*scale + mask) over ne0, f32.  mask (may be
+ * NULL) is F32 or F16 with ne0 == a->ne0, ne1 >= a->ne1, broadcast over dims 2
+ * and 3 by modulo (the complete-MoT mask of mot.cpp:1025-1027); -inf entries
+ * drop a key.  max_bias (ALiBi) must be 0.  op_params = {scale, max_bias}. */
 WAMX_API wamx_tensor * wamx_soft_max_ext(wamx_context * ctx, wamx_tensor * a, wamx_tensor * mask, float scale, float max_bias);
 WAMX_API wamx_tensor * wamx_rope_ext(wamx_context * ctx, wamx_tensor * a, wamx_tensor * positions, wamx_tensor * freq_factors,
                                      int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale,
@@ -537,12 +546,55 @@ WAMX_API int         wamx_gwp_graph_nodes(wamx_gwp_t m, int which);  /* 0 prompt
 /* Last error message of the calling thread ("" when none). */
 WAMX_API const char * wamx_last_error(void);
 
-/* ggml_op numbering correspondence: wamx_ggml_op_map[i] is the wamx_op for the
- * i-th name in wamx_ggml_op_names (ggml's GGML_OP_* names).  Numeric ggml
- * values are not reproduced because b9866 headers are not available. */
+/* ggml op correspondence by name: wamx_ggml_op_name(i) is the string
+ * ggml_op_name() returns for a ggml op ("MUL_MAT", "SOFT_MAX", ...) and
+ * wamx_ggml_op_to_wamx(i) the wamx_op it runs as.  Numeric ggml values are
+ * not reproduced because b9866 headers are not available.  The fused ops of
+ * this backend (LINEAR, QK_NORM_ROPE, JOINT_ATTN, MODULATION) have no ggml
+ * name. */
 WAMX_API int          wamx_ggml_op_count(void);
 WAMX_API const char * wamx_ggml_op_name(int i);
 WAMX_API int32_t      wamx_ggml_op_to_wamx(int i);
+
+/* ---------------------------------------------------------------------------
+ * Graph import from ggml (the drop-in path of ggml_backend_i::graph_compute).
+ *
+ * The ggml side of the shim fills one descriptor per tensor of a ggml graph
+ * (every node and every leaf or view source it reaches) straight from the
+ * ggml_tensor fields, with names instead of enum values:
+ *   op       = ggml_op_name(t->op)            ("NONE" for leaves)
+ *   unary_op = ggml_unary_op_name(ggml_get_unary_op(t)) for UNARY, else NULL
+ *   type     = ggml_type_name(t->type)        ("f32", "f16", "bf16", "i32")
+ *   ne, nb, op_params, flags, data, name      copied verbatim
+ *   src[i], view_src                           indices into the array, -1 = none
+ * op_params are read in ggml's layouts (ROPE, SOFT_MAX, SCALE, IM2COL, NORM,
+ * RMS_NORM, CONCAT, PERMUTE, MUL_MAT precision, the native-bf16 patch's
+ * src[] extensions of ADD/NORM/RMS_NORM/UNARY).  IM2COL takes its kernel size
+ * from src[0]->ne as ggml does.
+ *
+ * wamx_graph_from_ggml mirrors the tensors into ctx and returns a graph whose
+ * nodes are graph_nodes[0..n_graph_nodes) in ggml's order, or NULL with
+ * wamx_last_error() naming the first tensor it cannot represent (an unknown
+ * op, unary op or type).  Replaces the body of ggml_backend_cuda's
+ * graph_compute (ggml b9866, ggml-cuda.cu) as the engine reaches it from
+ * mot.cpp:589, cache.cpp:121, :440. */
+typedef struct wamx_ggml_tensor {
+    const char * op;
+    const char * unary_op;
+    const char * type;
+    int64_t ne[WAMX_MAX_DIMS];
+    size_t  nb[WAMX_MAX_DIMS];
+    int32_t op_params[WAMX_MAX_OP_PARAMS];
+    int32_t flags;
+    int32_t src[WAMX_MAX_SRC];
+    int32_t view_src;
+    size_t  view_offs;
+    void *  data;
+    const char * name;
+} wamx_ggml_tensor;
+
+WAMX_API wamx_cgraph * wamx_graph_from_ggml(wamx_context * ctx, const wamx_ggml_tensor * tensors, int n_tensors,
+                                            const int32_t * graph_nodes, int n_graph_nodes);
 
 #ifdef __cplusplus
 }

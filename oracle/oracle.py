@@ -279,6 +279,9 @@ class Gwp:
                 ("orc_gwp_prefix_key", C.c_void_p, [C.c_void_p, C.c_int]),
                 ("orc_gwp_prefix_value", C.c_void_p, [C.c_void_p, C.c_int]),
                 ("orc_gwp_prompt_key", C.c_void_p, [C.c_void_p, C.c_int]),
+                ("orc_gwp_prompt_value", C.c_void_p, [C.c_void_p, C.c_int]),
+                ("orc_gwp_prefix_hidden_in", C.c_void_p, [C.c_void_p, C.c_int]),
+                ("orc_gwp_set_visual_positions", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
                 ("orc_gwp_action_prompt", C.c_void_p, [C.c_void_p])):
             fn = getattr(lib, name)
             fn.restype = res
@@ -345,3 +348,97 @@ class Gwp:
     def action_prompt(self):
         c = self.cfg
         return self._arr(self.lib.orc_gwp_action_prompt(self.ptr), (c["n_lang"], c["action_hidden"]))
+
+    def prompt_value(self, layer):
+        c = self.cfg
+        return self._arr(self.lib.orc_gwp_prompt_value(self.ptr, layer), (c["n_heads"], c["head_dim"], c["n_lang"]))
+
+    def prefix_hidden_in(self, which):
+        """0: the state encoder's output [1][action_hidden]; 1: the patch
+        embedding's output [nimg][hidden] (the prefix pass's layer-0 inputs)."""
+        c = self.cfg
+        shape = (1, c["action_hidden"]) if which == 0 else (c["grid_h"] * c["grid_w"], self.d)
+        return self._arr(self.lib.orc_gwp_prefix_hidden_in(self.ptr, which), shape)
+
+    def set_visual_positions(self, t=None, h=None, w=None):
+        """(t, h, w) positions of the visual tokens for the next prefix pass
+        (None: the grid's own, semantics.cpp:235-257)."""
+        if t is None:
+            self.lib.orc_gwp_set_visual_positions(self.ptr, None, None, None)
+            return
+        self._pos = [_c(a, np.int32) for a in (t, h, w)]
+        self.lib.orc_gwp_set_visual_positions(self.ptr, *[_p(a) for a in self._pos])
+
+
+# ---------------------------------------------------------------------------
+# The synthetic weights of the model driver (wamx_gwp_create /
+# wamx_gwp_init_synthetic), generated on the host with fill_normal.
+# ---------------------------------------------------------------------------
+def fnv1a(s: str) -> int:
+    h = 1469598103934665603
+    for ch in s.encode():
+        h ^= ch
+        h = (h * 1099511628211) & (2**64 - 1)
+    return h
+
+
+def gwp_weight_specs(cfg: dict):
+    """[(name, elements)] of every named weight of the synthetic GWP-0.5
+    model, with the reference's GGUF names (weights.cpp:116-167)."""
+    c = cfg
+    d = c["n_heads"] * c["head_dim"]
+    da, E, A, L = c["action_hidden"], c["enc_hidden"], c["action_dim"], c["n_layers"]
+    out = [("gwp.patch_embedding.weight", 4 * c["z_dim"] * d), ("gwp.patch_embedding.bias", d)]
+
+    def lin(name, i, o):
+        out.extend([(name + ".weight", i * o), (name + ".bias", o)])
+
+    for p, i, o in (("gwp.state_encoder", A, da), ("gwp.action_encoder", A, da), ("gwp.action_decoder", da, A)):
+        lin(p + ".in_proj", i, E)
+        lin(p + ".mid_proj", E, E)
+        lin(p + ".out_proj", E, o)
+    for p, w in (("gwp.action_condition_embedder", da), ("gwp.condition_embedder", d)):
+        lin(p + ".time_embedder.linear_1", 256, w)
+        lin(p + ".time_embedder.linear_2", w, w)
+        lin(p + ".time_proj", w, 6 * w)
+        lin(p + ".text_embedder.linear_1", c["t5_hidden"], w)
+        lin(p + ".text_embedder.linear_2", w, w)
+    out.append(("gwp.action_scale_shift_table", 2 * da))
+    out.append(("gwp.blocks.action_expert.scale_shift_table", 6 * da * L))
+    out.append(("gwp.blocks.visual_expert.scale_shift_table", 6 * d * L))
+    for l in range(L):
+        for ex, w, f in (("action_expert", da, c["action_ffn_dim"]), ("visual_expert", d, c["ffn_dim"])):
+            p = f"gwp.blocks.{l}.{ex}"
+            lin(p + ".attn1.to_qkv", w, 3 * d)
+            out.extend([(p + ".attn1.norm_q.weight", d), (p + ".attn1.norm_k.weight", d)])
+            lin(p + ".attn1.to_out.0", d, w)
+            out.extend([(p + ".norm2.weight", w), (p + ".norm2.bias", w)])
+            lin(p + ".attn2.to_q", w, d)
+            lin(p + ".attn2.to_k", w, d)
+            lin(p + ".attn2.to_v", w, d)
+            out.extend([(p + ".attn2.norm_q.weight", d), (p + ".attn2.norm_k.weight", d)])
+            lin(p + ".attn2.to_out.0", d, w)
+            lin(p + ".ffn.net.0.proj", w, f)
+            lin(p + ".ffn.net.2", f, w)
+    return out
+
+
+def gwp_fill_rule(name: str, wstd: float):
+    """(mean, std) of a weight in the synthetic fill: biases N(0, 0.02), norm
+    weights 1 + N(0, 0.02), scale/shift tables N(0, 0.1), matrices N(0, wstd)."""
+    if name.endswith(".bias"):
+        return 0.0, 0.02
+    if name.endswith(("norm_q.weight", "norm_k.weight", "norm2.weight")):
+        return 1.0, 0.02
+    if "scale_shift_table" in name:
+        return 0.0, 0.1
+    return 0.0, wstd
+
+
+def gwp_synthetic_weight(name: str, n: int, seed: int, wstd: float = 0.02) -> np.ndarray:
+    mean, std = gwp_fill_rule(name, wstd)
+    return fill_normal(n, (seed ^ fnv1a(name)) & (2**64 - 1), mean, std, BF16)
+
+
+def gwp_synthetic_weights(cfg: dict, seed: int, wstd: float = 0.02) -> dict:
+    return {n: gwp_synthetic_weight(n, k, seed, wstd) for n, k in gwp_weight_specs(cfg)}

@@ -36,6 +36,9 @@ struct orc_gwp {
     uint16_t ** pv;                  /* [L] -> [H][dh][P] (V^T) */
     uint16_t ** lk;                  /* [L] -> [H][n_lang][dh] */
     uint16_t ** lv;                  /* [L] -> [H][dh][n_lang] */
+    uint16_t * state_in;             /* [da]: state encoder output (prefix_state_hidden_in) */
+    uint16_t * visual_in;            /* [nimg][d]: patch embedding output (prefix_visual_hidden_in) */
+    int32_t * vpos[3];               /* visual (t, h, w) positions, NULL: the grid's */
     int missing;
 };
 
@@ -276,6 +279,8 @@ orc_gwp * orc_gwp_new(const orc_gwp_config * cfg, orc_weight_fn wf, void * user)
     g->pv = (uint16_t **) calloc((size_t) L, sizeof(void *));
     g->lk = (uint16_t **) calloc((size_t) L, sizeof(void *));
     g->lv = (uint16_t **) calloc((size_t) L, sizeof(void *));
+    g->state_in = alloc16(cfg->action_hidden);
+    g->visual_in = alloc16(g->nimg * g->d);
     for (int64_t l = 0; l < L; ++l) {
         g->pk[l] = alloc16(H * g->P * dh);
         g->pv[l] = alloc16(H * dh * g->P);
@@ -298,7 +303,24 @@ void orc_gwp_free(orc_gwp * g) {
     free(g->lk);
     free(g->lv);
     free(g->action_prompt);
+    free(g->state_in);
+    free(g->visual_in);
+    for (int i = 0; i < 3; ++i) free(g->vpos[i]);
     free(g);
+}
+
+int orc_gwp_set_visual_positions(orc_gwp * g, const int32_t * t, const int32_t * h, const int32_t * w) {
+    for (int i = 0; i < 3; ++i) {
+        free(g->vpos[i]);
+        g->vpos[i] = NULL;
+    }
+    if (!t || !h || !w) return 0;
+    const int32_t * src[3] = {t, h, w};
+    for (int i = 0; i < 3; ++i) {
+        g->vpos[i] = (int32_t *) malloc((size_t) g->nimg * 4);
+        memcpy(g->vpos[i], src[i], (size_t) g->nimg * 4);
+    }
+    return 0;
 }
 
 int orc_gwp_prompt(orc_gwp * g, const float * prompt, int layers) {
@@ -349,11 +371,19 @@ int orc_gwp_prefix(orc_gwp * g, const float * state, const float * latent, const
     int32_t * vt = (int32_t *) calloc((size_t) nimg, 4);
     int32_t * vhp = (int32_t *) calloc((size_t) nimg, 4);
     int32_t * vwp = (int32_t *) calloc((size_t) nimg, 4);
+    /* visual_positions (semantics.cpp:235-257): t = 0, h = y, w = x. */
     for (int64_t y = 0; y < gh; ++y)
         for (int64_t x = 0; x < gw; ++x) {
             vhp[y * gw + x] = (int32_t) y;
             vwp[y * gw + x] = (int32_t) x;
         }
+    if (g->vpos[0]) {
+        memcpy(vt, g->vpos[0], (size_t) nimg * 4);
+        memcpy(vhp, g->vpos[1], (size_t) nimg * 4);
+        memcpy(vwp, g->vpos[2], (size_t) nimg * 4);
+    }
+    memcpy(g->state_in, sh, (size_t) da * 2);
+    memcpy(g->visual_in, vh, (size_t) nimg * d * 2);
     float * am = alloc32(6 * da);
     float * vm = alloc32(6 * d);
     const float scale = 1.0f / sqrtf((float) dh);
@@ -502,4 +532,6 @@ int orc_gwp_denoise(orc_gwp * g, const float * noise, float * action_out, int la
 const uint16_t * orc_gwp_prefix_key(orc_gwp * g, int layer) { return g->pk[layer]; }
 const uint16_t * orc_gwp_prefix_value(orc_gwp * g, int layer) { return g->pv[layer]; }
 const uint16_t * orc_gwp_prompt_key(orc_gwp * g, int layer) { return g->lk[layer]; }
+const uint16_t * orc_gwp_prompt_value(orc_gwp * g, int layer) { return g->lv[layer]; }
+const uint16_t * orc_gwp_prefix_hidden_in(orc_gwp * g, int which) { return which == 0 ? g->state_in : g->visual_in; }
 const uint16_t * orc_gwp_action_prompt(orc_gwp * g) { return g->action_prompt; }

@@ -38,6 +38,15 @@ int orc_gwp_denoise(orc_gwp * g, const float * noise, float * action_out, int la
 const uint16_t * orc_gwp_prefix_key(orc_gwp * g, int layer);    /* [H][P][dh] */
 const uint16_t * orc_gwp_prefix_value(orc_gwp * g, int layer);  /* [H][dh][P] */
 const uint16_t * orc_gwp_prompt_key(orc_gwp * g, int layer);    /* [H][n_lang][dh] */
+const uint16_t * orc_gwp_prompt_value(orc_gwp * g, int layer);  /* [H][dh][n_lang] (V^T) */
+/* The prefix pass's inputs to the first layer, as the reference dumps them
+ * (prefix_state_hidden_in / prefix_visual_hidden_in, cache.cpp:441-469):
+ * which 0: state encoder output [action_hidden]; 1: patch embedding output
+ * [nimg][hidden]. */
+const uint16_t * orc_gwp_prefix_hidden_in(orc_gwp * g, int which);
+/* Visual token positions (t, h, w), each [nimg], for the next prefix pass in
+ * place of visual_positions' grid (semantics.cpp:235-257); NULLs restore it. */
+int orc_gwp_set_visual_positions(orc_gwp * g, const int32_t * t, const int32_t * h, const int32_t * w);
 const uint16_t * orc_gwp_action_prompt(orc_gwp * g);            /* [n_lang][action_hidden] */
 
 #ifdef __cplusplus

@@ -88,7 +88,7 @@ def test_concat_and_fused_constructors(wx, ctx):
     assert gr.contents.op == wx.OP["ADD"] and bool(gr.contents.src[2])
     bias = lib.wamx_new_tensor_1d(ctx, wx.TYPE_BF16, 3072)
     bg = lib.wamx_bias_gelu_bf16(ctx, h, bias)
-    assert bg.contents.op == wx.OP["UNARY"] and bg.contents.op_params[0] == 0
+    assert bg.contents.op == wx.OP["UNARY"] and bg.contents.op_params[0] == wx.UNARY_GELU
     sc = lib.wamx_new_tensor_1d(ctx, wx.TYPE_F32, 3072)
     nm = lib.wamx_norm_modulation_bf16(ctx, h, sc, sc, 1e-6)
     assert nm.contents.op == wx.OP["NORM"] and nm.contents.type == wx.TYPE_BF16
@@ -140,8 +140,121 @@ def test_supports_op(wx, ctx):
 
 
 def test_ggml_op_map(wx):
+    """Names are the ones ggml_op_name() returns (bare, no GGML_OP_ prefix);
+    the fused ops of this backend have no ggml name, FLASH_ATTN_EXT is not
+    mapped (its operand layout is not JOINT_ATTN's)."""
     lib = wx.load()
     n = lib.wamx_ggml_op_count()
     names = {lib.wamx_ggml_op_name(i).decode(): lib.wamx_ggml_op_to_wamx(i) for i in range(n)}
-    for op in ("MUL_MAT", "NORM", "RMS_NORM", "ROPE", "SOFT_MAX", "ADD", "UNARY", "CONCAT", "CPY", "CONT"):
-        assert names[f"GGML_OP_{op}"] == wx.OP[op]
+    for op in ("MUL_MAT", "NORM", "RMS_NORM", "ROPE", "SOFT_MAX", "ADD", "UNARY", "CONCAT", "CPY", "CONT", "IM2COL",
+               "VIEW", "PERMUTE", "RESHAPE", "TRANSPOSE", "GET_ROWS", "SCALE", "MUL", "REPEAT", "DUP", "NONE"):
+        assert names[op] == wx.OP[op]
+    assert not any(k.startswith("GGML_OP_") for k in names)
+    assert "FLASH_ATTN_EXT" not in names
+    assert not {"LINEAR", "QK_NORM_ROPE", "JOINT_ATTN", "MODULATION"} & set(names)
+
+
+def test_supports_rejects_malformed_nodes(wx, ctx):
+    """supports_op checks what the launch path assumes, for nodes built
+    without the constructors (as a mirrored graph is)."""
+    lib = wx.load()
+    x = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 64, 8)
+    u = lib.wamx_gelu(ctx, x)
+    assert lib.wamx_backend_supports_op(None, u)
+    for code in (0, 1, 2, 3):        # ggml ABS, SGN, NEG, STEP: never run as GELU / SILU
+        u.contents.op_params[0] = code
+        assert not lib.wamx_backend_supports_op(None, u)
+    # IM2COL reads its kernel size from src[0]: a kernel whose shape does not
+    # give the output's shape is refused
+    k = lib.wamx_new_tensor_4d(ctx, wx.TYPE_BF16, 2, 2, 16, 256)
+    inp = lib.wamx_new_tensor_4d(ctx, wx.TYPE_F32, 16, 8, 16, 1)
+    col = lib.wamx_im2col(ctx, k, inp, 2, 2, 0, 0, 1, 1, wx.TYPE_BF16)
+    assert shape(col) == (64, 8, 4, 1) and list(col.contents.op_params)[:7] == [2, 2, 0, 0, 1, 1, 1]
+    assert lib.wamx_backend_supports_op(None, col)
+    col.contents.src[0] = lib.wamx_new_tensor_4d(ctx, wx.TYPE_BF16, 3, 3, 16, 256)
+    assert not lib.wamx_backend_supports_op(None, col)
+    # a JOINT_ATTN whose V^T does not cover the keys
+    q = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 128, 48, 4)
+    kk = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 128, 256, 4)
+    vt = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 256, 128, 4)
+    at = lib.wamx_joint_attn(ctx, q, kk, vt, None, None, 0, 0.088)
+    assert at and lib.wamx_backend_supports_op(None, at)
+    at.contents.src[2] = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 255, 128, 4)
+    assert not lib.wamx_backend_supports_op(None, at)
+    # MUL_MAT whose result shape does not follow from its operands
+    w = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 64, 32)
+    mm = lib.wamx_mul_mat(ctx, w, x)
+    assert lib.wamx_backend_supports_op(None, mm)
+    mm.contents.ne[0] = 31
+    assert not lib.wamx_backend_supports_op(None, mm)
+    # ROPE with YaRN / frequency scaling is not what the kernel computes
+    pos = lib.wamx_new_tensor_1d(ctx, wx.TYPE_I32, 8)
+    r = lib.wamx_rope_ext(ctx, lib.wamx_reshape_3d(ctx, x, 16, 4, 8), pos, None, 16, 0, 0, 10000.0, 1.0, 0.0,
+                          1.0, 32.0, 1.0)
+    assert lib.wamx_backend_supports_op(None, r)
+    r.contents.op_params[6] = 0x3F000000   # freq_scale 0.5
+    assert not lib.wamx_backend_supports_op(None, r)
+
+
+def test_soft_max_mask_constructor(wx, ctx):
+    lib = wx.load()
+    s = lib.wamx_new_tensor_3d(ctx, wx.TYPE_F32, 100, 48, 24)
+    m = lib.wamx_new_tensor_3d(ctx, wx.TYPE_F32, 100, 48, 24)
+    sm = lib.wamx_soft_max_ext(ctx, s, m, 0.088, 0.0)
+    assert sm and lib.wamx_backend_supports_op(None, sm)
+    assert C.addressof(sm.contents.src[1].contents) == C.addressof(m.contents)
+    m16 = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F16, 100, 64)      # broadcast over heads, padded rows
+    assert lib.wamx_soft_max_ext(ctx, s, m16, 0.088, 0.0)
+    assert not lib.wamx_soft_max_ext(ctx, s, lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 99, 48), 0.088, 0.0)
+    assert not lib.wamx_soft_max_ext(ctx, s, m, 0.088, 8.0)     # ALiBi
+
+
+def test_graph_from_ggml_translation(wx, ctx):
+    """A graph described the way a ggml shim describes it (names, ggml
+    op_params) mirrors into wamx tensors with the same shapes, strides, data
+    addresses and sources; unary ops are matched by name; unknown names fail
+    with the tensor named."""
+    import ggml_mirror as gm
+    lib = wx.load()
+    x = gm.new_tensor("bf16", 64, 8, name="x")
+    w = gm.new_tensor("bf16", 64, 32, name="w")
+    b = gm.new_tensor("bf16", 32, name="b")
+    y = gm.add(gm.mul_mat_out_type(w, x, "bf16"), b)
+    g = gm.gelu_erf(gm.cast(y, "f32"))
+    v = gm.view_2d(g, 16, 8, g.nb[1], 16 * 4)
+    out = gm.cont(gm.permute(gm.reshape(gm.cont(v), 4, 4, 8), 0, 2, 1, 3))
+    graph = gm.Graph()
+    graph.expand(out)
+    gm.place(graph.tensors(), 1 << 20, 1 << 20)
+    arr, nodes, _keep = gm.describe(graph)
+    wg = lib.wamx_graph_from_ggml(ctx, arr, len(arr), nodes, len(nodes))
+    assert wg, wx.last_error()
+    n = lib.wamx_graph_n_nodes(wg)
+    assert n == len(graph.nodes)
+    for i, t in enumerate(graph.nodes):
+        m = lib.wamx_graph_node(wg, i).contents
+        assert wx.OP_NAMES[m.op] == t.op
+        assert list(m.ne) == t.ne and list(m.nb) == t.nb and m.data == t.data
+        if t.op == "UNARY":
+            assert m.op_params[0] == wx.UNARY_GELU_ERF
+        assert lib.wamx_backend_supports_op(None, lib.wamx_graph_node(wg, i)), t.op
+    # a view keeps its root and offset
+    mv = [lib.wamx_graph_node(wg, i).contents for i in range(n) if graph.nodes[i] is v][0]
+    assert mv.view_offs == 64 and mv.view_src.contents.data == g.data
+    # unknown names are refused, naming the tensor
+    bad = gm.new_tensor("f32", 4, name="odd")
+    z = gm.T("f32", [4], op="FLASH_ATTN_EXT", src=[bad])
+    z.name = "fa"
+    gr2 = gm.Graph()
+    gr2.expand(z)
+    gm.place(gr2.tensors(), 1 << 20, 1 << 16)
+    arr2, nodes2, _k2 = gm.describe(gr2)
+    assert not lib.wamx_graph_from_ggml(ctx, arr2, len(arr2), nodes2, len(nodes2))
+    assert "FLASH_ATTN_EXT" in wx.last_error() and "fa" in wx.last_error()
+    ab = gm._unary(gm.new_tensor("f32", 4), "ABS")
+    gr3 = gm.Graph()
+    gr3.expand(ab)
+    gm.place(gr3.tensors(), 1 << 20, 1 << 16)
+    arr3, nodes3, _k3 = gm.describe(gr3)
+    assert not lib.wamx_graph_from_ggml(ctx, arr3, len(arr3), nodes3, len(nodes3))
+    assert "ABS" in wx.last_error()

@@ -482,7 +482,7 @@ static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
         case WAMX_OP_REPEAT:
             return launch_binary(2, ref_of(node), ref_of(s0), ref_of(node), s);
         case WAMX_OP_SCALE:
-            return launch_unary(3, ref_of(s0), ref_of(node), param_f32(node, 0), s);
+            return launch_unary(kUnaryScale, ref_of(s0), ref_of(node), param_f32(node, 0), param_f32(node, 1), s);
         case WAMX_OP_CONCAT:
             return launch_concat(ref_of(s0), ref_of(s1), ref_of(node), node->op_params[0], s);
         case WAMX_OP_NORM: {
@@ -511,20 +511,25 @@ static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
         }
         case WAMX_OP_MUL_MAT:
             return run_mul_mat(be, node);
-        case WAMX_OP_SOFT_MAX:
-            return launch_softmax_f32(ref_of(s0), ref_of(node), param_f32(node, 0), s);
+        case WAMX_OP_SOFT_MAX: {
+            TensorRef mask{};
+            if (s1) mask = ref_of(s1);
+            return launch_softmax_f32(ref_of(s0), mask, ref_of(node), param_f32(node, 0), s);
+        }
         case WAMX_OP_ROPE:
             return launch_rope_f32(ref_of(s0), (const int32_t *) s1->data, ref_of(node), node->op_params[1],
                                    param_f32(node, 5), s);
         case WAMX_OP_UNARY:
             if (node->src[1])
                 return launch_bias_gelu_bf16(s0->data, s1->data, node->data, wamx_nelements(s0), s1->ne[0], s);
-            return launch_unary(node->op_params[0], ref_of(s0), ref_of(node), 1.0f, s);
+            return launch_unary(node->op_params[0], ref_of(s0), ref_of(node), 1.0f, 0.0f, s);
         case WAMX_OP_GET_ROWS:
             return launch_get_rows(ref_of(s0), (const int32_t *) s1->data, ref_of(node), s);
         case WAMX_OP_IM2COL: {
+            // ggml_im2col: kernel size from the kernel tensor, op_params {s0, s1, p0, p1, d0, d1, is_2D}.
             const int32_t * pp = node->op_params;
-            return launch_im2col(ref_of(s1), ref_of(node), pp[7], pp[8], pp[0], pp[1], pp[2], pp[3], pp[4], pp[5], s);
+            return launch_im2col(ref_of(s1), ref_of(node), (int) s0->ne[0], (int) s0->ne[1], pp[0], pp[1], pp[2], pp[3],
+                                 pp[4], pp[5], s);
         }
         case WAMX_OP_LINEAR:
             return run_linear(be, node);
@@ -553,15 +558,31 @@ static bool tiled_product_ok(const wamx_tensor * x) {
            rows_contig(x);
 }
 
+// Whether b broadcasts onto a by modulo in every dim (ggml_can_repeat).
+static bool can_repeat(const wamx_tensor * b, const wamx_tensor * a) {
+    for (int i = 0; i < 4; ++i)
+        if (b->ne[i] <= 0 || a->ne[i] % b->ne[i] != 0) return false;
+    return true;
+}
+
+// Whether the backend can run node t as it stands.  Every shape and layout
+// assumption of the launch path is checked here, because a node may come
+// from a graph mirrored from ggml (wamx_graph_from_ggml) rather than from the
+// constructors of wamx.h.
 static bool supports(const wamx_tensor * t) {
     auto ok_type = [](const wamx_tensor * x) {
         return x && (x->type == WAMX_TYPE_F32 || x->type == WAMX_TYPE_BF16 || x->type == WAMX_TYPE_F16 ||
                      x->type == WAMX_TYPE_I32);
     };
+    auto float_type = [](const wamx_tensor * x) {
+        return x && (x->type == WAMX_TYPE_F32 || x->type == WAMX_TYPE_BF16 || x->type == WAMX_TYPE_F16);
+    };
     const wamx_tensor * s0 = t->src[0];
     const wamx_tensor * s1 = t->src[1];
     const bool view_op = t->op == WAMX_OP_NONE || t->op == WAMX_OP_VIEW || t->op == WAMX_OP_RESHAPE ||
                          t->op == WAMX_OP_PERMUTE || t->op == WAMX_OP_TRANSPOSE;
+    for (int i = 0; i < 4; ++i)
+        if (t->ne[i] < 0) return false;
     // A tiled weight is read only whole, as the weight of MUL_MAT / LINEAR:
     // any other reader, or a reader of a view of it, would see the tiled order.
     for (int i = 0; i < WAMX_MAX_SRC && !view_op; ++i) {
@@ -580,46 +601,102 @@ static bool supports(const wamx_tensor * t) {
         case WAMX_OP_DUP:
         case WAMX_OP_CONT:
         case WAMX_OP_CPY:
-            return ok_type(s0) && ok_type(t);
+            return ok_type(s0) && ok_type(t) && wamx_nelements(s0) == wamx_nelements(t);
         case WAMX_OP_ADD:
-            if (t->src[2])
-                return s0->type == WAMX_TYPE_BF16 && s1->type == WAMX_TYPE_BF16 && rows_contig(s0) && rows_contig(s1) &&
-                       rows_contig(t->src[2]) && s0->ne[2] == 1 && s0->ne[3] == 1;
-            return ok_type(s0) && ok_type(s1) && s0->type != WAMX_TYPE_I32;
+            if (t->src[2]) {  // gated residual bf16 (native-bf16.patch:594-612)
+                const wamx_tensor * g = t->src[2];
+                return s0 && s1 && s0->type == WAMX_TYPE_BF16 && s1->type == WAMX_TYPE_BF16 && t->type == WAMX_TYPE_BF16 &&
+                       (g->type == WAMX_TYPE_F32 || g->type == WAMX_TYPE_BF16) && wamx_are_same_shape(s0, s1) &&
+                       wamx_are_same_shape(s0, t) && g->ne[0] == s0->ne[0] &&
+                       (g->ne[1] == 1 || g->ne[1] == s0->ne[1]) && g->ne[2] == 1 && g->ne[3] == 1 && rows_contig(s0) &&
+                       rows_contig(s1) && rows_contig(g) && s0->ne[2] == 1 && s0->ne[3] == 1 && wamx_is_contiguous(t);
+            }
+            [[fallthrough]];
         case WAMX_OP_MUL:
+            return float_type(s0) && float_type(s1) && float_type(t) && can_repeat(s1, s0) && wamx_are_same_shape(s0, t);
         case WAMX_OP_REPEAT:
+            return ok_type(s0) && ok_type(t) && s0->type == t->type && can_repeat(s0, t);
         case WAMX_OP_SCALE:
-        case WAMX_OP_CONCAT:
+            return float_type(s0) && float_type(t) && wamx_are_same_shape(s0, t);
+        case WAMX_OP_CONCAT: {
+            const int dim = t->op_params[0];
+            if (!ok_type(s0) || !s1 || s0->type != s1->type || s0->type != t->type || dim < 0 || dim > 3) return false;
+            for (int i = 0; i < 4; ++i)
+                if (i != dim ? (s0->ne[i] != s1->ne[i] || s0->ne[i] != t->ne[i]) : t->ne[i] != s0->ne[i] + s1->ne[i])
+                    return false;
+            return true;
+        }
         case WAMX_OP_GET_ROWS:
-            return ok_type(s0);
+            return ok_type(s0) && s1 && s1->type == WAMX_TYPE_I32 && rows_contig(s1) && t->ne[0] == s0->ne[0] &&
+                   t->ne[1] == s1->ne[0] && t->ne[2] == s1->ne[1] && float_type(t);
         case WAMX_OP_NORM:
-            if (t->src[1])
-                return s0->type == WAMX_TYPE_BF16 && rows_contig(s0) && rows_contig(t->src[1]) &&
-                       rows_contig(t->src[2]) && s0->ne[2] == 1 && s0->ne[3] == 1 &&
-                       t->src[1]->ne[1] == t->src[2]->ne[1] &&
-                       (t->src[1]->ne[1] == 1 || t->src[1]->nb[1] / es(t->src[1]) == t->src[2]->nb[1] / es(t->src[2]));
-            return s0->type == WAMX_TYPE_F32 && rows_contig(s0);
+            if (t->src[1]) {  // norm_modulation_bf16 / layer_norm_bf16 (native-bf16.patch:630-663)
+                const wamx_tensor *sc = t->src[1], *sh = t->src[2];
+                return sh && s0->type == WAMX_TYPE_BF16 && t->type == WAMX_TYPE_BF16 && sc->type == sh->type &&
+                       (sc->type == WAMX_TYPE_F32 || sc->type == WAMX_TYPE_BF16) && sc->ne[0] == s0->ne[0] &&
+                       sh->ne[0] == s0->ne[0] && wamx_are_same_shape(s0, t) && rows_contig(s0) && rows_contig(t) &&
+                       rows_contig(sc) && rows_contig(sh) && s0->ne[2] == 1 && s0->ne[3] == 1 && t->nb[1] % 2 == 0 &&
+                       sc->ne[1] == sh->ne[1] && (sc->ne[1] == 1 || sc->ne[1] == s0->ne[1]) &&
+                       (sc->ne[1] == 1 || sc->nb[1] / es(sc) == sh->nb[1] / es(sh));
+            }
+            return s0->type == WAMX_TYPE_F32 && t->type == WAMX_TYPE_F32 && rows_contig(s0) && rows_contig(t) &&
+                   wamx_are_same_shape(s0, t);
         case WAMX_OP_RMS_NORM:
-            return rows_contig(s0) && (t->src[1] ? s0->type == WAMX_TYPE_BF16 : s0->type == WAMX_TYPE_F32);
-        case WAMX_OP_MUL_MAT:
-            if (tensor_is_tiled(s0)) return tiled_product_ok(s1);
+            if (t->src[1])  // rms_norm_bf16_f32 (native-bf16.patch:665-678)
+                return s0->type == WAMX_TYPE_BF16 && s1->type == WAMX_TYPE_BF16 && s1->ne[0] == s0->ne[0] &&
+                       rows_contig(s1) && t->type == WAMX_TYPE_F32 && rows_contig(s0) && rows_contig(t) &&
+                       wamx_are_same_shape(s0, t);
+            return s0->type == WAMX_TYPE_F32 && t->type == WAMX_TYPE_F32 && rows_contig(s0) && rows_contig(t) &&
+                   wamx_are_same_shape(s0, t);
+        case WAMX_OP_MUL_MAT: {
+            if (!s0 || !s1 || s0->ne[0] != s1->ne[0] || s0->ne[2] <= 0 || s0->ne[3] <= 0 ||
+                s1->ne[2] % s0->ne[2] != 0 || s1->ne[3] % s0->ne[3] != 0 || t->ne[0] != s0->ne[1] ||
+                t->ne[1] != s1->ne[1] || t->ne[2] != s1->ne[2] || t->ne[3] != s1->ne[3] ||
+                (t->type != WAMX_TYPE_F32 && t->type != WAMX_TYPE_BF16))
+                return false;
+            if (tensor_is_tiled(s0)) return tiled_product_ok(s1) && wamx_is_contiguous(t);
             return (s0->type == WAMX_TYPE_BF16 || s0->type == WAMX_TYPE_F32) &&
                    (s1->type == WAMX_TYPE_BF16 || s1->type == WAMX_TYPE_F32) && rows_contig(s0) && rows_contig(s1) &&
                    wamx_is_contiguous(t);
-        case WAMX_OP_SOFT_MAX:
-            return s0->type == WAMX_TYPE_F32 && t->src[1] == nullptr;
-        case WAMX_OP_ROPE:
-            return s0->type == WAMX_TYPE_F32 && t->op_params[2] == 0;
+        }
+        case WAMX_OP_SOFT_MAX: {
+            if (!s0 || s0->type != WAMX_TYPE_F32 || t->type != WAMX_TYPE_F32 || !wamx_are_same_shape(s0, t) ||
+                param_f32(t, 1) != 0.0f || t->src[2])
+                return false;
+            if (s1 && ((s1->type != WAMX_TYPE_F32 && s1->type != WAMX_TYPE_F16) || s1->ne[0] != s0->ne[0] ||
+                       s1->ne[1] < s0->ne[1] || s1->ne[2] <= 0 || s1->ne[3] <= 0 || s0->ne[2] % s1->ne[2] != 0 ||
+                       s0->ne[3] % s1->ne[3] != 0))
+                return false;
+            return true;
+        }
+        case WAMX_OP_ROPE: {
+            // NORMAL mode, no frequency factors, no YaRN: ggml_rope_ext with
+            // freq_scale 1, ext_factor 0, attn_factor 1 (mot.cpp:175-202).
+            const int n_dims = t->op_params[1];
+            return s0 && s0->type == WAMX_TYPE_F32 && t->type == WAMX_TYPE_F32 && wamx_are_same_shape(s0, t) && s1 &&
+                   s1->type == WAMX_TYPE_I32 && s1->ne[0] == s0->ne[2] && rows_contig(s1) && !t->src[2] &&
+                   t->op_params[2] == 0 && n_dims > 0 && !(n_dims & 1) && n_dims <= s0->ne[0] &&
+                   param_f32(t, 6) == 1.0f && param_f32(t, 7) == 0.0f && param_f32(t, 8) == 1.0f;
+        }
         case WAMX_OP_UNARY:
-            if (t->src[1]) return s0->type == WAMX_TYPE_BF16 && wamx_is_contiguous(s0);
-            return ok_type(s0) && t->op_params[0] >= 0 && t->op_params[0] <= 2;
+            if (t->src[1])  // bias + GELU-tanh bf16 (native-bf16.patch:614-628)
+                return t->op_params[0] == WAMX_UNARY_GELU && s0->type == WAMX_TYPE_BF16 && wamx_is_contiguous(s0) &&
+                       s1->type == WAMX_TYPE_BF16 && s1->ne[0] == s0->ne[0] && rows_contig(s1) &&
+                       t->type == WAMX_TYPE_BF16 && wamx_is_contiguous(t) && wamx_are_same_shape(s0, t);
+            return float_type(s0) && float_type(t) && wamx_are_same_shape(s0, t) &&
+                   (t->op_params[0] == WAMX_UNARY_GELU || t->op_params[0] == WAMX_UNARY_GELU_ERF ||
+                    t->op_params[0] == WAMX_UNARY_SILU);
         case WAMX_OP_LINEAR:
-            return !tensor_is_tiled(s0) || tiled_product_ok(s1);  // otherwise validated by the constructor
+            if (check_linear(t)) return false;
+            return !tensor_is_tiled(s0) || tiled_product_ok(s1);
         case WAMX_OP_IM2COL:
+            return check_im2col(t) == nullptr;
         case WAMX_OP_QK_NORM_ROPE:
+            return check_qk_norm_rope(t) == nullptr;
         case WAMX_OP_JOINT_ATTN:
+            return check_joint_attn(t) == nullptr;
         case WAMX_OP_MODULATION:
-            return true;  // validated by their constructors
+            return check_modulation(t) == nullptr;
         default:
             return false;
     }
@@ -1019,6 +1096,30 @@ static bool gallocr_alloc(wamx_gallocr * ga, wamx_cgraph * g) {
     }
     for (auto * t : order)
         if (lanes[t] == 3) last_use[t] = kForever;
+    // A LINEAR that run_nodes fuses with the row ops after it (match_row_post)
+    // runs them in one launch at its own position: the reduce reads the
+    // LINEAR's and the members' sources while it writes the members' outputs.
+    // Those sources therefore stay live through the last member, so no member
+    // output can take their memory.
+    if (ga->be->fuse_rows) {
+        bool two = false;
+        for (int i = 0; i < n && !two; ++i) two = wamx_graph_node(g, i)->lane != 0;
+        for (int i = 0; i < n; ++i) {
+            wamx_tensor * node = wamx_graph_node(g, i);
+            if (node->op != WAMX_OP_LINEAR) continue;
+            RowPost post;
+            const int last = match_row_post(g, i, n, post, two);
+            if (last <= i) continue;
+            for (int j = i; j <= last; ++j) {
+                wamx_tensor * m = wamx_graph_node(g, j);
+                if (j > i && (is_noop(m) || (two && m->lane != node->lane))) continue;
+                for (int k = 0; k < WAMX_MAX_SRC; ++k) {
+                    wamx_tensor * r = m->src[k] ? root_of(m->src[k]) : nullptr;
+                    if (r && last_use.count(r)) last_use[r] = std::max(last_use[r], last);
+                }
+            }
+        }
+    }
     // Leaf inputs and tensors first touched as sources are live from the start.
     FreeList fl[2];
     auto arena = [&](wamx_tensor * t) { return first_lane[t]; };
@@ -1405,7 +1506,8 @@ wamx_status wamx_op_soft_max_f32(wamx_backend_t be, const float * x, float * y, 
     TensorRef rx{(void *) x, WAMX_TYPE_F32, {cols, rows, 1, 1}, {4, 4 * cols, 4 * cols * rows, 4 * cols * rows}};
     TensorRef ry = rx;
     ry.data = y;
-    WAMX_LAUNCH(launch_softmax_f32(rx, ry, scale, be->stream));
+    const TensorRef no_mask{};
+    WAMX_LAUNCH(launch_softmax_f32(rx, no_mask, ry, scale, be->stream));
 }
 
 wamx_status wamx_fill_normal(wamx_backend_t be, void * dst, int32_t type, int64_t n, uint64_t seed, float mean,

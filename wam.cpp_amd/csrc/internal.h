@@ -10,6 +10,14 @@ namespace wamx {
 
 const char * last_error_cstr();
 
+// Validators of the ops a constructor checks (null when well formed, else the
+// reason); supports_op runs them on every node, whoever built it.
+const char * check_linear(const wamx_tensor * t);
+const char * check_qk_norm_rope(const wamx_tensor * t);
+const char * check_joint_attn(const wamx_tensor * t);
+const char * check_modulation(const wamx_tensor * t);
+const char * check_im2col(const wamx_tensor * t);
+
 // ---------------------------------------------------------------------------
 // GEMM: y[b][n][m] = sum_k w[b/r][m][k] * x[b][n][k]  (the ggml MUL_MAT layout:
 // both operands K-contiguous, "NT").  w is bf16 (or f32 for the SIMT path),
@@ -125,11 +133,16 @@ TensorRef ref_of(const wamx_tensor * t);
 hipError_t launch_copy(const TensorRef & src, const TensorRef & dst, hipStream_t s);
 // dst = a (op) b with b broadcast (ggml bin_bcast).  op: 0 add, 1 mul, 2 repeat b.
 hipError_t launch_binary(int op, const TensorRef & a, const TensorRef & b, const TensorRef & dst, hipStream_t s);
-// dst = unary(a) (0 gelu-tanh, 1 gelu-erf, 2 silu) or scale (op 3, with scale).
-hipError_t launch_unary(int op, const TensorRef & a, const TensorRef & dst, float scale, hipStream_t s);
+// dst = unary(a) for op = WAMX_UNARY_GELU / _GELU_ERF / _SILU, or
+// a * scale + bias for op = kUnaryScale (ggml_scale).
+constexpr int kUnaryScale = -1;
+hipError_t launch_unary(int op, const TensorRef & a, const TensorRef & dst, float scale, float bias, hipStream_t s);
 hipError_t launch_concat(const TensorRef & a, const TensorRef & b, const TensorRef & dst, int dim, hipStream_t s);
 hipError_t launch_get_rows(const TensorRef & a, const int32_t * rows, const TensorRef & dst, hipStream_t s);
-hipError_t launch_softmax_f32(const TensorRef & x, const TensorRef & y, float scale, hipStream_t s);
+// SOFT_MAX_EXT: y = softmax(x * scale + mask) over ne0; mask (data may be null)
+// F32 or F16, row i1 of plane (i2 % ne2, i3 % ne3).
+hipError_t launch_softmax_f32(const TensorRef & x, const TensorRef & mask, const TensorRef & y, float scale,
+                              hipStream_t s);
 hipError_t launch_rope_f32(const TensorRef & x, const int32_t * pos, const TensorRef & y, int n_dims, float freq_base,
                            hipStream_t s);
 hipError_t launch_im2col(const TensorRef & src, const TensorRef & dst, int KW, int KH, int s0, int s1, int p0, int p1,

@@ -101,6 +101,121 @@ static wamx_tensor * fail(const char * what) {
 
 static void set_param_f32(wamx_tensor * t, int i, float v) { memcpy(&t->op_params[i], &v, 4); }
 
+namespace wamx {
+
+// Node validators shared by the constructors and supports_op: a graph
+// mirrored from ggml (wamx_graph_from_ggml) or built by hand reaches
+// graph_compute without going through the constructors.  Each returns null
+// when the node is well formed, else the reason.
+static bool contig(const wamx_tensor * t) { return t && wamx_is_contiguous(t); }
+
+const char * check_linear(const wamx_tensor * t) {
+    const wamx_tensor *w = t->src[0], *x = t->src[1], *bias = t->src[2], *res = t->src[3], *gate = t->src[4];
+    const int32_t epi = t->op_params[0];
+    if (!is_bf16(w) || !x || (x->type != WAMX_TYPE_BF16 && x->type != WAMX_TYPE_F32)) return "types";
+    if (w->ne[0] != x->ne[0] || w->ne[2] != 1 || w->ne[3] != 1 || x->ne[2] != 1 || x->ne[3] != 1) return "shapes";
+    if (w->nb[0] != 2 || x->nb[0] != wamx_type_size(x->type)) return "rows must be contiguous";
+    const int64_t M = w->ne[1], N = x->ne[1];
+    if (epi < WAMX_EPI_NONE || epi > WAMX_EPI_BIAS_RESIDUAL) return "epilogue";
+    if (epi != WAMX_EPI_NONE && (!is_bf16(bias) || bias->ne[0] != M || bias->nb[0] != 2)) return "bias";
+    if (epi == WAMX_EPI_BIAS_GATED || epi == WAMX_EPI_BIAS_RESIDUAL) {
+        if (!is_bf16(res) || res->ne[0] != M || res->ne[1] != N || res->nb[0] != 2) return "residual";
+    }
+    if (epi == WAMX_EPI_BIAS_GATED && (!is_f32(gate) || gate->ne[0] != M || gate->nb[0] != 4)) return "gate";
+    if (!is_bf16(t) || t->ne[0] != M || t->ne[1] != N || !contig(t)) return "output";
+    return nullptr;
+}
+
+const char * check_qk_norm_rope(const wamx_tensor * t) {
+    const wamx_tensor *x = t->src[0], *weight = t->src[1], *dst = t->src[2];
+    if (!is_bf16(x) || !is_bf16(weight) || !is_bf16(dst) || !is_bf16(t)) return "types";
+    const int64_t dh = dst->ne[0], H = dst->ne[2], T = x->ne[1];
+    if (x->ne[0] != dh * H || weight->ne[0] != x->ne[0] || x->nb[0] != 2 || weight->nb[0] != 2 || !contig(dst) ||
+        x->ne[2] != 1 || x->ne[3] != 1 || dst->ne[3] != 1 || (dh & 1))
+        return "shapes";
+    for (int i = 0; i < 4; ++i)
+        if (t->ne[i] != dst->ne[i] || t->nb[i] != dst->nb[i]) return "result must be the destination";
+    const int64_t tok0 = t->op_params[0];
+    const int rope_mode = t->op_params[1];
+    if (tok0 < 0 || tok0 + T > dst->ne[1]) return "token range";
+    if (rope_mode < 0 || rope_mode > 2) return "rope mode";
+    auto pos_ok = [T](const wamx_tensor * p) { return p && p->type == WAMX_TYPE_I32 && p->ne[0] == T && p->nb[0] == 4; };
+    if (rope_mode == 0 && !pos_ok(t->src[3])) return "positions";
+    if (rope_mode == 1 && (dh != 128 || !pos_ok(t->src[3]) || !pos_ok(t->src[4]) || !pos_ok(t->src[5])))
+        return "3-D rope needs head_dim 128 and three position streams";
+    return nullptr;
+}
+
+const char * check_joint_attn(const wamx_tensor * t) {
+    const wamx_tensor *q = t->src[0], *k_a = t->src[1], *v_a = t->src[2], *k_b = t->src[3], *v_b = t->src[4];
+    if (!is_bf16(q) || !is_bf16(k_a) || !is_bf16(v_a)) return "types";
+    const int64_t dh = q->ne[0], Tq = q->ne[1], H = q->ne[2];
+    const int64_t na = k_a->ne[1];
+    if (dh != 128) return "head_dim must be 128";
+    if (k_a->ne[0] != dh || k_a->ne[2] != H || v_a->ne[0] != na || v_a->ne[1] != dh || v_a->ne[2] != H)
+        return "kv_a shapes";
+    if ((k_b == nullptr) != (v_b == nullptr)) return "kv_b pair";
+    if (k_b) {
+        const int64_t nb = k_b->ne[1];
+        if (!is_bf16(k_b) || !is_bf16(v_b) || k_b->ne[0] != dh || k_b->ne[2] != H || v_b->ne[0] != nb ||
+            v_b->ne[1] != dh || v_b->ne[2] != H)
+            return "kv_b shapes";
+    }
+    const int64_t na_split = t->op_params[0];
+    if (na_split < 0 || na_split > na) return "split";
+    for (const wamx_tensor * s : {q, k_a, k_b})
+        if (s && (!contig(s) || s->ne[3] != 1)) return "q and k must be contiguous";
+    // V^T rows may be padded: 8-byte aligned row stride covering ne[0] keys.
+    for (const wamx_tensor * s : {v_a, v_b})
+        if (s && (s->nb[0] != 2 || s->nb[1] % 8 != 0 || s->nb[1] < (size_t) s->ne[0] * 2 ||
+                  s->nb[2] != s->nb[1] * (size_t) s->ne[1] || s->ne[3] != 1))
+            return "V^T layout";
+    if (!is_bf16(t) || t->ne[0] != dh * H || t->ne[1] != Tq || !contig(t)) return "output";
+    return nullptr;
+}
+
+const char * check_modulation(const wamx_tensor * t) {
+    const wamx_tensor *mod = t->src[0], *tables = t->src[1];
+    if (!mod || !tables || !contig(mod) || !contig(tables)) return "contiguous operands";
+    if ((mod->type != WAMX_TYPE_BF16 && mod->type != WAMX_TYPE_F32) ||
+        (tables->type != WAMX_TYPE_BF16 && tables->type != WAMX_TYPE_F32))
+        return "types";
+    if (wamx_nelements(mod) != tables->ne[0] * tables->ne[1]) return "sizes";
+    if (!is_f32(t) || !contig(t) || wamx_nelements(t) != wamx_nelements(tables)) return "output";
+    return nullptr;
+}
+
+// ggml_im2col, 2-D only: op_params {s0, s1, p0, p1, d0, d1, is_2D}, kernel
+// shape from src[0]->ne, f32 input src[1].
+const char * check_im2col(const wamx_tensor * t) {
+    const wamx_tensor *kernel = t->src[0], *input = t->src[1];
+    const int32_t * p = t->op_params;
+    if (!kernel || !is_f32(input) || (t->type != WAMX_TYPE_F32 && t->type != WAMX_TYPE_BF16)) return "types";
+    if (p[6] != 1) return "only the 2-D form";
+    if (p[0] < 1 || p[1] < 1 || p[4] < 1 || p[5] < 1 || p[2] < 0 || p[3] < 0) return "stride/padding/dilation";
+    const int64_t KW = kernel->ne[0], KH = kernel->ne[1], IC = input->ne[2];
+    if (kernel->ne[2] != IC) return "channels";
+    const int64_t OW = (input->ne[0] + 2 * p[2] - p[4] * (KW - 1) - 1) / p[0] + 1;
+    const int64_t OH = (input->ne[1] + 2 * p[3] - p[5] * (KH - 1) - 1) / p[1] + 1;
+    if (OW <= 0 || OH <= 0 || t->ne[0] != IC * KH * KW || t->ne[1] != OW || t->ne[2] != OH || t->ne[3] != input->ne[3])
+        return "output shape";
+    return nullptr;
+}
+
+}  // namespace wamx
+
+// Builds node `t` of an op validated by `check`; on failure the (unlinked)
+// tensor stays in the context and NULL is returned with the reason.
+static wamx_tensor * checked(wamx_tensor * t, const char * (*check)(const wamx_tensor *), const char * what) {
+    if (!t) return nullptr;
+    const char * why = check(t);
+    if (why) {
+        set_errorf("%s: %s", what, why);
+        return nullptr;
+    }
+    return t;
+}
+
 extern "C" {
 
 const char * wamx_last_error(void) { return last_error_cstr(); }
@@ -417,10 +532,15 @@ void wamx_mul_mat_set_prec(wamx_tensor * a, int32_t prec) {
     if (a) a->op_params[0] = prec;
 }
 
+// ggml_soft_max_ext: mask rows i1, broadcast over dims 2 and 3 by modulo.
 wamx_tensor * wamx_soft_max_ext(wamx_context * ctx, wamx_tensor * a, wamx_tensor * mask, float scale, float max_bias) {
-    if (!is_f32(a) || mask || max_bias != 0.0f) return fail("wamx_soft_max_ext (f32, no mask, no ALiBi)");
+    if (!is_f32(a) || max_bias != 0.0f) return fail("wamx_soft_max_ext (f32, no ALiBi)");
+    if (mask && ((mask->type != WAMX_TYPE_F32 && mask->type != WAMX_TYPE_F16) || mask->ne[0] != a->ne[0] ||
+                 mask->ne[1] < a->ne[1] || a->ne[2] % mask->ne[2] != 0 || a->ne[3] % mask->ne[3] != 0))
+        return fail("wamx_soft_max_ext (mask: f32/f16, ne0 = a.ne0, ne1 >= a.ne1, broadcast over dims 2, 3)");
     wamx_tensor * t = unary_result(ctx, a, WAMX_OP_SOFT_MAX);
     if (!t) return nullptr;
+    t->src[1] = mask;
     set_param_f32(t, 0, scale);
     set_param_f32(t, 1, max_bias);
     return t;
@@ -469,9 +589,7 @@ wamx_tensor * wamx_get_rows(wamx_context * ctx, wamx_tensor * a, wamx_tensor * r
 
 wamx_tensor * wamx_im2col(wamx_context * ctx, wamx_tensor * kernel, wamx_tensor * input, int s0, int s1, int p0,
                           int p1, int d0, int d1, int32_t dst_type) {
-    if (!kernel || !is_f32(input) || (dst_type != WAMX_TYPE_F32 && dst_type != WAMX_TYPE_BF16) || s0 < 1 || s1 < 1 ||
-        d0 < 1 || d1 < 1 || kernel->ne[2] != input->ne[2])
-        return fail("wamx_im2col");
+    if (!kernel || !input || s0 < 1 || s1 < 1 || d0 < 1 || d1 < 1) return fail("wamx_im2col");
     const int64_t KW = kernel->ne[0], KH = kernel->ne[1], IC = input->ne[2];
     const int64_t OW = (input->ne[0] + 2 * p0 - d0 * (KW - 1) - 1) / s0 + 1;
     const int64_t OH = (input->ne[1] + 2 * p1 - d1 * (KH - 1) - 1) / s1 + 1;
@@ -480,12 +598,13 @@ wamx_tensor * wamx_im2col(wamx_context * ctx, wamx_tensor * kernel, wamx_tensor 
     wamx_tensor * t = new_tensor_impl(ctx, dst_type, 4, ne);
     if (!t) return nullptr;
     t->op = WAMX_OP_IM2COL;
-    const int32_t params[8] = {s0, s1, p0, p1, d0, d1, 1, (int32_t) KW};
+    // ggml's layout: {s0, s1, p0, p1, d0, d1, is_2D}; the kernel size is
+    // src[0]->ne[0..1] (ggml_im2col keeps the kernel tensor as src[0]).
+    const int32_t params[7] = {s0, s1, p0, p1, d0, d1, 1};
     memcpy(t->op_params, params, sizeof params);
-    t->op_params[8] = (int32_t) KH;
     t->src[0] = kernel;
     t->src[1] = input;
-    return t;
+    return checked(t, check_im2col, "wamx_im2col");
 }
 
 // --- native-bf16.patch:594-678 ---------------------------------------------
@@ -559,17 +678,8 @@ wamx_tensor * wamx_rms_norm_bf16_f32(wamx_context * ctx, wamx_tensor * input, wa
 // --- fused ops of this backend -------------------------------------------
 wamx_tensor * wamx_linear(wamx_context * ctx, wamx_tensor * w, wamx_tensor * x, wamx_tensor * bias, int32_t epilogue,
                           wamx_tensor * residual, wamx_tensor * gate) {
-    if (!is_bf16(w) || !x || (x->type != WAMX_TYPE_BF16 && x->type != WAMX_TYPE_F32)) return fail("wamx_linear (types)");
-    if (w->ne[0] != x->ne[0] || w->ne[2] != 1 || w->ne[3] != 1 || x->ne[2] != 1 || x->ne[3] != 1)
-        return fail("wamx_linear (shapes)");
-    const int64_t M = w->ne[1], N = x->ne[1];
-    if (epilogue < WAMX_EPI_NONE || epilogue > WAMX_EPI_BIAS_RESIDUAL) return fail("wamx_linear (epilogue)");
-    if (epilogue != WAMX_EPI_NONE && (!is_bf16(bias) || bias->ne[0] != M)) return fail("wamx_linear (bias)");
-    if (epilogue == WAMX_EPI_BIAS_GATED || epilogue == WAMX_EPI_BIAS_RESIDUAL) {
-        if (!is_bf16(residual) || residual->ne[0] != M || residual->ne[1] != N) return fail("wamx_linear (residual)");
-    }
-    if (epilogue == WAMX_EPI_BIAS_GATED && (!is_f32(gate) || gate->ne[0] != M)) return fail("wamx_linear (gate)");
-    wamx_tensor * t = wamx_new_tensor_2d(ctx, WAMX_TYPE_BF16, M, N);
+    if (!w || !x) return fail("wamx_linear");
+    wamx_tensor * t = wamx_new_tensor_2d(ctx, WAMX_TYPE_BF16, w->ne[1], x->ne[1]);
     if (!t) return nullptr;
     t->op = WAMX_OP_LINEAR;
     t->op_params[0] = epilogue;
@@ -578,24 +688,13 @@ wamx_tensor * wamx_linear(wamx_context * ctx, wamx_tensor * w, wamx_tensor * x, 
     t->src[2] = epilogue != WAMX_EPI_NONE ? bias : nullptr;
     t->src[3] = (epilogue == WAMX_EPI_BIAS_GATED || epilogue == WAMX_EPI_BIAS_RESIDUAL) ? residual : nullptr;
     t->src[4] = epilogue == WAMX_EPI_BIAS_GATED ? gate : nullptr;
-    return t;
+    return checked(t, check_linear, "wamx_linear");
 }
 
 wamx_tensor * wamx_qk_norm_rope(wamx_context * ctx, wamx_tensor * x, wamx_tensor * weight, wamx_tensor * dst,
                                 int64_t tok0, int rope_mode, wamx_tensor * pos0, wamx_tensor * pos1, wamx_tensor * pos2,
                                 float eps, float freq_base) {
-    if (!is_bf16(x) || !is_bf16(weight) || !is_bf16(dst)) return fail("wamx_qk_norm_rope (types)");
-    const int64_t dh = dst->ne[0], H = dst->ne[2], T = x->ne[1];
-    if (x->ne[0] != dh * H || weight->ne[0] != x->ne[0] || x->nb[0] != 2 || !wamx_is_contiguous(dst))
-        return fail("wamx_qk_norm_rope (shapes)");
-    if (tok0 < 0 || tok0 + T > dst->ne[1]) return fail("wamx_qk_norm_rope (token range)");
-    if (rope_mode < 0 || rope_mode > 2) return fail("wamx_qk_norm_rope (rope mode)");
-    if (rope_mode == 0 && (!pos0 || pos0->type != WAMX_TYPE_I32 || pos0->ne[0] != T)) return fail("wamx_qk_norm_rope (pos)");
-    if (rope_mode == 1) {
-        if (dh != 128) return fail("wamx_qk_norm_rope (3-D rope sections need head_dim 128)");
-        for (wamx_tensor * p : {pos0, pos1, pos2})
-            if (!p || p->type != WAMX_TYPE_I32 || p->ne[0] != T) return fail("wamx_qk_norm_rope (3-D pos)");
-    }
+    if (!x || !weight || !dst) return fail("wamx_qk_norm_rope");
     wamx_tensor * t = view_impl(ctx, dst, 4, dst->ne, 0);
     if (!t) return nullptr;
     memcpy(t->nb, dst->nb, sizeof t->nb);
@@ -610,32 +709,14 @@ wamx_tensor * wamx_qk_norm_rope(wamx_context * ctx, wamx_tensor * x, wamx_tensor
     t->src[3] = rope_mode <= 1 ? pos0 : nullptr;
     t->src[4] = rope_mode == 1 ? pos1 : nullptr;
     t->src[5] = rope_mode == 1 ? pos2 : nullptr;
-    return t;
+    if (tok0 != (int64_t) t->op_params[0]) return fail("wamx_qk_norm_rope (token offset)");
+    return checked(t, check_qk_norm_rope, "wamx_qk_norm_rope");
 }
 
 wamx_tensor * wamx_joint_attn(wamx_context * ctx, wamx_tensor * q, wamx_tensor * k_a, wamx_tensor * v_a,
                               wamx_tensor * k_b, wamx_tensor * v_b, int64_t na_split, float scale) {
-    if (!is_bf16(q) || !is_bf16(k_a) || !is_bf16(v_a)) return fail("wamx_joint_attn (types)");
-    const int64_t dh = q->ne[0], Tq = q->ne[1], H = q->ne[2];
-    const int64_t na = k_a->ne[1];
-    if (k_a->ne[0] != dh || k_a->ne[2] != H || v_a->ne[0] != na || v_a->ne[1] != dh || v_a->ne[2] != H)
-        return fail("wamx_joint_attn (kv_a shapes)");
-    if ((k_b == nullptr) != (v_b == nullptr)) return fail("wamx_joint_attn (kv_b pair)");
-    if (k_b) {
-        const int64_t nb = k_b->ne[1];
-        if (!is_bf16(k_b) || !is_bf16(v_b) || k_b->ne[0] != dh || k_b->ne[2] != H || v_b->ne[0] != nb ||
-            v_b->ne[1] != dh || v_b->ne[2] != H)
-            return fail("wamx_joint_attn (kv_b shapes)");
-    }
-    if (na_split < 0 || na_split > na) return fail("wamx_joint_attn (split)");
-    for (wamx_tensor * s : {q, k_a, k_b})
-        if (s && !wamx_is_contiguous(s)) return fail("wamx_joint_attn (contiguous q/k)");
-    // V^T rows may be padded: 8-byte aligned row stride covering ne[0] keys.
-    for (wamx_tensor * s : {v_a, v_b})
-        if (s && (s->nb[0] != 2 || s->nb[1] % 8 != 0 || s->nb[1] < (size_t) s->ne[0] * 2 ||
-                  s->nb[2] != s->nb[1] * (size_t) s->ne[1]))
-            return fail("wamx_joint_attn (V^T layout)");
-    wamx_tensor * t = wamx_new_tensor_2d(ctx, WAMX_TYPE_BF16, dh * H, Tq);
+    if (!q || !k_a || !v_a) return fail("wamx_joint_attn");
+    wamx_tensor * t = wamx_new_tensor_2d(ctx, WAMX_TYPE_BF16, q->ne[0] * q->ne[2], q->ne[1]);
     if (!t) return nullptr;
     t->op = WAMX_OP_JOINT_ATTN;
     t->op_params[0] = (int32_t) na_split;
@@ -645,22 +726,18 @@ wamx_tensor * wamx_joint_attn(wamx_context * ctx, wamx_tensor * q, wamx_tensor *
     t->src[2] = v_a;
     t->src[3] = k_b;
     t->src[4] = v_b;
-    return t;
+    if (na_split != (int64_t) t->op_params[0]) return fail("wamx_joint_attn (split)");
+    return checked(t, check_joint_attn, "wamx_joint_attn");
 }
 
 wamx_tensor * wamx_modulation(wamx_context * ctx, wamx_tensor * mod, wamx_tensor * tables) {
-    if (!mod || !tables || !wamx_is_contiguous(mod) || !wamx_is_contiguous(tables)) return fail("wamx_modulation");
-    const int64_t per = tables->ne[0] * tables->ne[1];
-    if (wamx_nelements(mod) != per) return fail("wamx_modulation (sizes)");
-    if ((mod->type != WAMX_TYPE_BF16 && mod->type != WAMX_TYPE_F32) ||
-        (tables->type != WAMX_TYPE_BF16 && tables->type != WAMX_TYPE_F32))
-        return fail("wamx_modulation (types)");
-    wamx_tensor * t = wamx_new_tensor_3d(ctx, WAMX_TYPE_F32, tables->ne[0], tables->ne[1], tables->ne[2]);
+    if (!mod || !tables) return fail("wamx_modulation");
+    wamx_tensor * t = wamx_new_tensor_3d(ctx, WAMX_TYPE_F32, tables->ne[0], tables->ne[1], tables->ne[2] * tables->ne[3]);
     if (!t) return nullptr;
     t->op = WAMX_OP_MODULATION;
     t->src[0] = mod;
     t->src[1] = tables;
-    return t;
+    return checked(t, check_modulation, "wamx_modulation");
 }
 
 // ---------------------------------------------------------------------------
@@ -726,23 +803,24 @@ void wamx_graph_assign_uid(wamx_cgraph * g) {
 uint64_t wamx_graph_uid(const wamx_cgraph * g) { return g ? g->uid : 0; }
 
 // ---------------------------------------------------------------------------
-// ggml op correspondence (names only; b9866 numeric values are unverified).
+// ggml op correspondence by the names ggml_op_name() returns (b9866 numeric
+// values are not available to verify, so nothing here depends on them).
 // ---------------------------------------------------------------------------
 static const struct {
     const char * ggml;
     int32_t wamx;
 } k_ggml_ops[] = {
-    {"GGML_OP_NONE", WAMX_OP_NONE},         {"GGML_OP_DUP", WAMX_OP_DUP},
-    {"GGML_OP_ADD", WAMX_OP_ADD},           {"GGML_OP_MUL", WAMX_OP_MUL},
-    {"GGML_OP_SCALE", WAMX_OP_SCALE},       {"GGML_OP_CPY", WAMX_OP_CPY},
-    {"GGML_OP_CONT", WAMX_OP_CONT},         {"GGML_OP_RESHAPE", WAMX_OP_RESHAPE},
-    {"GGML_OP_VIEW", WAMX_OP_VIEW},         {"GGML_OP_PERMUTE", WAMX_OP_PERMUTE},
-    {"GGML_OP_TRANSPOSE", WAMX_OP_TRANSPOSE}, {"GGML_OP_CONCAT", WAMX_OP_CONCAT},
-    {"GGML_OP_REPEAT", WAMX_OP_REPEAT},     {"GGML_OP_NORM", WAMX_OP_NORM},
-    {"GGML_OP_RMS_NORM", WAMX_OP_RMS_NORM}, {"GGML_OP_MUL_MAT", WAMX_OP_MUL_MAT},
-    {"GGML_OP_SOFT_MAX", WAMX_OP_SOFT_MAX}, {"GGML_OP_ROPE", WAMX_OP_ROPE},
-    {"GGML_OP_UNARY", WAMX_OP_UNARY},       {"GGML_OP_GET_ROWS", WAMX_OP_GET_ROWS},
-    {"GGML_OP_IM2COL", WAMX_OP_IM2COL},     {"GGML_OP_FLASH_ATTN_EXT", WAMX_OP_JOINT_ATTN},
+    {"NONE", WAMX_OP_NONE},         {"DUP", WAMX_OP_DUP},
+    {"ADD", WAMX_OP_ADD},           {"MUL", WAMX_OP_MUL},
+    {"SCALE", WAMX_OP_SCALE},       {"CPY", WAMX_OP_CPY},
+    {"CONT", WAMX_OP_CONT},         {"RESHAPE", WAMX_OP_RESHAPE},
+    {"VIEW", WAMX_OP_VIEW},         {"PERMUTE", WAMX_OP_PERMUTE},
+    {"TRANSPOSE", WAMX_OP_TRANSPOSE}, {"CONCAT", WAMX_OP_CONCAT},
+    {"REPEAT", WAMX_OP_REPEAT},     {"NORM", WAMX_OP_NORM},
+    {"RMS_NORM", WAMX_OP_RMS_NORM}, {"MUL_MAT", WAMX_OP_MUL_MAT},
+    {"SOFT_MAX", WAMX_OP_SOFT_MAX}, {"ROPE", WAMX_OP_ROPE},
+    {"UNARY", WAMX_OP_UNARY},       {"GET_ROWS", WAMX_OP_GET_ROWS},
+    {"IM2COL", WAMX_OP_IM2COL},
 };
 
 // ggml_backend_alloc_ctx_tensors: one buffer for every unallocated,
@@ -780,6 +858,113 @@ wamx_buffer_t wamx_backend_alloc_ctx_tensors_from_buft(wamx_context * ctx, wamx_
         }
     }
     return buf;
+}
+
+// ---------------------------------------------------------------------------
+// Graph import from ggml descriptors (wamx_ggml_tensor).  Everything is
+// matched by name, so no ggml enum value is assumed.
+// ---------------------------------------------------------------------------
+static int32_t ggml_type_by_name(const char * name) {
+    if (!name) return -1;
+    static const struct {
+        const char * n;
+        int32_t t;
+    } types[] = {{"f32", WAMX_TYPE_F32}, {"f16", WAMX_TYPE_F16}, {"bf16", WAMX_TYPE_BF16}, {"i32", WAMX_TYPE_I32}};
+    for (const auto & e : types)
+        if (!strcmp(name, e.n)) return e.t;
+    return -1;
+}
+
+static int32_t ggml_op_by_name(const char * name) {
+    if (!name) return -1;
+    for (const auto & e : k_ggml_ops)
+        if (!strcmp(name, e.ggml)) return e.wamx;
+    return -1;
+}
+
+// ggml_unary_op_name() strings of the unary ops this backend runs.
+static int32_t ggml_unary_by_name(const char * name) {
+    if (!name) return -1;
+    if (!strcmp(name, "GELU")) return WAMX_UNARY_GELU;
+    if (!strcmp(name, "GELU_ERF")) return WAMX_UNARY_GELU_ERF;
+    if (!strcmp(name, "SILU")) return WAMX_UNARY_SILU;
+    return -1;
+}
+
+wamx_cgraph * wamx_graph_from_ggml(wamx_context * ctx, const wamx_ggml_tensor * d, int n_tensors,
+                                   const int32_t * graph_nodes, int n_graph_nodes) {
+    if (!ctx || !d || n_tensors <= 0 || !graph_nodes || n_graph_nodes < 0) {
+        set_error("wamx_graph_from_ggml: bad arguments");
+        return nullptr;
+    }
+    std::vector<wamx_tensor *> t((size_t) n_tensors, nullptr);
+    for (int i = 0; i < n_tensors; ++i) {
+        const wamx_ggml_tensor & g = d[i];
+        const int32_t type = ggml_type_by_name(g.type);
+        const int32_t op = ggml_op_by_name(g.op);
+        const char * nm = g.name ? g.name : "";
+        if (type < 0) {
+            set_errorf("wamx_graph_from_ggml: tensor %d '%s': unsupported type '%s'", i, nm, g.type ? g.type : "(null)");
+            return nullptr;
+        }
+        if (op < 0) {
+            set_errorf("wamx_graph_from_ggml: tensor %d '%s': unsupported op '%s'", i, nm, g.op ? g.op : "(null)");
+            return nullptr;
+        }
+        wamx_tensor * w = new_tensor_impl(ctx, type, 4, g.ne);
+        if (!w) return nullptr;
+        memcpy(w->nb, g.nb, sizeof w->nb);
+        w->op = op;
+        memcpy(w->op_params, g.op_params, sizeof w->op_params);
+        w->flags = g.flags;
+        w->data = g.data;
+        w->view_offs = g.view_offs;
+        wamx_set_name(w, nm);
+        if (op == WAMX_OP_UNARY) {
+            const int32_t u = ggml_unary_by_name(g.unary_op);
+            if (u < 0) {
+                set_errorf("wamx_graph_from_ggml: tensor %d '%s': unsupported unary op '%s'", i, nm,
+                           g.unary_op ? g.unary_op : "(null)");
+                return nullptr;
+            }
+            w->op_params[0] = u;
+        }
+        t[(size_t) i] = w;
+    }
+    auto idx_ok = [n_tensors](int32_t k) { return k >= -1 && k < n_tensors; };
+    for (int i = 0; i < n_tensors; ++i) {
+        const wamx_ggml_tensor & g = d[i];
+        if (!idx_ok(g.view_src)) {
+            set_errorf("wamx_graph_from_ggml: tensor %d: view source index %d out of range", i, g.view_src);
+            return nullptr;
+        }
+        t[(size_t) i]->view_src = g.view_src >= 0 ? t[(size_t) g.view_src] : nullptr;
+        for (int k = 0; k < WAMX_MAX_SRC; ++k) {
+            if (!idx_ok(g.src[k])) {
+                set_errorf("wamx_graph_from_ggml: tensor %d: source %d index %d out of range", i, k, g.src[k]);
+                return nullptr;
+            }
+            t[(size_t) i]->src[k] = g.src[k] >= 0 ? t[(size_t) g.src[k]] : nullptr;
+        }
+    }
+    // A view's root is the root of its source chain, as in ggml.
+    for (int i = 0; i < n_tensors; ++i) {
+        wamx_tensor * w = t[(size_t) i];
+        int hops = 0;
+        while (w->view_src && w->view_src->view_src && hops++ < n_tensors) w->view_src = w->view_src->view_src;
+        if (w->view_src) w->buffer = w->view_src->buffer;
+    }
+    wamx_cgraph * graph = wamx_new_graph(ctx, (size_t) n_tensors + 16);
+    if (!graph) return nullptr;
+    for (int i = 0; i < n_graph_nodes; ++i) {
+        const int32_t k = graph_nodes[i];
+        if (k < 0 || k >= n_tensors) {
+            set_errorf("wamx_graph_from_ggml: graph node %d index %d out of range", i, k);
+            return nullptr;
+        }
+        if (!visit(graph, t[(size_t) k])) return nullptr;
+    }
+    return graph;
 }
 
 int wamx_ggml_op_count(void) { return (int) (sizeof k_ggml_ops / sizeof k_ggml_ops[0]); }

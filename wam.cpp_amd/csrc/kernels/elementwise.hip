@@ -158,7 +158,7 @@ __global__ void binary_kernel(int op, Ref4 a, Ref4 b, Ref4 dst, int64_t n) {
     st(dst, at(dst, i0, i1, i2, i3), op == 0 ? x + y : x * y);
 }
 
-__global__ void unary_kernel(int op, Ref4 a, Ref4 dst, float scale, int64_t n) {
+__global__ void unary_kernel(int op, Ref4 a, Ref4 dst, float scale, float bias, int64_t n) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     int64_t i0, i1, i2, i3;
@@ -166,10 +166,10 @@ __global__ void unary_kernel(int op, Ref4 a, Ref4 dst, float scale, int64_t n) {
     const float x = ld(a, at(a, i0, i1, i2, i3));
     float y;
     switch (op) {
-        case 0: y = gelu_tanh(x); break;
-        case 1: y = gelu_erf(x); break;
-        case 2: y = silu(x); break;
-        default: y = x * scale; break;
+        case WAMX_UNARY_GELU: y = gelu_tanh(x); break;
+        case WAMX_UNARY_GELU_ERF: y = gelu_erf(x); break;
+        case WAMX_UNARY_SILU: y = silu(x); break;
+        default: y = x * scale + bias; break;
     }
     st(dst, at(dst, i0, i1, i2, i3), y);
 }
@@ -203,16 +203,22 @@ __global__ void get_rows_kernel(Ref4 a, const int32_t * rows, int64_t rows_ld, R
     st(dst, at(dst, i0, i1, i2, i3), ld(a, at(a, i0, r, i2 % a.ne2, i3 % a.ne3)));
 }
 
-// SOFT_MAX_EXT without mask: y = exp(s*x - max) / sum over ne0.  One
-// workgroup per row.
-__global__ __launch_bounds__(256) void softmax_kernel(Ref4 x, Ref4 y, float scale) {
+// SOFT_MAX_EXT: y = exp(w - max) / sum over ne0 with w = scale * x + mask
+// (mask row i1 of plane (i2 % ne2, i3 % ne3); no mask when m.data is null).
+// One workgroup per row.
+__global__ __launch_bounds__(256) void softmax_kernel(Ref4 x, Ref4 m, Ref4 y, float scale) {
     __shared__ float red[4];
     const int64_t row = blockIdx.x;
     const int64_t r1 = row % x.ne1, r2 = (row / x.ne1) % x.ne2, r3 = row / (x.ne1 * x.ne2);
     const char * xr = at(x, 0, r1, r2, r3);
+    const char * mr = m.data ? at(m, 0, r1, r2 % m.ne2, r3 % m.ne3) : nullptr;
     char * yr = at(y, 0, r1, r2, r3);
+    auto w_at = [&](int64_t c) {
+        const float v = *(const float *) (xr + c * x.nb0) * scale;
+        return mr ? v + ld(m, mr + c * m.nb0) : v;
+    };
     float mx = -INFINITY;
-    for (int64_t c = threadIdx.x; c < x.ne0; c += 256) mx = fmaxf(mx, *(const float *) (xr + c * x.nb0) * scale);
+    for (int64_t c = threadIdx.x; c < x.ne0; c += 256) mx = fmaxf(mx, w_at(c));
     mx = wave_max(mx);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
@@ -220,7 +226,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(Ref4 x, Ref4 y, float scal
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float sum = 0.0f;
     for (int64_t c = threadIdx.x; c < x.ne0; c += 256) {
-        const float e = expf(*(const float *) (xr + c * x.nb0) * scale - mx);
+        const float e = expf(w_at(c) - mx);
         *(float *) (yr + c * y.nb0) = e;
         sum += e;
     }
@@ -352,10 +358,10 @@ hipError_t launch_binary(int op, const TensorRef & a, const TensorRef & b, const
     return hipGetLastError();
 }
 
-hipError_t launch_unary(int op, const TensorRef & a, const TensorRef & dst, float scale, hipStream_t s) {
+hipError_t launch_unary(int op, const TensorRef & a, const TensorRef & dst, float scale, float bias, hipStream_t s) {
     const int64_t n = nel(dst);
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(unary_kernel, grid1d(n), dim3(256), 0, s, op, to_ref4(a), to_ref4(dst), scale, n);
+    hipLaunchKernelGGL(unary_kernel, grid1d(n), dim3(256), 0, s, op, to_ref4(a), to_ref4(dst), scale, bias, n);
     return hipGetLastError();
 }
 
@@ -373,10 +379,12 @@ hipError_t launch_get_rows(const TensorRef & a, const int32_t * rows, const Tens
     return hipGetLastError();
 }
 
-hipError_t launch_softmax_f32(const TensorRef & x, const TensorRef & y, float scale, hipStream_t s) {
+hipError_t launch_softmax_f32(const TensorRef & x, const TensorRef & mask, const TensorRef & y, float scale,
+                              hipStream_t s) {
     const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(softmax_kernel, dim3((unsigned) rows), dim3(256), 0, s, to_ref4(x), to_ref4(y), scale);
+    hipLaunchKernelGGL(softmax_kernel, dim3((unsigned) rows), dim3(256), 0, s, to_ref4(x), to_ref4(mask), to_ref4(y),
+                       scale);
     return hipGetLastError();
 }
 

@@ -22,6 +22,7 @@ HEADER = REPO / "include" / "wamx" / "wamx.h"
 TYPE_F32, TYPE_F16, TYPE_I32, TYPE_BF16 = 0, 1, 26, 30
 STATUS_SUCCESS = 0
 EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_GATED, EPI_BIAS_RESIDUAL = 0, 1, 2, 3, 4
+UNARY_GELU, UNARY_SILU, UNARY_GELU_ERF = 8, 10, 14
 
 OP_NAMES = ["NONE", "DUP", "ADD", "MUL", "SCALE", "CPY", "CONT", "RESHAPE", "VIEW", "PERMUTE",
             "TRANSPOSE", "CONCAT", "REPEAT", "NORM", "RMS_NORM", "MUL_MAT", "SOFT_MAX", "ROPE",
@@ -156,6 +157,7 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_rope_ext": (TensorP, [vp, TensorP, TensorP, TensorP, C.c_int, C.c_int, C.c_int,
                                     f32, f32, f32, f32, f32, f32]),
         "wamx_get_rows": (TensorP, [vp, TensorP, TensorP]),
+        "wamx_im2col": (TensorP, [vp, TensorP, TensorP, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, i32]),
         "wamx_gated_residual_bf16": (TensorP, [vp, TensorP, TensorP, TensorP]),
         "wamx_bias_gelu_bf16": (TensorP, [vp, TensorP, TensorP]),
         "wamx_norm_modulation_bf16": (TensorP, [vp, TensorP, TensorP, TensorP, f32]),
@@ -190,6 +192,7 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_ggml_op_count": (C.c_int, []),
         "wamx_ggml_op_name": (C.c_char_p, [C.c_int]),
         "wamx_ggml_op_to_wamx": (i32, [C.c_int]),
+        "wamx_graph_from_ggml": (vp, [vp, vp, C.c_int, vp, C.c_int]),
         # model driver
         "wamx_gwp_default_config": (GwpConfig, []),
         "wamx_gwp_create": (vp, [vp, C.POINTER(GwpConfig)]),
