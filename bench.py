@@ -12,6 +12,11 @@ before the timed region):
          W_up [14336x3072] + bias + GELU-tanh -> W_down [3072x14336] + bias +
          gated residual (bf16 hidden state, fp32 accumulation).
   gemm   one MUL_MAT: W bf16 [3072x3072], X f32 [256x3072] -> Y f32.
+  decode the action-expert decode against a cached prefix (--batch B chunks):
+         the 10-step unrolled denoise graph of B independent chunks, each 48
+         action queries over its own resident bf16 KV (1 state + 3072 visual
+         self-attention keys and 512 prompt keys per layer, 30 layers, 24x128),
+         the projections on 48*B rows.
 
 Prints one JSON line (rank 0) with roofline and cpu_baseline objects.  The
 dominant kernel's duration is measured with HIP events on the backend's
@@ -350,7 +355,66 @@ def workload_chunk(be, args):
             "roofline": roof, "cpu_baseline": cpu}
 
 
-WORKLOADS = {"chunk": workload_chunk, "ffn": workload_ffn, "gemm": workload_gemm}
+def workload_decode(be, args):
+    """The action-expert decode against a cached prefix: prompt and prefix
+    caches of B chunks are filled once (untimed), then the 10-step unrolled
+    denoise graph runs on them.  One step reads every action-expert weight
+    once (289 MB per layer) and each chunk's KV (37.8 MB prefix + 6.3 MB
+    prompt per layer); the GEMMs do 2 * 48B * sum(M*K) flops."""
+    import ctypes as C
+    lib = be.lib
+    B = args.batch
+    c = lib.wamx_gwp_default_config()
+    c.batch = B
+    cfg = {k: getattr(c, k) for k, _ in wamx.GwpConfig._fields_}
+    m = lib.wamx_gwp_create(be.ptr, C.byref(c))
+    if not m:
+        raise RuntimeError(wamx.last_error())
+    wamx.check(lib.wamx_gwp_init_synthetic(m, 0x5EED0004, 0.02), "init_synthetic")
+    per = [_gwp_inputs(cfg, 0x5EED0004 + 17 * b) for b in range(B)]
+    ins = [np.ascontiguousarray(np.concatenate([p[i] for p in per])) for i in range(4)]
+    wamx.check(lib.wamx_gwp_set_inputs(m, *[a.ctypes.data for a in ins]), "set_inputs")
+    wamx.check(lib.wamx_gwp_run_prompt(m), "prompt")
+    wamx.check(lib.wamx_gwp_run_prefix(m), "prefix")
+    for _ in range(max(1, args.warmup)):
+        wamx.check(lib.wamx_gwp_run_denoise(m), "denoise")
+    be.sync()
+    t = wamx.Timer(be)
+    t.start()
+    for _ in range(args.steps):
+        wamx.check(lib.wamx_gwp_run_denoise(m), "denoise")
+    ms = t.stop_ms() / args.steps
+    action = np.empty(B * cfg["action_chunk"] * cfg["action_dim"], np.float32)
+    wamx.check(lib.wamx_gwp_get_action(m, action.ctypes.data), "get_action")
+    if not np.all(np.isfinite(action)):
+        raise RuntimeError("non-finite action chunk")
+    L, S, T = cfg["n_layers"], cfg["num_steps"], cfg["action_chunk"]
+    d, da, F, NL = cfg["hidden"], cfg["action_hidden"], cfg["action_ffn_dim"], cfg["n_lang"]
+    P = 1 + cfg["grid_h"] * cfg["grid_w"]
+    mk = 3 * d * da + da * d + d * da + da * d + 2 * F * da          # weight elements per layer
+    kv = 2 * (P + NL) * d * 2                                          # K + V bytes per chunk and layer
+    step_bytes = L * (2 * mk + B * kv)
+    step_flops = L * (2 * B * T * mk + 4 * B * T * (P + T + NL) * d)
+    gbs = step_bytes * S / (ms * 1e-3) / 1e9
+    nodes = int(lib.wamx_gwp_graph_nodes(m, 2))
+    lib.wamx_gwp_free(m)
+    roof = {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+            "traffic": None, "kernel": f"denoise graph, {B} chunk(s): {L} layers x {S} steps",
+            "bytes_per_step": step_bytes, "flops_per_step": step_flops,
+            "tflops": step_flops * S / (ms * 1e-3) / 1e12}
+    return {"metric": f"ms per decode of {B} action chunk(s) against a cached prefix (GWP-0.5-shape action "
+                      f"expert, bf16, 1 GPU)", "unit": "ms", "value": ms, "ms_per_step": ms,
+            "higher_is_better": False, "dtype": "bf16",
+            "config": {"workload": f"action-expert decode, batch {B}: 10 denoise steps, 48 queries per chunk over "
+                                   f"1+3072 self-attention and 512 prompt keys per layer, 30 layers, d=3072, 24x128, "
+                                   f"FFN 14336", "batch": B, "ms_per_chunk": ms / B,
+                       "chunks_per_s": B / (ms * 1e-3), "graph_nodes": nodes},
+            "roofline": roof,
+            "cpu_baseline": {"value": None, "unit": "ms", "cores": 0, "kind": "port",
+                             "sample": "not run for this workload (the chunk workload reports the CPU baseline)"}}
+
+
+WORKLOADS = {"chunk": workload_chunk, "ffn": workload_ffn, "gemm": workload_gemm, "decode": workload_decode}
 
 
 def probe_traffic(be, launches: int = 3):
@@ -404,6 +468,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="chunk", choices=sorted(WORKLOADS))
+    ap.add_argument("--batch", type=int, default=1, help="independent chunks (decode workload)")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="only launch the counter-calibration and roofline kernels (for rocprofv3 --pmc)")
     args = ap.parse_args()

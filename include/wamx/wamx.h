@@ -505,6 +505,10 @@ typedef struct wamx_gwp_config {
     int32_t enc_hidden;      /* action/state encoder and decoder MLP width (128) */
     float   shift;           /* flow-matching shift */
     float   eps;             /* norm eps */
+    int32_t batch;           /* independent action chunks per request (0 or 1: one).  Each chunk has
+                                its own inputs and prompt / prefix caches; the denoise graph runs all
+                                chunks' 48 tokens through each projection together (batch x chunk
+                                tokens) and each chunk's queries attend its own caches. */
 } wamx_gwp_config;
 
 typedef struct wamx_gwp_model * wamx_gwp_t;
@@ -527,8 +531,9 @@ WAMX_API uint64_t    wamx_gwp_param_count(wamx_gwp_t m);
 /* Random-init every weight on the device: bf16 matrices ~N(0, wstd), biases
  * ~N(0, 0.02), norm weights 1 + N(0, 0.02), scale/shift tables ~N(0, 0.1). */
 WAMX_API wamx_status wamx_gwp_init_synthetic(wamx_gwp_t m, uint64_t seed, float wstd);
-/* Inputs: state f32 [action_dim], latent f32 [z_dim][2*grid_h][2*grid_w] (CHW),
- * prompt f32 [n_lang][t5_hidden], noise f32 [action_chunk][action_dim]. */
+/* Inputs, chunk-major for batch > 1: state f32 [batch][action_dim], latent f32
+ * [batch][z_dim][2*grid_h][2*grid_w] (CHW), prompt f32 [batch][n_lang][t5_hidden],
+ * noise f32 [batch][action_chunk][action_dim]. */
 WAMX_API wamx_status wamx_gwp_set_inputs(wamx_gwp_t m, const float * state, const float * latent,
                                          const float * prompt, const float * noise);
 /* Run the three graphs (prompt projection, prefix, unrolled denoise). */
@@ -536,12 +541,13 @@ WAMX_API wamx_status wamx_gwp_predict(wamx_gwp_t m, wamx_gwp_timing * timing);
 WAMX_API wamx_status wamx_gwp_run_prompt(wamx_gwp_t m);
 WAMX_API wamx_status wamx_gwp_run_prefix(wamx_gwp_t m);
 WAMX_API wamx_status wamx_gwp_run_denoise(wamx_gwp_t m);
-/* Final action chunk (bf16 state widened to f32) [action_chunk][action_dim]. */
+/* Final action chunks (bf16 state widened to f32) [batch][action_chunk][action_dim]. */
 WAMX_API wamx_status wamx_gwp_get_action(wamx_gwp_t m, float * out);
-/* Prefix K/V cache of one layer as stored: K bf16 [H][P][dh], V bf16 [H][dh][P]. */
+/* Prefix K/V cache of one layer as stored: K bf16 [batch][H][P][dh] (ggml ne
+ * {dh, P, H, batch}), V^T bf16 [batch][H][dh][Ppad] viewed as ne {P, dh, H, batch}. */
 WAMX_API wamx_tensor * wamx_gwp_prefix_key(wamx_gwp_t m, int layer);
 WAMX_API wamx_tensor * wamx_gwp_prefix_value(wamx_gwp_t m, int layer);
-WAMX_API int         wamx_gwp_graph_nodes(wamx_gwp_t m, int which);  /* 0 prompt, 1 prefix, 2 denoise */
+WAMX_API int         wamx_gwp_graph_nodes(wamx_gwp_t m, int which);  /* 0 prompt, 1 prefix (chunk 0's), 2 denoise */
 
 /* Last error message of the calling thread ("" when none). */
 WAMX_API const char * wamx_last_error(void);

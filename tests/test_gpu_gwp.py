@@ -172,3 +172,60 @@ def test_baseline_size_runs_and_is_deterministic(wx, be):
         assert tuple(k.contents.ne)[:3] == (128, 3073, 24)
     finally:
         be.lib.wamx_gwp_free(m)
+
+
+def inputs_batch(cfg, B, seed):
+    """Chunk-major inputs of B independent chunks."""
+    per = [inputs(cfg, seed + 17 * b) for b in range(B)]
+    return tuple(np.concatenate([p[i] for p in per]) for i in range(4)), per
+
+
+def test_batched_chunks_match_oracle(wx, be, orc):
+    """Three independent chunks in one request (each with its own state,
+    latent, prompt and noise) against three oracle runs on the same weights."""
+    B = 3
+    cfg = dict(SMALL, batch=B)
+    print(f"gwp batch {B} vs oracle", flush=True)
+    m = make_model(wx, be, cfg, seed=0x5EED0008)
+    try:
+        w = read_weights(wx, be, m)
+        ins, per = inputs_batch(SMALL, B, 40)
+        got = run_gpu(wx, be, m, ins).reshape(B, -1)
+        k = tensor_bytes(wx, be, be.lib.wamx_gwp_prefix_key(m, 1), (B, SMALL["n_heads"], 1 + 32, 128))
+        for b in range(B):
+            ref_model = orc.Gwp(SMALL, w)
+            state, latent, prompt, noise = per[b]
+            ref_model.prompt(prompt)
+            ref_model.prefix(state, latent, prompt)
+            assert_parity(wx.bf16_to_f32(k[b]), wx.bf16_to_f32(ref_model.prefix_key(1)), what=f"chunk {b} prefix K 1")
+            action_gate(got[b], ref_model.denoise(noise), f"chunk {b} of {B}")
+        assert not np.array_equal(got[0], got[1])
+    finally:
+        be.lib.wamx_gwp_free(m)
+
+
+def test_batch8_full_width_properties(wx, be):
+    """Batch 8 at full width (d = 3072, 24 heads, FFN 14336, 512 prompt
+    tokens; 2 layers, 2 steps, 256 visual tokens): the denoise projections
+    run on 384 rows.  Reordering the chunks reorders the results bit for bit
+    (rows never mix), and each chunk matches a batch-1 model on its own."""
+    cfg = dict(n_layers=2, hidden=3072, n_heads=24, head_dim=128, ffn_dim=14336, action_hidden=3072,
+               action_ffn_dim=14336, action_chunk=48, action_dim=32, grid_h=8, grid_w=32, n_lang=512,
+               t5_hidden=4096, z_dim=48, num_steps=2, enc_hidden=128, shift=5.0, eps=1e-6)
+    B = 8
+    print("gwp batch 8 full width", flush=True)
+    m8 = make_model(wx, be, dict(cfg, batch=B), seed=0x5EED0009)
+    m1 = make_model(wx, be, cfg, seed=0x5EED0009)
+    try:
+        ins, per = inputs_batch(cfg, B, 70)
+        got = run_gpu(wx, be, m8, ins).reshape(B, -1)
+        perm = np.array([3, 0, 7, 1, 6, 2, 5, 4])
+        ins_p = tuple(np.concatenate([per[p][i] for p in perm]) for i in range(4))
+        got_p = run_gpu(wx, be, m8, ins_p).reshape(B, -1)
+        assert np.array_equal(got_p, got[perm])
+        for b in (0, 5):
+            one = run_gpu(wx, be, m1, per[b])
+            action_gate(got[b], one, f"batch-8 chunk {b} vs batch 1")
+    finally:
+        be.lib.wamx_gwp_free(m8)
+        be.lib.wamx_gwp_free(m1)

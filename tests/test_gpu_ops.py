@@ -271,3 +271,50 @@ def test_softmax_and_fill(wx, be, orc, rng):
     assert np.max(np.abs(got - ref) / np.maximum(1.0, np.abs(ref))) < 1e-4
     assert np.mean(np.abs(got - ref) > 1e-6 * np.maximum(1.0, np.abs(ref))) < 1e-2
     assert cosine(got, ref) > 0.999999
+
+
+# --- one DiT block's shapes (2048 video tokens on a t=4, h=16, w=32 grid + 48 action tokens) ---
+def test_qk_norm_rope_video_grid(wx, be, orc):
+    """3-D {44, 42, 42} RoPE with time positions t = 0..3 (frames), h = 0..15,
+    w = 0..31: 2048 video tokens x 24 heads (mot.cpp:182-202 on a multi-frame
+    grid; the reference itself uses t = 0)."""
+    print("qk_norm_rope 4x16x32 video grid", flush=True)
+    rng = np.random.default_rng(0x5EED0300)
+    H, dh, F, Hh, Ww = 24, 128, 4, 16, 32
+    T = F * Hh * Ww
+    x = bf16(rng.standard_normal((T, 3 * H * dh)))
+    w = bf16(1 + rng.standard_normal(H * dh) * 0.02)
+    idx = np.arange(T)
+    pt = (idx // (Hh * Ww)).astype(np.int32)
+    ph = ((idx // Ww) % Hh).astype(np.int32)
+    pw = (idx % Ww).astype(np.int32)
+    total = T + 48                                   # 48 action rows after the video rows
+    dx, dw = dev(be, x), dev(be, w)
+    d0, d1, d2 = dev(be, pt), dev(be, ph), dev(be, pw)
+    ddst = dev(be, np.zeros((H, total, dh), np.uint16))
+    for col in (0, H * dh):                          # Q and K sections of the packed projection
+        wx.check(be.lib.wamx_op_qk_norm_rope(be.ptr, dx.ptr + col * 2, 3 * H * dh, dw.ptr, ddst.ptr, H, dh, T, total,
+                                             0, 1, d0.ptr, d1.ptr, d2.ptr, 1e-6, 10000.0))
+        got = ddst.download(np.uint16, (H, total, dh))
+        ref = np.zeros((H, total, dh), np.uint16)
+        orc.qk_norm_rope(np.ascontiguousarray(x[:, col:col + H * dh]), w, H, dh, 1, pt, ph, pw, dst=ref, tok0=0)
+        assert_parity(f32(got), f32(ref), what="video-grid rope")
+        assert np.mean(got != ref) < 0.01
+
+
+def test_joint_attention_dit_block(wx, be, orc):
+    """Full bidirectional attention of one DiT block: 2096 queries over the
+    same 2096 keys (2048 video + 48 action tokens), 24 heads x 128."""
+    print("joint_attn 2096 x 2096 x 24", flush=True)
+    rng = np.random.default_rng(0x5EED0301)
+    H, n, dh = 24, 2096, 128
+    q = bf16(rng.standard_normal((H, n, dh)))
+    k = bf16(rng.standard_normal((H, n, dh)))
+    vt = bf16(rng.standard_normal((H, dh, n)))
+    dq, dk, dv = dev(be, q), dev(be, k), dev(be, vt)
+    dout = be.empty(n * H * dh * 2)
+    scale = 1.0 / np.sqrt(dh)
+    wx.check(be.lib.wamx_op_joint_attn(be.ptr, dq.ptr, dk.ptr, dv.ptr, n, None, None, 0, 0, dout.ptr, H, dh, n, scale))
+    got = dout.download(np.uint16, (n, H * dh))
+    ref = orc.attention(q, k, vt, scale=scale)
+    assert_parity(f32(got), f32(ref), what="dit-block attention")

@@ -386,7 +386,7 @@ static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post, bool la
             if (!column_view(x, lin, seg.col) || !t->src[1] || t->type != WAMX_TYPE_BF16) break;
             head_dim = t->ne[0];
             width = x->ne[0];
-            if (width != head_dim * t->ne[2]) break;
+            if (width != head_dim * t->ne[2] || t->ne[3] != 1) break;  // one chunk: the reduce has no chunk split
             seg.kind = kRowSegQk;
             seg.w = t->src[1]->data;
             seg.dst = t->data;
@@ -445,7 +445,8 @@ static hipError_t run_joint_attn(wamx_backend * be, const wamx_tensor * node) {
     }
     a.na_split = node->op_params[0];
     a.out = node->data;
-    a.heads = q->ne[2];
+    a.heads = q->ne[2] * q->ne[3];   // chunk b's heads follow chunk b - 1's
+    a.hb = q->ne[2];
     a.head_dim = q->ne[0];
     a.tq = q->ne[1];
     a.scale = param_f32(node, 1);
@@ -540,7 +541,8 @@ static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
                                        node->src[3] ? (const int32_t *) node->src[3]->data : nullptr,
                                        node->src[4] ? (const int32_t *) node->src[4]->data : nullptr,
                                        node->src[5] ? (const int32_t *) node->src[5]->data : nullptr,
-                                       param_f32(node, 2), param_f32(node, 3), s);
+                                       param_f32(node, 2), param_f32(node, 3), s, x->ne[1] / node->ne[3],
+                                       (int64_t) node->nb[3] / 2);
         }
         case WAMX_OP_JOINT_ATTN:
             return run_joint_attn(be, node);

@@ -61,6 +61,7 @@ struct wamx_gwp_model {
     wamx_backend_t be = nullptr;
     wamx_gwp_config cfg{};
     int64_t P = 0, Ppad = 0, nimg = 0, NLpad = 0, Tpad = 0;
+    int64_t B = 1;  // independent chunks (cfg.batch)
 
     wamx_context * wctx = nullptr;
     wamx_buffer_t wbuf = nullptr;
@@ -80,25 +81,32 @@ struct wamx_gwp_model {
     Cond acond{}, vcond{};
     std::vector<ExpertLayer> act, vis;
 
-    // Resident storage (prefix / prompt caches) and inputs.
+    // Resident storage (prefix / prompt caches) and inputs; the last dim of
+    // each is the chunk.
     wamx_context * sctx = nullptr;
     wamx_buffer_t sbuf = nullptr;
-    wamx_tensor * action_prompt = nullptr;
-    std::vector<wamx_tensor *> pk, pv_raw, pv;    // prefix K [dh,P,H]; V^T [Ppad,dh,H] and its [P,dh,H] view
-    std::vector<wamx_tensor *> lk, lv_raw, lv;    // prompt K [dh,NL,H]; V^T
+    wamx_tensor * action_prompt = nullptr;        // [da, NL, B]
+    std::vector<wamx_tensor *> pk, pv_raw, pv;    // prefix K [dh,P,H,B]; V^T [Ppad,dh,H,B] and its [P,dh,H,B] view
+    std::vector<wamx_tensor *> lk, lv_raw, lv;    // prompt K [dh,NL,H,B]; V^T
     wamx_tensor *in_state = nullptr, *in_latent = nullptr, *in_prompt = nullptr, *in_action = nullptr;
     wamx_tensor *in_apos = nullptr, *in_spos = nullptr, *in_vt = nullptr, *in_vh = nullptr, *in_vw = nullptr;
     wamx_tensor *in_freq0 = nullptr, *in_freqs = nullptr, *in_dts = nullptr;
 
-    // Graphs: 0 prompt, 1 prefix, 2 denoise.
-    wamx_context * gctx[3] = {nullptr, nullptr, nullptr};
-    wamx_cgraph * graph[3] = {nullptr, nullptr, nullptr};
-    wamx_gallocr_t galloc[3] = {nullptr, nullptr, nullptr};
+    // Graphs: a prompt and a prefix graph per chunk, then the denoise graph
+    // of all chunks (graphs[2B]).
+    std::vector<wamx_context *> gctx;
+    std::vector<wamx_cgraph *> graph;
+    std::vector<wamx_gallocr_t> galloc;
     wamx_tensor * action_out = nullptr;
     wamx_timer_t timer = nullptr;
 
+    int n_graphs() const { return (int) (2 * B + 1); }
+    int prompt_graph(int64_t b) const { return (int) b; }
+    int prefix_graph(int64_t b) const { return (int) (B + b); }
+    int denoise_graph() const { return (int) (2 * B); }
+
     ~wamx_gwp_model() {
-        for (int i = 0; i < 3; ++i) {
+        for (size_t i = 0; i < graph.size(); ++i) {
             wamx_gallocr_free(galloc[i]);
             wamx_free(gctx[i]);
         }
@@ -181,6 +189,11 @@ struct Builder {
         return lin(p.x2_w, p.x2_b, h);
     }
 
+    // The attention output [d, T, B] as the [d, B*T] rows the projections read.
+    wamx_tensor * rows(wamx_tensor * att) {
+        return att->ne[2] == 1 ? att : wamx_reshape_2d(ctx, att, att->ne[0], att->ne[1] * att->ne[2]);
+    }
+
     // View (layer l, part i) of a modulation tensor [width, 6, L] (f32).
     wamx_tensor * part(wamx_tensor * mods, int64_t width, int l, int i) {
         return wamx_view_1d(ctx, mods, width, (size_t) ((int64_t) l * 6 + i) * width * sizeof(float));
@@ -194,27 +207,39 @@ struct Builder {
     // V part of a packed [3d, tokens] projection, transposed into a V^T view
     // [tokens, dh, H] of `dst` (ggml_cont(ggml_permute(v, 1, 2, 0, 3)),
     // mot.cpp:397-401, written in place as cache.cpp:316-339 stores it).
+    // With chunks (dst_view [T, dh, H, B]) the rows of qkv are B chunks of T
+    // tokens.
     wamx_tensor * store_v(wamx_tensor * qkv, int64_t v_off, wamx_tensor * dst_view) {
-        const int64_t dh = c.head_dim, H = c.n_heads, T = qkv->ne[1];
-        wamx_tensor * v = wamx_view_3d(ctx, qkv, dh, H, T, (size_t) dh * 2, qkv->nb[1], (size_t) v_off * 2);
+        const int64_t dh = c.head_dim, H = c.n_heads, B = dst_view->ne[3], T = qkv->ne[1] / B;
+        wamx_tensor * v = B == 1 ? wamx_view_3d(ctx, qkv, dh, H, T, (size_t) dh * 2, qkv->nb[1], (size_t) v_off * 2)
+                                 : wamx_view_4d(ctx, qkv, dh, H, T, B, (size_t) dh * 2, qkv->nb[1],
+                                                qkv->nb[1] * (size_t) T, (size_t) v_off * 2);
         wamx_tensor * vp = wamx_permute(ctx, v, 1, 2, 0, 3);
         return wamx_cpy(ctx, vp, dst_view);
     }
 
-    // V^T view of `raw` [ld, dh, H] covering key columns [k0, k0+n).
+    // V^T view of `raw` [ld, dh, H(, B)] covering key columns [k0, k0+n).
     wamx_tensor * vt_view(wamx_tensor * raw, int64_t k0, int64_t n) {
-        return wamx_view_3d(ctx, raw, n, raw->ne[1], raw->ne[2], raw->nb[1], raw->nb[2], (size_t) k0 * 2);
+        if (raw->ne[3] == 1)
+            return wamx_view_3d(ctx, raw, n, raw->ne[1], raw->ne[2], raw->nb[1], raw->nb[2], (size_t) k0 * 2);
+        return wamx_view_4d(ctx, raw, n, raw->ne[1], raw->ne[2], raw->ne[3], raw->nb[1], raw->nb[2], raw->nb[3],
+                            (size_t) k0 * 2);
+    }
+
+    // Chunk b of a storage tensor whose last dim (dim 3) is the chunk.
+    wamx_tensor * chunk(wamx_tensor * t, int64_t b) {
+        return wamx_view_3d(ctx, t, t->ne[0], t->ne[1], t->ne[2], t->nb[1], t->nb[2], t->nb[3] * (size_t) b);
     }
 
     // expert_cross_ffn with cached prompt K/V (mot.cpp:284-347, cached branch).
     wamx_tensor * cross_ffn_cached(const ExpertLayer & e, wamx_tensor * h, wamx_tensor * pk, wamx_tensor * pv,
                                    wamx_tensor * cshift, wamx_tensor * cscale, wamx_tensor * cgate) {
-        const int64_t T = h->ne[1];
+        const int64_t B = pk->ne[3], T = h->ne[1] / B;  // rows: B chunks of T tokens
         wamx_tensor * n = wamx_layer_norm_bf16(ctx, h, e.n2_w, e.n2_b, c.eps);
         wamx_tensor * q = lin(e.cq_w, e.cq_b, n);
-        wamx_tensor * Q = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, c.head_dim, T, c.n_heads);
+        wamx_tensor * Q = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, c.head_dim, T, c.n_heads, B);
         Q = wamx_qk_norm_rope(ctx, q, e.cnq, Q, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
-        wamx_tensor * att = wamx_joint_attn(ctx, Q, pk, pv, nullptr, nullptr, 0, scale);
+        wamx_tensor * att = rows(wamx_joint_attn(ctx, Q, pk, pv, nullptr, nullptr, 0, scale));
         h = lin(e.co_w, e.co_b, att, WAMX_EPI_BIAS_RESIDUAL, h);
         return ffn(e, h, cshift, cscale, cgate);
     }
@@ -292,7 +317,9 @@ static bool create_weights(wamx_gwp_model * m) {
     m->v_tables = m->add_weight("gwp.blocks.visual_expert.scale_shift_table", d, 6, L);
     // The action expert's projections run on 48 denoise tokens (and the 1
     // state token of the prefix) and use the tiled layout; its cross-attention
-    // K/V projections run on the 512 prompt tokens and stay row-major.
+    // K/V projections run on the 512 prompt tokens and stay row-major.  With
+    // several chunks the denoise projections see batch x 48 tokens, past the
+    // few-token path the tiled layout serves, and every weight is row-major.
     // The prompt-token K/V projections of all layers are packed per expert, so
     // the prompt's K and V for every layer come out of one GEMM (one launch of
     // 2·L·d features instead of 2·L launches of d).
@@ -301,7 +328,8 @@ static bool create_weights(wamx_gwp_model * m) {
         m->kv_b[x] = wamx_new_tensor_1d(m->wctx, WAMX_TYPE_BF16, 2 * L * d);
         if (!m->kv_w[x] || !m->kv_b[x]) return false;
     }
-    auto expert = [&](const std::string & p, int64_t w, int64_t ffn, ExpertLayer & e, bool t, int64_t l) {
+    // x: 0 action expert, 1 visual expert (the packed K/V weight); t: tiled.
+    auto expert = [&](const std::string & p, int64_t w, int64_t ffn, ExpertLayer & e, int x, bool t, int64_t l) {
         m->add_linear(p + ".attn1.to_qkv", w, 3 * d, &e.qkv_w, &e.qkv_b, t);
         e.norm_q = m->add_weight(p + ".attn1.norm_q.weight", d);
         e.norm_k = m->add_weight(p + ".attn1.norm_k.weight", d);
@@ -309,9 +337,8 @@ static bool create_weights(wamx_gwp_model * m) {
         e.n2_w = m->add_weight(p + ".norm2.weight", w);
         e.n2_b = m->add_weight(p + ".norm2.bias", w);
         m->add_linear(p + ".attn2.to_q", w, d, &e.cq_w, &e.cq_b, t);
-        m->add_linear_view(p + ".attn2.to_k", m->kv_w[t ? 0 : 1], m->kv_b[t ? 0 : 1], 2 * l * d, d, &e.ck_w, &e.ck_b);
-        m->add_linear_view(p + ".attn2.to_v", m->kv_w[t ? 0 : 1], m->kv_b[t ? 0 : 1], (2 * l + 1) * d, d, &e.cv_w,
-                           &e.cv_b);
+        m->add_linear_view(p + ".attn2.to_k", m->kv_w[x], m->kv_b[x], 2 * l * d, d, &e.ck_w, &e.ck_b);
+        m->add_linear_view(p + ".attn2.to_v", m->kv_w[x], m->kv_b[x], (2 * l + 1) * d, d, &e.cv_w, &e.cv_b);
         e.cnq = m->add_weight(p + ".attn2.norm_q.weight", d);
         e.cnk = m->add_weight(p + ".attn2.norm_k.weight", d);
         m->add_linear(p + ".attn2.to_out.0", d, w, &e.co_w, &e.co_b, t);
@@ -322,8 +349,8 @@ static bool create_weights(wamx_gwp_model * m) {
     m->vis.resize(L);
     for (int64_t l = 0; l < L; ++l) {
         const std::string b = "gwp.blocks." + std::to_string(l);
-        expert(b + ".action_expert", da, c.action_ffn_dim, m->act[l], true, l);
-        expert(b + ".visual_expert", d, c.ffn_dim, m->vis[l], false, l);
+        expert(b + ".action_expert", da, c.action_ffn_dim, m->act[l], 0, m->B * c.action_chunk <= 64, l);
+        expert(b + ".visual_expert", d, c.ffn_dim, m->vis[l], 1, false, l);
     }
     for (auto & kv : m->weights)
         if (!kv.second) return false;
@@ -338,21 +365,21 @@ static bool create_weights(wamx_gwp_model * m) {
 
 static bool create_storage(wamx_gwp_model * m) {
     const wamx_gwp_config & c = m->cfg;
-    const int64_t dh = c.head_dim, H = c.n_heads, L = c.n_layers;
+    const int64_t dh = c.head_dim, H = c.n_heads, L = c.n_layers, B = m->B;
     m->sctx = wamx_init(16 * L + 64);
     if (!m->sctx) return false;
     wamx_context * s = m->sctx;
-    m->action_prompt = wamx_new_tensor_2d(s, WAMX_TYPE_BF16, c.action_hidden, c.n_lang);
+    m->action_prompt = wamx_new_tensor_3d(s, WAMX_TYPE_BF16, c.action_hidden, c.n_lang, B);
     for (int64_t l = 0; l < L; ++l) {
-        m->pk.push_back(wamx_new_tensor_3d(s, WAMX_TYPE_BF16, dh, m->P, H));
-        m->pv_raw.push_back(wamx_new_tensor_3d(s, WAMX_TYPE_BF16, m->Ppad, dh, H));
-        m->lk.push_back(wamx_new_tensor_3d(s, WAMX_TYPE_BF16, dh, c.n_lang, H));
-        m->lv_raw.push_back(wamx_new_tensor_3d(s, WAMX_TYPE_BF16, m->NLpad, dh, H));
+        m->pk.push_back(wamx_new_tensor_4d(s, WAMX_TYPE_BF16, dh, m->P, H, B));
+        m->pv_raw.push_back(wamx_new_tensor_4d(s, WAMX_TYPE_BF16, m->Ppad, dh, H, B));
+        m->lk.push_back(wamx_new_tensor_4d(s, WAMX_TYPE_BF16, dh, c.n_lang, H, B));
+        m->lv_raw.push_back(wamx_new_tensor_4d(s, WAMX_TYPE_BF16, m->NLpad, dh, H, B));
     }
-    m->in_state = wamx_new_tensor_2d(s, WAMX_TYPE_F32, c.action_dim, 1);
-    m->in_latent = wamx_new_tensor_4d(s, WAMX_TYPE_F32, 2 * c.grid_w, 2 * c.grid_h, c.z_dim, 1);
-    m->in_prompt = wamx_new_tensor_2d(s, WAMX_TYPE_F32, c.t5_hidden, c.n_lang);
-    m->in_action = wamx_new_tensor_2d(s, WAMX_TYPE_BF16, c.action_dim, c.action_chunk);
+    m->in_state = wamx_new_tensor_2d(s, WAMX_TYPE_F32, c.action_dim, B);
+    m->in_latent = wamx_new_tensor_4d(s, WAMX_TYPE_F32, 2 * c.grid_w, 2 * c.grid_h, c.z_dim, B);
+    m->in_prompt = wamx_new_tensor_3d(s, WAMX_TYPE_F32, c.t5_hidden, c.n_lang, B);
+    m->in_action = wamx_new_tensor_2d(s, WAMX_TYPE_BF16, c.action_dim, c.action_chunk * B);
     m->in_apos = wamx_new_tensor_1d(s, WAMX_TYPE_I32, c.action_chunk);
     m->in_spos = wamx_new_tensor_1d(s, WAMX_TYPE_I32, 1);
     m->in_vt = wamx_new_tensor_1d(s, WAMX_TYPE_I32, m->nimg);
@@ -366,9 +393,9 @@ static bool create_storage(wamx_gwp_model * m) {
     // Views of the padded V^T storage covering the real key columns.
     for (int64_t l = 0; l < L; ++l) {
         wamx_tensor * r = m->pv_raw[l];
-        m->pv.push_back(wamx_view_3d(s, r, m->P, dh, H, r->nb[1], r->nb[2], 0));
+        m->pv.push_back(wamx_view_4d(s, r, m->P, dh, H, B, r->nb[1], r->nb[2], r->nb[3], 0));
         wamx_tensor * q = m->lv_raw[l];
-        m->lv.push_back(wamx_view_3d(s, q, c.n_lang, dh, H, q->nb[1], q->nb[2], 0));
+        m->lv.push_back(wamx_view_4d(s, q, c.n_lang, dh, H, B, q->nb[1], q->nb[2], q->nb[3], 0));
     }
     // Zero the storage once so padded V^T columns hold finite values.
     for (auto * t : m->pv_raw) wamx_backend_tensor_memset(t, 0, 0, wamx_nbytes(t));
@@ -420,48 +447,64 @@ static bool create_storage(wamx_gwp_model * m) {
     return true;
 }
 
-// Graph 1: prompt projection (cache.cpp:53-137, build_cross_kv mot.cpp:101-128).
-static bool build_prompt_graph(wamx_gwp_model * m) {
+// Graph 1: prompt projection of chunk b (cache.cpp:53-137, build_cross_kv
+// mot.cpp:101-128).
+static bool build_prompt_graph(wamx_gwp_model * m, int64_t cb) {
     const wamx_gwp_config & c = m->cfg;
-    wamx_context * ctx = m->gctx[0] = wamx_init(64 * c.n_layers + 256);
+    const int gi = m->prompt_graph(cb);
+    wamx_context * ctx = m->gctx[gi] = wamx_init(64 * c.n_layers + 256);
     Builder b(m, ctx);
-    wamx_cgraph * g = m->graph[0] = wamx_new_graph(ctx, 64 * c.n_layers + 256);
-    wamx_tensor * txt = b.text(m->acond, m->in_prompt);
-    wamx_build_forward_expand(g, wamx_cpy(ctx, txt, m->action_prompt));
+    wamx_cgraph * g = m->graph[gi] = wamx_new_graph(ctx, 64 * c.n_layers + 256);
+    wamx_tensor * prompt = wamx_view_2d(ctx, m->in_prompt, c.t5_hidden, c.n_lang, m->in_prompt->nb[1],
+                                        m->in_prompt->nb[2] * (size_t) cb);
+    wamx_tensor * txt = b.text(m->acond, prompt);
+    wamx_tensor * ap = wamx_view_2d(ctx, m->action_prompt, c.action_hidden, c.n_lang, m->action_prompt->nb[1],
+                                    m->action_prompt->nb[2] * (size_t) cb);
+    wamx_build_forward_expand(g, wamx_cpy(ctx, txt, ap));
     const int64_t d = (int64_t) c.n_heads * c.head_dim;
     wamx_tensor * kv = b.lin(m->kv_w[0], m->kv_b[0], txt);  // every layer's prompt K/V [2·L·d, NL]
     for (int l = 0; l < c.n_layers; ++l) {
         const ExpertLayer & e = m->act[l];
         wamx_tensor * k = b.cols(kv, d, 2 * (int64_t) l * d);
+        wamx_build_forward_expand(g, wamx_qk_norm_rope(ctx, k, e.cnk, b.chunk(m->lk[l], cb), 0, 2, nullptr, nullptr,
+                                                       nullptr, c.eps, 10000.0f));
         wamx_build_forward_expand(
-            g, wamx_qk_norm_rope(ctx, k, e.cnk, m->lk[l], 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f));
-        wamx_build_forward_expand(g, b.store_v(kv, (2 * (int64_t) l + 1) * d, b.vt_view(m->lv_raw[l], 0, c.n_lang)));
+            g, b.store_v(kv, (2 * (int64_t) l + 1) * d, b.vt_view(b.chunk(m->lv_raw[l], cb), 0, c.n_lang)));
     }
     wamx_graph_assign_uid(g);
-    m->galloc[0] = wamx_gallocr_new(m->be);
-    return m->galloc[0] && wamx_gallocr_alloc_graph(m->galloc[0], g);
+    m->galloc[gi] = wamx_gallocr_new(m->be);
+    return m->galloc[gi] && wamx_gallocr_alloc_graph(m->galloc[gi], g);
 }
 
-// Graph 2: prefix pass (cache.cpp:139-485).
-static bool build_prefix_graph(wamx_gwp_model * m) {
+// Graph 2: prefix pass of chunk cb (cache.cpp:139-485), writing that chunk's
+// slice of the prefix cache.
+static bool build_prefix_graph(wamx_gwp_model * m, int64_t cb) {
     const wamx_gwp_config & c = m->cfg;
     const int64_t d = (int64_t) c.n_heads * c.head_dim, da = c.action_hidden, dh = c.head_dim, H = c.n_heads;
     const int64_t nimg = m->nimg, P = m->P;
-    wamx_context * ctx = m->gctx[1] = wamx_init(160 * c.n_layers + 512);
+    const int gi = m->prefix_graph(cb);
+    wamx_context * ctx = m->gctx[gi] = wamx_init(180 * c.n_layers + 512);
     Builder b(m, ctx);
-    wamx_cgraph * g = m->graph[1] = wamx_new_graph(ctx, 160 * c.n_layers + 512);
+    wamx_cgraph * g = m->graph[gi] = wamx_new_graph(ctx, 160 * c.n_layers + 512);
+    wamx_tensor * state = wamx_view_2d(ctx, m->in_state, c.action_dim, 1, m->in_state->nb[1],
+                                       m->in_state->nb[1] * (size_t) cb);
+    wamx_tensor * latent = wamx_view_4d(ctx, m->in_latent, m->in_latent->ne[0], m->in_latent->ne[1],
+                                        m->in_latent->ne[2], 1, m->in_latent->nb[1], m->in_latent->nb[2],
+                                        m->in_latent->nb[3], m->in_latent->nb[3] * (size_t) cb);
+    wamx_tensor * prompt = wamx_view_2d(ctx, m->in_prompt, c.t5_hidden, c.n_lang, m->in_prompt->nb[1],
+                                        m->in_prompt->nb[2] * (size_t) cb);
 
     // The state token's chain (its expert projections, row ops and attention
     // query) runs on lane 1, concurrently with the visual tokens' on lane 0;
     // the two meet only through the prefix K/V cache of each layer.
     wamx_set_lane(ctx, 1);
-    wamx_tensor * sh = b.mlp3(m->state_enc, m->in_state);  // [da, 1]
+    wamx_tensor * sh = b.mlp3(m->state_enc, state);  // [da, 1]
     wamx_tensor *stemb, *smod;
     b.condition(m->acond, m->in_freq0, &stemb, &smod);
     wamx_tensor * amods = wamx_modulation(ctx, smod, m->a_tables);  // [da, 6, L] f32
     wamx_set_lane(ctx, 0);
     // Patch embedding: conv 2x2 stride 2 as im2col + bf16 MUL_MAT + bias (cache.cpp:203-218).
-    wamx_tensor * cols = wamx_im2col(ctx, m->patch_w, m->in_latent, 2, 2, 0, 0, 1, 1, WAMX_TYPE_BF16);
+    wamx_tensor * cols = wamx_im2col(ctx, m->patch_w, latent, 2, 2, 0, 0, 1, 1, WAMX_TYPE_BF16);
     cols = wamx_reshape_2d(ctx, cols, cols->ne[0], nimg);
     wamx_tensor * pw = wamx_reshape_2d(ctx, m->patch_w, 4 * (int64_t) c.z_dim, d);
     wamx_tensor * vh = b.lin(pw, m->patch_b, cols);  // [d, nimg]
@@ -470,13 +513,15 @@ static bool build_prefix_graph(wamx_gwp_model * m) {
     // Every visual token has the timestep-0 embedding; its condition rows are
     // identical, so one row is computed and broadcast (bit-identical).
     b.condition(m->vcond, m->in_freq0, &vtemb, &vmod);
-    wamx_tensor * vtext = b.text(m->vcond, m->in_prompt);
+    wamx_tensor * vtext = b.text(m->vcond, prompt);
     wamx_tensor * vkv = b.lin(m->kv_w[1], m->kv_b[1], vtext);  // every layer's text K/V [2·L·d, NL]
     wamx_tensor * vmods = wamx_modulation(ctx, vmod, m->v_tables);  // [d, 6, L] f32
 
     for (int l = 0; l < c.n_layers; ++l) {
         const ExpertLayer & ea = m->act[l];
         const ExpertLayer & ev = m->vis[l];
+        wamx_tensor * pk = b.chunk(m->pk[l], cb);       // [dh, P, H]
+        wamx_tensor * pv_raw = b.chunk(m->pv_raw[l], cb);
         // State token (lane 1): its Q, and row 0 of the layer's K / V^T cache
         // (1-D rope at position 0).
         wamx_set_lane(ctx, 1);
@@ -485,9 +530,9 @@ static bool build_prefix_graph(wamx_gwp_model * m) {
         wamx_tensor * Qs = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, dh, 1, H);
         Qs = wamx_qk_norm_rope(ctx, b.cols(sqkv, d, 0), ea.norm_q, Qs, 0, 0, m->in_spos, nullptr, nullptr, c.eps,
                                10000.0f);
-        wamx_tensor * K = wamx_qk_norm_rope(ctx, b.cols(sqkv, d, d), ea.norm_k, m->pk[l], 0, 0, m->in_spos, nullptr,
-                                            nullptr, c.eps, 10000.0f);
-        wamx_tensor * v0 = b.store_v(sqkv, 2 * d, b.vt_view(m->pv_raw[l], 0, 1));
+        wamx_tensor * K = wamx_qk_norm_rope(ctx, b.cols(sqkv, d, d), ea.norm_k, pk, 0, 0, m->in_spos, nullptr, nullptr,
+                                            c.eps, 10000.0f);
+        wamx_tensor * v0 = b.store_v(sqkv, 2 * d, b.vt_view(pv_raw, 0, 1));
         // Visual tokens (lane 0): their Q, and rows 1..P of the cache (3-D
         // {44,42,42} rope).
         wamx_set_lane(ctx, 0);
@@ -498,8 +543,8 @@ static bool build_prefix_graph(wamx_gwp_model * m) {
                                10000.0f);
         K = wamx_qk_norm_rope(ctx, b.cols(vqkv, d, d), ev.norm_k, K, 1, 1, m->in_vt, m->in_vh, m->in_vw, c.eps,
                               10000.0f);
-        wamx_tensor * v1 = b.store_v(vqkv, 2 * d, after(b.vt_view(m->pv_raw[l], 1, nimg), v0));
-        wamx_tensor * V = after(b.vt_view(m->pv_raw[l], 0, P), v1);
+        wamx_tensor * v1 = b.store_v(vqkv, 2 * d, after(b.vt_view(pv_raw, 1, nimg), v0));
+        wamx_tensor * V = after(b.vt_view(pv_raw, 0, P), v1);
         wamx_set_output(K);
         wamx_set_output(V);
         wamx_build_forward_expand(g, K);
@@ -514,25 +559,28 @@ static bool build_prefix_graph(wamx_gwp_model * m) {
         wamx_set_lane(ctx, 1);
         wamx_tensor * satt = wamx_joint_attn(ctx, Qs, K, V, nullptr, nullptr, 0, b.scale);  // [d, 1]
         sh = b.lin(ea.o_w, ea.o_b, satt, WAMX_EPI_BIAS_GATED, sh, b.part(amods, da, l, 2));
-        sh = b.cross_ffn_cached(ea, sh, m->lk[l], m->lv[l], b.part(amods, da, l, 3), b.part(amods, da, l, 4),
-                                b.part(amods, da, l, 5));
+        sh = b.cross_ffn_cached(ea, sh, b.chunk(m->lk[l], cb), b.chunk(m->lv[l], cb), b.part(amods, da, l, 3),
+                                b.part(amods, da, l, 4), b.part(amods, da, l, 5));
         wamx_set_lane(ctx, 0);
     }
     wamx_set_lane(ctx, 0);
     wamx_graph_assign_uid(g);
-    m->galloc[1] = wamx_gallocr_new(m->be);
-    return m->galloc[1] && wamx_gallocr_alloc_graph(m->galloc[1], g);
+    m->galloc[gi] = wamx_gallocr_new(m->be);
+    return m->galloc[gi] && wamx_gallocr_alloc_graph(m->galloc[gi], g);
 }
 
 // Graph 3: unrolled denoise (mot.cpp:498-594 over build_cached_action_body).
+// The B chunks' tokens are the rows of every projection (B*T rows, chunk
+// after chunk); each chunk's queries attend its own prefix and prompt caches.
 static bool build_denoise_graph(wamx_gwp_model * m) {
     const wamx_gwp_config & c = m->cfg;
-    const int64_t da = c.action_hidden, dh = c.head_dim, H = c.n_heads, T = c.action_chunk;
+    const int64_t da = c.action_hidden, dh = c.head_dim, H = c.n_heads, T = c.action_chunk, B = m->B;
     const int64_t d = dh * H;
-    wamx_context * ctx = m->gctx[2] = wamx_init((size_t) (40 * c.n_layers + 64) * c.num_steps + 64);
+    const int gi = m->denoise_graph();
+    wamx_context * ctx = m->gctx[gi] = wamx_init((size_t) (48 * c.n_layers + 64) * c.num_steps + 64);
     Builder b(m, ctx);
-    wamx_cgraph * g = m->graph[2] = wamx_new_graph(ctx, (size_t) (40 * c.n_layers + 64) * c.num_steps + 64);
-    wamx_tensor * action = m->in_action;  // bf16 [A, T]
+    wamx_cgraph * g = m->graph[gi] = wamx_new_graph(ctx, (size_t) (40 * c.n_layers + 64) * c.num_steps + 64);
+    wamx_tensor * action = m->in_action;  // bf16 [A, B*T]
     for (int s = 0; s < c.num_steps; ++s) {
         wamx_tensor * freq = wamx_view_2d(ctx, m->in_freqs, 256, 1, m->in_freqs->nb[1], (size_t) s * 256 * 4);
         wamx_tensor * dt = wamx_view_1d(ctx, m->in_dts, 1, (size_t) s * 4);
@@ -544,16 +592,16 @@ static bool build_denoise_graph(wamx_gwp_model * m) {
             const ExpertLayer & e = m->act[l];
             wamx_tensor * n = wamx_norm_modulation_bf16(ctx, h, b.part(mods, da, l, 1), b.part(mods, da, l, 0), c.eps);
             wamx_tensor * qkv = b.lin(e.qkv_w, e.qkv_b, n);
-            wamx_tensor * Q = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, dh, T, H);
+            wamx_tensor * Q = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, dh, T, H, B);
             Q = wamx_qk_norm_rope(ctx, b.cols(qkv, d, 0), e.norm_q, Q, 0, 0, m->in_apos, nullptr, nullptr, c.eps,
                                   10000.0f);
-            wamx_tensor * Ka = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, dh, T, H);
+            wamx_tensor * Ka = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, dh, T, H, B);
             Ka = wamx_qk_norm_rope(ctx, b.cols(qkv, d, d), e.norm_k, Ka, 0, 0, m->in_apos, nullptr, nullptr, c.eps,
                                    10000.0f);
-            wamx_tensor * vraw = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, m->Tpad, dh, H);
+            wamx_tensor * vraw = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, m->Tpad, dh, H, B);
             wamx_tensor * Va = b.store_v(qkv, 2 * d, b.vt_view(vraw, 0, T));
             // Keys [state, action, reference]: prefix cache split after the state token.
-            wamx_tensor * att = wamx_joint_attn(ctx, Q, m->pk[l], m->pv[l], Ka, Va, 1, b.scale);
+            wamx_tensor * att = b.rows(wamx_joint_attn(ctx, Q, m->pk[l], m->pv[l], Ka, Va, 1, b.scale));
             h = b.lin(e.o_w, e.o_b, att, WAMX_EPI_BIAS_GATED, h, b.part(mods, da, l, 2));
             h = b.cross_ffn_cached(e, h, m->lk[l], m->lv[l], b.part(mods, da, l, 3), b.part(mods, da, l, 4),
                                    b.part(mods, da, l, 5));
@@ -574,8 +622,8 @@ static bool build_denoise_graph(wamx_gwp_model * m) {
     wamx_set_output(action);
     wamx_build_forward_expand(g, action);
     wamx_graph_assign_uid(g);
-    m->galloc[2] = wamx_gallocr_new(m->be);
-    return m->galloc[2] && wamx_gallocr_alloc_graph(m->galloc[2], g);
+    m->galloc[gi] = wamx_gallocr_new(m->be);
+    return m->galloc[gi] && wamx_gallocr_alloc_graph(m->galloc[gi], g);
 }
 
 // ---------------------------------------------------------------------------
@@ -603,6 +651,7 @@ wamx_gwp_config wamx_gwp_default_config(void) {
     c.enc_hidden = 128;
     c.shift = 5.0f;
     c.eps = 1e-6f;
+    c.batch = 1;
     return c;
 }
 
@@ -616,13 +665,20 @@ wamx_gwp_t wamx_gwp_create(wamx_backend_t be, const wamx_gwp_config * cfg) {
     if (c.n_layers < 1 || c.n_heads < 1 || c.head_dim != 128 || c.hidden != c.n_heads * c.head_dim ||
         c.action_hidden < 1 || c.ffn_dim < 1 || c.action_ffn_dim < 1 || c.action_chunk < 1 || c.action_chunk > 64 ||
         c.action_dim < 1 || c.grid_h < 1 || c.grid_w < 1 || c.n_lang < 1 || c.t5_hidden < 1 || c.z_dim < 1 ||
-        c.num_steps < 1 || c.enc_hidden < 1 || !(c.shift > 0.0f) || !(c.eps >= 0.0f)) {
-        set_error("wamx_gwp_create: invalid configuration (head_dim 128, hidden = heads*128, chunk <= 64)");
+        c.num_steps < 1 || c.enc_hidden < 1 || !(c.shift > 0.0f) || !(c.eps >= 0.0f) || c.batch < 0 ||
+        c.batch > 64) {
+        set_error("wamx_gwp_create: invalid configuration (head_dim 128, hidden = heads*128, chunk <= 64, "
+                  "batch <= 64)");
         return nullptr;
     }
     auto m = std::make_unique<wamx_gwp_model>();
     m->be = be;
     m->cfg = c;
+    m->B = c.batch > 1 ? c.batch : 1;
+    m->cfg.batch = (int32_t) m->B;
+    m->gctx.assign(m->n_graphs(), nullptr);
+    m->graph.assign(m->n_graphs(), nullptr);
+    m->galloc.assign(m->n_graphs(), nullptr);
     m->nimg = (int64_t) c.grid_h * c.grid_w;
     m->P = 1 + m->nimg;
     // V^T rows padded to 64 keys (128 bytes), so every 64-key block of a row
@@ -638,7 +694,9 @@ wamx_gwp_t wamx_gwp_create(wamx_backend_t be, const wamx_gwp_config * cfg) {
         set_errorf("wamx_gwp_create: cache allocation failed: %s", wamx_last_error());
         return nullptr;
     }
-    if (!build_prompt_graph(m.get()) || !build_prefix_graph(m.get()) || !build_denoise_graph(m.get())) {
+    bool ok = true;
+    for (int64_t cb = 0; cb < m->B && ok; ++cb) ok = build_prompt_graph(m.get(), cb) && build_prefix_graph(m.get(), cb);
+    if (!ok || !build_denoise_graph(m.get())) {
         set_errorf("wamx_gwp_create: graph construction failed: %s", wamx_last_error());
         return nullptr;
     }
@@ -722,19 +780,29 @@ wamx_status wamx_gwp_set_inputs(wamx_gwp_t m, const float * state, const float *
 }
 
 static wamx_status run_graph(wamx_gwp_t m, int which) {
-    WAMX_REQUIRE(m && m->graph[which], "wamx_gwp: graph %d missing", which);
+    WAMX_REQUIRE(m && which >= 0 && which < m->n_graphs() && m->graph[which], "wamx_gwp: graph %d missing", which);
     return wamx_backend_graph_compute(m->be, m->graph[which]);
 }
-wamx_status wamx_gwp_run_prompt(wamx_gwp_t m) { return run_graph(m, 0); }
-wamx_status wamx_gwp_run_prefix(wamx_gwp_t m) { return run_graph(m, 1); }
-wamx_status wamx_gwp_run_denoise(wamx_gwp_t m) { return run_graph(m, 2); }
+// Phase p (0 prompt, 1 prefix, 2 denoise) of every chunk.
+static wamx_status run_phase(wamx_gwp_t m, int phase) {
+    WAMX_REQUIRE(m, "wamx_gwp: null model");
+    if (phase == 2) return run_graph(m, m->denoise_graph());
+    for (int64_t cb = 0; cb < m->B; ++cb) {
+        const wamx_status st = run_graph(m, phase == 0 ? m->prompt_graph(cb) : m->prefix_graph(cb));
+        if (st != WAMX_STATUS_SUCCESS) return st;
+    }
+    return WAMX_STATUS_SUCCESS;
+}
+wamx_status wamx_gwp_run_prompt(wamx_gwp_t m) { return run_phase(m, 0); }
+wamx_status wamx_gwp_run_prefix(wamx_gwp_t m) { return run_phase(m, 1); }
+wamx_status wamx_gwp_run_denoise(wamx_gwp_t m) { return run_phase(m, 2); }
 
 wamx_status wamx_gwp_predict(wamx_gwp_t m, wamx_gwp_timing * timing) {
     WAMX_REQUIRE(m, "wamx_gwp_predict: null model");
     float ms[3] = {0, 0, 0};
     for (int i = 0; i < 3; ++i) {
         if (timing) wamx_timer_start(m->timer);
-        const wamx_status st = run_graph(m, i);
+        const wamx_status st = run_phase(m, i);
         if (st != WAMX_STATUS_SUCCESS) return st;
         if (timing) ms[i] = wamx_timer_stop_ms(m->timer);
     }
@@ -765,7 +833,9 @@ wamx_tensor * wamx_gwp_prefix_value(wamx_gwp_t m, int layer) {
     return (m && layer >= 0 && layer < m->cfg.n_layers) ? m->pv[layer] : nullptr;
 }
 int wamx_gwp_graph_nodes(wamx_gwp_t m, int which) {
-    return (m && which >= 0 && which < 3) ? wamx_graph_n_nodes(m->graph[which]) : 0;
+    if (!m || which < 0 || which > 2) return 0;
+    const int gi = which == 0 ? m->prompt_graph(0) : which == 1 ? m->prefix_graph(0) : m->denoise_graph();
+    return wamx_graph_n_nodes(m->graph[gi]);
 }
 
 }  // extern "C"

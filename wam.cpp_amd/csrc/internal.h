@@ -153,12 +153,15 @@ hipError_t launch_modulation(const void * mod, int32_t mod_type, const void * ta
 // ---------------------------------------------------------------------------
 // Fused attention-side kernels.
 // ---------------------------------------------------------------------------
+// Rows of x are chunk_tokens-token chunks (0: one chunk): token tl of chunk b
+// takes position pos[tl] and goes to dst + b * chunk_stride (elements).
 hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void * dst, int64_t heads, int64_t head_dim,
                                int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode, const int32_t * pos0,
-                               const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s);
+                               const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s,
+                               int64_t chunk_tokens = 0, int64_t chunk_stride = 0);
 
 struct AttnArgs {
-    const void * q = nullptr;      // bf16 [H][Tq][dh]
+    const void * q = nullptr;      // bf16 [batch][H][Tq][dh]
     const void * k_a = nullptr;    // bf16 [H][na][dh]
     const void * vt_a = nullptr;   // bf16 [H][dh][vt_ld_a]
     int64_t na = 0, vt_ld_a = 0;
@@ -168,6 +171,11 @@ struct AttnArgs {
     int64_t na_split = 0;          // reference key order: a[0,na_split), b, a[na_split,na)
     void * out = nullptr;          // bf16 [Tq][H*dh]
     int64_t heads = 0, head_dim = 0, tq = 0;
+    // Independent chunks: heads = batch x hb; chunk b's sources and queries
+    // are heads [b * hb, (b + 1) * hb) of the arrays above (each array
+    // contiguous across chunks) and its output rows [b * tq, (b + 1) * tq)
+    // of out [batch][tq][hb * head_dim].  0: one chunk (hb = heads).
+    int64_t hb = 0;
     float scale = 1.0f;
     void * ws = nullptr;           // fp32 partials of the key-split path
     size_t ws_bytes = 0;

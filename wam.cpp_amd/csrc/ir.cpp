@@ -129,9 +129,12 @@ const char * check_linear(const wamx_tensor * t) {
 const char * check_qk_norm_rope(const wamx_tensor * t) {
     const wamx_tensor *x = t->src[0], *weight = t->src[1], *dst = t->src[2];
     if (!is_bf16(x) || !is_bf16(weight) || !is_bf16(dst) || !is_bf16(t)) return "types";
-    const int64_t dh = dst->ne[0], H = dst->ne[2], T = x->ne[1];
+    // dst [dh, tokens, H, B]: the rows of x are B chunks of T tokens each.
+    const int64_t dh = dst->ne[0], H = dst->ne[2], B = dst->ne[3];
+    if (B < 1 || x->ne[1] % B != 0) return "rows must split into the destination's chunks";
+    const int64_t T = x->ne[1] / B;
     if (x->ne[0] != dh * H || weight->ne[0] != x->ne[0] || x->nb[0] != 2 || weight->nb[0] != 2 || !contig(dst) ||
-        x->ne[2] != 1 || x->ne[3] != 1 || dst->ne[3] != 1 || (dh & 1))
+        x->ne[2] != 1 || x->ne[3] != 1 || (dh & 1))
         return "shapes";
     for (int i = 0; i < 4; ++i)
         if (t->ne[i] != dst->ne[i] || t->nb[i] != dst->nb[i]) return "result must be the destination";
@@ -149,28 +152,32 @@ const char * check_qk_norm_rope(const wamx_tensor * t) {
 const char * check_joint_attn(const wamx_tensor * t) {
     const wamx_tensor *q = t->src[0], *k_a = t->src[1], *v_a = t->src[2], *k_b = t->src[3], *v_b = t->src[4];
     if (!is_bf16(q) || !is_bf16(k_a) || !is_bf16(v_a)) return "types";
-    const int64_t dh = q->ne[0], Tq = q->ne[1], H = q->ne[2];
+    // dim 3 is the chunk: B independent key sets and query sets.
+    const int64_t dh = q->ne[0], Tq = q->ne[1], H = q->ne[2], B = q->ne[3];
     const int64_t na = k_a->ne[1];
     if (dh != 128) return "head_dim must be 128";
-    if (k_a->ne[0] != dh || k_a->ne[2] != H || v_a->ne[0] != na || v_a->ne[1] != dh || v_a->ne[2] != H)
+    if (k_a->ne[0] != dh || k_a->ne[2] != H || k_a->ne[3] != B || v_a->ne[0] != na || v_a->ne[1] != dh ||
+        v_a->ne[2] != H || v_a->ne[3] != B)
         return "kv_a shapes";
     if ((k_b == nullptr) != (v_b == nullptr)) return "kv_b pair";
     if (k_b) {
         const int64_t nb = k_b->ne[1];
-        if (!is_bf16(k_b) || !is_bf16(v_b) || k_b->ne[0] != dh || k_b->ne[2] != H || v_b->ne[0] != nb ||
-            v_b->ne[1] != dh || v_b->ne[2] != H)
+        if (!is_bf16(k_b) || !is_bf16(v_b) || k_b->ne[0] != dh || k_b->ne[2] != H || k_b->ne[3] != B ||
+            v_b->ne[0] != nb || v_b->ne[1] != dh || v_b->ne[2] != H || v_b->ne[3] != B)
             return "kv_b shapes";
     }
     const int64_t na_split = t->op_params[0];
     if (na_split < 0 || na_split > na) return "split";
     for (const wamx_tensor * s : {q, k_a, k_b})
-        if (s && (!contig(s) || s->ne[3] != 1)) return "q and k must be contiguous";
-    // V^T rows may be padded: 8-byte aligned row stride covering ne[0] keys.
+        if (s && !contig(s)) return "q and k must be contiguous";
+    // V^T rows may be padded: 8-byte aligned row stride covering ne[0] keys;
+    // heads and chunks follow each other.
     for (const wamx_tensor * s : {v_a, v_b})
         if (s && (s->nb[0] != 2 || s->nb[1] % 8 != 0 || s->nb[1] < (size_t) s->ne[0] * 2 ||
-                  s->nb[2] != s->nb[1] * (size_t) s->ne[1] || s->ne[3] != 1))
+                  s->nb[2] != s->nb[1] * (size_t) s->ne[1] || s->nb[3] != s->nb[2] * (size_t) s->ne[2]))
             return "V^T layout";
-    if (!is_bf16(t) || t->ne[0] != dh * H || t->ne[1] != Tq || !contig(t)) return "output";
+    if (!is_bf16(t) || t->ne[0] != dh * H || t->ne[1] != Tq || t->ne[2] != B || t->ne[3] != 1 || !contig(t))
+        return "output";
     return nullptr;
 }
 
@@ -716,7 +723,7 @@ wamx_tensor * wamx_qk_norm_rope(wamx_context * ctx, wamx_tensor * x, wamx_tensor
 wamx_tensor * wamx_joint_attn(wamx_context * ctx, wamx_tensor * q, wamx_tensor * k_a, wamx_tensor * v_a,
                               wamx_tensor * k_b, wamx_tensor * v_b, int64_t na_split, float scale) {
     if (!q || !k_a || !v_a) return fail("wamx_joint_attn");
-    wamx_tensor * t = wamx_new_tensor_2d(ctx, WAMX_TYPE_BF16, q->ne[0] * q->ne[2], q->ne[1]);
+    wamx_tensor * t = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, q->ne[0] * q->ne[2], q->ne[1], q->ne[3]);
     if (!t) return nullptr;
     t->op = WAMX_OP_JOINT_ATTN;
     t->op_params[0] = (int32_t) na_split;

@@ -33,9 +33,12 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(const uint16_t
                                                                    const int32_t * __restrict__ pos0,
                                                                    const int32_t * __restrict__ pos1,
                                                                    const int32_t * __restrict__ pos2, float eps,
-                                                                   float ts128, float ts44, float ts42) {
+                                                                   float ts128, float ts44, float ts42,
+                                                                   int64_t chunk_tokens, int64_t chunk_stride) {
     __shared__ float red[kQkThreads / 64];
     const int64_t t = blockIdx.x;
+    // Row t is token tl of chunk cb: positions by tl, output in chunk cb's slice.
+    const int64_t cb = t / chunk_tokens, tl = t - cb * chunk_tokens;
     const int d = heads * head_dim;
     const int npairs = d / 2;
     const uint32_t * xr = (const uint32_t *) (x + t * ldx);
@@ -66,13 +69,13 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(const uint16_t
         if (rope_mode != 2) {
             float theta;
             if (rope_mode == 0) {
-                theta = (float) pos0[t] * powf(ts128, (float) (dd >> 1));
+                theta = (float) pos0[tl] * powf(ts128, (float) (dd >> 1));
             } else if (dd < 44) {
-                theta = (float) pos0[t] * powf(ts44, (float) (dd >> 1));
+                theta = (float) pos0[tl] * powf(ts44, (float) (dd >> 1));
             } else if (dd < 86) {
-                theta = (float) pos1[t] * powf(ts42, (float) ((dd - 44) >> 1));
+                theta = (float) pos1[tl] * powf(ts42, (float) ((dd - 44) >> 1));
             } else {
-                theta = (float) pos2[t] * powf(ts42, (float) ((dd - 86) >> 1));
+                theta = (float) pos2[tl] * powf(ts42, (float) ((dd - 86) >> 1));
             }
             float sn, cs;
             sincosf(theta, &sn, &cs);
@@ -81,7 +84,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(const uint16_t
             a = ra;
             b = rb;
         }
-        uint32_t * out = (uint32_t *) (dst + ((int64_t) h * dst_tokens + tok0 + t) * head_dim + dd);
+        uint32_t * out = (uint32_t *) (dst + cb * chunk_stride + ((int64_t) h * dst_tokens + tok0 + tl) * head_dim + dd);
         *out = pack_bf16x2(a, b);
     }
 }
@@ -97,9 +100,11 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
                                                           int rope_mode, const int32_t * __restrict__ pos0,
                                                           const int32_t * __restrict__ pos1,
                                                           const int32_t * __restrict__ pos2, float eps, float l2ts128,
-                                                          float l2ts44, float l2ts42) {
+                                                          float l2ts44, float l2ts42, int64_t chunk_tokens,
+                                                          int64_t chunk_stride) {
     __shared__ float red[16];
     const int64_t t = blockIdx.x;
+    const int64_t b = t / chunk_tokens, tl = t - b * chunk_tokens;
     const int d = heads * head_dim;
     const int nchunk = d >> 3;
     uint4 xv[CPT], wv[CPT];
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
         xv[i] = *(const uint4 *) (x + t * ldx + 8 * c);
         wv[i] = *(const uint4 *) (w + 8 * c);
     }
-    const RopeTok rt = rope_tok(rope_mode, pos0, pos1, pos2, t, l2ts128, l2ts44, l2ts42);
+    const RopeTok rt = rope_tok(rope_mode, pos0, pos1, pos2, tl, l2ts128, l2ts44, l2ts42);
     float v[CPT][8];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -124,14 +129,18 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
         const int c = (int) threadIdx.x + i * (int) blockDim.x;
         if (c >= nchunk) continue;
         const int e0 = 8 * c, h = e0 / head_dim, dd0 = e0 % head_dim;
-        *(uint4 *) (dst + ((int64_t) h * dst_tokens + tok0 + t) * head_dim + dd0) = qk_chunk(v[i], inv_rms, wv[i], dd0, rt);
+        *(uint4 *) (dst + b * chunk_stride + ((int64_t) h * dst_tokens + tok0 + tl) * head_dim + dd0) =
+            qk_chunk(v[i], inv_rms, wv[i], dd0, rt);
     }
 }
 
 hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void * dst, int64_t heads, int64_t head_dim,
                                int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode, const int32_t * pos0,
-                               const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s) {
+                               const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s,
+                               int64_t chunk_tokens, int64_t chunk_stride) {
     if (tokens <= 0) return hipSuccess;
+    if (chunk_tokens <= 0) chunk_tokens = tokens;
+    if (tokens % chunk_tokens != 0) return hipErrorInvalidValue;
     const int64_t d = heads * head_dim;
     if (d % 8 == 0 && head_dim % 8 == 0 && d / 8 <= 4096 && ldx % 8 == 0 && ((uintptr_t) x & 15) == 0 &&
         ((uintptr_t) w & 15) == 0 && ((uintptr_t) dst & 15) == 0) {
@@ -144,7 +153,8 @@ hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void
 #define WAMX_QK_VEC(CPT)                                                                                            \
     hipLaunchKernelGGL(qk_norm_rope_vec<CPT>, dim3((unsigned) tokens), dim3((unsigned) threads), 0, s,            \
                        (const uint16_t *) x, ldx, (const uint16_t *) w, (uint16_t *) dst, (int) heads, (int) head_dim, \
-                       dst_tokens, tok0, rope_mode, pos0, pos1, pos2, eps, l2ts128, l2ts44, l2ts42)
+                       dst_tokens, tok0, rope_mode, pos0, pos1, pos2, eps, l2ts128, l2ts44, l2ts42, chunk_tokens,    \
+                       chunk_stride)
         if (cpt == 1) WAMX_QK_VEC(1);
         else if (cpt == 2) WAMX_QK_VEC(2);
         else WAMX_QK_VEC(4);
@@ -159,7 +169,7 @@ hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void
     const float ts42 = powf(freq_base, -2.0f / 42.0f);
     hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned) tokens), dim3(kQkThreads), 0, s, (const uint16_t *) x, ldx,
                        (const uint16_t *) w, (uint16_t *) dst, (int) heads, (int) head_dim, dst_tokens, tok0, rope_mode,
-                       pos0, pos1, pos2, eps, ts128, ts44, ts42);
+                       pos0, pos1, pos2, eps, ts128, ts44, ts42, chunk_tokens, chunk_stride);
     return hipGetLastError();
 }
 
@@ -192,8 +202,9 @@ struct AttnParams {
     int64_t seg_len[2];
     int64_t seg_blocks[2];
     int64_t nblocks;
-    uint16_t * out;
-    int64_t heads, tq;
+    uint16_t * out;          // bf16 [batch][tq][hb * kDh]
+    int64_t heads, tq;       // heads: batch x hb (chunk b's head h is head b * hb + h)
+    int64_t hb;              // heads per chunk
     float scale_log2;
     // Key-split mode: workgroup z of gridDim.z covers key blocks
     // [z * split_blocks, (z + 1) * split_blocks) and writes fp32 partials.
@@ -202,6 +213,12 @@ struct AttnParams {
     float * part_m;          // [split][head][query] running max (log2 domain)
     float * part_l;          // [split][head][query] running sum
 };
+
+// Output row of query q of head h: chunk b = h / hb writes rows [b * tq, (b + 1) * tq).
+__device__ __forceinline__ uint16_t * out_row(const AttnParams & p, int64_t h, int64_t q) {
+    const int64_t b = h / p.hb;
+    return p.out + ((b * p.tq + q) * p.hb + (h - b * p.hb)) * kDh;
+}
 
 // Zero the bf16 values of keys >= valid in 4 packed keys starting at first_key.
 __device__ __forceinline__ uint2 mask4(uint2 v, int first_key, int valid) {
@@ -414,7 +431,7 @@ __global__ __launch_bounds__(NW * 64) void joint_attn_kernel(AttnParams p) {
             p.part_o[(((int64_t) blockIdx.z * p.heads + h) * p.tq + q0 + q) * kDh + d] = s_o[q][d];
         } else {
             const float l = s_lstar[q];
-            p.out[(q0 + q) * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? s_o[q][d] / l : 0.0f);
+            out_row(p, h, q0 + q)[d] = f32_to_bf16(l > 0.0f ? s_o[q][d] / l : 0.0f);
         }
     }
 }
@@ -454,7 +471,7 @@ __global__ __launch_bounds__(kDh) void joint_attn_merge(AttnParams p, int nsplit
             o += oz[u] * w;
         }
     }
-    p.out[q * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
+    out_row(p, h, q)[d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
 }
 
 
@@ -700,7 +717,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
     const int64_t nq = min((int64_t) kPfQueries, p.tq - q0);
     for (int c = tid; c < nq * (kDh / 8); c += kPfWaves * 64) {
         const int q = c / (kDh / 8), dc = c % (kDh / 8);
-        *(uint4 *) (p.out + (q0 + q) * (p.heads * kDh) + h * kDh + 8 * dc) = *(const uint4 *) (ot + q * kDh + 8 * dc);
+        *(uint4 *) (out_row(p, h, q0 + q) + 8 * dc) = *(const uint4 *) (ot + q * kDh + 8 * dc);
     }
 }
 
@@ -943,7 +960,7 @@ __global__ __launch_bounds__(kPfWaves * 64, S == 2 ? 2 : 1) void attn_decode_ker
                 }
             } else {
                 const float l = s_lstar[q], inv = l > 0.0f ? 1.0f / l : 0.0f;
-                *(uint2 *) (p.out + (q0 + q) * (p.heads * kDh) + h * kDh + d) =
+                *(uint2 *) (out_row(p, h, q0 + q) + d) =
                     make_uint2(pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv));
             }
         }
@@ -979,7 +996,7 @@ __global__ __launch_bounds__(kDh) void attn_merge_kernel(AttnParams p, int nspli
         l += lz[u] * w;
         o += oz[u] * w;
     }
-    p.out[q * (p.heads * kDh) + h * kDh + d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
+    out_row(p, h, q)[d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
 }
 constexpr int kDecMaxSplits = 32;
 // About one workgroup per CU in all: more ranges shorten each workgroup's
@@ -1022,6 +1039,8 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     p.nblocks = p.seg_blocks[0] + p.seg_blocks[1];
     p.out = (uint16_t *) a.out;
     p.heads = a.heads;
+    p.hb = a.hb > 0 ? a.hb : a.heads;
+    if (p.heads % p.hb != 0) return hipErrorInvalidValue;
     p.tq = a.tq;
     p.scale_log2 = a.scale * kLog2e;
     // 8-byte V^T loads of 4 keys need rows padded to a multiple of 4 keys.

@@ -57,7 +57,7 @@ class GwpConfig(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "n_layers", "hidden", "n_heads", "head_dim", "ffn_dim", "action_hidden", "action_ffn_dim",
         "action_chunk", "action_dim", "grid_h", "grid_w", "n_lang", "t5_hidden", "z_dim",
-        "num_steps", "enc_hidden")] + [("shift", C.c_float), ("eps", C.c_float)]
+        "num_steps", "enc_hidden")] + [("shift", C.c_float), ("eps", C.c_float), ("batch", C.c_int32)]
 
 
 class GwpTiming(C.Structure):
