@@ -416,6 +416,19 @@ WAMX_API wamx_status wamx_op_linear(wamx_backend_t be, const void * w, const voi
 WAMX_API wamx_status wamx_op_linear_tiled(wamx_backend_t be, const void * w, const void * x, int32_t x_type,
                                           const void * bias, int32_t epilogue, const void * residual,
                                           const float * gate, void * y, int64_t M, int64_t N, int64_t K);
+/* wamx_op_linear that allocates nothing: no counterpart in the reference; it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, hosts that forbid hipMalloc).  stream is a
+ * hipStream_t (NULL: the null stream); the caller owns w, x, bias, residual,
+ * gate and y.  The split-K partials of products on <= 64 tokens live in a
+ * library-owned device array of 32 MiB per GPU, held until the process ends;
+ * a product whose partials would not fit is refused (status FAILED, reason in
+ * wamx_last_error) before anything runs.  Every call on one GPU shares that
+ * array: calls that overlap on one GPU race and must be serialised by the
+ * caller.  Same kernels, same bits as wamx_op_linear. */
+WAMX_API wamx_status wamx_op_linear_noalloc(void * stream, const void * w, const void * x, int32_t x_type,
+                                            const void * bias, int32_t epilogue, const void * residual,
+                                            const float * gate, void * y, int64_t M, int64_t N, int64_t K);
 /* norm_bf16_fused<bs,false> (native-bf16.patch:368-409): y = bf16(n*(1+scale)+shift).
  * scale/shift f32, row stride ss (0 = broadcast). */
 WAMX_API wamx_status wamx_op_norm_modulation_bf16(wamx_backend_t be, const void * x, int64_t ldx,

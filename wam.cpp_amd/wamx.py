@@ -91,6 +91,7 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_backend_free": (None, [vp]),
         "wamx_backend_name": (C.c_char_p, [vp]),
         "wamx_backend_synchronize": (None, [vp]),
+        "wamx_backend_stream": (vp, [vp]),
         "wamx_device_malloc": (vp, [vp, sz]),
         "wamx_device_free": (None, [vp, vp]),
         "wamx_memcpy_h2d": (C.c_int, [vp, vp, vp, sz]),
@@ -98,6 +99,7 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_op_mul_mat": (C.c_int, [vp, vp, i64, vp, i32, i64, vp, i32, i64, i64, i64, i64]),
         "wamx_op_linear": (C.c_int, [vp, vp, vp, i32, vp, i32, vp, vp, vp, i64, i64, i64]),
         "wamx_op_linear_tiled": (C.c_int, [vp, vp, vp, i32, vp, i32, vp, vp, vp, i64, i64, i64]),
+        "wamx_op_linear_noalloc": (C.c_int, [vp, vp, vp, i32, vp, i32, vp, vp, vp, i64, i64, i64]),
         "wamx_op_norm_modulation_bf16": (C.c_int, [vp, vp, i64, vp, vp, i64, vp, i64, i64, f32]),
         "wamx_op_layer_norm_bf16": (C.c_int, [vp, vp, i64, vp, vp, vp, i64, i64, f32]),
         "wamx_op_rms_norm_bf16_f32": (C.c_int, [vp, vp, i64, vp, vp, i64, i64, f32]),
