@@ -199,3 +199,69 @@ def test_v_transpose_store_is_exact(wx, be, rng, T, k0):
         assert np.array_equal(got, want)
     finally:
         g.close()
+
+
+def _f32_chains(wx, lib, g, rows, cols):
+    """The F32 profile's modulated norm (mot.cpp:154-158: norm + norm * scale
+    + shift, scale and shift views of the modulation rows) and gated residual
+    (mot.cpp:161-164: residual + branch * gate view), unfused ggml ops."""
+    x = g.t(wx.TYPE_F32, cols, rows)
+    comb = g.t(wx.TYPE_F32, cols, 6, 1)
+    res = g.t(wx.TYPE_F32, cols, rows)
+    br = g.t(wx.TYPE_F32, cols, rows)
+    part = [lib.wamx_view_2d(g.ctx, comb, cols, 1, comb.contents.nb[2], i * comb.contents.nb[1]) for i in range(6)]
+    n = lib.wamx_norm(g.ctx, x, 1e-6)
+    y = lib.wamx_add(g.ctx, lib.wamx_add(g.ctx, n, lib.wamx_mul(g.ctx, n, part[1])), part[0])
+    out = lib.wamx_add(g.ctx, res, lib.wamx_mul(g.ctx, br, part[2]))
+    return x, comb, res, br, y, out
+
+
+def test_f32_profile_fusions(wx, be, orc, rng):
+    """The F32 chains run as norm_modulation_f32 and gated_residual_f32
+    (p7-fusions.patch:173-245): the graph's results equal the standalone
+    fused kernels bit for bit and the oracle's restatement of them; with the
+    fusions switched off the unfused ops agree with the oracle too."""
+    import os
+    rows, cols = 2048, 3072
+    print("f32 profile fusions", flush=True)
+    xv = (rng.standard_normal((rows, cols)) * 2 + 0.5).astype(np.float32)
+    cv = (rng.standard_normal((1, 6, cols)) * 0.1).astype(np.float32)
+    rv = rng.standard_normal((rows, cols)).astype(np.float32)
+    bv = rng.standard_normal((rows, cols)).astype(np.float32)
+    ref_y = orc.norm_mod_f32(xv, cv[0, 1], cv[0, 0], 1e-6)
+    ref_out = orc.gated_residual_f32(rv, bv, cv[0, 2])
+    results = {}
+    backends = {"fused": be}
+    os.environ["WAMX_DISABLE_NORM_MODULATION_FUSION"] = "1"
+    os.environ["WAMX_DISABLE_GATED_RESIDUAL_FUSION"] = "1"
+    try:
+        backends["unfused"] = wx.Backend(0)
+    finally:
+        del os.environ["WAMX_DISABLE_NORM_MODULATION_FUSION"]
+        del os.environ["WAMX_DISABLE_GATED_RESIDUAL_FUSION"]
+    for key, b in backends.items():
+        g = Graph(wx, b)
+        try:
+            x, comb, res, br, y, out = _f32_chains(wx, b.lib, g, rows, cols)
+            g.alloc()
+            for t, a in ((x, xv), (comb, cv), (res, rv), (br, bv)):
+                g.set(t, a)
+            g.compute(y, out)
+            results[key] = (g.get(y, np.float32, (rows, cols)), g.get(out, np.float32, (rows, cols)))
+        finally:
+            g.close()
+    backends["unfused"].close()
+    # the standalone fused kernels on the same inputs
+    lib = be.lib
+    dx, ds, dsh, dy = be.array(xv), be.array(cv[0, 1].copy()), be.array(cv[0, 0].copy()), be.empty(xv.nbytes)
+    wx.check(lib.wamx_op_norm_modulation_f32(be.ptr, dx.ptr, cols, ds.ptr, dsh.ptr, 0, dy.ptr, rows, cols, 1e-6))
+    dr, db, dg, do = be.array(rv), be.array(bv), be.array(cv[0, 2].copy()), be.empty(rv.nbytes)
+    wx.check(lib.wamx_op_gated_residual_f32(be.ptr, dr.ptr, db.ptr, dg.ptr, 0, do.ptr, rows, cols))
+    k_y, k_out = dy.download(np.float32, (rows, cols)), do.download(np.float32, (rows, cols))
+    f_y, f_out = results["fused"]
+    u_y, u_out = results["unfused"]
+    assert np.array_equal(f_y, k_y) and np.array_equal(f_out, k_out)
+    assert np.array_equal(f_out, ref_out)            # exact: r + b*g rounded per op
+    for got in (f_y, u_y):
+        assert np.max(np.abs(got - ref_y)) <= 1e-4 * np.max(np.abs(ref_y))
+    assert np.max(np.abs(u_out - ref_out)) <= 1e-6 * np.max(np.abs(ref_out))

@@ -318,3 +318,46 @@ def test_joint_attention_dit_block(wx, be, orc):
     got = dout.download(np.uint16, (n, H * dh))
     ref = orc.attention(q, k, vt, scale=scale)
     assert_parity(f32(got), f32(ref), what="dit-block attention")
+
+
+def test_visual_cross_attention_against_f32_qk(wx, be, orc):
+    """The prefix's visual cross-attention (build_attention,
+    text_encoder.cpp:26-73) keeps RMSNorm'd Q and K in f32 and takes f32 Q.K
+    products; this backend rounds Q and K to bf16 after RMSNorm and runs the
+    bf16 MFMA flash kernel.  Bound at 3072 queries x 512 keys x 24 heads
+    against the f32-Q.K path (probabilities rounded to bf16 for P.V as the
+    reference does): max-rel <= 1e-2, cosine >= 0.9999."""
+    print("visual cross-attention vs f32 Q.K", flush=True)
+    rng = np.random.default_rng(0x5EED0302)
+    H, dh, NQ, NK = 24, 128, 3072, 512
+    d = H * dh
+    q = bf16(rng.standard_normal((NQ, d)))
+    k = bf16(rng.standard_normal((NK, d)))
+    v = bf16(rng.standard_normal((NK, d)))
+    wq = bf16(1 + rng.standard_normal(d) * 0.02)
+    wk = bf16(1 + rng.standard_normal(d) * 0.02)
+    dq, dk, dwq, dwk = dev(be, q), dev(be, k), dev(be, wq), dev(be, wk)
+    dQ, dK = be.empty(H * NQ * dh * 2), be.empty(H * NK * dh * 2)
+    for src, w, dst, n in ((dq, dwq, dQ, NQ), (dk, dwk, dK, NK)):
+        wx.check(be.lib.wamx_op_qk_norm_rope(be.ptr, src.ptr, d, w.ptr, dst.ptr, H, dh, n, n, 0, 2, None, None, None,
+                                             1e-6, 10000.0))
+    vt = np.ascontiguousarray(v.reshape(NK, H, dh).transpose(1, 2, 0))
+    dvt = dev(be, vt)
+    dout = be.empty(NQ * d * 2)
+    scale = 1.0 / np.sqrt(dh)
+    wx.check(be.lib.wamx_op_joint_attn(be.ptr, dQ.ptr, dK.ptr, dvt.ptr, NK, None, None, 0, 0, dout.ptr, H, dh, NQ,
+                                       scale))
+    got = f32(dout.download(np.uint16, (NQ, d)))
+    qf = orc.rms_norm_bf16_f32(q, wq, 1e-6).astype(np.float64)
+    kf = orc.rms_norm_bf16_f32(k, wk, 1e-6).astype(np.float64)
+    vf = f32(v).astype(np.float64)
+    ref = np.empty((NQ, d), np.float32)
+    for h in range(H):
+        sl = slice(h * dh, (h + 1) * dh)
+        s = (qf[:, sl] @ kf[:, sl].T).astype(np.float32).astype(np.float64) * scale
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        p = f32(bf16((p / p.sum(axis=1, keepdims=True)).astype(np.float32))).astype(np.float64)
+        ref[:, sl] = (p @ vf[:, sl]).astype(np.float32)
+    ref = f32(bf16(ref))
+    assert_parity(got, ref, what="visual cross-attention (bf16 Q.K) vs f32 Q.K")
+    print(f"max-rel {rel_err(got, ref):.3e} cosine {cosine(got, ref):.7f}")

@@ -64,6 +64,8 @@ struct wamx_backend {
     std::vector<hipEvent_t> events;  // cross-lane ordering, reused from graph to graph
     bool use_graphs = true;
     bool fuse_rows = true;       // split-K reduce + consuming row op in one launch
+    bool fuse_norm_mod_f32 = true;       // F32 NORM -> MUL -> ADD -> ADD as one launch
+    bool fuse_gated_residual_f32 = true; // F32 MUL -> ADD as one launch
     std::unordered_map<uint64_t, GraphCacheEntry> graphs;
 };
 
@@ -427,6 +429,113 @@ static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post, bool la
         j = next_compute(g, j, n, lanes);
     }
     return post.nseg > 0 ? last : -1;
+}
+
+// ---------------------------------------------------------------------------
+// The reference's F32-profile fusions (p7-fusions.patch:173-245), matched in
+// the graph the way ggml-cuda's evaluator matches them:
+//   NORM -> VIEW(scale) -> MUL -> ADD -> VIEW(shift) -> ADD, the modulated
+//     norm of mot.cpp:154-158 (norm + norm * scale + shift), with every
+//     intermediate used once, becomes norm_modulation_f32;
+//   MUL(branch, gate view) -> ADD(residual), the gated residual of
+//     mot.cpp:161-164, becomes gated_residual_f32.
+// Both kernels round each operation separately (no FMA), as the reference's.
+// ---------------------------------------------------------------------------
+struct F32Fusion {
+    int kind = 0;  // 1 norm-modulation, 2 gated residual
+    const wamx_tensor *x = nullptr, *scale = nullptr, *shift = nullptr, *branch = nullptr, *gate = nullptr;
+    wamx_tensor * out = nullptr;
+    float eps = 0.0f;
+};
+
+static int uses_of(wamx_cgraph * g, int n, const wamx_tensor * t) {
+    int u = 0;
+    for (int j = 0; j < n; ++j) {
+        const wamx_tensor * m = wamx_graph_node(g, j);
+        for (int k = 0; k < WAMX_MAX_SRC; ++k) u += m->src[k] == t;
+    }
+    return u;
+}
+
+static bool row_broadcast_or_same(const wamx_tensor * a, const wamx_tensor * v) {
+    return wamx_are_same_shape(a, v) || (a->ne[0] == v->ne[0] && v->ne[1] == 1 && v->ne[2] == 1 && v->ne[3] == 1);
+}
+
+// Returns the last node the fusion starting at node i covers (> i), or -1.
+static int match_f32_fusion(const wamx_backend * be, wamx_cgraph * g, int i, int n, F32Fusion & f) {
+    wamx_tensor * node = wamx_graph_node(g, i);
+    auto same_lane = [&](int a, int b) {
+        for (int j = a; j <= b; ++j)
+            if (wamx_graph_node(g, j)->lane != node->lane) return false;
+        return true;
+    };
+    auto f32 = [](const wamx_tensor * t) { return t && t->type == WAMX_TYPE_F32; };
+    if (be->fuse_norm_mod_f32 && node->op == WAMX_OP_NORM && !node->src[1] && i + 5 < n) {
+        wamx_tensor *sc = wamx_graph_node(g, i + 1), *mul = wamx_graph_node(g, i + 2), *as = wamx_graph_node(g, i + 3);
+        wamx_tensor *sh = wamx_graph_node(g, i + 4), *ash = wamx_graph_node(g, i + 5);
+        auto has = [](const wamx_tensor * t, const wamx_tensor * a, const wamx_tensor * b) {
+            return (t->src[0] == a && t->src[1] == b) || (t->src[0] == b && t->src[1] == a);
+        };
+        const bool ok = sc->op == WAMX_OP_VIEW && mul->op == WAMX_OP_MUL && as->op == WAMX_OP_ADD && !as->src[2] &&
+                        sh->op == WAMX_OP_VIEW && ash->op == WAMX_OP_ADD && !ash->src[2] && has(mul, node, sc) &&
+                        has(as, node, mul) && has(ash, as, sh) && uses_of(g, n, node) == 2 && uses_of(g, n, sc) == 1 &&
+                        uses_of(g, n, mul) == 1 && uses_of(g, n, as) == 1 && uses_of(g, n, sh) == 1 &&
+                        !(as->flags & WAMX_TENSOR_FLAG_OUTPUT) && !(mul->flags & WAMX_TENSOR_FLAG_OUTPUT) &&
+                        !(node->flags & WAMX_TENSOR_FLAG_OUTPUT) && f32(node) && f32(node->src[0]) && f32(sc) &&
+                        f32(sh) && f32(ash) && row_broadcast_or_same(node, sc) && row_broadcast_or_same(node, sh) &&
+                        wamx_are_same_shape(node, ash) && node->ne[2] == 1 && node->ne[3] == 1 &&
+                        node->src[0]->nb[0] == 4 && sc->nb[0] == 4 && sh->nb[0] == 4 && wamx_is_contiguous(ash) &&
+                        (sc->ne[1] == 1 ? sh->ne[1] == 1 : sc->nb[1] == sh->nb[1]) && same_lane(i, i + 5);
+        if (ok) {
+            f.kind = 1;
+            f.x = node->src[0];
+            f.scale = sc;
+            f.shift = sh;
+            f.out = ash;
+            memcpy(&f.eps, &node->op_params[0], 4);
+            return i + 5;
+        }
+    }
+    if (be->fuse_gated_residual_f32 && node->op == WAMX_OP_MUL && i + 1 < n) {
+        wamx_tensor * add = wamx_graph_node(g, i + 1);
+        const wamx_tensor *a = node->src[0], *b = node->src[1];
+        if (add->op != WAMX_OP_ADD || add->src[2] || !(add->src[0] == node || add->src[1] == node) ||
+            uses_of(g, n, node) != 1 || (node->flags & WAMX_TENSOR_FLAG_OUTPUT) || !a || !b)
+            return -1;
+        const wamx_tensor * residual = add->src[0] == node ? add->src[1] : add->src[0];
+        auto gate_like = [](const wamx_tensor * x, const wamx_tensor * other) {
+            return x->op == WAMX_OP_VIEW && (!wamx_is_contiguous(x) || (x->ne[1] == 1 && other->ne[1] > 1));
+        };
+        const bool a_gate = gate_like(a, b), b_gate = gate_like(b, a);
+        const wamx_tensor * gate = a_gate ? a : b;
+        const wamx_tensor * branch = a_gate ? b : a;
+        const bool ok = a_gate != b_gate && f32(node) && f32(branch) && f32(gate) && f32(residual) && f32(add) &&
+                        branch->ne[2] == 1 && branch->ne[3] == 1 && wamx_are_same_shape(node, branch) &&
+                        row_broadcast_or_same(branch, gate) && wamx_are_same_shape(node, residual) &&
+                        wamx_are_same_shape(node, add) && branch->nb[0] == 4 && gate->nb[0] == 4 &&
+                        residual->nb[0] == 4 && wamx_is_contiguous(add) && same_lane(i, i + 1);
+        if (ok) {
+            f.kind = 2;
+            f.x = residual;
+            f.branch = branch;
+            f.gate = gate;
+            f.out = add;
+            return i + 1;
+        }
+    }
+    return -1;
+}
+
+static hipError_t run_f32_fusion(wamx_backend * be, const F32Fusion & f) {
+    const int64_t rows = wamx_nrows(f.out), cols = f.out->ne[0];
+    if (f.kind == 1)
+        return launch_norm_mod_f32((const float *) f.x->data, (int64_t) f.x->nb[1] / 4, (const float *) f.scale->data,
+                                   (const float *) f.shift->data, f.scale->ne[1] == 1 ? 0 : (int64_t) f.scale->nb[1] / 4,
+                                   (float *) f.out->data, rows, cols, f.eps, be->cs);
+    return launch_gated_residual_f32((const float *) f.x->data, (int64_t) f.x->nb[1] / 4,
+                                     (const float *) f.branch->data, (int64_t) f.branch->nb[1] / 4,
+                                     (const float *) f.gate->data, f.gate->ne[1] == 1 ? 0 : (int64_t) f.gate->nb[1] / 4,
+                                     (float *) f.out->data, rows, cols, be->cs);
 }
 
 static hipError_t run_joint_attn(wamx_backend * be, const wamx_tensor * node) {
@@ -867,6 +976,28 @@ static wamx_status run_nodes(wamx_backend * be, wamx_cgraph * g) {
                 }
             }
         }
+        if (!fused && (node->op == WAMX_OP_NORM || node->op == WAMX_OP_MUL)) {
+            F32Fusion f;
+            const int last = match_f32_fusion(be, g, i, n, f);
+            int dep = -1;
+            for (int j = i; j <= last; ++j) dep = std::max(dep, two ? wait_for[j] : -1);
+            if (last > i && dep < i) {
+                if (dep >= 0) hipStreamWaitEvent(be->cs, be->events[slot[dep]], 0);
+                const hipError_t err = run_f32_fusion(be, f);
+                if (err != hipSuccess) {
+                    set_errorf("graph_compute: node %d (%s '%s') fused with its F32 chain failed: %s", i,
+                               wamx_op_name(node->op), node->name, hipGetErrorString(err));
+                    status = WAMX_STATUS_FAILED;
+                    break;
+                }
+                nm = 0;
+                for (int j = i; j <= last && nm < 8; ++j) {
+                    done[j] = 1;
+                    members[nm++] = j;
+                }
+                fused = true;
+            }
+        }
         if (!fused) {
             if (two && wait_for[i] >= 0) hipStreamWaitEvent(be->cs, be->events[slot[wait_for[i]]], 0);
             const hipError_t err = compute_node(be, node);
@@ -1103,6 +1234,20 @@ static bool gallocr_alloc(wamx_gallocr * ga, wamx_cgraph * g) {
     // LINEAR's and the members' sources while it writes the members' outputs.
     // Those sources therefore stay live through the last member, so no member
     // output can take their memory.
+    // The F32 fusions read their chain's first inputs while writing its last
+    // output: those inputs stay live through the last member too.
+    for (int i = 0; i < n; ++i) {
+        F32Fusion f;
+        const int last = match_f32_fusion(ga->be, g, i, n, f);
+        if (last <= i) continue;
+        for (int j = i; j <= last; ++j) {
+            wamx_tensor * m = wamx_graph_node(g, j);
+            for (int k = 0; k < WAMX_MAX_SRC; ++k) {
+                wamx_tensor * r = m->src[k] ? root_of(m->src[k]) : nullptr;
+                if (r && last_use.count(r)) last_use[r] = std::max(last_use[r], last);
+            }
+        }
+    }
     if (ga->be->fuse_rows) {
         bool two = false;
         for (int i = 0; i < n && !two; ++i) two = wamx_graph_node(g, i)->lane != 0;
@@ -1204,6 +1349,11 @@ wamx_backend_t wamx_backend_init(int device) {
     be->use_graphs = !(env && env[0] && env[0] != '0');
     env = getenv("WAMX_DISABLE_ROW_FUSION");
     be->fuse_rows = !(env && env[0] && env[0] != '0');
+    // The reference's switches for its F32 fusions (p7-fusions.patch:173-174, :216-217).
+    env = getenv("WAMX_DISABLE_NORM_MODULATION_FUSION");
+    be->fuse_norm_mod_f32 = !(env && env[0] && env[0] != '0');
+    env = getenv("WAMX_DISABLE_GATED_RESIDUAL_FUSION");
+    be->fuse_gated_residual_f32 = !(env && env[0] && env[0] != '0');
     // A blocking stream, so synchronous tensor_set/get on the null stream are
     // ordered with the graph work (default priority).
     if (hipStreamCreate(&be->stream) != hipSuccess || hipMalloc(&be->workspace, kWorkspaceBytes) != hipSuccess) {
