@@ -963,12 +963,13 @@ __device__ __forceinline__ void skinny_stage_x(const GemmParams & p, uint16_t * 
                                                int klen, Prologue && prologue) {
     const int tid = threadIdx.x, pitch = ks + 8;
     const int cpr = ks / 8, total = rows * cpr;
-    constexpr int kStageBatch = 8, kThreads = kSkinnyWaves * 64;
-    for (int c0 = 0; c0 < total; c0 += kStageBatch * kThreads) {
+    constexpr int kStageBatch = 8;
+    const int nthr = (int) blockDim.x;
+    for (int c0 = 0; c0 < total; c0 += kStageBatch * nthr) {
         uint4 v[kStageBatch];
 #pragma unroll
         for (int u = 0; u < kStageBatch; ++u) {
-            const int c = min(c0 + u * kThreads + tid, total - 1);
+            const int c = min(c0 + u * nthr + tid, total - 1);
             const int r = c / cpr, kc = c % cpr;
             const bool ok = r < p.N && kc * 8 < klen;
             const int64_t idx = (int64_t) min(r, (int) p.N - 1) * p.ldx + kb + min(kc * 8, klen - 8);
@@ -978,7 +979,7 @@ __device__ __forceinline__ void skinny_stage_x(const GemmParams & p, uint16_t * 
         if (c0 == 0) prologue();
 #pragma unroll
         for (int u = 0; u < kStageBatch; ++u) {
-            const int c = c0 + u * kThreads + tid;
+            const int c = c0 + u * nthr + tid;
             if (c < total) *(uint4 *) (xs + (c / cpr) * pitch + (c % cpr) * 8) = v[u];
         }
     }
@@ -1130,22 +1131,23 @@ hipError_t launch_tile_weights(const void * src, void * dst, int64_t M, int64_t 
     return hipGetLastError();
 }
 
-// gemm_skinny_part on tiled weights: each of the 8 waves owns one 16-row
-// group (a workgroup covers 128 features), streams its tiles DEPTH steps ahead
-// and feeds them to the MFMAs as loaded, with no LDS on the weight path.  The
-// accumulation order over K is that of gemm_skinny_part, so both give the same
-// bits.  K % 32 == 0 and M % 16 == 0 (the tiled layout's conditions).
-constexpr int kTiledFeat = 16 * kSkinnyWaves;
+// gemm_skinny_part on tiled weights: each wave of the workgroup owns one
+// 16-row group (a workgroup of G waves covers 16 G features, G chosen with the
+// K slice so the grid fills the CUs evenly), streams its tiles DEPTH steps
+// ahead and feeds them to the MFMAs as loaded, with no LDS on the weight path.
+// Within a K slice the accumulation order is that of gemm_skinny_part.
+// K % 32 == 0 and M % 16 == 0 (the tiled layout's conditions).
+constexpr int kTiledMaxWaves = 16;
 
 template <bool XF32, int NT, int DEPTH = kSkinnyDepth>
-__global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_tiled(GemmParams p, float * part, int ks) {
+__global__ __launch_bounds__(kTiledMaxWaves * 64) void gemm_skinny_tiled(GemmParams p, float * part, int ks) {
     extern __shared__ __align__(16) uint16_t xs[];  // [16*NT][ks + 8]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r16 = lane & 15;
     const int64_t M = p.M, K = p.K;
     const int pitch = ks + 8;
     const int64_t ngrp = M / 16, kt = K / 32;
-    const int64_t grp = (int64_t) blockIdx.x * kSkinnyWaves + wave;
+    const int64_t grp = (int64_t) blockIdx.x * (blockDim.x >> 6) + wave;
     const int64_t kb = (int64_t) blockIdx.y * ks;
     const int klen = (int) (min(K, kb + ks) - kb);
     const int nsteps = (klen + 127) / 128, ntiles = klen / 32;
@@ -1404,25 +1406,55 @@ size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K) {
 
 // gemm_skinny_part over `splits` K slices of ks columns; part == nullptr
 // (single slice only) applies the epilogue in the part kernel.
-// K slices of the tiled kernel (128 features per workgroup): the shortest of
-// 384..1536 that keeps the grid within about two workgroups per CU (measured
-// on the 48-token shapes: 384 for 3072 x 3072, 512 for QKV, 768 for the FFN).
-static void skinny_tiled_plan(int64_t M, int64_t N, int64_t K, int & splits, int & ks) {
-    const int64_t nfb = (M / 16 + kSkinnyWaves - 1) / kSkinnyWaves;
+// Workgroup shape of the tiled kernel: G waves (16 G features) by a K slice
+// of ks columns.  Measured on the action expert's projections (48 and 1
+// tokens, part + reduce, weights streamed from HBM) over G = 4..12 and ks =
+// 256..1536:
+//   * one workgroup per CU (grid <= 256) of many waves beats two or more
+//     smaller ones per CU, and a grid that leaves CUs idle or uneven costs
+//     less than a longer slice;
+//   * a wave's time grows with its slice (16 ks bf16 per step), the reduce's
+//     with the partials (splits x M);
+// so the plan takes the smallest G that fits the grid in `rounds` x 256
+// workgroups for each slice, scores ks + 64 splits M / 3072, and widens the
+// grid (rounds) only when no G <= 12 fits.  Chosen: 3072 x 3072 G6/384,
+// QKV 9216 x 3072 G9/768, FFN-up 14336 x 3072 G11/1024, FFN-down
+// 3072 x 14336 G12/896 (each within 0.1-0.7 us of the sweep's best).
+static void skinny_tiled_plan(int64_t M, int64_t N, int64_t K, int & splits, int & ks, int & waves) {
+    const int64_t ngrp = M / 16;
     const int nt = (int) ((N + 15) / 16);
-    static const int kSlices[] = {384, 512, 768, 1024, 1536};
+    const int64_t kwhole = (K + 127) / 128 * 128;  // one slice over all of K
     splits = (int) ((K + 383) / 384);
     ks = 384;
-    for (int c : kSlices) {
-        if ((size_t) 16 * nt * (c + 8) * sizeof(uint16_t) > kSkinnyLdsMax) break;
-        ks = c;
-        splits = (int) ((K + c - 1) / c);
-        if (nfb * splits <= 480 || c >= K) break;
+    waves = kSkinnyWaves;
+    // Slices of 384..1536 columns, or all of a shorter K in one.  One always
+    // fits the LDS (a 16 x 64-token activation slice of 384 columns is 49 KB),
+    // and with G = 4 every grid fits some number of rounds, so the search
+    // ends; the bound on rounds is a guard.
+    for (int64_t rounds = 1; rounds <= (int64_t) 1 << 30; rounds *= 2) {
+        double best = 1e30;
+        for (int64_t c = 128; c <= 1536; c += 128) {
+            const int64_t s = (K + c - 1) / c;
+            if (s == 1 ? c != kwhole : c < 384) continue;
+            if ((size_t) 16 * nt * (c + 8) * sizeof(uint16_t) > kSkinnyLdsMax) continue;
+            int G = (int) std::min<int64_t>(4, std::max<int64_t>(1, ngrp));
+            while (G <= 12 && (ngrp + G - 1) / G * s > 256 * rounds) ++G;
+            if (G > 12) continue;
+            const double score = (double) c + 64.0 * (double) s * (double) M / 3072.0;
+            if (score < best) {
+                best = score;
+                splits = (int) s;
+                ks = (int) c;
+                waves = G;
+            }
+        }
+        if (best < 1e30) return;
     }
 }
 
-static void skinny_plan_for(const GemmParams & p, bool tiled, int & splits, int & ks) {
-    if (tiled) skinny_tiled_plan(p.M, p.N, p.K, splits, ks);
+static void skinny_plan_for(const GemmParams & p, bool tiled, int & splits, int & ks, int & waves) {
+    waves = kSkinnyWaves;
+    if (tiled) skinny_tiled_plan(p.M, p.N, p.K, splits, ks, waves);
     else skinny_plan(p.M, p.N, p.K, splits, ks);
 }
 
@@ -1430,13 +1462,13 @@ static void skinny_plan_for(const GemmParams & p, bool tiled, int & splits, int 
 // columns; part == nullptr (single slice only) applies the epilogue in the
 // part kernel.
 static void launch_skinny_part(const GemmParams & p, bool xf32, bool tiled, float * part, int splits, int ks,
-                               hipStream_t s) {
+                               int waves, hipStream_t s) {
     const int nt = (int) ((p.N + 15) / 16);
     const dim3 block(kSkinnyWaves * 64);
     if (tiled) {
         const size_t lds = (size_t) 16 * nt * (ks + 8) * sizeof(uint16_t);
-        const dim3 grid((unsigned) ((p.M / 16 + kSkinnyWaves - 1) / kSkinnyWaves), (unsigned) splits);
-#define WAMX_TILED(XF, NT) hipLaunchKernelGGL((gemm_skinny_tiled<XF, NT>), grid, block, lds, s, p, part, ks)
+        const dim3 grid((unsigned) ((p.M / 16 + waves - 1) / waves), (unsigned) splits), tblock((unsigned) (64 * waves));
+#define WAMX_TILED(XF, NT) hipLaunchKernelGGL((gemm_skinny_tiled<XF, NT>), grid, tblock, lds, s, p, part, ks)
         switch (nt) {
             case 1: if (xf32) WAMX_TILED(true, 1); else WAMX_TILED(false, 1); break;
             case 2: if (xf32) WAMX_TILED(true, 2); else WAMX_TILED(false, 2); break;
@@ -1459,12 +1491,12 @@ static void launch_skinny_part(const GemmParams & p, bool xf32, bool tiled, floa
 }
 
 static hipError_t run_skinny(const GemmParams & p, bool xf32, bool tiled, void * ws, size_t ws_bytes, hipStream_t s) {
-    int splits, ks;
-    skinny_plan_for(p, tiled, splits, ks);
+    int splits, ks, waves;
+    skinny_plan_for(p, tiled, splits, ks, waves);
     if (splits > 1 && (!ws || (size_t) splits * p.N * p.M * sizeof(float) > ws_bytes || ((uintptr_t) ws & 15)))
         return hipErrorInvalidValue;
     float * part = splits > 1 ? (float *) ws : nullptr;
-    launch_skinny_part(p, xf32, tiled, part, splits, ks, s);
+    launch_skinny_part(p, xf32, tiled, part, splits, ks, waves, s);
     if (splits > 1) {
         const int64_t total = p.N * p.M;
         if (p.M % 4 == 0)
@@ -1617,8 +1649,8 @@ hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStre
         !vec_operands(a) || !p.vec_out || E == kEpiF32 || !a.ws || !aligned16(a.ws))
         return hipErrorNotSupported;
     if (a.w_tiled && (p.M % 16 != 0 || p.K % 32 != 0)) return hipErrorNotSupported;
-    int splits, ks;
-    skinny_plan_for(p, a.w_tiled, splits, ks);
+    int splits, ks, waves;
+    skinny_plan_for(p, a.w_tiled, splits, ks, waves);
     if ((size_t) splits * p.N * p.M * sizeof(float) > a.ws_bytes) return hipErrorNotSupported;
 
     // The row op: one thread per 8-column chunk, the whole row (or segment)
@@ -1682,7 +1714,7 @@ hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStre
 
     allow_skinny_lds();
     const float * part = (const float *) a.ws;
-    launch_skinny_part(p, a.x_type == WAMX_TYPE_F32, a.w_tiled, (float *) a.ws, splits, ks, s);
+    launch_skinny_part(p, a.x_type == WAMX_TYPE_F32, a.w_tiled, (float *) a.ws, splits, ks, waves, s);
     const dim3 grid((unsigned) p.N, (unsigned) nseg), block((unsigned) nchunk);
 #define WAMX_ROW(EK, PK) hipLaunchKernelGGL((skinny_reduce_row<EK, PK>), grid, block, 0, s, p, part, splits, d)
 #define WAMX_ROW_NORM(EK)                                                   \
