@@ -13,9 +13,12 @@
  *   2. A backend plugin interface mirroring ggml-backend-impl.h of llama.cpp b9866
  *      (ggml_backend_i / ggml_backend_device_i / buffer types / buffers).  ggml is
  *      not vendored in the reference (cmake/Dependencies.cmake:73-89), so the
- *      struct layouts and enum values are restated, not copied: numeric enum
- *      values that must line up with ggml are listed in wamx_ggml_op_map (see
- *      the end of this file) and are unverified against b9866 headers.
+ *      struct layouts are restated, not copied.  Graphs cross the boundary by
+ *      name (wamx_graph_from_ggml: ggml_op_name / ggml_unary_op_name /
+ *      ggml_type_name strings and ggml's op_params layouts), so no ggml enum
+ *      value has to line up; the only ggml numbers read are the
+ *      GGML_UNARY_OP_* codes inside UNARY's op_params (GELU 8, SILU 10,
+ *      GELU_ERF 14), restated from b9866's ggml.h and unverified against it.
  *   3. Single-op entry points on device pointers (wamx_op_*), used by the parity
  *      tests and by callers that do not build graphs.
  *   4. A synthetic GWP-0.5-shaped model driver (wamx_gwp_*) that builds the
