@@ -16,9 +16,10 @@
  *      struct layouts are restated, not copied.  Graphs cross the boundary by
  *      name (wamx_graph_from_ggml: ggml_op_name / ggml_unary_op_name /
  *      ggml_type_name strings and ggml's op_params layouts), so no ggml enum
- *      value has to line up; the only ggml numbers read are the
- *      GGML_UNARY_OP_* codes inside UNARY's op_params (GELU 8, SILU 10,
- *      GELU_ERF 14), restated from b9866's ggml.h and unverified against it.
+ *      value is read: UNARY's sub-op comes by its name as well.  The internal
+ *      unary codes (GELU 8, SILU 10, GELU_ERF 14) are the GGML_UNARY_OP_*
+ *      values of b9866 as restated (unverified against its headers), so a
+ *      UNARY's op_params mean the same on both sides.
  *   3. Single-op entry points on device pointers (wamx_op_*), used by the parity
  *      tests and by callers that do not build graphs.
  *   4. A synthetic GWP-0.5-shaped model driver (wamx_gwp_*) that builds the
