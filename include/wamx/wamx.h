@@ -566,6 +566,73 @@ WAMX_API wamx_tensor * wamx_gwp_prefix_key(wamx_gwp_t m, int layer);
 WAMX_API wamx_tensor * wamx_gwp_prefix_value(wamx_gwp_t m, int layer);
 WAMX_API int         wamx_gwp_graph_nodes(wamx_gwp_t m, int which);  /* 0 prompt, 1 prefix (chunk 0's), 2 denoise */
 
+/* ---------------------------------------------------------------------------
+ * GGUF artifacts.  wamx_gguf_* replaces wam.cpp's GgufReader
+ * (src/models/common/gguf_reader.h:26-66, .cpp:26-227), which parses through
+ * ggml's gguf library; this one reads the GGUF v2/v3 container directly.
+ * Opening reads the header (metadata and tensor descriptors) and checks every
+ * count, length and offset against the file; payloads are read on request.
+ * No GPU is needed.
+ * ------------------------------------------------------------------------- */
+typedef struct wamx_gguf * wamx_gguf_t;
+
+WAMX_API wamx_gguf_t  wamx_gguf_open(const char * path);          /* GgufReader::open; NULL + wamx_last_error() */
+WAMX_API void         wamx_gguf_close(wamx_gguf_t g);
+WAMX_API uint32_t     wamx_gguf_version(wamx_gguf_t g);
+WAMX_API uint64_t     wamx_gguf_data_offset(wamx_gguf_t g);       /* GgufReader::data_offset */
+WAMX_API int64_t      wamx_gguf_n_keys(wamx_gguf_t g);
+WAMX_API const char * wamx_gguf_key(wamx_gguf_t g, int64_t i);
+/* GGUF value type of a key (0 u8 .. 12 f64, 9 array), -1 when absent (GgufReader::has). */
+WAMX_API int32_t      wamx_gguf_key_type(wamx_gguf_t g, const char * key);
+WAMX_API bool         wamx_gguf_has(wamx_gguf_t g, const char * key);
+/* GgufReader::require_u32 / require_u64 / require_f32 / require_string /
+ * require_f32_array: FAILED (NULL, -1) with a message when the key is missing
+ * or of another type.  The f32 array getter copies up to cap values (F32 or
+ * F64 elements) and returns the array length. */
+WAMX_API wamx_status  wamx_gguf_get_u32(wamx_gguf_t g, const char * key, uint32_t * out);
+WAMX_API wamx_status  wamx_gguf_get_u64(wamx_gguf_t g, const char * key, uint64_t * out);
+WAMX_API wamx_status  wamx_gguf_get_f32(wamx_gguf_t g, const char * key, float * out);
+WAMX_API const char * wamx_gguf_get_str(wamx_gguf_t g, const char * key);
+WAMX_API int64_t      wamx_gguf_get_f32_array(wamx_gguf_t g, const char * key, float * out, int64_t cap);
+/* Tensor descriptors (GgufTensorInfo): name, ggml type (0 F32, 1 F16, 30 BF16,
+ * ...), n_dims, ne[dim] (1 past n_dims), absolute file offset, payload bytes
+ * (0 for a type this reader does not size).  find returns -1 when absent. */
+WAMX_API int64_t      wamx_gguf_n_tensors(wamx_gguf_t g);
+WAMX_API int64_t      wamx_gguf_find_tensor(wamx_gguf_t g, const char * name);
+WAMX_API const char * wamx_gguf_tensor_name(wamx_gguf_t g, int64_t i);
+WAMX_API int32_t      wamx_gguf_tensor_type(wamx_gguf_t g, int64_t i);
+WAMX_API int32_t      wamx_gguf_tensor_n_dims(wamx_gguf_t g, int64_t i);
+WAMX_API int64_t      wamx_gguf_tensor_ne(wamx_gguf_t g, int64_t i, int32_t dim);
+WAMX_API uint64_t     wamx_gguf_tensor_offset(wamx_gguf_t g, int64_t i);
+WAMX_API uint64_t     wamx_gguf_tensor_bytes(wamx_gguf_t g, int64_t i);
+/* GgufReader::read_tensor: the payload of tensor i into dst (bytes must equal
+ * its size). */
+WAMX_API wamx_status  wamx_gguf_read_tensor(wamx_gguf_t g, int64_t i, void * dst, uint64_t bytes);
+
+/* The GGUF tensor-name ABI: the compact name under which a GWP artifact
+ * stores a weight the engine addresses by its framework name (weights.cpp
+ * compact_tensor_name, :116-167; scripts/convert/convert_gwp05.py:57-140),
+ * e.g. "gwp.blocks.3.action_expert.attn1.to_qkv.weight" ->
+ * "gwp.blk.3.a.sa.qkv.weight".  Writes at most cap bytes (NUL included);
+ * returns the full length, -1 for an unknown component. */
+WAMX_API int32_t      wamx_gguf_compact_name(const char * name, char * out, int32_t cap);
+
+/* A GWP-0.5 model from a GGUF artifact, with its weights resident on the
+ * backend (the MoT component of wam.cpp's load_resident_weights,
+ * weights.cpp:702-770, and the geometry / schema checks of inspect_artifact,
+ * artifact.cpp:20-120, 232-292).  The geometry comes from the gwp05.* keys:
+ * grid = image_height/32 x image_width/32 (semantics.cpp:58-66), latent
+ * channels vae_z_dim, flow steps / shift, norm eps; n_lang prompt tokens (0:
+ * the reference's 64, semantics.h:11) and batch are the caller's.  The
+ * artifact's policy must store the MoT in BF16 (mot-bf16-v1, mot-vae-bf16-v1,
+ * mot-vae-bf16-qkv-v1): this backend runs the BF16 latency profile only.
+ * Weights are repacked as the model holds them: the per-layer adaLN tables
+ * into [width, 6, L], the embodiment_id slice of the category-specific
+ * encoder / decoder projections transposed to [out][in] (mot.cpp:1-53), and
+ * separate attn1 q / k / v into the packed QKV when the artifact is not
+ * packed.  T5, VAE and statistic tensors are not read. */
+WAMX_API wamx_gwp_t  wamx_gwp_create_from_gguf(wamx_backend_t be, wamx_gguf_t g, int32_t n_lang, int32_t batch);
+
 /* Last error message of the calling thread ("" when none). */
 WAMX_API const char * wamx_last_error(void);
 

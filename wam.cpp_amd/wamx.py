@@ -213,6 +213,30 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_gwp_prefix_key": (TensorP, [vp, C.c_int]),
         "wamx_gwp_prefix_value": (TensorP, [vp, C.c_int]),
         "wamx_gwp_graph_nodes": (C.c_int, [vp, C.c_int]),
+        "wamx_gguf_open": (vp, [C.c_char_p]),
+        "wamx_gguf_close": (None, [vp]),
+        "wamx_gguf_version": (C.c_uint32, [vp]),
+        "wamx_gguf_data_offset": (C.c_uint64, [vp]),
+        "wamx_gguf_n_keys": (i64, [vp]),
+        "wamx_gguf_key": (C.c_char_p, [vp, i64]),
+        "wamx_gguf_key_type": (i32, [vp, C.c_char_p]),
+        "wamx_gguf_has": (C.c_bool, [vp, C.c_char_p]),
+        "wamx_gguf_get_u32": (C.c_int, [vp, C.c_char_p, C.POINTER(C.c_uint32)]),
+        "wamx_gguf_get_u64": (C.c_int, [vp, C.c_char_p, C.POINTER(C.c_uint64)]),
+        "wamx_gguf_get_f32": (C.c_int, [vp, C.c_char_p, C.POINTER(C.c_float)]),
+        "wamx_gguf_get_str": (C.c_char_p, [vp, C.c_char_p]),
+        "wamx_gguf_get_f32_array": (i64, [vp, C.c_char_p, C.POINTER(C.c_float), i64]),
+        "wamx_gguf_n_tensors": (i64, [vp]),
+        "wamx_gguf_find_tensor": (i64, [vp, C.c_char_p]),
+        "wamx_gguf_tensor_name": (C.c_char_p, [vp, i64]),
+        "wamx_gguf_tensor_type": (i32, [vp, i64]),
+        "wamx_gguf_tensor_n_dims": (i32, [vp, i64]),
+        "wamx_gguf_tensor_ne": (i64, [vp, i64, i32]),
+        "wamx_gguf_tensor_offset": (C.c_uint64, [vp, i64]),
+        "wamx_gguf_tensor_bytes": (C.c_uint64, [vp, i64]),
+        "wamx_gguf_read_tensor": (C.c_int, [vp, i64, vp, C.c_uint64]),
+        "wamx_gguf_compact_name": (i32, [C.c_char_p, C.c_char_p, i32]),
+        "wamx_gwp_create_from_gguf": (vp, [vp, vp, i32, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name, None)
