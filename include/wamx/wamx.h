@@ -633,6 +633,48 @@ WAMX_API int32_t      wamx_gguf_compact_name(const char * name, char * out, int3
  * packed.  T5, VAE and statistic tensors are not read. */
 WAMX_API wamx_gwp_t  wamx_gwp_create_from_gguf(wamx_backend_t be, wamx_gguf_t g, int32_t n_lang, int32_t batch);
 
+/* ---------------------------------------------------------------------------
+ * UMT5 text encoder: prompt tokens -> the f32 prompt embedding [max_tokens]
+ * [hidden] (the reference's run_t5, src/models/gwp05/engine/text_encoder.cpp
+ * :112-204, for its `resident` / `fixed` language policies).  Built on this
+ * backend's IR op for op and run through wamx_backend_graph_compute: token
+ * rows by GET_ROWS, per layer RMSNorm x weight, self-attention with a
+ * relative-position bias (32 buckets, max distance 128) as the SOFT_MAX mask
+ * and scale 1, gated-GELU FFN, residual adds; a final RMSNorm.  Weights are
+ * bf16 with the reference's names ("t5.shared.weight",
+ * "t5.encoder.block.{l}.layer.0.SelfAttention.{q,k,v,o}.weight", ...).
+ * ------------------------------------------------------------------------- */
+typedef struct wamx_t5_config {
+    int32_t vocab;       /* gwp05.t5_vocab_size */
+    int32_t hidden;      /* gwp05.t5_hidden */
+    int32_t ffn_dim;     /* gwp05.t5_ffn_dim */
+    int32_t heads;       /* gwp05.t5_heads */
+    int32_t head_dim;    /* gwp05.t5_head_dim */
+    int32_t layers;      /* gwp05.t5_layers */
+    int32_t max_tokens;  /* prompt rows returned (the GWP prompt: 64) */
+    float   eps;         /* RMSNorm eps (1e-6) */
+} wamx_t5_config;
+typedef struct wamx_t5 * wamx_t5_t;
+
+WAMX_API wamx_t5_t    wamx_t5_create(wamx_backend_t be, const wamx_t5_config * cfg);  /* weights allocated, unset */
+WAMX_API void         wamx_t5_free(wamx_t5_t t);
+WAMX_API int          wamx_t5_n_weights(wamx_t5_t t);
+WAMX_API const char * wamx_t5_weight_name(wamx_t5_t t, int i);
+WAMX_API wamx_tensor * wamx_t5_weight(wamx_t5_t t, const char * name);
+/* The t5.* tensors of a GWP artifact (BF16, compact names). */
+WAMX_API wamx_status  wamx_t5_load_gguf(wamx_t5_t t, wamx_gguf_t g);
+/* Configuration from the gwp05.t5_* keys, 64 prompt tokens, weights loaded. */
+WAMX_API wamx_t5_t    wamx_t5_create_from_gguf(wamx_backend_t be, wamx_gguf_t g);
+/* Encode n (1..max_tokens) tokens; mask (nullable) holds 0/1 with the valid
+ * tokens a contiguous prefix, as validate_prompt_mask requires
+ * (text_encoder.cpp:75-110).  out: f32 [max_tokens][hidden], rows past the
+ * valid prefix zero.  Synchronous. */
+WAMX_API wamx_status  wamx_t5_encode(wamx_t5_t t, const int32_t * tokens, const int32_t * mask, int32_t n,
+                                     float * out);
+/* T5's bidirectional relative-position bucket of key - query
+ * (text_encoder.cpp:13-24); -1 for invalid bucket parameters. */
+WAMX_API int32_t      wamx_t5_relative_bucket(int32_t relative, int32_t buckets, int32_t max_distance);
+
 /* Last error message of the calling thread ("" when none). */
 WAMX_API const char * wamx_last_error(void);
 

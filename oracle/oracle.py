@@ -442,3 +442,115 @@ def gwp_synthetic_weight(name: str, n: int, seed: int, wstd: float = 0.02) -> np
 
 def gwp_synthetic_weights(cfg: dict, seed: int, wstd: float = 0.02) -> dict:
     return {n: gwp_synthetic_weight(n, k, seed, wstd) for n, k in gwp_weight_specs(cfg)}
+
+
+# ---------------------------------------------------------------------------
+# UMT5 text encoder (src/models/gwp05/engine/text_encoder.cpp:13-24, :26-73,
+# :112-204), restated in numpy with float64 accumulation and the reference's
+# rounding points: activations rounded to bf16 where a bf16 weight multiplies
+# them (stock MUL_MAT converts src1 to the weight's vec-dot type), f32 K.Q and
+# V.P kept unrounded, bf16 weights widened exactly.
+# ---------------------------------------------------------------------------
+_libm = None
+
+
+def _logf(x: float) -> float:
+    """The C library's single-precision log (the reference's std::log(float))."""
+    global _libm
+    if _libm is None:
+        import ctypes.util
+        _libm = C.CDLL(ctypes.util.find_library("m"))
+        _libm.logf.restype, _libm.logf.argtypes = C.c_float, [C.c_float]
+    return _libm.logf(x)
+
+
+def t5_relative_bucket(relative: int, buckets: int = 32, max_distance: int = 128) -> int:
+    """text_encoder.cpp:13-24: half the buckets per direction (key after the
+    query: upper half), exact below half/2, logarithmic up to max_distance,
+    in single precision."""
+    half = buckets // 2
+    base = half if relative > 0 else 0
+    d = abs(relative)
+    exact = half // 2
+    if d < exact:
+        return base + d
+    r = np.float32(_logf(np.float32(d) / np.float32(exact))) / np.float32(_logf(np.float32(max_distance) / np.float32(exact)))
+    return base + min(half - 1, exact + int(np.float32(r) * np.float32(half - exact)))
+
+
+def t5_weight_specs(c: dict):
+    """[(name, ggml ne)] of the UMT5 encoder's weights (reference names)."""
+    d, inner, F, H = c["hidden"], c["heads"] * c["head_dim"], c["ffn_dim"], c["heads"]
+    out = [("t5.shared.weight", (d, c["vocab"]))]
+    for l in range(c["layers"]):
+        p = f"t5.encoder.block.{l}.layer"
+        a = p + ".0.SelfAttention"
+        out += [(a + ".q.weight", (d, inner)), (a + ".k.weight", (d, inner)), (a + ".v.weight", (d, inner)),
+                (a + ".o.weight", (inner, d)), (a + ".relative_attention_bias.weight", (H, 32)),
+                (p + ".0.layer_norm.weight", (d,)), (p + ".1.DenseReluDense.wi_0.weight", (d, F)),
+                (p + ".1.DenseReluDense.wi_1.weight", (d, F)), (p + ".1.DenseReluDense.wo.weight", (F, d)),
+                (p + ".1.layer_norm.weight", (d,))]
+    out.append(("t5.encoder.final_layer_norm.weight", (d,)))
+    return out
+
+
+def _bf(a) -> np.ndarray:
+    """bf16 bit patterns -> float64."""
+    return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def bf16_rne(x) -> np.ndarray:
+    """f32 -> bf16 bit patterns, round to nearest even, NaN kept quiet: the
+    element rule of orc_f32_to_bf16, vectorised (tests check the two agree)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    return np.where(nan, (u >> 16) | 0x40, r).astype(np.uint16)
+
+
+def _r(x) -> np.ndarray:
+    """Round to bf16 (RNE) and widen: a bf16-weight MUL_MAT's view of its f32 input."""
+    return _bf(bf16_rne(np.asarray(x, np.float32)))
+
+
+def _rms(x, w, eps):
+    """ggml_rms_norm over the row, then MUL by the widened weight (weights.cpp:904-917)."""
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w
+
+
+def _gelu(x):
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+def t5_encode(c: dict, weights: dict, tokens, mask=None, eps: float = 1e-6) -> np.ndarray:
+    """run_t5 (text_encoder.cpp:112-204): f32 [max_tokens][hidden], rows past
+    the mask's valid prefix zero.  weights: name -> bf16 bit patterns in the
+    ggml layout of t5_weight_specs (row-major [ne1][ne0])."""
+    tokens = np.asarray(tokens, np.int64)
+    n = tokens.size if mask is None else int(np.sum(mask))
+    d, H, dh, F = c["hidden"], c["heads"], c["head_dim"], c["ffn_dim"]
+    W = {k: _bf(v).reshape(tuple(reversed(s))) for (k, s), v in ((ks, weights[ks[0]]) for ks in t5_weight_specs(c))}
+    h = W["t5.shared.weight"][tokens[:n]]                                   # get_rows: [n, d]
+    bucket = np.array([[t5_relative_bucket(k - q) for k in range(n)] for q in range(n)])  # [query, key]
+    for l in range(c["layers"]):
+        p = f"t5.encoder.block.{l}.layer"
+        a = p + ".0.SelfAttention"
+        bias = W[a + ".relative_attention_bias.weight"][bucket]           # [query, key, head]
+        x = _rms(h, W[p + ".0.layer_norm.weight"], eps)
+        xr = _r(x)
+        q, k, v = (xr @ W[a + f".{m}.weight"].T for m in "qkv")          # [n, H*dh] f32 outputs
+        q, k, v = (t.reshape(n, H, dh).transpose(1, 0, 2) for t in (q, k, v))
+        s = q @ k.transpose(0, 2, 1) + bias.transpose(2, 0, 1)              # scale 1, bias as the mask
+        s = s - s.max(axis=-1, keepdims=True)
+        pr = np.exp(s)
+        pr /= pr.sum(axis=-1, keepdims=True)
+        att = (pr @ v).transpose(1, 0, 2).reshape(n, H * dh)
+        h = h + _r(att) @ W[a + ".o.weight"].T
+        f = p + ".1.DenseReluDense"
+        xr = _r(_rms(h, W[p + ".1.layer_norm.weight"], eps))
+        g = _gelu(xr @ W[f + ".wi_0.weight"].T) * (xr @ W[f + ".wi_1.weight"].T)
+        h = h + _r(g) @ W[f + ".wo.weight"].T
+    y = _rms(h, W["t5.encoder.final_layer_norm.weight"], eps)
+    out = np.zeros((c["max_tokens"], d))
+    out[:n] = y
+    return out

@@ -60,6 +60,11 @@ class GwpConfig(C.Structure):
         "num_steps", "enc_hidden")] + [("shift", C.c_float), ("eps", C.c_float), ("batch", C.c_int32)]
 
 
+class T5Config(C.Structure):
+    _fields_ = [(k, C.c_int32) for k in ("vocab", "hidden", "ffn_dim", "heads", "head_dim", "layers", "max_tokens")] + \
+               [("eps", C.c_float)]
+
+
 class GwpTiming(C.Structure):
     _fields_ = [("prompt_ms", C.c_float), ("prefix_ms", C.c_float), ("denoise_ms", C.c_float),
                 ("total_ms", C.c_float)]
@@ -237,6 +242,15 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_gguf_read_tensor": (C.c_int, [vp, i64, vp, C.c_uint64]),
         "wamx_gguf_compact_name": (i32, [C.c_char_p, C.c_char_p, i32]),
         "wamx_gwp_create_from_gguf": (vp, [vp, vp, i32, i32]),
+        "wamx_t5_create": (vp, [vp, vp]),
+        "wamx_t5_free": (None, [vp]),
+        "wamx_t5_n_weights": (C.c_int, [vp]),
+        "wamx_t5_weight_name": (C.c_char_p, [vp, C.c_int]),
+        "wamx_t5_weight": (TensorP, [vp, C.c_char_p]),
+        "wamx_t5_load_gguf": (C.c_int, [vp, vp]),
+        "wamx_t5_create_from_gguf": (vp, [vp, vp]),
+        "wamx_t5_encode": (C.c_int, [vp, vp, vp, i32, vp]),
+        "wamx_t5_relative_bucket": (i32, [i32, i32, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name, None)
