@@ -90,6 +90,7 @@ typedef enum wamx_op {
     WAMX_OP_UNARY,      /* GELU with src[1]: bias + GELU-tanh bf16 (patch:614-628) */
     WAMX_OP_GET_ROWS,
     WAMX_OP_IM2COL,
+    WAMX_OP_CONV_2D,    /* ggml_conv_2d_direct (bf16: the patch's cuDNN path, native-bf16.patch:174-218) */
     /* Fused ops with no single ggml counterpart.  They are what the engine's
      * attention hook native_attention_context (mot.cpp:269-282) and a fused
      * linear would emit.  Each one documents the unfused ggml subgraph it
@@ -221,6 +222,14 @@ WAMX_API wamx_tensor * wamx_get_rows(wamx_context * ctx, wamx_tensor * a, wamx_t
  * ic*KH*KW + kh*KW + kw (the patch embedding of cache.cpp:203-218). */
 WAMX_API wamx_tensor * wamx_im2col(wamx_context * ctx, wamx_tensor * kernel, wamx_tensor * input, int s0, int s1,
                                    int p0, int p1, int d0, int d1, int32_t dst_type);
+
+/* ggml_conv_2d_direct: kernel ne={KW,KH,IC,OC}, input ne={IW,IH,IC,N} (both
+ * bf16, or both f32); result ne={OW,OH,OC,N} of the input's type,
+ * op_params {s0, s1, p0, p1, d0, d1} (ggml's layout).  BF16 is the VAE's
+ * convolution (vae.cpp:139-157; native-bf16.patch:174-218: f32 accumulation,
+ * bf16 out). */
+WAMX_API wamx_tensor * wamx_conv_2d_direct(wamx_context * ctx, wamx_tensor * kernel, wamx_tensor * input, int s0,
+                                           int s1, int p0, int p1, int d0, int d1);
 
 /* The fused ops of patches/llama-b9866-native-bf16.patch:566-678. */
 WAMX_API wamx_tensor * wamx_gated_residual_bf16(wamx_context * ctx, wamx_tensor * hidden, wamx_tensor * branch, wamx_tensor * gate);
@@ -632,6 +641,27 @@ WAMX_API int32_t      wamx_gguf_compact_name(const char * name, char * out, int3
  * separate attn1 q / k / v into the packed QKV when the artifact is not
  * packed.  T5, VAE and statistic tensors are not read. */
 WAMX_API wamx_gwp_t  wamx_gwp_create_from_gguf(wamx_backend_t be, wamx_gguf_t g, int32_t n_lang, int32_t batch);
+
+/* ---------------------------------------------------------------------------
+ * Camera views -> VAE input (gwp05_cuda_preprocessor_create / _destroy /
+ * gwp05_cuda_preprocess, src/models/gwp05/kernels/cuda_preprocess.h:8-15,
+ * .cu:45-200): three host images (camera_high, camera_left_wrist,
+ * camera_right_wrist) composed into an out_w x out_h canvas (top half; bottom
+ * left; bottom right), each resized to cover its region with an antialiased
+ * triangle filter and centre-cropped, written 2x2 pixel-unshuffled as f32
+ * [12][out_h/2][out_w/2] in [-1, 1] to device memory.  The preprocessor keeps
+ * the per-view device staging buffers; the call is synchronous.
+ * ------------------------------------------------------------------------- */
+typedef struct wamx_image_view {
+    const void * data;   /* host RGB, row-major [h][w][3] */
+    int32_t w, h;
+    int32_t format;      /* 0: u8 (value / 255), 1: f32 in [0, 1] (PixelFormat U8 / F32_RGB_01) */
+} wamx_image_view;
+typedef struct wamx_preprocessor * wamx_preprocessor_t;
+WAMX_API wamx_preprocessor_t wamx_preprocessor_create(wamx_backend_t be);
+WAMX_API void                wamx_preprocessor_free(wamx_preprocessor_t p);
+WAMX_API wamx_status         wamx_preprocess_views(wamx_preprocessor_t p, const wamx_image_view * views,
+                                                   int32_t n_views, int32_t out_w, int32_t out_h, float * out_device);
 
 /* ---------------------------------------------------------------------------
  * UMT5 text encoder: prompt tokens -> the f32 prompt embedding [max_tokens]

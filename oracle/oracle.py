@@ -554,3 +554,95 @@ def t5_encode(c: dict, weights: dict, tokens, mask=None, eps: float = 1e-6) -> n
     out = np.zeros((c["max_tokens"], d))
     out[:n] = y
     return out
+
+
+# ---------------------------------------------------------------------------
+# Vision front-end: the three-view canvas and its 2x2 patchify
+# (src/models/gwp05/engine/vae.cpp:1-133, compose_and_patchify and
+# resize_center_crop), and ggml_conv_2d_direct (the VAE convolution,
+# vae.cpp:140-157).  Filter parameters in float32 as the reference computes
+# them; the resampling sums in float64.
+# ---------------------------------------------------------------------------
+def _resize_axis(src: int, resized: int, dst: int):
+    """Taps of every output position of one axis (vae.cpp:17-44): the
+    triangle filter of support max(1, 1/scale) around the source centre of
+    the cropped output position, zero taps dropped, indices clamped to the
+    image, weights normalised to sum 1.  Returns (indices, weights) lists."""
+    f = np.float32
+    crop = (resized - dst) // 2
+    scale = f(resized) / f(src)
+    support = max(f(1.0), f(1.0) / scale)
+    out = []
+    for o in range(dst):
+        center = (f(o + crop) + f(0.5)) / scale - f(0.5)
+        first, last = int(np.ceil(center - support)), int(np.floor(center + support))
+        idx, wts = [], []
+        for s in range(first, last + 1):
+            w = max(f(0.0), f(1.0) - f(abs(f(s) - center)) / support)
+            if w == 0.0:
+                continue
+            idx.append(min(max(s, 0), src - 1))
+            wts.append(w)
+        total = f(0.0)
+        for w in wts:
+            total = f(total + w)
+        out.append((np.array(idx), np.array([f(w / total) for w in wts], np.float64)))
+    return out
+
+
+def resize_center_crop(img: np.ndarray, dst_w: int, dst_h: int) -> np.ndarray:
+    """One view [h][w][3] (float, in [0, 1]) resized to cover dst_w x dst_h
+    (scale = max of the axis ratios, sizes rounded half away from zero) and
+    centre-cropped: x first, then y (vae.cpp:1-87)."""
+    h, w = img.shape[:2]
+    f = np.float32
+    scale = max(f(dst_w) / f(w), f(dst_h) / f(h))
+    rw = int(np.floor(np.float64(f(w) * scale) + 0.5))
+    rh = int(np.floor(np.float64(f(h) * scale) + 0.5))
+    ax, ay = _resize_axis(w, rw, dst_w), _resize_axis(h, rh, dst_h)
+    src = np.asarray(img, np.float64)
+    horiz = np.stack([np.einsum("hkc,k->hc", src[:, i, :], wt) for i, wt in ax], axis=1)   # [h][dst_w][3]
+    return np.stack([np.einsum("kwc,k->wc", horiz[i], wt) for i, wt in ay], axis=0)     # [dst_h][dst_w][3]
+
+
+def view_pixels(data: np.ndarray) -> np.ndarray:
+    """A camera view as the reference reads it: u8 -> v / 255 (in float32), f32 as is."""
+    a = np.asarray(data)
+    return (a.astype(np.float32) * np.float32(1.0 / 255.0)) if a.dtype == np.uint8 else a.astype(np.float32)
+
+
+def compose_and_patchify(views, width: int, height: int) -> np.ndarray:
+    """vae.cpp:89-133: the high camera on the top half, the two wrist cameras
+    on the bottom-left / bottom-right, the canvas 2x2 pixel-unshuffled to
+    f32 [12][height/2][width/2] (channel 4c + 2dx + dy), mapped v * 2 - 1."""
+    top, left = height // 2, width // 2
+    canvas = np.zeros((height, width, 3))
+    canvas[:top, :] = resize_center_crop(view_pixels(views[0]), width, top)
+    canvas[top:, :left] = resize_center_crop(view_pixels(views[1]), left, height - top)
+    canvas[top:, left:] = resize_center_crop(view_pixels(views[2]), width - left, height - top)
+    ow, oh = width // 2, height // 2
+    c = canvas[:2 * oh, :2 * ow].reshape(oh, 2, ow, 2, 3)                # [y][dy][x][dx][c]
+    out = c.transpose(4, 3, 1, 0, 2).reshape(12, oh, ow)                 # channel (c, dx, dy)
+    return out * 2.0 - 1.0
+
+
+def conv_2d(kernel: np.ndarray, inp: np.ndarray, s0=1, s1=1, p0=0, p1=0, d0=1, d1=1) -> np.ndarray:
+    """ggml_conv_2d_direct: kernel [OC][IC][KH][KW], input [N][IC][IH][IW]
+    (float arrays: bf16 operands widened exactly), out [N][OC][OH][OW] in
+    float64; out = sum over ic, ky, kx of kernel * input at
+    (oy*s1 - p1 + ky*d1, ox*s0 - p0 + kx*d0), zero outside the image."""
+    k = np.asarray(kernel, np.float64)
+    x = np.asarray(inp, np.float64)
+    OC, IC, KH, KW = k.shape
+    N, _, IH, IW = x.shape
+    OW = (IW + 2 * p0 - d0 * (KW - 1) - 1) // s0 + 1
+    OH = (IH + 2 * p1 - d1 * (KH - 1) - 1) // s1 + 1
+    xp = np.zeros((N, IC, IH + 2 * p1, IW + 2 * p0))
+    xp[:, :, p1:p1 + IH, p0:p0 + IW] = x
+    out = np.zeros((N, OC, OH, OW))
+    for ky in range(KH):
+        for kx in range(KW):
+            y0, x0 = ky * d1, kx * d0
+            patch = xp[:, :, y0:y0 + s1 * (OH - 1) + 1:s1, x0:x0 + s0 * (OW - 1) + 1:s0]   # [N][IC][OH][OW]
+            out += np.einsum("nchw,oc->nohw", patch, k[:, :, ky, kx], optimize=True)
+    return out

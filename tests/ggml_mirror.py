@@ -247,6 +247,15 @@ def im2col(kernel, inp, s0, s1, p0, p1, d0, d1, is_2d, dst_type):
     return t
 
 
+def conv_2d_direct(kernel, inp, s0, s1, p0, p1, d0, d1):
+    KW, KH = kernel.ne[0], kernel.ne[1]
+    OW = (inp.ne[0] + 2 * p0 - d0 * (KW - 1) - 1) // s0 + 1
+    OH = (inp.ne[1] + 2 * p1 - d1 * (KH - 1) - 1) // s1 + 1
+    t = T(inp.type, [OW, OH, kernel.ne[3], inp.ne[3]], op="CONV_2D", src=[kernel, inp])
+    t.params[0:6] = [s0, s1, p0, p1, d0, d1]
+    return t
+
+
 # --- graphs ------------------------------------------------------------------
 class Graph:
     """ggml_cgraph: nodes in post-order of ggml_build_forward_expand (sources

@@ -641,6 +641,8 @@ static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
             return launch_im2col(ref_of(s1), ref_of(node), (int) s0->ne[0], (int) s0->ne[1], pp[0], pp[1], pp[2], pp[3],
                                  pp[4], pp[5], s);
         }
+        case WAMX_OP_CONV_2D:
+            return launch_conv2d(ref_of(s0), ref_of(s1), ref_of(node), node->op_params, be->cws, kWorkspaceBytes, s);
         case WAMX_OP_LINEAR:
             return run_linear(be, node);
         case WAMX_OP_QK_NORM_ROPE: {
@@ -802,6 +804,8 @@ static bool supports(const wamx_tensor * t) {
             return !tensor_is_tiled(s0) || tiled_product_ok(s1);
         case WAMX_OP_IM2COL:
             return check_im2col(t) == nullptr;
+        case WAMX_OP_CONV_2D:
+            return check_conv_2d(t) == nullptr;
         case WAMX_OP_QK_NORM_ROPE:
             return check_qk_norm_rope(t) == nullptr;
         case WAMX_OP_JOINT_ATTN:

@@ -17,6 +17,7 @@ const char * check_qk_norm_rope(const wamx_tensor * t);
 const char * check_joint_attn(const wamx_tensor * t);
 const char * check_modulation(const wamx_tensor * t);
 const char * check_im2col(const wamx_tensor * t);
+const char * check_conv_2d(const wamx_tensor * t);
 
 // ---------------------------------------------------------------------------
 // GEMM: y[b][n][m] = sum_k w[b/r][m][k] * x[b][n][k]  (the ggml MUL_MAT layout:
@@ -147,6 +148,11 @@ hipError_t launch_rope_f32(const TensorRef & x, const int32_t * pos, const Tenso
                            hipStream_t s);
 hipError_t launch_im2col(const TensorRef & src, const TensorRef & dst, int KW, int KH, int s0, int s1, int p0, int p1,
                          int d0, int d1, hipStream_t s);
+// ggml_conv_2d_direct (kernel [KW,KH,IC,OC], input [IW,IH,IC,N], dst
+// [OW,OH,OC,N]; pp = {s0, s1, p0, p1, d0, d1}): im2col row chunks in the
+// upper half of ws, the GEMM's partials in the lower half.
+hipError_t launch_conv2d(const TensorRef & kernel, const TensorRef & input, const TensorRef & dst, const int32_t * pp,
+                         void * ws, size_t ws_bytes, hipStream_t s);
 hipError_t launch_modulation(const void * mod, int32_t mod_type, const void * tables, int32_t tab_type, float * out,
                              int64_t per_layer, int64_t layers, hipStream_t s);
 

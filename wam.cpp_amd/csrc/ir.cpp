@@ -209,6 +209,29 @@ const char * check_im2col(const wamx_tensor * t) {
     return nullptr;
 }
 
+// ggml_conv_2d_direct: kernel [KW,KH,IC,OC], input [IW,IH,IC,N] of one type
+// (bf16 or f32, contiguous), dst [OW,OH,OC,N] of that type, op_params
+// {s0, s1, p0, p1, d0, d1}.
+const char * check_conv_2d(const wamx_tensor * t) {
+    const wamx_tensor *kernel = t->src[0], *input = t->src[1];
+    const int32_t * p = t->op_params;
+    if (!kernel || !input) return "operands";
+    if (!((kernel->type == WAMX_TYPE_BF16 && input->type == WAMX_TYPE_BF16) ||
+          (kernel->type == WAMX_TYPE_F32 && input->type == WAMX_TYPE_F32)) ||
+        t->type != input->type)
+        return "types (bf16 or f32 throughout)";
+    if (!wamx_is_contiguous(kernel) || !wamx_is_contiguous(input) || !wamx_is_contiguous(t)) return "layout";
+    if (p[0] < 1 || p[1] < 1 || p[4] < 1 || p[5] < 1 || p[2] < 0 || p[3] < 0) return "stride/padding/dilation";
+    const int64_t KW = kernel->ne[0], KH = kernel->ne[1];
+    if (kernel->ne[2] != input->ne[2]) return "channels";
+    const int64_t OW = (input->ne[0] + 2 * p[2] - p[4] * (KW - 1) - 1) / p[0] + 1;
+    const int64_t OH = (input->ne[1] + 2 * p[3] - p[5] * (KH - 1) - 1) / p[1] + 1;
+    if (OW <= 0 || OH <= 0 || t->ne[0] != OW || t->ne[1] != OH || t->ne[2] != kernel->ne[3] ||
+        t->ne[3] != input->ne[3])
+        return "output shape";
+    return nullptr;
+}
+
 }  // namespace wamx
 
 // Builds node `t` of an op validated by `check`; on failure the (unlinked)
@@ -261,7 +284,7 @@ const char * wamx_op_name(int32_t op) {
     static const char * names[WAMX_OP_COUNT] = {
         "NONE", "DUP", "ADD", "MUL", "SCALE", "CPY", "CONT", "RESHAPE", "VIEW", "PERMUTE",
         "TRANSPOSE", "CONCAT", "REPEAT", "NORM", "RMS_NORM", "MUL_MAT", "SOFT_MAX", "ROPE",
-        "UNARY", "GET_ROWS", "IM2COL", "LINEAR", "QK_NORM_ROPE", "JOINT_ATTN", "MODULATION",
+        "UNARY", "GET_ROWS", "IM2COL", "CONV_2D", "LINEAR", "QK_NORM_ROPE", "JOINT_ATTN", "MODULATION",
     };
     return (op >= 0 && op < WAMX_OP_COUNT) ? names[op] : "?";
 }
@@ -614,6 +637,24 @@ wamx_tensor * wamx_im2col(wamx_context * ctx, wamx_tensor * kernel, wamx_tensor 
     return checked(t, check_im2col, "wamx_im2col");
 }
 
+wamx_tensor * wamx_conv_2d_direct(wamx_context * ctx, wamx_tensor * kernel, wamx_tensor * input, int s0, int s1, int p0,
+                                  int p1, int d0, int d1) {
+    if (!kernel || !input || s0 < 1 || s1 < 1 || d0 < 1 || d1 < 1) return fail("wamx_conv_2d_direct");
+    const int64_t KW = kernel->ne[0], KH = kernel->ne[1];
+    const int64_t OW = (input->ne[0] + 2 * p0 - d0 * (KW - 1) - 1) / s0 + 1;
+    const int64_t OH = (input->ne[1] + 2 * p1 - d1 * (KH - 1) - 1) / s1 + 1;
+    if (OW <= 0 || OH <= 0) return fail("wamx_conv_2d_direct (output size)");
+    int64_t ne[4] = {OW, OH, kernel->ne[3], input->ne[3]};
+    wamx_tensor * t = new_tensor_impl(ctx, input->type, 4, ne);
+    if (!t) return nullptr;
+    t->op = WAMX_OP_CONV_2D;
+    const int32_t params[6] = {s0, s1, p0, p1, d0, d1};  // ggml's layout
+    memcpy(t->op_params, params, sizeof params);
+    t->src[0] = kernel;
+    t->src[1] = input;
+    return checked(t, check_conv_2d, "wamx_conv_2d_direct");
+}
+
 // --- native-bf16.patch:594-678 ---------------------------------------------
 wamx_tensor * wamx_gated_residual_bf16(wamx_context * ctx, wamx_tensor * hidden, wamx_tensor * branch, wamx_tensor * gate) {
     if (!is_bf16(hidden) || !is_bf16(branch) || !gate || (gate->type != WAMX_TYPE_F32 && gate->type != WAMX_TYPE_BF16))
@@ -828,6 +869,7 @@ static const struct {
     {"SOFT_MAX", WAMX_OP_SOFT_MAX}, {"ROPE", WAMX_OP_ROPE},
     {"UNARY", WAMX_OP_UNARY},       {"GET_ROWS", WAMX_OP_GET_ROWS},
     {"IM2COL", WAMX_OP_IM2COL},
+    {"CONV_2D", WAMX_OP_CONV_2D},
 };
 
 // ggml_backend_alloc_ctx_tensors: one buffer for every unallocated,

@@ -26,7 +26,7 @@ UNARY_GELU, UNARY_SILU, UNARY_GELU_ERF = 8, 10, 14
 
 OP_NAMES = ["NONE", "DUP", "ADD", "MUL", "SCALE", "CPY", "CONT", "RESHAPE", "VIEW", "PERMUTE",
             "TRANSPOSE", "CONCAT", "REPEAT", "NORM", "RMS_NORM", "MUL_MAT", "SOFT_MAX", "ROPE",
-            "UNARY", "GET_ROWS", "IM2COL", "LINEAR", "QK_NORM_ROPE", "JOINT_ATTN", "MODULATION"]
+            "UNARY", "GET_ROWS", "IM2COL", "CONV_2D", "LINEAR", "QK_NORM_ROPE", "JOINT_ATTN", "MODULATION"]
 OP = {name: i for i, name in enumerate(OP_NAMES)}
 
 
@@ -58,6 +58,10 @@ class GwpConfig(C.Structure):
         "n_layers", "hidden", "n_heads", "head_dim", "ffn_dim", "action_hidden", "action_ffn_dim",
         "action_chunk", "action_dim", "grid_h", "grid_w", "n_lang", "t5_hidden", "z_dim",
         "num_steps", "enc_hidden")] + [("shift", C.c_float), ("eps", C.c_float), ("batch", C.c_int32)]
+
+
+class ImageView(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("w", C.c_int32), ("h", C.c_int32), ("format", C.c_int32)]
 
 
 class T5Config(C.Structure):
@@ -243,6 +247,10 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_gguf_compact_name": (i32, [C.c_char_p, C.c_char_p, i32]),
         "wamx_gwp_create_from_gguf": (vp, [vp, vp, i32, i32]),
         "wamx_t5_create": (vp, [vp, vp]),
+        "wamx_conv_2d_direct": (TensorP, [vp, TensorP, TensorP, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+        "wamx_preprocessor_create": (vp, [vp]),
+        "wamx_preprocessor_free": (None, [vp]),
+        "wamx_preprocess_views": (C.c_int, [vp, vp, i32, i32, i32, vp]),
         "wamx_t5_free": (None, [vp]),
         "wamx_t5_n_weights": (C.c_int, [vp]),
         "wamx_t5_weight_name": (C.c_char_p, [vp, C.c_int]),
