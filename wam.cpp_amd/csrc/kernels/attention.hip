@@ -212,7 +212,16 @@ struct AttnParams {
     float * part_o;          // [split][head][query][kDh], unnormalised, scaled to part_m
     float * part_m;          // [split][head][query] running max (log2 domain)
     float * part_l;          // [split][head][query] running sum
+    // Unit-mapped attn_prefill launches (units > 0): workgroup x takes unit
+    // unit0 + x, i.e. head u % heads and query block u / heads; key-split
+    // partials are then indexed [split][x][query of the block] and
+    // joint_attn_merge maps its rows the same way.
+    int64_t unit0, units;
 };
+
+// attn_prefill's workgroup: 4 waves x 32 queries of one head.
+constexpr int kPfWaves = 4;
+constexpr int kPfQueries = 32 * kPfWaves;
 
 // Output row of query q of head h: chunk b = h / hb writes rows [b * tq, (b + 1) * tq).
 __device__ __forceinline__ uint16_t * out_row(const AttnParams & p, int64_t h, int64_t q) {
@@ -441,9 +450,15 @@ __global__ __launch_bounds__(NW * 64) void joint_attn_kernel(AttnParams p) {
 // out = sum o_z 2^(m_z - m*) / l*.
 // All loads of a batch of eight splits are issued before they are combined.
 __global__ __launch_bounds__(kDh) void joint_attn_merge(AttnParams p, int nsplit) {
-    const int64_t hq = blockIdx.x, h = hq / p.tq, q = hq % p.tq;
+    int64_t hq = blockIdx.x, h = hq / p.tq, q = hq % p.tq, stride = p.heads * p.tq;
+    if (p.units) {  // row hq = query hq % 128 of unit unit0 + hq / 128
+        const int64_t u = p.unit0 + hq / kPfQueries;
+        h = u % p.heads;
+        q = u / p.heads * kPfQueries + hq % kPfQueries;
+        stride = p.units * kPfQueries;
+        if (q >= p.tq) return;
+    }
     const int d = threadIdx.x;
-    const int64_t stride = p.heads * p.tq;
     constexpr int kB = 8;
     float mstar = -INFINITY;
     for (int z0 = 0; z0 < nsplit; z0 += kB) {
@@ -497,8 +512,6 @@ __global__ __launch_bounds__(kDh) void joint_attn_merge(AttnParams p, int nsplit
 // c ^ (r & 15), V^T chunk c of row d at c ^ ((d >> 1) & 7).
 // ---------------------------------------------------------------------------
 constexpr int kPfKeys = 64;
-constexpr int kPfWaves = 4;
-constexpr int kPfQueries = 32 * kPfWaves;
 constexpr int kPfStageElems = kPfKeys * kDh + kDh * kPfKeys;  // K tile + V^T tile
 
 __device__ __forceinline__ int pf_kswz(int key, int c) { return c ^ (key & 15); }
@@ -553,7 +566,11 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
     __shared__ __align__(16) uint16_t st1[kPfStageElems];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, hl = lane >> 5;
-    const int64_t h = blockIdx.x, q0 = (int64_t) blockIdx.y * kPfQueries;
+    // Work of this workgroup: head h, queries from q0 (and key range
+    // blockIdx.z with SPLIT).
+    const int64_t unit = p.unit0 + blockIdx.x;
+    const int64_t h = p.units ? unit % p.heads : (int64_t) blockIdx.x;
+    const int64_t q0 = (p.units ? unit / p.heads : (int64_t) blockIdx.y) * kPfQueries;
     const int nblk_a = (int) ((p.seg_len[0] + kPfKeys - 1) / kPfKeys);
     const int nblk = nblk_a + (int) ((p.seg_len[1] + kPfKeys - 1) / kPfKeys);
     const int b_begin = SPLIT ? (int) blockIdx.z * (int) p.split_blocks : 0;
@@ -682,10 +699,11 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
 
     if constexpr (SPLIT) {
         // Unnormalised O^T with its running max (log2 domain) and sum, for
-        // joint_attn_merge: part_o [split][head][query][dh].
-        const int64_t qi = q0 + 32 * wave + l32;
+        // joint_attn_merge: part_o [split][head][query][dh] (unit-mapped:
+        // [split][workgroup][query of the block][dh]).
+        const int64_t z = blockIdx.z, qi = q0 + 32 * wave + l32;
         if (qi < p.tq) {
-            const int64_t pi = ((int64_t) blockIdx.z * p.heads + h) * p.tq + qi;
+            const int64_t pi = p.units ? (z * p.units + blockIdx.x) * kPfQueries + (qi - q0) : (z * p.heads + h) * p.tq + qi;
             if (hl == 0) {
                 p.part_m[pi] = m_run;
                 p.part_l[pi] = l_run;
@@ -1021,6 +1039,19 @@ constexpr int64_t kSplitBlocks = 8;   // key blocks (of 32) per split workgroup
 constexpr int64_t kMaxSplits = 32;
 constexpr int64_t kFlashSplitBlocks = 4;  // 64-key blocks per split of the LDS-tiled decode
 constexpr int kSplitWaves = 4;
+// Compute units of the current device, per device.
+static int device_cus() {
+    static int cus[64] = {0};
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 0;
+    if (!cus[d]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess) n = 0;
+        cus[d] = n > 0 ? n : -1;
+    }
+    return cus[d] > 0 ? cus[d] : 0;
+}
+
 hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     if (a.head_dim != kDh) return hipErrorInvalidValue;
     if (a.tq <= 0) return hipSuccess;
@@ -1058,6 +1089,35 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
                        ((uintptr_t) p.out & 15) == 0;
     if (flash && a.tq > 64 && p.seg_len[1] == 0) {
         const int64_t qblocks = (a.tq + kPfQueries - 1) / kPfQueries;
+        // The (head, query block) units fill rounds of two workgroups per CU.
+        // When the last round would run at most a quarter full (3072 queries
+        // x 24 heads: 576 units on 512 slots), its units are split into key
+        // ranges that fill it instead, with their partials merged after.
+        // Sources of fewer than 16 blocks (the 512-key prompt) keep the plain
+        // grid: their ranges would be one or two blocks long.
+        const int64_t units = a.heads * qblocks, slots = 2 * (int64_t) device_cus();
+        const int64_t tail = slots > 0 ? units % slots : 0;
+        const int64_t nblk = (p.seg_len[0] + kPfKeys - 1) / kPfKeys;
+        if (units > slots && tail > 0 && 4 * tail <= slots && nblk >= 16) {
+            int64_t nsplit = std::min<int64_t>({slots / tail, nblk / 2, (int64_t) kMaxSplits});
+            p.split_blocks = (nblk + nsplit - 1) / nsplit;
+            nsplit = (nblk + p.split_blocks - 1) / p.split_blocks;
+            const size_t rows = (size_t) tail * kPfQueries;
+            if (nsplit >= 2 && a.ws && (size_t) nsplit * rows * (kDh + 2) * sizeof(float) <= a.ws_bytes) {
+                p.unit0 = 0;
+                p.units = units - tail;
+                hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3((unsigned) p.units), dim3(kPfWaves * 64), 0, s, p);
+                p.unit0 = units - tail;
+                p.units = tail;
+                p.part_o = (float *) a.ws;
+                p.part_m = p.part_o + (size_t) nsplit * rows * kDh;
+                p.part_l = p.part_m + (size_t) nsplit * rows;
+                hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3((unsigned) tail, 1, (unsigned) nsplit),
+                                   dim3(kPfWaves * 64), 0, s, p);
+                hipLaunchKernelGGL(joint_attn_merge, dim3((unsigned) rows), dim3(kDh), 0, s, p, (int) nsplit);
+                return hipGetLastError();
+            }
+        }
         hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3((unsigned) a.heads, (unsigned) qblocks),
                            dim3(kPfWaves * 64), 0, s, p);
         return hipGetLastError();
