@@ -529,6 +529,14 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_dma(GemmParams p, int 
     __shared__ __align__(16) uint16_t st1[E];
     __shared__ __align__(16) uint16_t st2[S > 2 ? E : 8];
     __shared__ __align__(16) uint16_t st3[S > 3 ? E : 8];
+    // Batches along blockIdx.y (run_dma_splitk: K slices, each into its own
+    // f32 partial plane): x, w and y advance by their batch strides.
+    if (blockIdx.y) {
+        const int64_t z = blockIdx.y;
+        p.x = (const uint16_t *) p.x + z * p.x_bs2;
+        p.w += z * p.w_bs2;
+        p.y = (char *) p.y + z * p.y_bs2 * (p.y_type == WAMX_TYPE_F32 ? 4 : 2);
+    }
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave / WN, wc = wave % WN;
@@ -1569,6 +1577,74 @@ static hipError_t run_dma_pipe(const GemmParams & p, hipStream_t s) {
 
 static int64_t tiles_of(const GemmParams & p, int bm, int bn) { return ((p.N + bm - 1) / bm) * ((p.M + bn - 1) / bn); }
 
+// Compute units of the current device, per device.
+static int device_cus() {
+    static int cus[64] = {0};
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 0;
+    if (!cus[d]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess) n = 0;
+        cus[d] = n > 0 ? n : -1;
+    }
+    return cus[d] > 0 ? cus[d] : 0;
+}
+
+// Split-K for the 128 x 128 tiles (two workgroups per CU) when the tiles
+// alone fill few of the CUs' slots: 384 tokens (eight 48-token chunks) x 3072
+// features makes 72 tiles for 512 slots.  Returns the number of K slices (1:
+// no split): the divisor s of K/64 that fills the slots best, if that beats
+// the unsplit grid by a fifth of the slots, with at least 4 k-steps per slice
+// and the s f32 partial planes within the workspace.
+static int dma_splitk_plan(const GemmParams & p, size_t ws_bytes) {
+    const int64_t tiles = tiles_of(p, 128, 128), slots = 2 * (int64_t) device_cus(), kb = p.K / 64;
+    if (slots <= 0 || tiles >= slots || p.K % 64 != 0) return 1;
+    auto fill = [&](int64_t sp) {
+        const int64_t w = tiles * sp;
+        return (double) w / (double) (slots * ((w + slots - 1) / slots));
+    };
+    int best = 1;
+    double best_fill = fill(1);
+    for (int sp = 2; sp <= 16; ++sp) {
+        if (kb % sp != 0 || kb / sp < 4 || (size_t) sp * p.N * p.M * sizeof(float) > ws_bytes) continue;
+        const double f = fill(sp);
+        if (f > best_fill + 0.2 * (best == 1) && f > best_fill) {
+            best = sp;
+            best_fill = f;
+        }
+    }
+    return best;
+}
+
+// K split over blockIdx.y of gemm_dma<128, 128>: slice z multiplies K columns
+// [z*K/s, (z+1)*K/s) into f32 partial plane z of ws, then gemm_skinny_reduce
+// sums the planes in slice order (deterministic) and applies the epilogue.
+static hipError_t run_dma_splitk(const GemmParams & p, int splits, void * ws, hipStream_t s) {
+    GemmParams q = p;
+    const int64_t ks = p.K / splits;
+    q.K = ks;
+    q.x_bs2 = ks;
+    q.w_bs2 = ks;
+    q.y = ws;
+    q.y_type = WAMX_TYPE_F32;
+    q.ldy = p.M;
+    q.y_bs2 = p.N * p.M;
+    q.epi = WAMX_EPI_NONE;
+    q.vec_out = 0;
+    const int nt_m = (int) ((p.M + 127) / 128), nt_n = (int) ((p.N + 127) / 128);
+    constexpr int occ = dma_occupancy<128, 128, 2, 2, 64, 2>();
+    hipLaunchKernelGGL((gemm_dma<128, 128, 2, 2, 64, 2, occ>), dim3((unsigned) (nt_m * nt_n), (unsigned) splits),
+                       dim3(256), 0, s, q, nt_m, nt_n);
+    const int64_t total = p.N * p.M;
+    if (p.M % 4 == 0)
+        hipLaunchKernelGGL(gemm_skinny_reduce<4>, dim3((unsigned) ((total / 4 + 255) / 256)), dim3(256), 0, s, p,
+                           (const float *) ws, splits);
+    else
+        hipLaunchKernelGGL(gemm_skinny_reduce<1>, dim3((unsigned) ((total + 255) / 256)), dim3(256), 0, s, p,
+                           (const float *) ws, splits);
+    return hipGetLastError();
+}
+
 // Tile shape of the bf16 x bf16 DMA path, chosen so the grid fills the 256 CUs
 // (measured on the 3072-token products of the prefix pass):
 //  * 256 x 256, 8 waves: when it gives at least one tile per CU (QKV 9216 x
@@ -1581,15 +1657,19 @@ static int64_t tiles_of(const GemmParams & p, int bm, int bn) { return ((p.N + b
 //  * 128 x 128, BK 64, 2 stages, 4 waves, two workgroups per CU: small grids
 //    (512-token prompt projections).
 // Returns false when the shape does not meet the path's preconditions.
-static bool dispatch_dma(const GemmParams & p, hipStream_t s, hipError_t & err) {
+static bool dispatch_dma(const GemmParams & p, void * ws, size_t ws_bytes, hipStream_t s, hipError_t & err) {
     if (p.K % 32 != 0) return false;
     if (tiles_of(p, 256, 256) >= 256) {
         err = run_dma_pipe<256, 256, 4, 2, 4, 32, 3, kSchedPingPong>(p, s);
         return true;
     }
     if (p.K % 64 != 0) return false;
-    if (tiles_of(p, 192, 192) >= 192) err = run_dma_pipe<192, 192, 2, 2, 4, 64, 3, kSchedProducer>(p, s);
-    else err = run_dma<128, 128, 2, 2, 64, 2>(p, s);
+    if (tiles_of(p, 192, 192) >= 192) {
+        err = run_dma_pipe<192, 192, 2, 2, 4, 64, 3, kSchedProducer>(p, s);
+        return true;
+    }
+    const int splits = ws && ((uintptr_t) ws & 15) == 0 ? dma_splitk_plan(p, ws_bytes) : 1;
+    err = splits > 1 ? run_dma_splitk(p, splits, ws, s) : run_dma<128, 128, 2, 2, 64, 2>(p, s);
     return true;
 }
 
@@ -1765,7 +1845,7 @@ hipError_t launch_gemm(const GemmArgs & a, hipStream_t s) {
     }
     if (vec && !xf32 && batches == 1) {
         hipError_t err = hipSuccess;
-        if (dispatch_dma(p, s, err)) return err;
+        if (dispatch_dma(p, a.ws, a.ws_bytes, s, err)) return err;
     }
     if (vec) return xf32 ? run_tile<128, 128, 2, 2, true, true>(p, batches, s) : run_tile<128, 128, 2, 2, false, true>(p, batches, s);
     return xf32 ? run_tile<128, 128, 2, 2, true, false>(p, batches, s) : run_tile<128, 128, 2, 2, false, false>(p, batches, s);
