@@ -445,12 +445,16 @@ __global__ __launch_bounds__(NW * 64) void joint_attn_kernel(AttnParams p) {
     }
 }
 
-// Combines the key-split partials of one (head, query) per 128-thread
-// workgroup, splits in order: m* = max m_z, l* = sum l_z 2^(m_z - m*),
-// out = sum o_z 2^(m_z - m*) / l*.
-// All loads of a batch of eight splits are issued before they are combined.
-__global__ __launch_bounds__(kDh) void joint_attn_merge(AttnParams p, int nsplit) {
-    int64_t hq = blockIdx.x, h = hq / p.tq, q = hq % p.tq, stride = p.heads * p.tq;
+// Combines the key-split partials of (head, query) rows, splits in order:
+// m* = max m_z, l* = sum l_z 2^(m_z - m*), out = sum o_z 2^(m_z - m*) / l*.
+// A workgroup takes kMergeRows rows, 32 lanes per row and 4 head dims per
+// lane (16-byte partial loads, 8-byte output stores); all loads of a batch of
+// eight splits are issued before they are combined.
+constexpr int kMergeRows = 8;
+__global__ __launch_bounds__(32 * kMergeRows) void joint_attn_merge(AttnParams p, int nsplit, int64_t rows) {
+    const int64_t hq = (int64_t) blockIdx.x * kMergeRows + (threadIdx.x >> 5);
+    if (hq >= rows) return;
+    int64_t h = hq / p.tq, q = hq % p.tq, stride = p.heads * p.tq;
     if (p.units) {  // row hq = query hq % 128 of unit unit0 + hq / 128
         const int64_t u = p.unit0 + hq / kPfQueries;
         h = u % p.heads;
@@ -458,7 +462,7 @@ __global__ __launch_bounds__(kDh) void joint_attn_merge(AttnParams p, int nsplit
         stride = p.units * kPfQueries;
         if (q >= p.tq) return;
     }
-    const int d = threadIdx.x;
+    const int d = 4 * (threadIdx.x & 31);
     constexpr int kB = 8;
     float mstar = -INFINITY;
     for (int z0 = 0; z0 < nsplit; z0 += kB) {
@@ -468,25 +472,32 @@ __global__ __launch_bounds__(kDh) void joint_attn_merge(AttnParams p, int nsplit
 #pragma unroll
         for (int u = 0; u < kB; ++u) mstar = fmaxf(mstar, m[u]);
     }
-    float l = 0.0f, o = 0.0f;
+    float l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int z0 = 0; z0 < nsplit; z0 += kB) {
-        float m[kB], lz[kB], oz[kB];
+        float m[kB], lz[kB];
+        float4 oz[kB];
 #pragma unroll
         for (int u = 0; u < kB; ++u) {
             const int64_t z = min(z0 + u, nsplit - 1);
             m[u] = p.part_m[z * stride + hq];
             lz[u] = p.part_l[z * stride + hq];
-            oz[u] = p.part_o[(z * stride + hq) * kDh + d];
+            oz[u] = *(const float4 *) (p.part_o + (z * stride + hq) * kDh + d);
         }
 #pragma unroll
         for (int u = 0; u < kB; ++u) {
             if (z0 + u >= nsplit || m[u] == -INFINITY) continue;
             const float w = exp2f(m[u] - mstar);
             l += lz[u] * w;
-            o += oz[u] * w;
+            o[0] += oz[u].x * w;
+            o[1] += oz[u].y * w;
+            o[2] += oz[u].z * w;
+            o[3] += oz[u].w * w;
         }
     }
-    out_row(p, h, q)[d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
+    uint2 out;
+    out.x = pack_bf16x2(l > 0.0f ? o[0] / l : 0.0f, l > 0.0f ? o[1] / l : 0.0f);
+    out.y = pack_bf16x2(l > 0.0f ? o[2] / l : 0.0f, l > 0.0f ? o[3] / l : 0.0f);
+    *(uint2 *) (out_row(p, h, q) + d) = out;
 }
 
 
@@ -1114,7 +1125,8 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
                 p.part_l = p.part_m + (size_t) nsplit * rows;
                 hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3((unsigned) tail, 1, (unsigned) nsplit),
                                    dim3(kPfWaves * 64), 0, s, p);
-                hipLaunchKernelGGL(joint_attn_merge, dim3((unsigned) rows), dim3(kDh), 0, s, p, (int) nsplit);
+                hipLaunchKernelGGL(joint_attn_merge, dim3((unsigned) ((rows + kMergeRows - 1) / kMergeRows)),
+                                   dim3(32 * kMergeRows), 0, s, p, (int) nsplit, (int64_t) rows);
                 return hipGetLastError();
             }
         }
@@ -1180,7 +1192,9 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
             p.part_l = p.part_m + (size_t) nsplit * a.heads * a.tq;
             hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3((unsigned) a.heads, 1, (unsigned) nsplit),
                                dim3(kPfWaves * 64), 0, s, p);
-            hipLaunchKernelGGL(joint_attn_merge, dim3((unsigned) (a.heads * a.tq)), dim3(kDh), 0, s, p, (int) nsplit);
+            const int64_t rows = a.heads * a.tq;
+            hipLaunchKernelGGL(joint_attn_merge, dim3((unsigned) ((rows + kMergeRows - 1) / kMergeRows)),
+                               dim3(32 * kMergeRows), 0, s, p, (int) nsplit, rows);
             return hipGetLastError();
         }
     }
@@ -1212,7 +1226,9 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     p.part_l = p.part_m + (size_t) nsplit * a.heads * a.tq;
     hipLaunchKernelGGL((joint_attn_kernel<1, kSplitWaves, true>),
                        dim3((unsigned) a.heads, (unsigned) qgroups, (unsigned) nsplit), dim3(kSplitWaves * 64), 0, s, p);
-    hipLaunchKernelGGL(joint_attn_merge, dim3((unsigned) (a.heads * a.tq)), dim3(kDh), 0, s, p, (int) nsplit);
+    const int64_t rows = a.heads * a.tq;
+    hipLaunchKernelGGL(joint_attn_merge, dim3((unsigned) ((rows + kMergeRows - 1) / kMergeRows)),
+                       dim3(32 * kMergeRows), 0, s, p, (int) nsplit, rows);
     return hipGetLastError();
 }
 
