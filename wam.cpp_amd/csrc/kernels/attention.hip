@@ -1001,31 +1001,41 @@ __global__ __launch_bounds__(kPfWaves * 64, S == 2 ? 2 : 1) void attn_decode_ker
 // out = sum o_z 2^(m_z - m*) / l*.  Every partial is requested before the
 // first is combined (nsplit <= MAXS), so the merge costs one memory latency.
 template <int MAXS>
-__global__ __launch_bounds__(kDh) void attn_merge_kernel(AttnParams p, int nsplit) {
-    const int64_t hq = blockIdx.x;
-    const int d = threadIdx.x;
-    const int64_t h = hq / p.tq, q = hq % p.tq, stride = p.heads * p.tq;
-    float m[MAXS], lz[MAXS], oz[MAXS];
+__global__ __launch_bounds__(32 * kMergeRows) void attn_merge_kernel(AttnParams p, int nsplit) {
+    // kMergeRows (head, query) rows per workgroup, 32 lanes per row, 4 head
+    // dims per lane: 16-byte partial loads, all issued before they combine.
+    const int64_t hq = (int64_t) blockIdx.x * kMergeRows + (threadIdx.x >> 5), stride = p.heads * p.tq;
+    if (hq >= stride) return;
+    const int d = 4 * (threadIdx.x & 31);
+    const int64_t h = hq / p.tq, q = hq % p.tq;
+    float m[MAXS], lz[MAXS];
+    float4 oz[MAXS];
 #pragma unroll
     for (int u = 0; u < MAXS; ++u) {
         const int64_t z = min(u, nsplit - 1);
         m[u] = p.part_m[z * stride + hq];
         lz[u] = p.part_l[z * stride + hq];
-        oz[u] = p.part_o[(z * stride + hq) * kDh + d];
+        oz[u] = *(const float4 *) (p.part_o + (z * stride + hq) * kDh + d);
     }
     float mstar = -INFINITY;
 #pragma unroll
     for (int u = 0; u < MAXS; ++u)
         if (u < nsplit) mstar = fmaxf(mstar, m[u]);
-    float l = 0.0f, o = 0.0f;
+    float l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < MAXS; ++u) {
         if (u >= nsplit || m[u] == -INFINITY) continue;
         const float w = __builtin_amdgcn_exp2f(m[u] - mstar);
         l += lz[u] * w;
-        o += oz[u] * w;
+        o[0] += oz[u].x * w;
+        o[1] += oz[u].y * w;
+        o[2] += oz[u].z * w;
+        o[3] += oz[u].w * w;
     }
-    out_row(p, h, q)[d] = f32_to_bf16(l > 0.0f ? o / l : 0.0f);
+    uint2 out;
+    out.x = pack_bf16x2(l > 0.0f ? o[0] / l : 0.0f, l > 0.0f ? o[1] / l : 0.0f);
+    out.y = pack_bf16x2(l > 0.0f ? o[2] / l : 0.0f, l > 0.0f ? o[3] / l : 0.0f);
+    *(uint2 *) (out_row(p, h, q) + d) = out;
 }
 constexpr int kDecMaxSplits = 32;
 // About one workgroup per CU in all: more ranges shorten each workgroup's
@@ -1167,7 +1177,7 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
             case 3: hipLaunchKernelGGL((attn_decode_kernel<3, 2>), grid, block, 0, s, p); break;
             default: hipLaunchKernelGGL((attn_decode_kernel<4, 4>), grid, block, 0, s, p); break;
         }
-        const dim3 mgrid((unsigned) (a.heads * a.tq)), mblock(kDh);
+        const dim3 mgrid((unsigned) ((a.heads * a.tq + kMergeRows - 1) / kMergeRows)), mblock(32 * kMergeRows);
         if (nsplit > 16) hipLaunchKernelGGL(attn_merge_kernel<kDecMaxSplits>, mgrid, mblock, 0, s, p, (int) nsplit);
         else if (nsplit > 8) hipLaunchKernelGGL(attn_merge_kernel<16>, mgrid, mblock, 0, s, p, (int) nsplit);
         else if (nsplit > 1) hipLaunchKernelGGL(attn_merge_kernel<8>, mgrid, mblock, 0, s, p, (int) nsplit);
