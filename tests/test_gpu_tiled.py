@@ -133,6 +133,35 @@ def test_integer_products_exact(wx, be, M, K, N):
         B.close()
 
 
+@pytest.mark.parametrize("M,K,N", [(14336, 3072, 48), (14336, 3072, 1), (12288, 4096, 17), (14336, 2048, 33),
+                                   (14336, 3072, 64)])
+def test_integer_products_bf16_out_exact(wx, be, M, K, N):
+    """bf16 outputs of tiled few-token products with at least 192 groups of 64
+    features: the K split over the waves of one workgroup (gemm_skinny_wk).
+    The fp32 sums of small-integer products are exact, so the bf16 output
+    equals the RNE rounding of the exact product."""
+    print(f"tiled integer product, bf16 out, M={M} K={K} N={N}", flush=True)
+    lib = be.lib
+    rng = np.random.default_rng(M + 5 * K + 11 * N)
+    w = rng.integers(-4, 5, (M, K))
+    x = rng.integers(-4, 5, (N, K))
+    B = Bufs(wx, be)
+    try:
+        wt = B.tiled(K, M)
+        xt = B.plain(wx.TYPE_BF16, K, N)
+        y = lib.wamx_mul_mat_out_type(B.pctx, wt, xt, wx.TYPE_BF16)
+        B.alloc()
+        B.set(wt, wx.f32_to_bf16(w.astype(np.float32)))
+        B.set(xt, wx.f32_to_bf16(x.astype(np.float32)))
+        for rep in range(2):
+            B.compute(y)
+            got = B.get(y, np.uint16, (N, M))
+            ref = wx.f32_to_bf16((x @ w.T).astype(np.float32))
+            assert np.array_equal(got, ref), f"launch {rep}: {np.count_nonzero(got != ref)} outputs differ"
+    finally:
+        B.close()
+
+
 @pytest.mark.parametrize("epi", ["gelu", "gated"])
 def test_linear_and_fused_reduce_match_row_major(wx, be, rng, epi):
     """The same LINEAR (and LINEAR -> adaLN norm, which runs fused) with the

@@ -1289,6 +1289,89 @@ __device__ __forceinline__ void epi_apply(const EpiIn<E> & in, const float (&acc
     }
 }
 
+// gemm_skinny_wk: few-token product on MFMA-tiled weights with the K split
+// over the waves of one workgroup instead of over workgroups, so the output
+// (with its epilogue) is written directly: no fp32 partials, no reduce launch.
+// For products no row op follows (the action expert's FFN-up + GELU).
+//   Workgroup: 8 waves x kWkGroups 16-row groups (64 features); wave w takes
+//   K/32/8 consecutive k-tiles of every group.  Weight tiles and activation
+//   fragments (straight from memory: the 48 x K activations stay in L2) are
+//   loaded D k-tiles ahead.  The waves' accumulators meet in LDS and are
+//   summed in wave order (deterministic); one thread per (token, 8 features)
+//   applies the epilogue and writes 16 bytes.
+constexpr int kWkWaves = 8, kWkGroups = 4, kWkDepth = 4;
+
+template <int NT, int E>
+__global__ __launch_bounds__(kWkWaves * 64) void gemm_skinny_wk(GemmParams p) {
+    __shared__ __align__(16) float red[kWkWaves][kWkGroups * NT * 4 * 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int64_t kt = p.K / 32, grp0 = (int64_t) blockIdx.x * kWkGroups;
+    const int ktw = (int) (kt / kWkWaves);
+    const int64_t kt0 = (int64_t) wave * ktw;
+    const uint16_t * wb0 = p.w + (grp0 * kt + kt0) * 512 + lane * 8;
+    const uint16_t * x = (const uint16_t *) p.x;
+    int64_t xoff[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) xoff[t] = min<int64_t>(16 * t + r16, p.N - 1) * p.ldx + kt0 * 32 + 8 * g;
+    uint4 wv[kWkDepth][kWkGroups], xv[kWkDepth][NT];
+    auto load = [&](int kk, uint4 (&w)[kWkGroups], uint4 (&xa)[NT]) {
+        kk = min(kk, ktw - 1);
+#pragma unroll
+        for (int rg = 0; rg < kWkGroups; ++rg) w[rg] = *(const uint4 *) (wb0 + ((int64_t) rg * kt + kk) * 512);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) xa[t] = *(const uint4 *) (x + xoff[t] + kk * 32);
+    };
+#pragma unroll
+    for (int i = 0; i < kWkDepth; ++i) load(i, wv[i], xv[i]);
+    f32x4_t acc[kWkGroups][NT];
+#pragma unroll
+    for (int rg = 0; rg < kWkGroups; ++rg)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[rg][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int kk0 = 0; kk0 < ktw; kk0 += kWkDepth) {
+#pragma unroll
+        for (int i = 0; i < kWkDepth; ++i) {
+#pragma unroll
+            for (int rg = 0; rg < kWkGroups; ++rg)
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    acc[rg][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xv[i][t]),
+                                                                       __builtin_bit_cast(bf16x8_t, wv[i][rg]),
+                                                                       acc[rg][t], 0, 0, 0);
+            load(kk0 + i + kWkDepth, wv[i], xv[i]);
+        }
+    }
+    // Accumulator lane (g, r16), element v: token 16t + 4g + v, feature
+    // 16(grp0 + rg) + r16.  Stored as [rg][t][v][lane] per wave.
+    float * my = red[wave];
+#pragma unroll
+    for (int rg = 0; rg < kWkGroups; ++rg)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) my[((rg * NT + t) * 4 + v) * 64 + lane] = acc[rg][t][v];
+    __syncthreads();
+    if (tid >= kWkGroups * NT * 4 * 4 * 2) return;
+    const int half = tid & 1, gg = (tid >> 1) & 3, v = (tid >> 3) & 3, t = (tid >> 5) % NT, rg = (tid >> 5) / NT;
+    const int64_t n = 16 * t + 4 * gg + v, m = 16 * (grp0 + rg) + 8 * half;
+    if (n >= p.N) return;
+    EpiIn<E> in;
+    epi_load<E>(p, n, m, in);
+    const int base = ((rg * NT + t) * 4 + v) * 64 + 16 * gg + 8 * half;
+    float sum[8];
+#pragma unroll
+    for (int w = 0; w < kWkWaves; ++w) {
+        const float4 a = *(const float4 *) (red[w] + base), b = *(const float4 *) (red[w] + base + 4);
+        const float r[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum[e] = w == 0 ? r[e] : sum[e] + r[e];
+    }
+    float o[8];
+    epi_apply<E>(in, sum, o);
+    *(uint4 *) ((uint16_t *) p.y + n * p.ldy + m) = pack8(o);
+}
+
 // Device copy of the row op (RowPost with the RoPE scales precomputed).
 struct RowSegDev {
     int32_t kind, rope_mode;
@@ -1498,7 +1581,44 @@ static void launch_skinny_part(const GemmParams & p, bool xf32, bool tiled, floa
 #undef WAMX_SKINNY
 }
 
+// WAMX_DISABLE_SKINNY_WK=1 keeps the split-K path for these products (read at
+// every launch, so one process can compare the two).
+static bool skinny_wk_enabled() {
+    const char * e = getenv("WAMX_DISABLE_SKINNY_WK");
+    return !(e && e[0] && e[0] != '0');
+}
+
+// Whether gemm_skinny_wk takes the product: tiled weights, bf16 activations
+// and output with the vector epilogue, 64-feature groups filling most of the
+// CUs, and whole k-tile steps per wave.
+static bool skinny_wk_ok(const GemmParams & p, bool xf32, bool tiled) {
+    const int64_t kt = p.K / 32;
+    return tiled && !xf32 && p.vec_out && epi_kind(p) != kEpiF32 && p.N <= 64 && p.M % (16 * kWkGroups) == 0 &&
+           p.M / (16 * kWkGroups) >= 192 && p.K % 32 == 0 && kt % kWkWaves == 0 && (kt / kWkWaves) % kWkDepth == 0;
+}
+
+template <int NT>
+static void launch_skinny_wk(const GemmParams & p, hipStream_t s) {
+    const dim3 grid((unsigned) (p.M / (16 * kWkGroups))), block(kWkWaves * 64);
+    switch (epi_kind(p)) {
+        case kEpiBias: hipLaunchKernelGGL((gemm_skinny_wk<NT, kEpiBias>), grid, block, 0, s, p); break;
+        case kEpiBiasGelu: hipLaunchKernelGGL((gemm_skinny_wk<NT, kEpiBiasGelu>), grid, block, 0, s, p); break;
+        case kEpiBiasGated: hipLaunchKernelGGL((gemm_skinny_wk<NT, kEpiBiasGated>), grid, block, 0, s, p); break;
+        case kEpiBiasResidual: hipLaunchKernelGGL((gemm_skinny_wk<NT, kEpiBiasResidual>), grid, block, 0, s, p); break;
+        default: hipLaunchKernelGGL((gemm_skinny_wk<NT, kEpiBf16>), grid, block, 0, s, p); break;
+    }
+}
+
 static hipError_t run_skinny(const GemmParams & p, bool xf32, bool tiled, void * ws, size_t ws_bytes, hipStream_t s) {
+    if (skinny_wk_ok(p, xf32, tiled) && skinny_wk_enabled()) {
+        switch ((p.N + 15) / 16) {
+            case 1: launch_skinny_wk<1>(p, s); break;
+            case 2: launch_skinny_wk<2>(p, s); break;
+            case 3: launch_skinny_wk<3>(p, s); break;
+            default: launch_skinny_wk<4>(p, s); break;
+        }
+        return hipGetLastError();
+    }
     int splits, ks, waves;
     skinny_plan_for(p, tiled, splits, ks, waves);
     if (splits > 1 && (!ws || (size_t) splits * p.N * p.M * sizeof(float) > ws_bytes || ((uintptr_t) ws & 15)))
