@@ -313,8 +313,8 @@ def workload_chunk(be, args):
             "kernel": "gemm_dma_pipe<256,256>: prefix visual FFN-up 3072 tok x [14336 x 3072] + bias + GELU",
             "kernel_ms": up_ms, "flops_per_launch": flops,
             "algorithmic_bytes": T * D * 2 + F * D * 2 + F * 2 + T * F * 2,
-            "skinny": {"kernel": "gemm_skinny_tiled + gemm_skinny_reduce: denoise FFN-up 48 tok x [14336 x 3072] (tiled) "
-                                 "+ bias + GELU",
+            "skinny": {"kernel": "gemm_skinny_wk: denoise FFN-up 48 tok x [14336 x 3072] (tiled), K split over the "
+                                 "waves of one workgroup, + bias + GELU",
                        "kernel_ms": aup_ms, "achieved_gbs": aup_bytes / (aup_ms * 1e-3) / 1e9,
                        "frac_hbm": aup_bytes / (aup_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": aup_bytes,
                        "traffic": measured_traffic("gemm_skinny_ffn_up")}}
