@@ -1294,11 +1294,16 @@ __device__ __forceinline__ void epi_apply(const EpiIn<E> & in, const float (&acc
 // (with its epilogue) is written directly: no fp32 partials, no reduce launch.
 // For products no row op follows (the action expert's FFN-up + GELU).
 //   Workgroup: 8 waves x kWkGroups 16-row groups (64 features); wave w takes
-//   K/32/8 consecutive k-tiles of every group.  Weight tiles and activation
-//   fragments (straight from memory: the 48 x K activations stay in L2) are
-//   loaded D k-tiles ahead.  The waves' accumulators meet in LDS and are
-//   summed in wave order (deterministic); one thread per (token, 8 features)
-//   applies the epilogue and writes 16 bytes.
+//   k-tiles w, w + 8, w + 16, ... of every group, so at each step the eight
+//   waves read eight adjacent 1 KB tiles of a group (25.1 -> 22.1 us on the
+//   14336 x 3072 FFN-up against K/32/8 consecutive tiles per wave).  Weight
+//   tiles and activation fragments (straight from memory: the 48 x K
+//   activations stay in L2) are written as a D-step prefetch; the optimizer
+//   folds it into loads a few instructions ahead of their MFMAs, which
+//   measured faster than a pinned D-deep schedule of buffer loads.  The
+//   waves' accumulators meet in LDS and are summed in wave order
+//   (deterministic); one thread per (token, 8 features) applies the epilogue
+//   and writes 16 bytes.
 constexpr int kWkWaves = 8, kWkGroups = 4, kWkDepth = 4;
 
 template <int NT, int E>
@@ -1308,7 +1313,7 @@ __global__ __launch_bounds__(kWkWaves * 64) void gemm_skinny_wk(GemmParams p) {
     const int g = lane >> 4, r16 = lane & 15;
     const int64_t kt = p.K / 32, grp0 = (int64_t) blockIdx.x * kWkGroups;
     const int ktw = (int) (kt / kWkWaves);
-    const int64_t kt0 = (int64_t) wave * ktw;
+    const int64_t kt0 = wave;
     const uint16_t * wb0 = p.w + (grp0 * kt + kt0) * 512 + lane * 8;
     const uint16_t * x = (const uint16_t *) p.x;
     int64_t xoff[NT];
@@ -1318,9 +1323,9 @@ __global__ __launch_bounds__(kWkWaves * 64) void gemm_skinny_wk(GemmParams p) {
     auto load = [&](int kk, uint4 (&w)[kWkGroups], uint4 (&xa)[NT]) {
         kk = min(kk, ktw - 1);
 #pragma unroll
-        for (int rg = 0; rg < kWkGroups; ++rg) w[rg] = *(const uint4 *) (wb0 + ((int64_t) rg * kt + kk) * 512);
+        for (int rg = 0; rg < kWkGroups; ++rg) w[rg] = *(const uint4 *) (wb0 + ((int64_t) rg * kt + kk * kWkWaves) * 512);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) xa[t] = *(const uint4 *) (x + xoff[t] + kk * 32);
+        for (int t = 0; t < NT; ++t) xa[t] = *(const uint4 *) (x + xoff[t] + kk * kWkWaves * 32);
     };
 #pragma unroll
     for (int i = 0; i < kWkDepth; ++i) load(i, wv[i], xv[i]);
