@@ -17,6 +17,7 @@
 #include "rowops.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace wamx {
 
@@ -571,11 +572,36 @@ __device__ __forceinline__ void pf_dma(const PfBlk & bl, uint16_t * stage, int w
 }
 constexpr int kPfDmaPerBlock = 8;  // global_load_lds per thread per block
 
+// A full block's copies (pf_dma's slots without the clamping of a source's
+// partial last block): 32-bit byte offsets of this thread's K and V^T chunks
+// from the block's first key row / first V^T column (V^T rows vld apart; the
+// launcher keeps 128 rows within 2^31 bytes) on 64-bit block base addresses.
+__device__ __forceinline__ void pf_dma_full(const PfBlk & bl, uint16_t * stage, int wave, int lane) {
+    const char * kb = (const char *) (bl.kb + bl.k0 * kDh);
+    const char * vb = (const char *) (bl.vb + bl.k0);
+    const uint32_t vld = (uint32_t) bl.vld;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t slot = (uint32_t) ((i * kPfWaves + wave) * 64 + lane), key = slot >> 4;
+        const uint32_t off = (key * kDh + 8 * (uint32_t) pf_kswz((int) key, (int) (slot & 15))) * 2;
+        __builtin_amdgcn_global_load_lds((glb_void_t *) (kb + off),
+                                         (lds_void_t *) (stage + (i * kPfWaves + wave) * 512), 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t slot = (uint32_t) ((i * kPfWaves + wave) * 64 + lane), d = slot >> 3;
+        const uint32_t off = (d * vld + 8 * (uint32_t) pf_vswz((int) d, (int) (slot & 7))) * 2;
+        __builtin_amdgcn_global_load_lds((glb_void_t *) (vb + off),
+                                         (lds_void_t *) (stage + kPfKeys * kDh + (i * kPfWaves + wave) * 512), 16, 0,
+                                         0);
+    }
+}
+
 template <bool SPLIT>
 __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnParams p) {
     __shared__ __align__(16) uint16_t st0[kPfStageElems];
     __shared__ __align__(16) uint16_t st1[kPfStageElems];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, hl = lane >> 5;
     // Work of this workgroup: head h, queries from q0 (and key range
     // blockIdx.z with SPLIT).
@@ -587,7 +613,15 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
     const int b_begin = SPLIT ? (int) blockIdx.z * (int) p.split_blocks : 0;
     const int b_end = SPLIT ? min(nblk, b_begin + (int) p.split_blocks) : nblk;
     auto locate = [&](int blk) { return pf_locate(p, h, nblk_a, blk); };
-    auto dma = [&](int blk, uint16_t * stage) { pf_dma(locate(min(blk, b_end - 1)), stage, wave, lane); };
+    // Copies of block blk into a stage: full blocks by pf_dma_full, a
+    // source's partial last block by pf_dma, which clamps its rows.  Both
+    // issue kPfDmaPerBlock copies.
+    auto dma = [&](int blk, uint16_t * stage) {
+        blk = min(blk, b_end - 1);
+        const PfBlk bl = locate(blk);
+        if (bl.k0 + kPfKeys <= bl.nk) pf_dma_full(bl, stage, wave, lane);
+        else pf_dma(bl, stage, wave, lane);
+    };
 
     // Q^T fragments (B operand of S^T = K Q^T): lane holds query l32 of the
     // wave, dims 16s + 8hl .. +8 for k-step s.
@@ -598,6 +632,15 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
 #pragma unroll
         for (int s = 0; s < 8; ++s) qf[s] = *(const bf16x8_t *) (qrow + 16 * s);
     }
+    // This lane's operand positions in a stage (elements): the K fragment of
+    // k-step s is row l32 of key tile t (t adds 32 rows), chunk 2s + hl; the
+    // V^T operand of PV k-step g = 2t + hh is row l32 of dim tile i (i adds
+    // 32 rows), chunk 2g + hl: keys 32t + 16hh + 8hl .. +8.
+    int kro[8], vro[4];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) kro[s] = l32 * kDh + 8 * pf_kswz(l32, 2 * s + hl);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) vro[g] = kPfKeys * kDh + l32 * kPfKeys + 8 * pf_vswz(l32, 2 * g + hl);
 
     f32x16_t o[4];
 #pragma unroll
@@ -605,38 +648,72 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
+    const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
 
     // Softmax state per lane (its query): m_run is the running max of
     // scale*log2(e)*s used as the exponent offset.  It is raised lazily, only
     // when a block's max exceeds it by more than kPfSlack, so most blocks skip
     // rescaling O; probabilities stay <= 2^kPfSlack and O / l is unchanged.
+    //
+    // The block is written out in its issue order, fenced by scheduling
+    // barriers so the LDS reads run ahead of the MFMAs that use them: K
+    // fragments two k-steps per batch with two batches in flight, the S^T
+    // MFMAs (the two key tiles' chains interleaved), the first PV k-step's
+    // V^T reads, the softmax, then per PV k-step the next one's reads and
+    // this one's MFMAs.  A source's partial last block also masks the scores
+    // of keys past its end (a uniform branch around that step only, so the
+    // block body exists once); its V^T columns there are zeroed in the stage
+    // before the block.
     constexpr float kPfSlack = 8.0f;
-    auto block = [&](int blk, const uint16_t * stage, bool partial) __attribute__((always_inline)) {
-        const uint16_t * kt = stage;
-        const uint16_t * vt = stage + kPfKeys * kDh;
-        const PfBlk bl = locate(blk);
-        const int valid = partial ? (int) (bl.nk - bl.k0) : kPfKeys;
-        // S^T tiles: key tile t (32 keys) x the wave's 32 queries.
+    auto block = [&](int valid, const uint16_t * stage) __attribute__((always_inline)) {
+        // S^T tiles: key tile t (32 keys) x the wave's 32 queries.  K
+        // fragments in batches of two k-steps (both tiles), two batches in
+        // flight ahead of the MFMAs.
         f32x16_t sacc[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int v = 0; v < 16; ++v) sacc[t][v] = 0.0f;
-            const uint16_t * krow = kt + (32 * t + l32) * kDh;
+        bf16x8_t kf[2][2][2];  // [batch buffer][k-step of the batch][tile]
+        auto kread = [&](int b, bf16x8_t (&kb)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const bf16x8_t kf = *(const bf16x8_t *) (krow + 8 * pf_kswz(l32, 2 * s + hl));
-                sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sacc[t], 0, 0, 0);
-            }
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) kb[j][t] = *(const bf16x8_t *) (stage + 32 * t * kDh + kro[2 * b + j]);
+        };
+        kread(0, kf[0]);
+        kread(1, kf[1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[b & 1][j][t], qf[2 * b + j], sacc[t], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (b + 2 < 4) kread(b + 2, kf[b & 1]);
         }
+        // V^T operands of PV k-step g = 2t + hh (dim tile i), one k-step read
+        // ahead.
+        uint4 vbuf[2][4];
+        auto vread = [&](int g, uint4 (&vb)[4]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vb[i] = *(const uint4 *) (stage + 32 * i * kPfKeys + vro[g]);
+        };
+        vread(0, vbuf[0]);
+        __builtin_amdgcn_sched_barrier(0);
         // Lane holds query l32, keys 32t + 8(v/4) + 4hl + v%4; the other keys
         // of its query are in lane ^ 32.
-        if (partial) {
+        if (valid < kPfKeys) {
+            // Scores of keys >= valid to -inf (bit masks, computed in place).
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    if (32 * t + 8 * (v >> 2) + 4 * hl + (v & 3) >= valid) sacc[t][v] = -INFINITY;
+                for (int v = 0; v < 16; ++v) {
+                    const uint32_t m = (uint32_t) ((valid - 1 - (32 * t + 8 * (v >> 2) + 4 * hl + (v & 3))) >> 31);
+                    sacc[t][v] = __uint_as_float((__float_as_uint(sacc[t][v]) & ~m) | (0xff800000u & m));
+                }
         }
         float mx = sacc[0][0];
 #pragma unroll
@@ -655,9 +732,9 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
                 for (int v = 0; v < 16; ++v) o[i][v] *= corr;
         }
         // P = bf16(2^(scale*log2e*s - m)), packed in pairs for the PV operand;
-        // the row sum adds the rounded values.
+        // the row sum adds the rounded values (a bf16 dot with 1.0 per pair).
         uint32_t pk[2][8];
-        float ps = 0.0f;
+        float ps[2] = {0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -665,39 +742,50 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
                 const float e0 = __builtin_amdgcn_exp2f(fmaf(sacc[t][2 * j], p.scale_log2, -m_run));
                 const float e1 = __builtin_amdgcn_exp2f(fmaf(sacc[t][2 * j + 1], p.scale_log2, -m_run));
                 pk[t][j] = pack_bf16x2(e0, e1);
-                ps += __uint_as_float(pk[t][j] << 16) + __uint_as_float(pk[t][j] & 0xffff0000u);
+                ps[t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk[t][j]), ones, ps[t], false);
             }
-        l_run += sum_xor32(ps);
-        // O^T += V^T P^T, k-step (t, hh): key slots 0-3 = keys 32t+16hh+4hl+{0..3},
-        // slots 4-7 = keys 32t+16hh+8+4hl+{0..3}.
+        l_run += sum_xor32(ps[0] + ps[1]);
+        // O^T += V^T P^T, k-step g = (t, hh) over keys 32t + 16hh + 0..15:
+        // lane half hl takes key slots 8hl..8hl+7 = keys 32t + 16hh + 8hl ..
+        // +8, one 16-byte V^T chunk.  The S^T layout gives lane half hl keys
+        // 16hh + 4hl + {0..3} (pk[4hh], pk[4hh+1]) and 16hh + 8 + 4hl + {0..3}
+        // (pk[4hh+2], pk[4hh+3]); v_permlane32_swap (upper 32 lanes of the
+        // first operand with lower 32 lanes of the second) trades the middle
+        // two 4-key groups between the halves, so each half holds its 8 keys
+        // in order.
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int g = 0; g < 4; ++g) {
+            const int t = g >> 1, hh = g & 1;
+            if (g + 1 < 4) vread(g + 1, vbuf[(g + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            const auto s0 = __builtin_amdgcn_permlane32_swap(pk[t][4 * hh], pk[t][4 * hh + 2], false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap(pk[t][4 * hh + 1], pk[t][4 * hh + 3], false, false);
+            const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, make_uint4(s0[0], s1[0], s0[1], s1[1]));
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const bf16x8_t pf = __builtin_bit_cast(
-                    bf16x8_t, make_uint4(pk[t][4 * hh], pk[t][4 * hh + 1], pk[t][4 * hh + 2], pk[t][4 * hh + 3]));
-                const int ka = 32 * t + 16 * hh + 4 * hl;  // first key of each 8-byte piece: ka, ka + 8
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int d = 32 * i + l32;
-                    const uint16_t * row = vt + d * kPfKeys;
-                    uint2 a = *(const uint2 *) (row + 8 * pf_vswz(d, ka >> 3) + (ka & 7));
-                    uint2 b = *(const uint2 *) (row + 8 * pf_vswz(d, (ka + 8) >> 3) + ((ka + 8) & 7));
-                    if (partial) {
-                        a = mask4(a, ka, valid);
-                        b = mask4(b, ka + 8, valid);
-                    }
-                    const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, make_uint4(a.x, a.y, b.x, b.y));
-                    o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[i], 0, 0, 0);
-                }
-            }
+            for (int i = 0; i < 4; ++i)
+                o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vbuf[g & 1][i]), pf, o[i],
+                                                               0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
     auto step = [&](int blk, const uint16_t * cur, uint16_t * nxt) __attribute__((always_inline)) {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         cta_barrier();
         if (blk + 1 < b_end) dma(blk + 1, nxt);
         const PfBlk bl = locate(blk);
-        block(blk, cur, bl.k0 + kPfKeys > bl.nk);
+        if (bl.k0 + kPfKeys > bl.nk) {
+            // A source's partial last block: the V^T columns of keys past its
+            // end (clamped or padding data) are zeroed in the stage, so the
+            // masked keys' P = 0 meets V^T = 0, and their scores are masked.
+            const int valid = (int) (bl.nk - bl.k0);
+            uint16_t * vt = (uint16_t *) cur + kPfKeys * kDh;
+            for (int e = tid; e < kDh * kPfKeys; e += kPfWaves * 64) {
+                const int d = e / kPfKeys, key = e % kPfKeys;
+                if (key >= valid) vt[d * kPfKeys + 8 * pf_vswz(d, key >> 3) + (key & 7)] = 0;
+            }
+            __syncthreads();
+        }
+        block((int) min((int64_t) kPfKeys, bl.nk - bl.k0), cur);
     };
 
     dma(b_begin, st0);
@@ -1103,7 +1191,8 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     // Many queries over one key source (the prefix self-attention, the
     // visual cross-attention): the LDS-tiled flash kernel.
     auto flash_ok = [&](int i) {
-        return p.seg_len[i] == 0 || (p.seg_len[i] >= 8 && p.vt_ld[i] % 8 == 0 && ((uintptr_t) p.vt[i] & 15) == 0 &&
+        return p.seg_len[i] == 0 || (p.seg_len[i] >= 8 && p.vt_ld[i] % 8 == 0 && p.vt_ld[i] < (1 << 20) &&
+                                     ((uintptr_t) p.vt[i] & 15) == 0 &&
                                      ((uintptr_t) p.k[i] & 15) == 0);
     };
     const bool flash = flash_ok(0) && flash_ok(1) && p.seg_len[0] > 0 && ((uintptr_t) p.q & 15) == 0 &&
