@@ -1,7 +1,9 @@
 """Row fusion in the graph executor: a LINEAR on a few tokens followed by the
 row ops that consume its output (LayerNorm / adaLN modulation of the residual
 stream; RMSNorm + RoPE of the Q and K column ranges and the V^T copy) runs as
-the skinny GEMM plus one reduce that applies the row ops.  The fused graph
+the skinny GEMM plus one reduce that applies the row ops; on eight 48-token
+chunks (384 rows, the batched denoise step) as the K-sliced 128 x 128 GEMM
+plus the same reduce, with chunk-major Q/K and V^T destinations.  The fused graph
 must produce the same bits as the standalone ops launched one at a time
 (wamx_op_linear, wamx_op_norm_modulation_bf16 / wamx_op_layer_norm_bf16,
 wamx_op_qk_norm_rope and a host transpose for V^T), which the per-op tests
@@ -60,7 +62,7 @@ def data(t):
     return t.contents.data
 
 
-@pytest.mark.parametrize("T", [48, 17, 1])
+@pytest.mark.parametrize("T", [48, 17, 1, 384])
 @pytest.mark.parametrize("kind", ["modulation", "layer_norm"])
 def test_linear_then_norm_is_bit_exact(wx, be, rng, T, kind):
     print(f"fusion linear->norm {kind} T={T}", flush=True)
@@ -164,6 +166,71 @@ def test_qkv_split_is_bit_exact(wx, be, rng, T):
         assert np.array_equal(got_q, ref_q.download(np.uint16, (H, T, DH)))
         assert np.array_equal(got_k, ref_k.download(np.uint16, (H, T, DH)))
         assert np.array_equal(got_vt, rq[:, 2 * D:].reshape(T, H, DH).transpose(1, 2, 0))
+    finally:
+        g.close()
+
+
+def test_qkv_split_chunked_is_bit_exact(wx, be, rng):
+    """Eight chunks of 48 tokens: Q and K into [dh, 48, H, 8], V^T into
+    [pad, dh, H, 8], each chunk's RoPE positions 1..48."""
+    B, Tc = 8, 48
+    T = B * Tc
+    print(f"fusion qkv chunked B={B} Tc={Tc}", flush=True)
+    lib = be.lib
+    g = Graph(wx, be)
+    try:
+        w = g.t(wx.TYPE_BF16, D, 3 * D)
+        x = g.t(wx.TYPE_BF16, D, T)
+        b = g.t(wx.TYPE_BF16, 3 * D)
+        nq, nk = g.t(wx.TYPE_BF16, D), g.t(wx.TYPE_BF16, D)
+        pos = g.t(wx.TYPE_I32, Tc)
+        tpad = 52
+        vraw = g.t(wx.TYPE_BF16, tpad, DH, H, B)
+        qkv = lib.wamx_linear(g.ctx, w, x, b, wx.EPI_BIAS, None, None)
+        pitch = qkv.contents.nb[1]
+        q = lib.wamx_qk_norm_rope(g.ctx, lib.wamx_view_2d(g.ctx, qkv, D, T, pitch, 0), nq,
+                                  g.t(wx.TYPE_BF16, DH, Tc, H, B), 0, 0, pos, None, None, 1e-6, 10000.0)
+        k = lib.wamx_qk_norm_rope(g.ctx, lib.wamx_view_2d(g.ctx, qkv, D, T, pitch, 2 * D), nk,
+                                  g.t(wx.TYPE_BF16, DH, Tc, H, B), 0, 0, pos, None, None, 1e-6, 10000.0)
+        vsrc = lib.wamx_permute(g.ctx, lib.wamx_view_4d(g.ctx, qkv, DH, H, Tc, B, DH * 2, pitch, pitch * Tc, 4 * D),
+                                1, 2, 0, 3)
+        vr = vraw.contents
+        vdst = lib.wamx_view_4d(g.ctx, vraw, Tc, DH, H, B, vr.nb[1], vr.nb[2], vr.nb[3], 0)
+        v = lib.wamx_cpy(g.ctx, vsrc, vdst)
+        g.alloc()
+        hw = wx.f32_to_bf16(rng.standard_normal(3 * D * D).astype(np.float32) * 0.02)
+        hx = wx.f32_to_bf16(rng.standard_normal(D * T).astype(np.float32))
+        hb = wx.f32_to_bf16(rng.standard_normal(3 * D).astype(np.float32) * 0.02)
+        hnq = wx.f32_to_bf16(1.0 + rng.standard_normal(D).astype(np.float32) * 0.1)
+        hnk = wx.f32_to_bf16(1.0 + rng.standard_normal(D).astype(np.float32) * 0.1)
+        hpos = np.arange(1, Tc + 1, dtype=np.int32)
+        for t, a in ((w, hw), (x, hx), (b, hb), (nq, hnq), (nk, hnk), (pos, hpos),
+                     (vraw, np.zeros(tpad * DH * H * B, np.uint16))):
+            g.set(t, a)
+        g.compute(q, k, v)
+        got_qkv = g.get(qkv, np.uint16, (T, 3 * D))
+        got_q = g.get(q, np.uint16, (B, H, Tc, DH))
+        got_k = g.get(k, np.uint16, (B, H, Tc, DH))
+        got_vt = g.get(vraw, np.uint16, (B, H, DH, tpad))[..., :Tc]
+
+        ref_qkv, ref_q, ref_k = be.empty(T * 3 * D * 2), be.empty(Tc * D * 2), be.empty(Tc * D * 2)
+        wx.check(lib.wamx_op_linear(be.ptr, data(w), data(x), wx.TYPE_BF16, data(b), wx.EPI_BIAS, None, None,
+                                    ref_qkv.ptr, 3 * D, T, D))
+        be.sync()
+        rq = ref_qkv.download(np.uint16, (T, 3 * D))
+        assert np.array_equal(got_qkv, rq)
+        pp = C.cast(data(pos), C.POINTER(C.c_int32))
+        for c in range(B):
+            row0 = ref_qkv.ptr + c * Tc * 3 * D * 2
+            wx.check(lib.wamx_op_qk_norm_rope(be.ptr, row0, 3 * D, data(nq), ref_q.ptr, H, DH, Tc, Tc, 0, 0, pp,
+                                              None, None, 1e-6, 10000.0))
+            wx.check(lib.wamx_op_qk_norm_rope(be.ptr, row0 + 2 * D, 3 * D, data(nk), ref_k.ptr, H, DH, Tc, Tc, 0,
+                                              0, pp, None, None, 1e-6, 10000.0))
+            be.sync()
+            assert np.array_equal(got_q[c], ref_q.download(np.uint16, (H, Tc, DH))), f"Q chunk {c}"
+            assert np.array_equal(got_k[c], ref_k.download(np.uint16, (H, Tc, DH))), f"K chunk {c}"
+            vt = rq[c * Tc:(c + 1) * Tc, 2 * D:].reshape(Tc, H, DH).transpose(1, 2, 0)
+            assert np.array_equal(got_vt[c], vt), f"V^T chunk {c}"
     finally:
         g.close()
 

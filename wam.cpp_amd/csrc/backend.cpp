@@ -353,7 +353,9 @@ static bool column_view(const wamx_tensor * x, const wamx_tensor * base, int64_t
 // they cover (> i), or -1.
 static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post, bool lanes) {
     const wamx_tensor * lin = wamx_graph_node(g, i);
-    if (lin->type != WAMX_TYPE_BF16 || lin->ne[1] > 64 || lin->ne[2] != 1 || lin->ne[3] != 1 || lin->view_src)
+    // Up to 64 tokens (the skinny path) or a few chunks of them (the batched
+    // denoise step's K-sliced products); launch_gemm_rowpost refuses the rest.
+    if (lin->type != WAMX_TYPE_BF16 || lin->ne[1] > 512 || lin->ne[2] != 1 || lin->ne[3] != 1 || lin->view_src)
         return -1;
     int j = next_compute(g, i, n, lanes);
     if (j >= n) return -1;
@@ -388,7 +390,9 @@ static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post, bool la
             if (!column_view(x, lin, seg.col) || !t->src[1] || t->type != WAMX_TYPE_BF16) break;
             head_dim = t->ne[0];
             width = x->ne[0];
-            if (width != head_dim * t->ne[2] || t->ne[3] != 1) break;  // one chunk: the reduce has no chunk split
+            if (width != head_dim * t->ne[2] || x->ne[1] % t->ne[3] != 0) break;
+            seg.chunk_tokens = t->ne[3] > 1 ? x->ne[1] / t->ne[3] : 0;  // rows of chunk b at dst + b * nb[3]
+            seg.chunk_stride = (int64_t) t->nb[3] / 2;
             seg.kind = kRowSegQk;
             seg.w = t->src[1]->data;
             seg.dst = t->data;
@@ -409,9 +413,13 @@ static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post, bool la
                 break;
             head_dim = p->ne[1];
             width = head_dim * p->ne[2];
-            if (p->ne[0] != T || p->ne[3] != 1 || p->nb[0] != lin->nb[1] || p->nb[1] != 2 ||
-                p->nb[2] != (size_t) head_dim * 2 || !wamx_are_same_shape(t, p) || t->nb[0] != 2)
+            // Chunks (ne[3] > 1): consecutive row ranges of the product.
+            if (p->ne[0] * p->ne[3] != T || (p->ne[3] > 1 && p->nb[3] != (size_t) p->ne[0] * lin->nb[1]) ||
+                p->nb[0] != lin->nb[1] || p->nb[1] != 2 || p->nb[2] != (size_t) head_dim * 2 ||
+                !wamx_are_same_shape(t, p) || t->nb[0] != 2)
                 break;
+            seg.chunk_tokens = p->ne[3] > 1 ? p->ne[0] : 0;
+            seg.chunk_stride = (int64_t) t->nb[3] / 2;
             if (v->view_offs % 2 != 0 || v->view_offs + (size_t) width * 2 > lin->nb[1]) break;
             seg.kind = kRowSegVt;
             seg.col = (int64_t) (v->view_offs / 2);

@@ -77,6 +77,11 @@ struct RowSeg {
     // kRowSegVt: bf16 copy into dst[h * vt_hs + dd * vt_ld + t] (V^T storage).
     int64_t vt_ld = 0, vt_hs = 0;
     void * dst = nullptr;
+    // Rows of the product in chunks of chunk_tokens (0: one chunk): row n is
+    // token t = n % chunk_tokens of chunk n / chunk_tokens, whose destination
+    // starts chunk_stride elements after the previous chunk's (the RoPE
+    // position is t's).
+    int64_t chunk_tokens = 0, chunk_stride = 0;
 };
 enum { kRowPostNorm = 1, kRowPostSegs = 2 };
 struct RowPost {
@@ -96,7 +101,9 @@ struct RowPost {
     int64_t width = 0, head_dim = 0;
     RowSeg seg[3];
 };
-// The skinny GEMM whose reduce applies `post`.  Returns hipErrorNotSupported,
+// The split-K GEMM whose reduce applies `post`: the skinny part kernel for up
+// to 64 tokens, the K-sliced 128 x 128 DMA GEMM for more tokens on grids
+// that it splits (the batched denoise step).  Returns hipErrorNotSupported,
 // launching nothing, when the product or the row op does not fit that path.
 hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStream_t s);
 

@@ -1380,7 +1380,7 @@ __global__ __launch_bounds__(kWkWaves * 64) void gemm_skinny_wk(GemmParams p) {
 // Device copy of the row op (RowPost with the RoPE scales precomputed).
 struct RowSegDev {
     int32_t kind, rope_mode;
-    int64_t col, dst_tokens, tok0, vt_ld, vt_hs;
+    int64_t col, dst_tokens, tok0, vt_ld, vt_hs, chunk_tokens, chunk_stride;
     const uint16_t * w;
     uint16_t * dst;
     const int32_t *pos0, *pos1, *pos2;
@@ -1425,9 +1425,14 @@ __global__ __launch_bounds__(512) void skinny_reduce_row(GemmParams p, const flo
             load8_f32((const float *) rp.scale + so, a);
             load8_f32((const float *) rp.shift + so, b);
         }
-    } else if (sg.kind == kRowSegQk) {
-        wv = *(const uint4 *) (sg.w + 8 * c);
-        rt = rope_tok(sg.rope_mode, sg.pos0, sg.pos1, sg.pos2, n, sg.l2ts128, sg.l2ts44, sg.l2ts42);
+    }
+    // Chunk of row n and its token within the chunk (segment stores).
+    const int64_t cb = POST == kPostSegs ? n / sg.chunk_tokens : 0, tl = n - cb * (POST == kPostSegs ? sg.chunk_tokens : 0);
+    if constexpr (!kNorm) {
+        if (sg.kind == kRowSegQk) {
+            wv = *(const uint4 *) (sg.w + 8 * c);
+            rt = rope_tok(sg.rope_mode, sg.pos0, sg.pos1, sg.pos2, tl, sg.l2ts128, sg.l2ts44, sg.l2ts42);
+        }
     }
     constexpr int kB = 20;
     float acc[8];
@@ -1454,10 +1459,10 @@ __global__ __launch_bounds__(512) void skinny_reduce_row(GemmParams p, const flo
         const int hd = rp.head_dim, e0 = 8 * c, h = e0 / hd, dd0 = e0 % hd;
         if (sg.kind == kRowSegQk) {
             const float inv_rms = row_inv_rms<1>(v, rp.width, sg.eps, red);
-            *(uint4 *) (sg.dst + ((int64_t) h * sg.dst_tokens + sg.tok0 + n) * hd + dd0) =
+            *(uint4 *) (sg.dst + cb * sg.chunk_stride + ((int64_t) h * sg.dst_tokens + sg.tok0 + tl) * hd + dd0) =
                 qk_chunk(v[0], inv_rms, wv, dd0, rt);
         } else {
-            uint16_t * d = sg.dst + (int64_t) h * sg.vt_hs + sg.tok0 + n;
+            uint16_t * d = sg.dst + cb * sg.chunk_stride + (int64_t) h * sg.vt_hs + sg.tok0 + tl;
 #pragma unroll
             for (int e = 0; e < 8; ++e) d[(int64_t) (dd0 + e) * sg.vt_ld] = f32_to_bf16(v[0][e]);
         }
@@ -1744,7 +1749,7 @@ static int dma_splitk_plan(const GemmParams & p, size_t ws_bytes) {
 // K split over blockIdx.y of gemm_dma<128, 128>: slice z multiplies K columns
 // [z*K/s, (z+1)*K/s) into f32 partial plane z of ws, then gemm_skinny_reduce
 // sums the planes in slice order (deterministic) and applies the epilogue.
-static hipError_t run_dma_splitk(const GemmParams & p, int splits, void * ws, hipStream_t s) {
+static void launch_dma_splitk_parts(const GemmParams & p, int splits, void * ws, hipStream_t s) {
     GemmParams q = p;
     const int64_t ks = p.K / splits;
     q.K = ks;
@@ -1760,6 +1765,9 @@ static hipError_t run_dma_splitk(const GemmParams & p, int splits, void * ws, hi
     constexpr int occ = dma_occupancy<128, 128, 2, 2, 64, 2>();
     hipLaunchKernelGGL((gemm_dma<128, 128, 2, 2, 64, 2, occ>), dim3((unsigned) (nt_m * nt_n), (unsigned) splits),
                        dim3(256), 0, s, q, nt_m, nt_n);
+}
+static hipError_t run_dma_splitk(const GemmParams & p, int splits, void * ws, hipStream_t s) {
+    launch_dma_splitk_parts(p, splits, ws, s);
     const int64_t total = p.N * p.M;
     if (p.M % 4 == 0)
         hipLaunchKernelGGL(gemm_skinny_reduce<4>, dim3((unsigned) ((total / 4 + 255) / 256)), dim3(256), 0, s, p,
@@ -1850,12 +1858,23 @@ hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStre
     const GemmParams p = make_params(a);
     const int E = epi_kind(p);
     if (a.w_type != WAMX_TYPE_BF16 || (a.x_type != WAMX_TYPE_BF16 && a.x_type != WAMX_TYPE_F32) ||
-        a.y_type != WAMX_TYPE_BF16 || a.B2 * a.B3 != 1 || a.N <= 0 || a.N > 64 || a.M <= 0 || a.K <= 0 ||
-        !vec_operands(a) || !p.vec_out || E == kEpiF32 || !a.ws || !aligned16(a.ws))
+        a.y_type != WAMX_TYPE_BF16 || a.B2 * a.B3 != 1 || a.N <= 0 || a.M <= 0 || a.K <= 0 || !vec_operands(a) ||
+        !p.vec_out || E == kEpiF32 || !a.ws || !aligned16(a.ws))
         return hipErrorNotSupported;
     if (a.w_tiled && (p.M % 16 != 0 || p.K % 32 != 0)) return hipErrorNotSupported;
-    int splits, ks, waves;
-    skinny_plan_for(p, a.w_tiled, splits, ks, waves);
+    // More than 64 tokens: only the products that dispatch_dma runs as the
+    // K-sliced 128 x 128 GEMM (its partial planes are the reduce's layout).
+    const bool dma = a.N > 64;
+    int splits = 1, ks = 0, waves = 0;
+    if (dma) {
+        if (a.w_tiled || a.x_type != WAMX_TYPE_BF16 || p.K % 64 != 0 || tiles_of(p, 256, 256) >= 256 ||
+            tiles_of(p, 192, 192) >= 192)
+            return hipErrorNotSupported;
+        splits = dma_splitk_plan(p, a.ws_bytes);
+        if (splits <= 1) return hipErrorNotSupported;
+    } else {
+        skinny_plan_for(p, a.w_tiled, splits, ks, waves);
+    }
     if ((size_t) splits * p.N * p.M * sizeof(float) > a.ws_bytes) return hipErrorNotSupported;
 
     // The row op: one thread per 8-column chunk, the whole row (or segment)
@@ -1910,6 +1929,9 @@ hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStre
             o.pos1 = g.pos1;
             o.pos2 = g.pos2;
             o.eps = g.eps;
+            o.chunk_tokens = g.chunk_tokens > 0 ? g.chunk_tokens : p.N;
+            o.chunk_stride = g.chunk_tokens > 0 ? g.chunk_stride : 0;
+            if (p.N % o.chunk_tokens != 0) return hipErrorNotSupported;
             rope_scales(post.head_dim, g.freq_base, o.l2ts128, o.l2ts44, o.l2ts42);
         }
     } else {
@@ -1917,9 +1939,13 @@ hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStre
     }
     if (nchunk <= 0 || nchunk > 512 || nchunk % 64 != 0) return hipErrorNotSupported;
 
-    allow_skinny_lds();
     const float * part = (const float *) a.ws;
-    launch_skinny_part(p, a.x_type == WAMX_TYPE_F32, a.w_tiled, (float *) a.ws, splits, ks, waves, s);
+    if (dma) {
+        launch_dma_splitk_parts(p, splits, a.ws, s);
+    } else {
+        allow_skinny_lds();
+        launch_skinny_part(p, a.x_type == WAMX_TYPE_F32, a.w_tiled, (float *) a.ws, splits, ks, waves, s);
+    }
     const dim3 grid((unsigned) p.N, (unsigned) nseg), block((unsigned) nchunk);
 #define WAMX_ROW(EK, PK) hipLaunchKernelGGL((skinny_reduce_row<EK, PK>), grid, block, 0, s, p, part, splits, d)
 #define WAMX_ROW_NORM(EK)                                                   \

@@ -144,6 +144,7 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_view_1d": (TensorP, [vp, TensorP, i64, sz]),
         "wamx_view_2d": (TensorP, [vp, TensorP, i64, i64, sz, sz]),
         "wamx_view_3d": (TensorP, [vp, TensorP, i64, i64, i64, sz, sz, sz]),
+        "wamx_view_4d": (TensorP, [vp, TensorP, i64, i64, i64, i64, sz, sz, sz, sz]),
         "wamx_reshape_2d": (TensorP, [vp, TensorP, i64, i64]),
         "wamx_reshape_3d": (TensorP, [vp, TensorP, i64, i64, i64]),
         "wamx_permute": (TensorP, [vp, TensorP, C.c_int, C.c_int, C.c_int, C.c_int]),
