@@ -44,12 +44,14 @@ def gpu_mul_mat(wx, be, w, x, y_type):
 # Shapes cover every kernel and tile configuration of the dispatcher, with
 # ragged edges: skinny (N <= 64), 128x128 / 192x192 / 256x256 LDS-DMA tiles
 # (bf16 activations, K % 32 == 0), the 128x128 tiles with K split into f32
-# partial planes (eight 48-token chunks: 384 tokens; 200 ragged tokens), and
+# partial planes (eight 48-token chunks: 384 tokens; 200 ragged tokens), the
+# 192x192 tiles with the 5-stage ring of long K (FFN-down depth, 14336), and
 # the register-staged tile for the rest.
 @pytest.mark.parametrize("M,N,K", [(64, 48, 256), (96, 1, 136), (200, 64, 3072), (3072, 48, 3072),
                                    (128, 65, 64), (300, 300, 520), (1000, 129, 72), (77, 33, 31),
                                    (3072, 3000, 128), (4096, 4100, 64), (256, 200, 96), (640, 520, 192),
-                                   (3072, 384, 3072), (3072, 384, 14336), (9216, 384, 3072), (1000, 200, 2048)])
+                                   (3072, 384, 3072), (3072, 384, 14336), (9216, 384, 3072), (1000, 200, 2048),
+                                   (3072, 2304, 14336)])
 @pytest.mark.parametrize("xt", ["f32", "bf16"])
 def test_mul_mat_integer_kat_exact(wx, be, M, N, K, xt):
     print(f"mul_mat KAT M={M} N={N} K={K} x={xt}", flush=True)

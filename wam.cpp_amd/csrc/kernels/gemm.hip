@@ -1784,8 +1784,9 @@ static hipError_t run_dma_splitk(const GemmParams & p, int splits, void * ws, hi
 //    3072, FFN-up 14336 x 3072), ping-pong with BK 32 and 4 stages (6-9%
 //    faster than the single-group schedule on both);
 //  * 192 x 192, 4 waves: 3072 x 3072 products, which it cuts into exactly 256
-//    tiles (256 x 256 leaves 112 CUs idle), pipelined with BK 32 and 4 stages,
-//    copies issued by 4 producer waves (2-4% faster on O and FFN-down);
+//    tiles (256 x 256 leaves 112 CUs idle), pipelined with BK 32 and 4 stages
+//    (5 for K >= 8192), copies issued by 4 producer waves (2-4% faster on O
+//    and FFN-down);
 //  (f32 or unaligned outputs take gemm_dma with BK 32 / 64 and 3 stages);
 //  * 128 x 128, BK 64, 2 stages, 4 waves, two workgroups per CU: small grids
 //    (512-token prompt projections).
@@ -1798,7 +1799,10 @@ static bool dispatch_dma(const GemmParams & p, void * ws, size_t ws_bytes, hipSt
     }
     if (p.K % 64 != 0) return false;
     if (tiles_of(p, 192, 192) >= 192) {
-        err = run_dma_pipe<192, 192, 2, 2, 4, 64, 3, kSchedProducer>(p, s);
+        // Long K (FFN-down, 14336): a 5-stage ring, 268-271 against 279-283 us
+        // (same bits); on 3072-deep products 4 stages stay (64.1 against 64.6).
+        if (p.K >= 8192) err = run_dma_pipe<192, 192, 2, 2, 5, 64, 3, kSchedProducer>(p, s);
+        else err = run_dma_pipe<192, 192, 2, 2, 4, 64, 3, kSchedProducer>(p, s);
         return true;
     }
     const int splits = ws && ((uintptr_t) ws & 15) == 0 ? dma_splitk_plan(p, ws_bytes) : 1;
