@@ -1800,7 +1800,8 @@ static bool dispatch_dma(const GemmParams & p, void * ws, size_t ws_bytes, hipSt
     if (p.K % 64 != 0) return false;
     if (tiles_of(p, 192, 192) >= 192) {
         // Long K (FFN-down, 14336): a 5-stage ring, 268-271 against 279-283 us
-        // (same bits); on 3072-deep products 4 stages stay (64.1 against 64.6).
+        // on one box, 278 against 280 (within noise) on another; same bits.
+        // On 3072-deep products 4 stages stay (64.1 against 64.6).
         if (p.K >= 8192) err = run_dma_pipe<192, 192, 2, 2, 5, 64, 3, kSchedProducer>(p, s);
         else err = run_dma_pipe<192, 192, 2, 2, 4, 64, 3, kSchedProducer>(p, s);
         return true;
