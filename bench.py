@@ -267,6 +267,28 @@ def workload_chunk(be, args):
         wamx.check(lib.wamx_gwp_get_action(m, action.ctypes.data), "get_action")
     ms_with_upload = (time.perf_counter() - t0) * 1e3 / args.steps
     upload_bytes = 4 * (state.size + latent.size + prompt.size + noise.size)
+    # The same requests with the projected-prompt cache on, as the reference's
+    # wam-bench --mode steady runs them (apps/wam-bench.cpp:83): after the
+    # first request the prompt upload and the prompt graphs are skipped
+    # (cache.cpp:53-67).  Reported beside `value`, which projects every
+    # request's prompt (--mode raw).
+    wamx.check(lib.wamx_gwp_set_prompt_cache(m, 4), "set_prompt_cache")
+    wamx.check(lib.wamx_gwp_set_inputs(m, state.ctypes.data, latent.ctypes.data, prompt.ctypes.data,
+                                       noise.ctypes.data), "set_inputs")
+    wamx.check(lib.wamx_gwp_predict(m, None), "predict")
+    wamx.check(lib.wamx_gwp_get_action(m, action.ctypes.data), "get_action")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        wamx.check(lib.wamx_gwp_set_inputs(m, state.ctypes.data, latent.ctypes.data, prompt.ctypes.data,
+                                           noise.ctypes.data), "set_inputs")
+        wamx.check(lib.wamx_gwp_predict(m, None), "predict")
+        wamx.check(lib.wamx_gwp_get_action(m, action.ctypes.data), "get_action")
+    ms_steady = (time.perf_counter() - t0) * 1e3 / args.steps
+    hits, misses = C.c_uint64(), C.c_uint64()
+    wamx.check(lib.wamx_gwp_prompt_cache_stats(m, C.byref(hits), C.byref(misses)), "prompt_cache_stats")
+    if hits.value != args.steps:
+        raise RuntimeError(f"projected-prompt cache: {hits.value} hits in {args.steps} repeated requests")
+    wamx.check(lib.wamx_gwp_set_prompt_cache(m, 0), "set_prompt_cache")
     for _ in range(3):
         wamx.check(lib.wamx_gwp_predict(m, C.byref(tm)), "predict")
         phases += np.array([tm.prompt_ms, tm.prefix_ms, tm.denoise_ms]) / 3
@@ -351,6 +373,8 @@ def workload_chunk(be, args):
                        "phase_ms": {"prompt": phases[0], "prefix": phases[1], "denoise": phases[2]},
                        "ms_per_chunk_back_to_back": ms_pipelined,
                        "ms_per_request_with_upload": ms_with_upload, "upload_bytes_per_request": upload_bytes,
+                       "prompt_projection": "every request (wam-bench --mode raw)",
+                       "ms_per_request_steady_prompt_cache": ms_steady,
                        "gemm_mfma_frac": roof["frac"]},
             "roofline": roof, "cpu_baseline": cpu}
 

@@ -565,6 +565,19 @@ WAMX_API wamx_status wamx_gwp_set_inputs(wamx_gwp_t m, const float * state, cons
 /* Run the three graphs (prompt projection, prefix, unrolled denoise). */
 WAMX_API wamx_status wamx_gwp_predict(wamx_gwp_t m, wamx_gwp_timing * timing);
 WAMX_API wamx_status wamx_gwp_run_prompt(wamx_gwp_t m);
+/* Projected-prompt reuse across requests, replacing wam.cpp's
+ * update_projected_prompt_cache (src/models/gwp05/engine/cache.cpp:53-67,
+ * :131) as enabled by ModelOptions::prompt_cache_capacity (include/wam/types.h:193,
+ * default 0; apps/wam-bench.cpp:83 sets 4 in --mode steady, 0 in raw).  With a
+ * nonzero capacity, set_inputs keeps a host copy of the prompt it uploads;
+ * a later request whose prompt has the same bytes skips the prompt upload,
+ * and predict skips the prompt graphs (the prompt K/V caches already hold its
+ * projection).  0 (the default) projects every request's prompt and drops
+ * the copy.  The prefix pass still reads the resident prompt every request. */
+WAMX_API wamx_status wamx_gwp_set_prompt_cache(wamx_gwp_t m, size_t capacity);
+/* Projected-prompt hits and misses counted by set_inputs while enabled
+ * (the reference's projected_prompt_hits / _misses, cache.cpp:61-68). */
+WAMX_API wamx_status wamx_gwp_prompt_cache_stats(wamx_gwp_t m, uint64_t * hits, uint64_t * misses);
 WAMX_API wamx_status wamx_gwp_run_prefix(wamx_gwp_t m);
 WAMX_API wamx_status wamx_gwp_run_denoise(wamx_gwp_t m);
 /* Final action chunks (bf16 state widened to f32) [batch][action_chunk][action_dim]. */

@@ -127,6 +127,46 @@ def test_graph_replay_is_deterministic(wx, be):
         be.lib.wamx_gwp_free(m)
 
 
+def test_projected_prompt_cache(wx, be):
+    """Projected-prompt reuse across requests (cache.cpp:53-67, :131): with a
+    nonzero capacity a request whose prompt has the same bytes as the last
+    projected one skips the prompt graphs, and its action equals, bit for bit,
+    that of a model that projects every prompt; a changed prompt, new weights
+    and a zero capacity all project again."""
+    print("gwp projected-prompt cache", flush=True)
+    lib = be.lib
+    ref = make_model(wx, be, SMALL, seed=21)
+    m = make_model(wx, be, SMALL, seed=21)
+
+    def stats():
+        h, mi = C.c_uint64(), C.c_uint64()
+        wx.check(lib.wamx_gwp_prompt_cache_stats(m, C.byref(h), C.byref(mi)), "stats")
+        return h.value, mi.value
+
+    try:
+        wx.check(lib.wamx_gwp_set_prompt_cache(m, 4), "set_prompt_cache")
+        a, b = inputs(SMALL, seed=5), inputs(SMALL, seed=9)
+        a_other = (b[0], b[1], a[2], b[3])  # prompt a, everything else from b
+        expect = [(0, 1), (1, 1), (1, 2), (2, 2)]
+        for req, st in zip((a, a_other, b, b), expect):
+            got = run_gpu(wx, be, m, req)
+            assert np.array_equal(got, run_gpu(wx, be, ref, req))
+            assert stats() == st
+        # New weights: the caches no longer hold the prompt's projection.
+        for x in (m, ref):
+            wx.check(lib.wamx_gwp_init_synthetic(x, 0x77, 0.02), "init_synthetic")
+        assert np.array_equal(run_gpu(wx, be, m, b), run_gpu(wx, be, ref, b))
+        assert stats() == (2, 3)
+        # Capacity 0: every prompt is projected again and nothing is counted.
+        wx.check(lib.wamx_gwp_set_prompt_cache(m, 0), "set_prompt_cache")
+        assert np.array_equal(run_gpu(wx, be, m, a), run_gpu(wx, be, ref, a))
+        assert np.array_equal(run_gpu(wx, be, m, a_other), run_gpu(wx, be, ref, a_other))
+        assert stats() == (2, 3)
+    finally:
+        lib.wamx_gwp_free(m)
+        lib.wamx_gwp_free(ref)
+
+
 def test_full_width_one_layer_matches_oracle(wx, be, orc):
     """Full GWP-0.5 widths (d = 3072, 24 heads, FFN 14336, 48 action tokens,
     512 prompt tokens) on two layers and 2 denoise steps with 256 visual tokens."""

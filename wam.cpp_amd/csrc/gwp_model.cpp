@@ -99,6 +99,14 @@ struct wamx_gwp_model {
     std::vector<wamx_gallocr_t> galloc;
     wamx_tensor * action_out = nullptr;
     wamx_timer_t timer = nullptr;
+    // Projected-prompt reuse across requests (cache.cpp:53-137): with a
+    // nonzero capacity, the prompt whose K/V the prompt caches hold is kept on
+    // the host; a request whose prompt has the same bytes skips the upload and
+    // the prompt graphs.  prompt_stale: the uploaded prompt is not projected.
+    size_t prompt_cache_capacity = 0;
+    std::vector<float> prompt_sig;
+    bool prompt_stale = true;
+    uint64_t prompt_hits = 0, prompt_misses = 0;
 
     int n_graphs() const { return (int) (2 * B + 1); }
     int prompt_graph(int64_t b) const { return (int) b; }
@@ -762,6 +770,7 @@ wamx_status wamx_gwp_init_synthetic(wamx_gwp_t m, uint64_t seed, float wstd) {
     }
     wamx_backend_synchronize(m->be);
     if (stage) wamx_device_free(m->be, stage);
+    m->prompt_stale = true;  // new weights: the prompt caches no longer hold its projection
     return WAMX_STATUS_SUCCESS;
 }
 
@@ -770,7 +779,15 @@ wamx_status wamx_gwp_set_inputs(wamx_gwp_t m, const float * state, const float *
     WAMX_REQUIRE(m && state && latent && prompt && noise, "wamx_gwp_set_inputs: null argument");
     wamx_status st = wamx_backend_tensor_set(m->in_state, state, 0, wamx_nbytes(m->in_state));
     if (st == WAMX_STATUS_SUCCESS) st = wamx_backend_tensor_set(m->in_latent, latent, 0, wamx_nbytes(m->in_latent));
-    if (st == WAMX_STATUS_SUCCESS) st = wamx_backend_tensor_set(m->in_prompt, prompt, 0, wamx_nbytes(m->in_prompt));
+    const size_t np = (size_t) wamx_nelements(m->in_prompt);
+    const bool hit = m->prompt_cache_capacity > 0 && !m->prompt_stale && m->prompt_sig.size() == np &&
+                     memcmp(m->prompt_sig.data(), prompt, np * sizeof(float)) == 0;
+    if (m->prompt_cache_capacity > 0) ++(hit ? m->prompt_hits : m->prompt_misses);
+    if (st == WAMX_STATUS_SUCCESS && !hit) {
+        m->prompt_stale = true;
+        st = wamx_backend_tensor_set(m->in_prompt, prompt, 0, wamx_nbytes(m->in_prompt));
+        if (st == WAMX_STATUS_SUCCESS && m->prompt_cache_capacity > 0) m->prompt_sig.assign(prompt, prompt + np);
+    }
     if (st != WAMX_STATUS_SUCCESS) return st;
     // The action state is bf16 in the native profile (mot.cpp:523-525, set_f32_tensor).
     const int64_t n = wamx_nelements(m->in_action);
@@ -793,7 +810,27 @@ static wamx_status run_phase(wamx_gwp_t m, int phase) {
     }
     return WAMX_STATUS_SUCCESS;
 }
-wamx_status wamx_gwp_run_prompt(wamx_gwp_t m) { return run_phase(m, 0); }
+wamx_status wamx_gwp_set_prompt_cache(wamx_gwp_t m, size_t capacity) {
+    WAMX_REQUIRE(m, "wamx_gwp_set_prompt_cache: null model");
+    m->prompt_cache_capacity = capacity;
+    if (capacity == 0) {
+        m->prompt_sig.clear();
+        m->prompt_sig.shrink_to_fit();
+    }
+    return WAMX_STATUS_SUCCESS;
+}
+wamx_status wamx_gwp_prompt_cache_stats(wamx_gwp_t m, uint64_t * hits, uint64_t * misses) {
+    WAMX_REQUIRE(m && hits && misses, "wamx_gwp_prompt_cache_stats: null argument");
+    *hits = m->prompt_hits;
+    *misses = m->prompt_misses;
+    return WAMX_STATUS_SUCCESS;
+}
+wamx_status wamx_gwp_run_prompt(wamx_gwp_t m) {
+    WAMX_REQUIRE(m, "wamx_gwp_run_prompt: null model");
+    const wamx_status st = run_phase(m, 0);
+    if (st == WAMX_STATUS_SUCCESS) m->prompt_stale = false;
+    return st;
+}
 wamx_status wamx_gwp_run_prefix(wamx_gwp_t m) { return run_phase(m, 1); }
 wamx_status wamx_gwp_run_denoise(wamx_gwp_t m) { return run_phase(m, 2); }
 
@@ -802,7 +839,10 @@ wamx_status wamx_gwp_predict(wamx_gwp_t m, wamx_gwp_timing * timing) {
     float ms[3] = {0, 0, 0};
     for (int i = 0; i < 3; ++i) {
         if (timing) wamx_timer_start(m->timer);
-        const wamx_status st = run_phase(m, i);
+        // The prompt graphs run unless the prompt caches already hold the
+        // projection of the uploaded prompt (a projected-prompt cache hit).
+        const bool skip = i == 0 && m->prompt_cache_capacity > 0 && !m->prompt_stale;
+        const wamx_status st = skip ? WAMX_STATUS_SUCCESS : i == 0 ? wamx_gwp_run_prompt(m) : run_phase(m, i);
         if (st != WAMX_STATUS_SUCCESS) return st;
         if (timing) ms[i] = wamx_timer_stop_ms(m->timer);
     }

@@ -217,6 +217,8 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_gwp_set_inputs": (C.c_int, [vp, vp, vp, vp, vp]),
         "wamx_gwp_predict": (C.c_int, [vp, C.POINTER(GwpTiming)]),
         "wamx_gwp_run_prompt": (C.c_int, [vp]),
+        "wamx_gwp_set_prompt_cache": (C.c_int, [vp, sz]),
+        "wamx_gwp_prompt_cache_stats": (C.c_int, [vp, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
         "wamx_gwp_run_prefix": (C.c_int, [vp]),
         "wamx_gwp_run_denoise": (C.c_int, [vp]),
         "wamx_gwp_get_action": (C.c_int, [vp, vp]),
