@@ -181,6 +181,17 @@ def test_supports_rejects_malformed_nodes(wx, ctx):
     assert at and lib.wamx_backend_supports_op(None, at)
     at.contents.src[2] = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 255, 128, 4)
     assert not lib.wamx_backend_supports_op(None, at)
+    # no keys at all (softmax over an empty set): refused by the constructor,
+    # and by supports_op when a mirrored graph arrives without it
+    k0 = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 128, 0, 4)
+    v0 = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 0, 128, 4)
+    assert not lib.wamx_joint_attn(ctx, q, k0, v0, None, None, 0, 0.088)
+    assert b"no keys" in lib.wamx_last_error()
+    at0 = lib.wamx_joint_attn(ctx, q, kk, vt, None, None, 0, 0.088)
+    at0.contents.src[1], at0.contents.src[2] = k0, v0
+    assert not lib.wamx_backend_supports_op(None, at0)
+    # an empty first source beside a non-empty second one is a valid key set
+    assert lib.wamx_joint_attn(ctx, q, k0, v0, kk, vt, 0, 0.088)
     # MUL_MAT whose result shape does not follow from its operands
     w = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 64, 32)
     mm = lib.wamx_mul_mat(ctx, w, x)

@@ -366,3 +366,30 @@ def test_visual_cross_attention_against_f32_qk(wx, be, orc):
     ref = f32(bf16(ref))
     assert_parity(got, ref, what="visual cross-attention (bf16 Q.K) vs f32 Q.K")
     print(f"max-rel {rel_err(got, ref):.3e} cosine {cosine(got, ref):.7f}")
+
+
+def test_empty_and_refused_sizes(wx, be):
+    """Edge sizes through the C ABI: zero queries and zero rows are no-ops; an
+    attention over no keys and a linear over no tokens are refused with an
+    error before any launch.  The output buffer stays untouched throughout."""
+    print("edge sizes", flush=True)
+    lib = be.lib
+    sentinel = np.full(4096, 0x3F80, np.uint16)  # bf16 1.0
+    y = dev(be, sentinel)
+    q = dev(be, np.zeros(128 * 8, np.uint16))
+    k = dev(be, np.zeros(128 * 8, np.uint16))
+    sc = dev(be, np.zeros(128, np.float32))
+    # no queries: nothing to compute
+    wx.check(lib.wamx_op_joint_attn(be.ptr, q.ptr, k.ptr, k.ptr, 8, None, None, 0, 0, y.ptr, 1, 128, 0, 0.088))
+    # no keys: softmax over an empty set is refused
+    assert lib.wamx_op_joint_attn(be.ptr, q.ptr, k.ptr, k.ptr, 0, None, None, 0, 0, y.ptr, 1, 128, 1, 0.088) != 0
+    assert "no keys" in wx.last_error()
+    # negative key count
+    assert lib.wamx_op_joint_attn(be.ptr, q.ptr, k.ptr, k.ptr, -4, None, None, 0, 0, y.ptr, 1, 128, 1, 0.088) != 0
+    # LayerNorm + modulation over zero rows
+    wx.check(lib.wamx_op_norm_modulation_bf16(be.ptr, q.ptr, 128, sc.ptr, sc.ptr, 0, y.ptr, 0, 128, 1e-6))
+    # linear over zero tokens is refused
+    assert lib.wamx_op_linear(be.ptr, k.ptr, q.ptr, wx.TYPE_BF16, None, wx.EPI_NONE, None, None, y.ptr, 8, 0,
+                              128) != 0
+    be.sync()
+    assert np.array_equal(y.download(np.uint16, (4096,)), sentinel)

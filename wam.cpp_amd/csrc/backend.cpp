@@ -1644,6 +1644,9 @@ wamx_status wamx_op_joint_attn(wamx_backend_t be, const void * q, const void * k
     WAMX_REQUIRE(head_dim == 128, "wamx_op_joint_attn: head_dim must be 128");
     WAMX_REQUIRE(na % 4 == 0 && (!k_b || nb % 4 == 0),
                  "wamx_op_joint_attn: key counts must be multiples of 4 (pad V^T rows)");
+    WAMX_REQUIRE(na >= 0 && nb >= 0 && heads > 0 && tq >= 0 && na_split >= 0 && na_split <= na,
+                 "wamx_op_joint_attn: negative size or split outside the first source");
+    WAMX_REQUIRE(na + (k_b ? nb : 0) > 0, "wamx_op_joint_attn: no keys (softmax over an empty key set)");
     AttnArgs a;
     a.q = q;
     a.k_a = k_a;

@@ -166,6 +166,7 @@ const char * check_joint_attn(const wamx_tensor * t) {
             v_b->ne[0] != nb || v_b->ne[1] != dh || v_b->ne[2] != H || v_b->ne[3] != B)
             return "kv_b shapes";
     }
+    if (na + (k_b ? k_b->ne[1] : 0) <= 0) return "no keys (softmax over an empty key set)";
     const int64_t na_split = t->op_params[0];
     if (na_split < 0 || na_split > na) return "split";
     for (const wamx_tensor * s : {q, k_a, k_b})

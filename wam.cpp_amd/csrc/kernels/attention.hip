@@ -1164,6 +1164,8 @@ static int device_cus() {
 hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     if (a.head_dim != kDh) return hipErrorInvalidValue;
     if (a.tq <= 0) return hipSuccess;
+    // Every path below plans key ranges over the key blocks: at least one key.
+    if (a.na < 0 || a.nb < 0 || a.na + (a.k_b ? a.nb : 0) <= 0 || a.heads <= 0) return hipErrorInvalidValue;
     AttnParams p{};
     p.q = (const uint16_t *) a.q;
     p.k[0] = (const uint16_t *) a.k_a;
