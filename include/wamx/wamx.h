@@ -559,7 +559,10 @@ WAMX_API uint64_t    wamx_gwp_param_count(wamx_gwp_t m);
 WAMX_API wamx_status wamx_gwp_init_synthetic(wamx_gwp_t m, uint64_t seed, float wstd);
 /* Inputs, chunk-major for batch > 1: state f32 [batch][action_dim], latent f32
  * [batch][z_dim][2*grid_h][2*grid_w] (CHW), prompt f32 [batch][n_lang][t5_hidden],
- * noise f32 [batch][action_chunk][action_dim]. */
+ * noise f32 [batch][action_chunk][action_dim].  A NaN or Inf anywhere is
+ * refused (WAMX_STATUS_FAILED) before anything is uploaded, as the reference
+ * refuses state, latent, prompt and noise (src/models/gwp05/engine/engine.cpp
+ * :238-247, :274, :320, :350-357). */
 WAMX_API wamx_status wamx_gwp_set_inputs(wamx_gwp_t m, const float * state, const float * latent,
                                          const float * prompt, const float * noise);
 /* Run the three graphs (prompt projection, prefix, unrolled denoise). */
@@ -580,8 +583,28 @@ WAMX_API wamx_status wamx_gwp_set_prompt_cache(wamx_gwp_t m, size_t capacity);
 WAMX_API wamx_status wamx_gwp_prompt_cache_stats(wamx_gwp_t m, uint64_t * hits, uint64_t * misses);
 WAMX_API wamx_status wamx_gwp_run_prefix(wamx_gwp_t m);
 WAMX_API wamx_status wamx_gwp_run_denoise(wamx_gwp_t m);
-/* Final action chunks (bf16 state widened to f32) [batch][action_chunk][action_dim]. */
+/* Final action chunks (bf16 state widened to f32) [batch][action_chunk][action_dim].
+ * Waits for the request.  A non-finite element returns WAMX_STATUS_FAILED
+ * with wamx_last_error() naming it, as the reference's prediction check
+ * (src/models/gwp05/model.cpp:246-251) fails the request; out is still
+ * written. */
 WAMX_API wamx_status wamx_gwp_get_action(wamx_gwp_t m, float * out);
+/* The velocity of denoise step `step` of the last request: the action
+ * decoder's bf16 output widened to f32, [batch][action_chunk][action_dim],
+ * the tensor the scheduler step adds as dt * v.  It replaces the reference's
+ * velocity_step0 / denoise_%02d_velocity debug dumps
+ * (src/models/gwp05/engine/engine.cpp:416-421, gwp-f32-dump-v1 format
+ * weights.cpp:13-104), which exist there only on its stepwise path; here the
+ * velocities are outputs of the unrolled denoise graph.  Waits for the
+ * request. */
+WAMX_API wamx_status wamx_gwp_get_velocity(wamx_gwp_t m, int step, float * out);
+/* First non-finite element check of a host f32 array, the finite-value test
+ * of the reference's copy_f32_tensor (src/models/common/input_validation.cpp
+ * :37-42).  WAMX_STATUS_FAILED and wamx_last_error() "<field> contains NaN or
+ * Inf (element i)" on the first one; no GPU call.  wamx_gwp_set_inputs
+ * applies it to state, latent, prompt and noise before uploading anything,
+ * wamx_gwp_get_action and wamx_t5_encode to their outputs. */
+WAMX_API wamx_status wamx_check_finite_f32(const float * values, size_t n, const char * field);
 /* Prefix K/V cache of one layer as stored: K bf16 [batch][H][P][dh] (ggml ne
  * {dh, P, H, batch}), V^T bf16 [batch][H][dh][Ppad] viewed as ne {P, dh, H, batch}. */
 WAMX_API wamx_tensor * wamx_gwp_prefix_key(wamx_gwp_t m, int layer);
@@ -711,7 +734,9 @@ WAMX_API wamx_t5_t    wamx_t5_create_from_gguf(wamx_backend_t be, wamx_gguf_t g)
 /* Encode n (1..max_tokens) tokens; mask (nullable) holds 0/1 with the valid
  * tokens a contiguous prefix, as validate_prompt_mask requires
  * (text_encoder.cpp:75-110).  out: f32 [max_tokens][hidden], rows past the
- * valid prefix zero.  Synchronous. */
+ * valid prefix zero.  Synchronous.  A non-finite embedding returns
+ * WAMX_STATUS_FAILED (the engine's check, engine.cpp:314-320); out is still
+ * written. */
 WAMX_API wamx_status  wamx_t5_encode(wamx_t5_t t, const int32_t * tokens, const int32_t * mask, int32_t n,
                                      float * out);
 /* T5's bidirectional relative-position bucket of key - query

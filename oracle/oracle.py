@@ -282,7 +282,8 @@ class Gwp:
                 ("orc_gwp_prompt_value", C.c_void_p, [C.c_void_p, C.c_int]),
                 ("orc_gwp_prefix_hidden_in", C.c_void_p, [C.c_void_p, C.c_int]),
                 ("orc_gwp_set_visual_positions", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
-                ("orc_gwp_action_prompt", C.c_void_p, [C.c_void_p])):
+                ("orc_gwp_action_prompt", C.c_void_p, [C.c_void_p]),
+                ("orc_gwp_velocity", C.c_void_p, [C.c_void_p, C.c_int])):
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
@@ -328,6 +329,16 @@ class Gwp:
         if self.lib.orc_gwp_denoise(self.ptr, _p(n), _p(out), layers, steps) != 0:
             raise RuntimeError("oracle denoise failed (missing weight)")
         return out
+
+    def velocity(self, step):
+        """The decoder output (velocity) of denoise step `step` of the last
+        denoise, f32 [T * A]."""
+        c = self.cfg
+        ptr = self.lib.orc_gwp_velocity(self.ptr, step)
+        if not ptr:
+            raise RuntimeError(f"oracle velocity of step {step} unavailable")
+        n = c["action_chunk"] * c["action_dim"]
+        return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_float)), shape=(n,)).copy()
 
     def _arr(self, ptr, shape):
         n = int(np.prod(shape))

@@ -39,6 +39,7 @@ struct orc_gwp {
     uint16_t * state_in;             /* [da]: state encoder output (prefix_state_hidden_in) */
     uint16_t * visual_in;            /* [nimg][d]: patch embedding output (prefix_visual_hidden_in) */
     int32_t * vpos[3];               /* visual (t, h, w) positions, NULL: the grid's */
+    float * velocity;                /* [num_steps][T][A]: the decoder output of each denoise step */
     int missing;
 };
 
@@ -306,6 +307,7 @@ void orc_gwp_free(orc_gwp * g) {
     free(g->state_in);
     free(g->visual_in);
     for (int i = 0; i < 3; ++i) free(g->vpos[i]);
+    free(g->velocity);
     free(g);
 }
 
@@ -462,6 +464,8 @@ int orc_gwp_denoise(orc_gwp * g, const float * noise, float * action_out, int la
     int32_t * apos = (int32_t *) calloc((size_t) T, 4);
     for (int64_t i = 0; i < T; ++i) apos[i] = (int32_t) (i + 1);
     float * mods = alloc32(6 * da);
+    free(g->velocity);
+    g->velocity = (float *) calloc((size_t) (c->num_steps * T * A), sizeof(float));
     const float scale = 1.0f / sqrtf((float) dh);
     for (int s = 0; s < S; ++s) {
         float freq[256];
@@ -507,6 +511,9 @@ int orc_gwp_denoise(orc_gwp * g, const float * noise, float * action_out, int la
         uint16_t * n = alloc16(T * da);
         orc_norm_mod_bf16(h, da, om + da, om, 0, n, T, da, c->eps);
         uint16_t * pred = mlp3(g, "gwp.action_decoder", n, ORC_BF16, T, da, A);
+        /* The velocity of this step (engine.cpp:416-421 dumps it as
+           velocity_step0 / denoise_%02d_velocity). */
+        for (int64_t i = 0; i < T * A; ++i) g->velocity[(int64_t) s * T * A + i] = b2f(pred[i]);
         const float dt = sig[s + 1] - sig[s];
         for (int64_t i = 0; i < T * A; ++i) {
             volatile float vdt = b2f(pred[i]) * dt;
@@ -535,3 +542,8 @@ const uint16_t * orc_gwp_prompt_key(orc_gwp * g, int layer) { return g->lk[layer
 const uint16_t * orc_gwp_prompt_value(orc_gwp * g, int layer) { return g->lv[layer]; }
 const uint16_t * orc_gwp_prefix_hidden_in(orc_gwp * g, int which) { return which == 0 ? g->state_in : g->visual_in; }
 const uint16_t * orc_gwp_action_prompt(orc_gwp * g) { return g->action_prompt; }
+
+const float * orc_gwp_velocity(orc_gwp * g, int step) {
+    if (!g || !g->velocity || step < 0 || step >= g->c.num_steps) return NULL;
+    return g->velocity + (int64_t) step * g->c.action_chunk * g->c.action_dim;
+}

@@ -48,6 +48,9 @@ const uint16_t * orc_gwp_prefix_hidden_in(orc_gwp * g, int which);
  * place of visual_positions' grid (semantics.cpp:235-257); NULLs restore it. */
 int orc_gwp_set_visual_positions(orc_gwp * g, const int32_t * t, const int32_t * h, const int32_t * w);
 const uint16_t * orc_gwp_action_prompt(orc_gwp * g);            /* [n_lang][action_hidden] */
+/* Velocity (action decoder output, bf16 widened) of denoise step `step` of
+   the last orc_gwp_denoise: [T][A]; NULL before a denoise or out of range. */
+const float * orc_gwp_velocity(orc_gwp * g, int step);
 
 #ifdef __cplusplus
 }

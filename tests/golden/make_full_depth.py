@@ -1,4 +1,5 @@
-"""Writes tests/golden/gwp_full_depth.json: the oracle's action chunk for the
+"""Writes tests/golden/gwp_full_depth.json: the oracle's action chunk, and the
+velocity (action decoder output) of every denoise step, for the
 synthetic GWP-0.5 MoT at full depth and width (30 layers, d = 3072, 24 x 128
 heads, FFN 14336 in both experts, 48 x 32 actions, 10 flow-matching steps,
 512 prompt tokens of width 4096, 8 x 32 visual tokens from a 48-channel
@@ -57,6 +58,7 @@ def main(out: Path = HERE / "gwp_full_depth.json") -> None:
         "weights": "oracle.gwp_synthetic_weights(config, weight_seed, weight_std)",
         "inputs": "make_full_depth.inputs(config, input_seed)",
         "action": [float(v) for v in action.ravel()],
+        "velocity": [[float(v) for v in g.velocity(s)] for s in range(CONFIG["num_steps"])],
         "noise_bf16_rel_change": float(np.linalg.norm(action - noise) / np.linalg.norm(noise)),
         "oracle_threads": oracle.num_threads(), "weights_s": round(t1 - t0, 1), "oracle_s": round(t2 - t1, 1),
     }

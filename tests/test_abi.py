@@ -20,6 +20,25 @@ def test_no_device_needed_to_load(wx):
     assert wx.load().wamx_get_device_count() >= 0
 
 
+def test_check_finite_f32(wx):
+    """The finite-value check the model driver applies to its inputs and
+    outputs (copy_f32_tensor, input_validation.cpp:37-42): host only."""
+    import numpy as np
+    lib = wx.load()
+    a = np.linspace(-3, 3, 1000).astype(np.float32)
+    assert lib.wamx_check_finite_f32(a.ctypes.data, a.size, b"state") == 0
+    assert lib.wamx_check_finite_f32(None, 0, b"state") == 0
+    for i, bad in ((0, np.nan), (517, np.inf), (999, -np.inf)):
+        b = a.copy()
+        b[i] = bad
+        assert lib.wamx_check_finite_f32(b.ctypes.data, b.size, b"noise") != 0
+        assert wx.last_error() == f"noise contains NaN or Inf (element {i})"
+    # the largest finite value and subnormals are finite
+    c = np.array([np.finfo(np.float32).max, -np.finfo(np.float32).max, 1e-45], np.float32)
+    assert lib.wamx_check_finite_f32(c.ctypes.data, c.size, b"x") == 0
+    assert lib.wamx_check_finite_f32(None, 4, b"prompt") != 0
+
+
 @pytest.fixture
 def ctx(wx):
     lib = wx.load()

@@ -78,7 +78,7 @@ def test_artifact_model_matches_direct_upload_and_oracle(wx, be, orc, tmp_path, 
         g = orc.Gwp(CFG, weights)
         g.prompt(ins[2])
         g.prefix(ins[0], ins[1], ins[2])
-        action_gate(got, g.denoise(ins[3]).ravel(), "artifact model vs oracle")
+        action_gate(got, g.denoise(ins[3]).ravel(), "artifact model vs oracle", ins[3])
     finally:
         lib.wamx_gwp_free(m)
         lib.wamx_gwp_free(ref)

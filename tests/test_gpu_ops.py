@@ -233,12 +233,18 @@ def test_qk_norm_rope(wx, be, orc, rng, mode):
 #    16-query groups over short sources (ragged last group);
 #  * register-streamed key-split decode and its single-workgroup form (V^T rows
 #    a multiple of 4 keys only);
-#  * the generic many-query kernel (two sources, tq > 64).
+#  * the generic many-query kernel (two sources, tq > 64);
+#  * the prefix self-attention at 24 heads x 3072-3073 queries: (head,
+#    128-query) units beyond one round of two workgroups per CU, so the first
+#    launch runs the whole rounds and the last round's units are split into
+#    key ranges whose partials are merged (the shape the chunk's prefix pass
+#    runs, 3073 prefix keys there).
 @pytest.mark.parametrize("H,tq,na,nb,split", [(24, 48, 3076, 48, 1), (4, 48, 1028, 48, 1), (2, 5, 64, 0, 0),
                                               (3, 200, 200, 0, 0), (2, 48, 512, 0, 0), (1, 1, 4, 4, 2),
                                               (2, 3073, 3072, 0, 0), (1, 130, 520, 0, 0), (2, 100, 96, 8, 1),
                                               (8, 48, 3080, 48, 1), (3, 48, 520, 0, 0), (2, 17, 64, 8, 1),
-                                              (1, 64, 200, 16, 1), (5, 40, 700, 24, 1)])
+                                              (1, 64, 200, 16, 1), (5, 40, 700, 24, 1),
+                                              (24, 3073, 3076, 0, 0), (24, 3072, 3080, 0, 0)])
 def test_joint_attention(wx, be, orc, H, tq, na, nb, split):
     print(f"joint_attn H={H} tq={tq} na={na} nb={nb}", flush=True)
     rng = np.random.default_rng(H * tq + na)

@@ -98,6 +98,10 @@ struct wamx_gwp_model {
     std::vector<wamx_cgraph *> graph;
     std::vector<wamx_gallocr_t> galloc;
     wamx_tensor * action_out = nullptr;
+    // The action decoder's output of every denoise step, bf16 [A, B*T] (the
+    // velocity the scheduler step adds, kept as graph outputs so the
+    // allocator never reuses their memory).
+    std::vector<wamx_tensor *> velocity;
     wamx_timer_t timer = nullptr;
     // Projected-prompt reuse across requests (cache.cpp:53-137): with a
     // nonzero capacity, the prompt whose K/V the prompt caches hold is kept on
@@ -621,6 +625,8 @@ static bool build_denoise_graph(wamx_gwp_model * m) {
         wamx_tensor * oscale = wamx_view_1d(ctx, om, da, (size_t) da * 4);
         wamx_tensor * n = wamx_norm_modulation_bf16(ctx, h, oscale, oshift, c.eps);
         wamx_tensor * pred = b.mlp3(m->action_dec, n);  // bf16 [A, T]
+        wamx_set_output(pred);
+        m->velocity.push_back(pred);
         // scheduler_step (weights.cpp:885-902): bf16(f32(a) + f32(v) * dt).
         wamx_tensor * a32 = wamx_cast(ctx, action, WAMX_TYPE_F32);
         wamx_tensor * v32 = wamx_cast(ctx, pred, WAMX_TYPE_F32);
@@ -774,9 +780,31 @@ wamx_status wamx_gwp_init_synthetic(wamx_gwp_t m, uint64_t seed, float wstd) {
     return WAMX_STATUS_SUCCESS;
 }
 
+wamx_status wamx_check_finite_f32(const float * values, size_t n, const char * field) {
+    WAMX_REQUIRE(values || n == 0, "%s: null array", field ? field : "tensor");
+    for (size_t i = 0; i < n; ++i)
+        WAMX_REQUIRE(isfinite(values[i]), "%s contains NaN or Inf (element %zu)", field ? field : "tensor", i);
+    return WAMX_STATUS_SUCCESS;
+}
+
 wamx_status wamx_gwp_set_inputs(wamx_gwp_t m, const float * state, const float * latent, const float * prompt,
                                 const float * noise) {
     WAMX_REQUIRE(m && state && latent && prompt && noise, "wamx_gwp_set_inputs: null argument");
+    // Non-finite inputs are refused before anything is uploaded, as the
+    // reference refuses them before its graphs run (engine.cpp:238-247 state,
+    // :274 reference latent, :320 prompt, :350-357 noise).
+    const struct {
+        const float * p;
+        wamx_tensor * t;
+        const char * name;
+    } checks[] = {{state, m->in_state, "wamx_gwp_set_inputs: state"},
+                  {latent, m->in_latent, "wamx_gwp_set_inputs: latent"},
+                  {prompt, m->in_prompt, "wamx_gwp_set_inputs: prompt"},
+                  {noise, m->in_action, "wamx_gwp_set_inputs: noise"}};
+    for (const auto & ck : checks) {
+        const wamx_status fs = wamx_check_finite_f32(ck.p, (size_t) wamx_nelements(ck.t), ck.name);
+        if (fs != WAMX_STATUS_SUCCESS) return fs;
+    }
     wamx_status st = wamx_backend_tensor_set(m->in_state, state, 0, wamx_nbytes(m->in_state));
     if (st == WAMX_STATUS_SUCCESS) st = wamx_backend_tensor_set(m->in_latent, latent, 0, wamx_nbytes(m->in_latent));
     const size_t np = (size_t) wamx_nelements(m->in_prompt);
@@ -861,6 +889,22 @@ wamx_status wamx_gwp_get_action(wamx_gwp_t m, float * out) {
     const int64_t n = wamx_nelements(m->action_out);
     std::vector<uint16_t> a(n);
     const wamx_status st = wamx_backend_tensor_get(m->action_out, a.data(), 0, n * 2);
+    if (st != WAMX_STATUS_SUCCESS) return st;
+    for (int64_t i = 0; i < n; ++i) out[i] = bf16_to_f32_host(a[i]);
+    // A non-finite action is an inference failure (model.cpp:246-251); the
+    // values are still written for inspection.
+    return wamx_check_finite_f32(out, (size_t) n, "wamx_gwp_get_action: action");
+}
+
+wamx_status wamx_gwp_get_velocity(wamx_gwp_t m, int step, float * out) {
+    WAMX_REQUIRE(m && out, "wamx_gwp_get_velocity: null argument");
+    WAMX_REQUIRE(step >= 0 && step < (int) m->velocity.size() && m->velocity[step]->data,
+                 "wamx_gwp_get_velocity: step %d outside 0..%d", step, (int) m->velocity.size() - 1);
+    wamx_backend_synchronize(m->be);
+    wamx_tensor * v = m->velocity[step];
+    const int64_t n = wamx_nelements(v);
+    std::vector<uint16_t> a(n);
+    const wamx_status st = wamx_backend_tensor_get(v, a.data(), 0, n * 2);
     if (st != WAMX_STATUS_SUCCESS) return st;
     for (int64_t i = 0; i < n; ++i) out[i] = bf16_to_f32_host(a[i]);
     return WAMX_STATUS_SUCCESS;

@@ -277,7 +277,10 @@ wamx_status wamx_t5_encode(wamx_t5_t t5, const int32_t * tokens, const int32_t *
     const wamx_status st = wamx_backend_graph_compute(t5->be, g);
     if (st != WAMX_STATUS_SUCCESS) return st;
     memset(out, 0, (size_t) c.max_tokens * (size_t) d * sizeof(float));
-    return wamx_backend_tensor_get(y, out, 0, (size_t) V * (size_t) d * sizeof(float));
+    const wamx_status gs = wamx_backend_tensor_get(y, out, 0, (size_t) V * (size_t) d * sizeof(float));
+    if (gs != WAMX_STATUS_SUCCESS) return gs;
+    // The engine refuses a non-finite T5 embedding (engine.cpp:314-320).
+    return wamx_check_finite_f32(out, (size_t) V * (size_t) d, "wamx_t5_encode: embedding");
 }
 
 }  // extern "C"

@@ -222,6 +222,8 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_gwp_run_prefix": (C.c_int, [vp]),
         "wamx_gwp_run_denoise": (C.c_int, [vp]),
         "wamx_gwp_get_action": (C.c_int, [vp, vp]),
+        "wamx_gwp_get_velocity": (C.c_int, [vp, C.c_int, vp]),
+        "wamx_check_finite_f32": (C.c_int, [vp, sz, C.c_char_p]),
         "wamx_gwp_prefix_key": (TensorP, [vp, C.c_int]),
         "wamx_gwp_prefix_value": (TensorP, [vp, C.c_int]),
         "wamx_gwp_graph_nodes": (C.c_int, [vp, C.c_int]),
