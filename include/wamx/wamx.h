@@ -262,6 +262,19 @@ WAMX_API wamx_tensor * wamx_rms_norm_bf16_f32(wamx_context * ctx, wamx_tensor * 
  *   transposed [ne={n, dh, H}] (cache.cpp:22-25).  kv_b may be NULL.  Output bf16
  *   [ne={dh*H, Tq}], the layout the output projection consumes (mot.cpp:437-445).
  *
+ * wamx_qk_norm_rope_hilo / wamx_joint_attn_hilo: the f32-score attention of
+ *   build_attention (src/models/gwp05/engine/text_encoder.cpp:26-73), used by
+ *   the prefix's visual cross-attention (mot.cpp:326-337): there RMSNorm keeps
+ *   Q and K in f32 (rms_norm_bf16_f32) and the scores are an f32 x f32
+ *   MUL_MAT at GGML_PREC_F32.  wamx_qk_norm_rope_hilo writes dst
+ *   [ne={head_dim, T_total, H, 2}]: plane 0 the bf16 rounding of the f32
+ *   result, plane 1 its remainder bf16(v - plane0).  wamx_joint_attn_hilo
+ *   takes q [ne={dh, Tq, H, 2}] and k [ne={dh, n, H, 2}] in that form, V^T
+ *   bf16 [ne={n, dh, H}] (rows a multiple of 8 keys, n >= 8), and forms
+ *   every score as K.Q + K.Q_lo + K_lo.Q with fp32 accumulation (the
+ *   dropped K_lo.Q_lo is below 2^-16 of the product); softmax and P.V as
+ *   wamx_joint_attn.  Output bf16 [ne={dh*H, Tq}].
+ *
  * wamx_modulation: f32 [ne={d, 6, L}] = f32(mod [ne={d,6}]) + f32(table_l) for the
  *   L per-layer tables packed in `tables` [ne={d, 6, L}] (mot.cpp:137-145, 380-393).
  */
@@ -273,6 +286,11 @@ WAMX_API wamx_tensor * wamx_qk_norm_rope(wamx_context * ctx, wamx_tensor * x, wa
 WAMX_API wamx_tensor * wamx_joint_attn(wamx_context * ctx, wamx_tensor * q, wamx_tensor * k_a, wamx_tensor * v_a,
                                        wamx_tensor * k_b, wamx_tensor * v_b, int64_t na_split, float scale);
 WAMX_API wamx_tensor * wamx_modulation(wamx_context * ctx, wamx_tensor * mod, wamx_tensor * tables);
+WAMX_API wamx_tensor * wamx_qk_norm_rope_hilo(wamx_context * ctx, wamx_tensor * x, wamx_tensor * weight,
+                                              wamx_tensor * dst, int64_t tok0, int rope_mode, wamx_tensor * pos0,
+                                              wamx_tensor * pos1, wamx_tensor * pos2, float eps, float freq_base);
+WAMX_API wamx_tensor * wamx_joint_attn_hilo(wamx_context * ctx, wamx_tensor * q, wamx_tensor * k, wamx_tensor * v,
+                                            float scale);
 
 /* Graphs. */
 WAMX_API wamx_cgraph * wamx_new_graph(wamx_context * ctx, size_t max_nodes);
@@ -487,6 +505,19 @@ WAMX_API wamx_status wamx_op_joint_attn(wamx_backend_t be, const void * q, const
                                         const void * vt_b, int64_t nb, int64_t na_split,
                                         void * out, int64_t heads, int64_t head_dim, int64_t tq,
                                         float scale);
+/* The hi/lo forms on device pointers (f32-score attention of build_attention,
+ * text_encoder.cpp:26-73).  wamx_op_qk_norm_rope_hilo: as wamx_op_qk_norm_rope,
+ * plus the remainder plane at dst_lo (16-byte aligned offset from dst_hi).
+ * wamx_op_joint_attn_hilo: q / q_lo [H][Tq][dh], k / k_lo [H][nk][dh], vt
+ * [H][dh][vt_ld] (vt_ld % 8 == 0, nk >= 8), out bf16 [Tq][H*dh]. */
+WAMX_API wamx_status wamx_op_qk_norm_rope_hilo(wamx_backend_t be, const void * x, int64_t ldx, const void * w,
+                                               void * dst_hi, void * dst_lo, int64_t heads, int64_t head_dim,
+                                               int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode,
+                                               const int32_t * pos0, const int32_t * pos1, const int32_t * pos2,
+                                               float eps, float freq_base);
+WAMX_API wamx_status wamx_op_joint_attn_hilo(wamx_backend_t be, const void * q, const void * q_lo, const void * k,
+                                             const void * k_lo, const void * vt, int64_t nk, int64_t vt_ld,
+                                             void * out, int64_t heads, int64_t head_dim, int64_t tq, float scale);
 /* SOFT_MAX_EXT without mask: y[r][:] = softmax(scale * x[r][:]) over ne0=cols, f32. */
 WAMX_API wamx_status wamx_op_soft_max_f32(wamx_backend_t be, const float * x, float * y,
                                           int64_t rows, int64_t cols, float scale);

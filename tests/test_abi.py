@@ -119,6 +119,34 @@ def test_concat_and_fused_constructors(wx, ctx):
     assert not lib.wamx_linear(ctx, w, h, bias, wx.EPI_BIAS, None, None)  # bias length must be M
 
 
+def test_hilo_constructors(wx, ctx):
+    """The f32-score attention pair (build_attention, text_encoder.cpp:26-73):
+    QK norm into two bf16 planes, joint attention over one hi/lo source."""
+    lib = wx.load()
+    x = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 3072, 300)
+    w = lib.wamx_new_tensor_1d(ctx, wx.TYPE_BF16, 3072)
+    q2 = lib.wamx_new_tensor_4d(ctx, wx.TYPE_BF16, 128, 300, 24, 2)
+    q = lib.wamx_qk_norm_rope_hilo(ctx, x, w, q2, 0, 2, None, None, None, 1e-6, 10000.0)
+    assert q and q.contents.op == wx.OP["QK_NORM_ROPE"] and q.contents.op_params[4] == 1
+    assert lib.wamx_backend_supports_op(None, q)
+    # one plane is not a hi/lo destination
+    assert not lib.wamx_qk_norm_rope_hilo(ctx, x, w, lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 128, 300, 24), 0, 2,
+                                          None, None, None, 1e-6, 10000.0)
+    kx = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 3072, 64)
+    k = lib.wamx_qk_norm_rope_hilo(ctx, kx, w, lib.wamx_new_tensor_4d(ctx, wx.TYPE_BF16, 128, 64, 24, 2), 0, 2,
+                                   None, None, None, 1e-6, 10000.0)
+    vt = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 64, 128, 24)
+    att = lib.wamx_joint_attn_hilo(ctx, q, k, vt, 0.088)
+    assert att and shape(att) == (3072, 300, 1, 1) and att.contents.op_params[2] == 1
+    assert lib.wamx_backend_supports_op(None, att)
+    # planes of the bf16 q alone, too few keys, and V^T rows off 8 keys are refused
+    assert not lib.wamx_joint_attn_hilo(ctx, lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 128, 300, 24), k, vt, 0.088)
+    k4 = lib.wamx_new_tensor_4d(ctx, wx.TYPE_BF16, 128, 4, 24, 2)
+    assert not lib.wamx_joint_attn_hilo(ctx, q, k4, lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 4, 128, 24), 0.088)
+    k12 = lib.wamx_new_tensor_4d(ctx, wx.TYPE_BF16, 128, 12, 24, 2)
+    assert not lib.wamx_joint_attn_hilo(ctx, q, k12, lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 12, 128, 24), 0.088)
+
+
 def test_graph_order_and_uid(wx, ctx):
     lib = wx.load()
     x = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 16, 4)

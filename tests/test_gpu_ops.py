@@ -10,7 +10,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import assert_parity, cosine, rel_err
+from conftest import REL_TOL, assert_parity, cosine, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -331,47 +331,75 @@ def test_joint_attention_dit_block(wx, be, orc):
     assert_parity(f32(got), f32(ref), what="dit-block attention")
 
 
-def test_visual_cross_attention_against_f32_qk(wx, be, orc):
+@pytest.mark.parametrize("wscale", [1.0, 4.0])
+def test_visual_cross_attention_f32_scores(wx, be, orc, wscale):
     """The prefix's visual cross-attention (build_attention,
     text_encoder.cpp:26-73) keeps RMSNorm'd Q and K in f32 and takes f32 Q.K
-    products; this backend rounds Q and K to bf16 after RMSNorm and runs the
-    bf16 MFMA flash kernel.  Bound at 3072 queries x 512 keys x 24 heads
-    against the f32-Q.K path (probabilities rounded to bf16 for P.V as the
-    reference does): max-rel <= 1e-2, cosine >= 0.9999."""
-    print("visual cross-attention vs f32 Q.K", flush=True)
+    scores.  At 3072 queries x 512 keys x 24 heads, against that f32-score
+    reference (normalised probabilities rounded to bf16 for P.V, bf16
+    output):
+    * the hi/lo planes: hi is the bf16 rounding of the f32 RMSNorm output and
+      hi + lo carries it to 2^-16;
+    * the hi/lo attention (wamx_op_joint_attn_hilo) passes the per-op bar
+      with mean |delta| <= 3e-4 of max |ref| at norm-weight scale 1 and 4.
+      (Its floor is the bf16 output and the flash form's rounding of
+      unnormalised probabilities: about 2e-4, max-rel 4-7e-3 in a float64
+      simulation; rounding Q and K to bf16 instead gives 2.9e-4 at scale 1
+      and 9.2e-4 at scale 4.)
+    * at scale 4 (scores of std ~16) the bf16-Q.K path fails the per-op bar:
+      f32-accurate scores are what keeps it."""
+    print(f"visual cross-attention, f32 scores, norm-weight scale {wscale}", flush=True)
     rng = np.random.default_rng(0x5EED0302)
     H, dh, NQ, NK = 24, 128, 3072, 512
     d = H * dh
     q = bf16(rng.standard_normal((NQ, d)))
     k = bf16(rng.standard_normal((NK, d)))
     v = bf16(rng.standard_normal((NK, d)))
-    wq = bf16(1 + rng.standard_normal(d) * 0.02)
-    wk = bf16(1 + rng.standard_normal(d) * 0.02)
+    wq = bf16(wscale * (1 + rng.standard_normal(d) * 0.02))
+    wk = bf16(wscale * (1 + rng.standard_normal(d) * 0.02))
     dq, dk, dwq, dwk = dev(be, q), dev(be, k), dev(be, wq), dev(be, wk)
-    dQ, dK = be.empty(H * NQ * dh * 2), be.empty(H * NK * dh * 2)
+    # hi/lo planes [2][H][n][dh]
+    dQ, dK = be.empty(2 * H * NQ * dh * 2), be.empty(2 * H * NK * dh * 2)
     for src, w, dst, n in ((dq, dwq, dQ, NQ), (dk, dwk, dK, NK)):
-        wx.check(be.lib.wamx_op_qk_norm_rope(be.ptr, src.ptr, d, w.ptr, dst.ptr, H, dh, n, n, 0, 2, None, None, None,
-                                             1e-6, 10000.0))
-    vt = np.ascontiguousarray(v.reshape(NK, H, dh).transpose(1, 2, 0))
-    dvt = dev(be, vt)
-    dout = be.empty(NQ * d * 2)
-    scale = 1.0 / np.sqrt(dh)
-    wx.check(be.lib.wamx_op_joint_attn(be.ptr, dQ.ptr, dK.ptr, dvt.ptr, NK, None, None, 0, 0, dout.ptr, H, dh, NQ,
-                                       scale))
-    got = f32(dout.download(np.uint16, (NQ, d)))
+        wx.check(be.lib.wamx_op_qk_norm_rope_hilo(be.ptr, src.ptr, d, w.ptr, dst.ptr, dst.ptr + H * n * dh * 2, H, dh,
+                                                  n, n, 0, 2, None, None, None, 1e-6, 10000.0), "qk_norm hilo")
     qf = orc.rms_norm_bf16_f32(q, wq, 1e-6).astype(np.float64)
     kf = orc.rms_norm_bf16_f32(k, wk, 1e-6).astype(np.float64)
+    planes = dQ.download(np.uint16, (2, H, NQ, dh))
+    qf_hm = qf.reshape(NQ, H, dh).transpose(1, 0, 2)
+    hi, lo = f32(planes[0]).astype(np.float64), f32(planes[1]).astype(np.float64)
+    assert np.mean(planes[0] != bf16(qf_hm)) < 1e-3  # hi = bf16(f32 value) but for rounding ties
+    assert np.max(np.abs(hi + lo - qf_hm) / np.maximum(np.abs(qf_hm), 1e-30)) < 2.0 ** -15
+    vt = np.ascontiguousarray(v.reshape(NK, H, dh).transpose(1, 2, 0))
+    dvt = dev(be, vt)
+    scale = 1.0 / np.sqrt(dh)
+    dout = be.empty(NQ * d * 2)
+    wx.check(be.lib.wamx_op_joint_attn_hilo(be.ptr, dQ.ptr, dQ.ptr + H * NQ * dh * 2, dK.ptr, dK.ptr + H * NK * dh * 2,
+                                            dvt.ptr, NK, NK, dout.ptr, H, dh, NQ, scale), "joint_attn_hilo")
+    got = f32(dout.download(np.uint16, (NQ, d)))
+    # bf16-Q.K path for comparison: the hi planes through the bf16 kernel
+    dout_b = be.empty(NQ * d * 2)
+    wx.check(be.lib.wamx_op_joint_attn(be.ptr, dQ.ptr, dK.ptr, dvt.ptr, NK, None, None, 0, 0, dout_b.ptr, H, dh, NQ,
+                                       scale))
+    got_b = f32(dout_b.download(np.uint16, (NQ, d)))
     vf = f32(v).astype(np.float64)
     ref = np.empty((NQ, d), np.float32)
     for h in range(H):
         sl = slice(h * dh, (h + 1) * dh)
-        s = (qf[:, sl] @ kf[:, sl].T).astype(np.float32).astype(np.float64) * scale
-        p = np.exp(s - s.max(axis=1, keepdims=True))
+        sc = (qf[:, sl] @ kf[:, sl].T).astype(np.float32).astype(np.float64) * scale
+        p = np.exp(sc - sc.max(axis=1, keepdims=True))
         p = f32(bf16((p / p.sum(axis=1, keepdims=True)).astype(np.float32))).astype(np.float64)
         ref[:, sl] = (p @ vf[:, sl]).astype(np.float32)
     ref = f32(bf16(ref))
-    assert_parity(got, ref, what="visual cross-attention (bf16 Q.K) vs f32 Q.K")
-    print(f"max-rel {rel_err(got, ref):.3e} cosine {cosine(got, ref):.7f}")
+    M = float(np.max(np.abs(ref)))
+    mean_h = float(np.mean(np.abs(got - ref))) / M
+    mean_b = float(np.mean(np.abs(got_b - ref))) / M
+    print(f"hi/lo scores: max-rel {rel_err(got, ref):.3e} mean {mean_h:.2e} cosine {cosine(got, ref):.7f}; "
+          f"bf16 scores: max-rel {rel_err(got_b, ref):.3e} mean {mean_b:.2e} cosine {cosine(got_b, ref):.7f}")
+    assert_parity(got, ref, what="visual cross-attention (hi/lo scores) vs f32 Q.K")
+    assert mean_h <= 3e-4
+    if wscale >= 4.0:
+        assert rel_err(got_b, ref) > REL_TOL, "bf16 scores pass at large scores: the test does not discriminate"
 
 
 def test_empty_and_refused_sizes(wx, be):

@@ -387,7 +387,7 @@ static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post, bool la
         int64_t width, head_dim;
         if (t->op == WAMX_OP_QK_NORM_ROPE) {
             const wamx_tensor * x = t->src[0];
-            if (!column_view(x, lin, seg.col) || !t->src[1] || t->type != WAMX_TYPE_BF16) break;
+            if (!column_view(x, lin, seg.col) || !t->src[1] || t->type != WAMX_TYPE_BF16 || t->op_params[4]) break;
             head_dim = t->ne[0];
             width = x->ne[0];
             if (width != head_dim * t->ne[2] || x->ne[1] % t->ne[3] != 0) break;
@@ -569,6 +569,11 @@ static hipError_t run_joint_attn(wamx_backend * be, const wamx_tensor * node) {
     a.scale = param_f32(node, 1);
     a.ws = be->cws;
     a.ws_bytes = kWorkspaceBytes;
+    if (node->op_params[2]) {  // hi/lo planes: plane 1 of q and k
+        a.heads = a.hb = q->ne[2];
+        a.q_lo = (const char *) q->data + q->nb[3];
+        a.k_lo = (const char *) node->src[1]->data + node->src[1]->nb[3];
+    }
     return launch_joint_attn(a, be->cs);
 }
 
@@ -655,13 +660,15 @@ static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
             return run_linear(be, node);
         case WAMX_OP_QK_NORM_ROPE: {
             const wamx_tensor * x = node->src[0];
+            const bool hilo = node->op_params[4] != 0;  // plane 1 takes the lo parts
             return launch_qk_norm_rope(x->data, (int64_t) x->nb[1] / 2, node->src[1]->data, node->data, node->ne[2],
                                        node->ne[0], x->ne[1], node->ne[1], node->op_params[0], node->op_params[1],
                                        node->src[3] ? (const int32_t *) node->src[3]->data : nullptr,
                                        node->src[4] ? (const int32_t *) node->src[4]->data : nullptr,
                                        node->src[5] ? (const int32_t *) node->src[5]->data : nullptr,
-                                       param_f32(node, 2), param_f32(node, 3), s, x->ne[1] / node->ne[3],
-                                       (int64_t) node->nb[3] / 2);
+                                       param_f32(node, 2), param_f32(node, 3), s,
+                                       hilo ? x->ne[1] : x->ne[1] / node->ne[3], hilo ? 0 : (int64_t) node->nb[3] / 2,
+                                       hilo ? (int64_t) node->nb[3] / 2 : 0);
         }
         case WAMX_OP_JOINT_ATTN:
             return run_joint_attn(be, node);
@@ -1635,6 +1642,44 @@ wamx_status wamx_op_qk_norm_rope(wamx_backend_t be, const void * x, int64_t ldx,
     WAMX_REQUIRE(tok0 >= 0 && tok0 + tokens <= dst_tokens, "wamx_op_qk_norm_rope: token range");
     WAMX_LAUNCH(launch_qk_norm_rope(x, ldx, w, dst, heads, head_dim, tokens, dst_tokens, tok0, rope_mode, pos0, pos1,
                                     pos2, eps, freq_base, be->stream));
+}
+
+wamx_status wamx_op_qk_norm_rope_hilo(wamx_backend_t be, const void * x, int64_t ldx, const void * w, void * dst_hi,
+                                      void * dst_lo, int64_t heads, int64_t head_dim, int64_t tokens, int64_t dst_tokens,
+                                      int64_t tok0, int rope_mode, const int32_t * pos0, const int32_t * pos1,
+                                      const int32_t * pos2, float eps, float freq_base) {
+    WAMX_REQUIRE(be && x && w && dst_hi && dst_lo, "wamx_op_qk_norm_rope_hilo: null argument");
+    WAMX_REQUIRE(rope_mode >= 0 && rope_mode <= 2, "wamx_op_qk_norm_rope_hilo: rope mode");
+    WAMX_REQUIRE(rope_mode == 2 || pos0, "wamx_op_qk_norm_rope_hilo: positions required");
+    WAMX_REQUIRE(rope_mode != 1 || (pos1 && pos2 && head_dim == 128), "wamx_op_qk_norm_rope_hilo: 3-D positions");
+    WAMX_REQUIRE(tok0 >= 0 && tok0 + tokens <= dst_tokens, "wamx_op_qk_norm_rope_hilo: token range");
+    const ptrdiff_t off = (const char *) dst_lo - (const char *) dst_hi;
+    WAMX_REQUIRE(off != 0 && off % 16 == 0, "wamx_op_qk_norm_rope_hilo: the lo plane must be 16-byte aligned to the hi plane");
+    WAMX_LAUNCH(launch_qk_norm_rope(x, ldx, w, dst_hi, heads, head_dim, tokens, dst_tokens, tok0, rope_mode, pos0, pos1,
+                                    pos2, eps, freq_base, be->stream, 0, 0, (int64_t) (off / 2)));
+}
+
+wamx_status wamx_op_joint_attn_hilo(wamx_backend_t be, const void * q, const void * q_lo, const void * k,
+                                    const void * k_lo, const void * vt, int64_t nk, int64_t vt_ld, void * out,
+                                    int64_t heads, int64_t head_dim, int64_t tq, float scale) {
+    WAMX_REQUIRE(be && q && q_lo && k && k_lo && vt && out, "wamx_op_joint_attn_hilo: null argument");
+    WAMX_REQUIRE(head_dim == 128, "wamx_op_joint_attn_hilo: head_dim must be 128");
+    WAMX_REQUIRE(nk >= 8 && vt_ld >= nk && vt_ld % 8 == 0 && heads > 0 && tq >= 0,
+                 "wamx_op_joint_attn_hilo: at least 8 keys, V^T rows a multiple of 8 keys");
+    AttnArgs a;
+    a.q = q;
+    a.q_lo = q_lo;
+    a.k_a = k;
+    a.k_lo = k_lo;
+    a.vt_a = vt;
+    a.na = nk;
+    a.vt_ld_a = vt_ld;
+    a.out = out;
+    a.heads = heads;
+    a.head_dim = head_dim;
+    a.tq = tq;
+    a.scale = scale;
+    WAMX_LAUNCH(launch_joint_attn(a, be->stream));
 }
 
 wamx_status wamx_op_joint_attn(wamx_backend_t be, const void * q, const void * k_a, const void * vt_a, int64_t na,

@@ -259,19 +259,22 @@ struct Builder {
     // expert_cross_ffn against uncached text (build_attention, text_encoder.cpp:26-73).
     // `kv` is the packed K/V projection of the text for every layer
     // [2·L·d, NL]; layer l's K columns start at 2l·d, its V columns at (2l+1)·d.
+    // RMSNorm keeps Q and K in f32 there and the scores are f32 x f32
+    // (rms_norm_bf16_f32, then MUL_MAT at GGML_PREC_F32): Q and K are held as
+    // bf16 hi/lo planes and the scores formed f32-accurate from them.
     wamx_tensor * cross_ffn_uncached(const ExpertLayer & e, wamx_tensor * h, wamx_tensor * kv, int64_t l,
                                      wamx_tensor * cshift, wamx_tensor * cscale, wamx_tensor * cgate) {
         const int64_t T = h->ne[1], NL = kv->ne[1], d = (int64_t) c.n_heads * c.head_dim;
         wamx_tensor * n = wamx_layer_norm_bf16(ctx, h, e.n2_w, e.n2_b, c.eps);
         wamx_tensor * q = lin(e.cq_w, e.cq_b, n);
         wamx_tensor * k = cols(kv, d, 2 * l * d);
-        wamx_tensor * Q = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, c.head_dim, T, c.n_heads);
-        Q = wamx_qk_norm_rope(ctx, q, e.cnq, Q, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
-        wamx_tensor * K = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, c.head_dim, NL, c.n_heads);
-        K = wamx_qk_norm_rope(ctx, k, e.cnk, K, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
-        wamx_tensor * vraw = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, round_up(NL, 4), c.head_dim, c.n_heads);
+        wamx_tensor * Q = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, c.head_dim, T, c.n_heads, 2);
+        Q = wamx_qk_norm_rope_hilo(ctx, q, e.cnq, Q, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
+        wamx_tensor * K = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, c.head_dim, NL, c.n_heads, 2);
+        K = wamx_qk_norm_rope_hilo(ctx, k, e.cnk, K, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
+        wamx_tensor * vraw = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, round_up(NL, 8), c.head_dim, c.n_heads);
         wamx_tensor * V = store_v(kv, (2 * l + 1) * d, vt_view(vraw, 0, NL));
-        wamx_tensor * att = wamx_joint_attn(ctx, Q, K, V, nullptr, nullptr, 0, scale);
+        wamx_tensor * att = wamx_joint_attn_hilo(ctx, Q, K, V, scale);
         h = lin(e.co_w, e.co_b, att, WAMX_EPI_BIAS_RESIDUAL, h);
         return ffn(e, h, cshift, cscale, cgate);
     }

@@ -171,7 +171,7 @@ hipError_t launch_modulation(const void * mod, int32_t mod_type, const void * ta
 hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void * dst, int64_t heads, int64_t head_dim,
                                int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode, const int32_t * pos0,
                                const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s,
-                               int64_t chunk_tokens = 0, int64_t chunk_stride = 0);
+                               int64_t chunk_tokens = 0, int64_t chunk_stride = 0, int64_t lo_off = 0);
 
 struct AttnArgs {
     const void * q = nullptr;      // bf16 [batch][H][Tq][dh]
@@ -192,6 +192,11 @@ struct AttnArgs {
     float scale = 1.0f;
     void * ws = nullptr;           // fp32 partials of the key-split path
     size_t ws_bytes = 0;
+    // f32-accurate scores: q and k_a are the bf16 roundings of f32 Q and K
+    // and q_lo / k_lo the rest (same layouts); S = K Q^T + K Q_lo^T +
+    // K_lo Q^T.  One key source, one chunk.
+    const void * q_lo = nullptr;
+    const void * k_lo = nullptr;
 };
 hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s);
 

@@ -130,7 +130,11 @@ const char * check_qk_norm_rope(const wamx_tensor * t) {
     const wamx_tensor *x = t->src[0], *weight = t->src[1], *dst = t->src[2];
     if (!is_bf16(x) || !is_bf16(weight) || !is_bf16(dst) || !is_bf16(t)) return "types";
     // dst [dh, tokens, H, B]: the rows of x are B chunks of T tokens each.
-    const int64_t dh = dst->ne[0], H = dst->ne[2], B = dst->ne[3];
+    // Hi/lo form (op_params[4] = 1): dst [dh, tokens, H, 2] holds the bf16
+    // rounding of the f32 result in plane 0 and the rest in plane 1, one chunk.
+    const bool hilo = t->op_params[4] != 0;
+    const int64_t dh = dst->ne[0], H = dst->ne[2], B = hilo ? 1 : dst->ne[3];
+    if (hilo && dst->ne[3] != 2) return "hi/lo destination needs two planes";
     if (B < 1 || x->ne[1] % B != 0) return "rows must split into the destination's chunks";
     const int64_t T = x->ne[1] / B;
     if (x->ne[0] != dh * H || weight->ne[0] != x->ne[0] || x->nb[0] != 2 || weight->nb[0] != 2 || !contig(dst) ||
@@ -152,6 +156,22 @@ const char * check_qk_norm_rope(const wamx_tensor * t) {
 const char * check_joint_attn(const wamx_tensor * t) {
     const wamx_tensor *q = t->src[0], *k_a = t->src[1], *v_a = t->src[2], *k_b = t->src[3], *v_b = t->src[4];
     if (!is_bf16(q) || !is_bf16(k_a) || !is_bf16(v_a)) return "types";
+    if (t->op_params[2]) {
+        // f32-accurate scores from hi/lo planes: q [dh, Tq, H, 2], k [dh, nk, H, 2],
+        // V^T [nk, dh, H] with rows of a multiple of 8 keys; one key source.
+        const int64_t dh = q->ne[0], Tq = q->ne[1], H = q->ne[2], nk = k_a->ne[1];
+        if (dh != 128) return "head_dim must be 128";
+        if (q->ne[3] != 2 || k_a->ne[3] != 2 || k_a->ne[0] != dh || k_a->ne[2] != H || !contig(q) || !contig(k_a))
+            return "hi/lo q and k: two contiguous planes";
+        if (k_b || v_b || t->op_params[0] != 0) return "hi/lo scores take one key source";
+        if (nk < 8) return "hi/lo scores need at least 8 keys";
+        if (v_a->ne[0] != nk || v_a->ne[1] != dh || v_a->ne[2] != H || v_a->ne[3] != 1 || v_a->nb[0] != 2 ||
+            v_a->nb[1] % 16 != 0 || v_a->nb[1] < (size_t) nk * 2 || v_a->nb[2] != v_a->nb[1] * (size_t) dh)
+            return "V^T layout";
+        if (!is_bf16(t) || t->ne[0] != dh * H || t->ne[1] != Tq || t->ne[2] != 1 || t->ne[3] != 1 || !contig(t))
+            return "output";
+        return nullptr;
+    }
     // dim 3 is the chunk: B independent key sets and query sets.
     const int64_t dh = q->ne[0], Tq = q->ne[1], H = q->ne[2], B = q->ne[3];
     const int64_t na = k_a->ne[1];
@@ -760,6 +780,44 @@ wamx_tensor * wamx_qk_norm_rope(wamx_context * ctx, wamx_tensor * x, wamx_tensor
     t->src[5] = rope_mode == 1 ? pos2 : nullptr;
     if (tok0 != (int64_t) t->op_params[0]) return fail("wamx_qk_norm_rope (token offset)");
     return checked(t, check_qk_norm_rope, "wamx_qk_norm_rope");
+}
+
+wamx_tensor * wamx_qk_norm_rope_hilo(wamx_context * ctx, wamx_tensor * x, wamx_tensor * weight, wamx_tensor * dst,
+                                     int64_t tok0, int rope_mode, wamx_tensor * pos0, wamx_tensor * pos1,
+                                     wamx_tensor * pos2, float eps, float freq_base) {
+    if (!x || !weight || !dst) return fail("wamx_qk_norm_rope_hilo");
+    wamx_tensor * t = view_impl(ctx, dst, 4, dst->ne, 0);
+    if (!t) return nullptr;
+    memcpy(t->nb, dst->nb, sizeof t->nb);
+    t->op = WAMX_OP_QK_NORM_ROPE;
+    t->op_params[0] = (int32_t) tok0;
+    t->op_params[1] = rope_mode;
+    set_param_f32(t, 2, eps);
+    set_param_f32(t, 3, freq_base);
+    t->op_params[4] = 1;
+    t->src[0] = x;
+    t->src[1] = weight;
+    t->src[2] = dst;
+    t->src[3] = rope_mode <= 1 ? pos0 : nullptr;
+    t->src[4] = rope_mode == 1 ? pos1 : nullptr;
+    t->src[5] = rope_mode == 1 ? pos2 : nullptr;
+    if (tok0 != (int64_t) t->op_params[0]) return fail("wamx_qk_norm_rope_hilo (token offset)");
+    return checked(t, check_qk_norm_rope, "wamx_qk_norm_rope_hilo");
+}
+
+wamx_tensor * wamx_joint_attn_hilo(wamx_context * ctx, wamx_tensor * q, wamx_tensor * k, wamx_tensor * v,
+                                   float scale) {
+    if (!q || !k || !v) return fail("wamx_joint_attn_hilo");
+    wamx_tensor * t = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, q->ne[0] * q->ne[2], q->ne[1], 1);
+    if (!t) return nullptr;
+    t->op = WAMX_OP_JOINT_ATTN;
+    t->op_params[0] = 0;
+    set_param_f32(t, 1, scale);
+    t->op_params[2] = 1;
+    t->src[0] = q;
+    t->src[1] = k;
+    t->src[2] = v;
+    return checked(t, check_joint_attn, "wamx_joint_attn_hilo");
 }
 
 wamx_tensor * wamx_joint_attn(wamx_context * ctx, wamx_tensor * q, wamx_tensor * k_a, wamx_tensor * v_a,

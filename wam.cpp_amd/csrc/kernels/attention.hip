@@ -35,7 +35,8 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(const uint16_t
                                                                    const int32_t * __restrict__ pos1,
                                                                    const int32_t * __restrict__ pos2, float eps,
                                                                    float ts128, float ts44, float ts42,
-                                                                   int64_t chunk_tokens, int64_t chunk_stride) {
+                                                                   int64_t chunk_tokens, int64_t chunk_stride,
+                                                                   int64_t lo_off) {
     __shared__ float red[kQkThreads / 64];
     const int64_t t = blockIdx.x;
     // Row t is token tl of chunk cb: positions by tl, output in chunk cb's slice.
@@ -86,7 +87,12 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(const uint16_t
             b = rb;
         }
         uint32_t * out = (uint32_t *) (dst + cb * chunk_stride + ((int64_t) h * dst_tokens + tok0 + tl) * head_dim + dd);
-        *out = pack_bf16x2(a, b);
+        const uint32_t hi = pack_bf16x2(a, b);
+        *out = hi;
+        // lo plane: the f32 value less its bf16 rounding (exact in f32).
+        if (lo_off)
+            *(uint32_t *) ((uint16_t *) out + lo_off) =
+                pack_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
     }
 }
 
@@ -102,7 +108,7 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
                                                           const int32_t * __restrict__ pos1,
                                                           const int32_t * __restrict__ pos2, float eps, float l2ts128,
                                                           float l2ts44, float l2ts42, int64_t chunk_tokens,
-                                                          int64_t chunk_stride) {
+                                                          int64_t chunk_stride, int64_t lo_off) {
     __shared__ float red[16];
     const int64_t t = blockIdx.x;
     const int64_t b = t / chunk_tokens, tl = t - b * chunk_tokens;
@@ -130,16 +136,24 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
         const int c = (int) threadIdx.x + i * (int) blockDim.x;
         if (c >= nchunk) continue;
         const int e0 = 8 * c, h = e0 / head_dim, dd0 = e0 % head_dim;
-        *(uint4 *) (dst + b * chunk_stride + ((int64_t) h * dst_tokens + tok0 + tl) * head_dim + dd0) =
-            qk_chunk(v[i], inv_rms, wv[i], dd0, rt);
+        uint16_t * o = dst + b * chunk_stride + ((int64_t) h * dst_tokens + tok0 + tl) * head_dim + dd0;
+        if (lo_off) {
+            uint4 hi, lo;
+            qk_chunk_hilo(v[i], inv_rms, wv[i], dd0, rt, hi, lo);
+            *(uint4 *) o = hi;
+            *(uint4 *) (o + lo_off) = lo;
+        } else {
+            *(uint4 *) o = qk_chunk(v[i], inv_rms, wv[i], dd0, rt);
+        }
     }
 }
 
 hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void * dst, int64_t heads, int64_t head_dim,
                                int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode, const int32_t * pos0,
                                const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s,
-                               int64_t chunk_tokens, int64_t chunk_stride) {
+                               int64_t chunk_tokens, int64_t chunk_stride, int64_t lo_off) {
     if (tokens <= 0) return hipSuccess;
+    if (lo_off && ((lo_off & 7) || (chunk_tokens != tokens && chunk_tokens > 0))) return hipErrorInvalidValue;
     if (chunk_tokens <= 0) chunk_tokens = tokens;
     if (tokens % chunk_tokens != 0) return hipErrorInvalidValue;
     const int64_t d = heads * head_dim;
@@ -155,7 +169,7 @@ hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void
     hipLaunchKernelGGL(qk_norm_rope_vec<CPT>, dim3((unsigned) tokens), dim3((unsigned) threads), 0, s,            \
                        (const uint16_t *) x, ldx, (const uint16_t *) w, (uint16_t *) dst, (int) heads, (int) head_dim, \
                        dst_tokens, tok0, rope_mode, pos0, pos1, pos2, eps, l2ts128, l2ts44, l2ts42, chunk_tokens,    \
-                       chunk_stride)
+                       chunk_stride, lo_off)
         if (cpt == 1) WAMX_QK_VEC(1);
         else if (cpt == 2) WAMX_QK_VEC(2);
         else WAMX_QK_VEC(4);
@@ -170,7 +184,7 @@ hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void
     const float ts42 = powf(freq_base, -2.0f / 42.0f);
     hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned) tokens), dim3(kQkThreads), 0, s, (const uint16_t *) x, ldx,
                        (const uint16_t *) w, (uint16_t *) dst, (int) heads, (int) head_dim, dst_tokens, tok0, rope_mode,
-                       pos0, pos1, pos2, eps, ts128, ts44, ts42, chunk_tokens, chunk_stride);
+                       pos0, pos1, pos2, eps, ts128, ts44, ts42, chunk_tokens, chunk_stride, lo_off);
     return hipGetLastError();
 }
 
@@ -218,6 +232,10 @@ struct AttnParams {
     // partials are then indexed [split][x][query of the block] and
     // joint_attn_merge maps its rows the same way.
     int64_t unit0, units;
+    // f32-accurate scores (attn_prefill_kernel<., true>): the remainders of
+    // Q and of source a's K, laid out as q and k[0].
+    const uint16_t * q_lo;
+    const uint16_t * k_lo;
 };
 
 // attn_prefill's workgroup: 4 waves x 32 queries of one head.
@@ -534,8 +552,10 @@ __device__ __forceinline__ int pf_vswz(int d, int c) { return c ^ ((d >> 1) & 7)
 struct PfBlk {
     const uint16_t * kb;
     const uint16_t * vb;
+    const uint16_t * klb;  // K remainder (f32-accurate scores), source a only
     int64_t vld, k0, nk;
 };
+template <bool HILO = false>
 __device__ __forceinline__ PfBlk pf_locate(const AttnParams & p, int64_t h, int nblk_a, int blk) {
     const int seg = blk < nblk_a ? 0 : 1;
     PfBlk r;
@@ -544,6 +564,7 @@ __device__ __forceinline__ PfBlk pf_locate(const AttnParams & p, int64_t h, int 
     r.k0 = (int64_t) (blk - (seg ? nblk_a : 0)) * kPfKeys;
     r.kb = p.k[seg] + h * r.nk * kDh;
     r.vb = p.vt[seg] + h * kDh * r.vld;
+    r.klb = HILO ? p.k_lo + h * r.nk * kDh : nullptr;
     return r;
 }
 
@@ -551,6 +572,8 @@ __device__ __forceinline__ PfBlk pf_locate(const AttnParams & p, int64_t h, int 
 // kPfWaves waves: 8 global_load_lds_dwordx4 per thread.  DMA slots: K tile
 // 1024 chunks (key = s / 16), V^T tile 1024 chunks (row = s / 8).  Rows past
 // the source end are clamped to its last key (the consumer masks them).
+// HILO: the K remainder tile follows the V^T tile, same layout (4 more).
+template <bool HILO = false>
 __device__ __forceinline__ void pf_dma(const PfBlk & bl, uint16_t * stage, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -559,6 +582,10 @@ __device__ __forceinline__ void pf_dma(const PfBlk & bl, uint16_t * stage, int w
         const int64_t kr = min(bl.k0 + key, bl.nk - 1);
         __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.kb + kr * kDh + 8 * c),
                                          (lds_void_t *) (stage + (i * kPfWaves + wave) * 512), 16, 0, 0);
+        if constexpr (HILO)
+            __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.klb + kr * kDh + 8 * c),
+                                             (lds_void_t *) (stage + kPfStageElems + (i * kPfWaves + wave) * 512), 16,
+                                             0, 0);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -576,6 +603,7 @@ constexpr int kPfDmaPerBlock = 8;  // global_load_lds per thread per block
 // partial last block): 32-bit byte offsets of this thread's K and V^T chunks
 // from the block's first key row / first V^T column (V^T rows vld apart; the
 // launcher keeps 128 rows within 2^31 bytes) on 64-bit block base addresses.
+template <bool HILO = false>
 __device__ __forceinline__ void pf_dma_full(const PfBlk & bl, uint16_t * stage, int wave, int lane) {
     const char * kb = (const char *) (bl.kb + bl.k0 * kDh);
     const char * vb = (const char *) (bl.vb + bl.k0);
@@ -586,6 +614,10 @@ __device__ __forceinline__ void pf_dma_full(const PfBlk & bl, uint16_t * stage, 
         const uint32_t off = (key * kDh + 8 * (uint32_t) pf_kswz((int) key, (int) (slot & 15))) * 2;
         __builtin_amdgcn_global_load_lds((glb_void_t *) (kb + off),
                                          (lds_void_t *) (stage + (i * kPfWaves + wave) * 512), 16, 0, 0);
+        if constexpr (HILO)
+            __builtin_amdgcn_global_load_lds((glb_void_t *) ((const char *) (bl.klb + bl.k0 * kDh) + off),
+                                             (lds_void_t *) (stage + kPfStageElems + (i * kPfWaves + wave) * 512), 16,
+                                             0, 0);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -597,10 +629,15 @@ __device__ __forceinline__ void pf_dma_full(const PfBlk & bl, uint16_t * stage, 
     }
 }
 
-template <bool SPLIT>
-__global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnParams p) {
-    __shared__ __align__(16) uint16_t st0[kPfStageElems];
-    __shared__ __align__(16) uint16_t st1[kPfStageElems];
+// HILO: f32-accurate scores from bf16 hi/lo planes of Q and K (q_lo, k_lo):
+// S^T = K Q^T + K Q_lo^T + K_lo Q^T with fp32 accumulation, the K remainder
+// tile staged after V^T (48 KB stages, one workgroup per CU).  One key
+// source; no key split.
+template <bool SPLIT, bool HILO = false>
+__global__ __launch_bounds__(kPfWaves * 64, HILO ? 1 : 2) void attn_prefill_kernel(AttnParams p) {
+    constexpr int kStage = kPfStageElems + (HILO ? kPfKeys * kDh : 0);
+    __shared__ __align__(16) uint16_t st0[kStage];
+    __shared__ __align__(16) uint16_t st1[kStage];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, hl = lane >> 5;
     // Work of this workgroup: head h, queries from q0 (and key range
@@ -612,25 +649,30 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
     const int nblk = nblk_a + (int) ((p.seg_len[1] + kPfKeys - 1) / kPfKeys);
     const int b_begin = SPLIT ? (int) blockIdx.z * (int) p.split_blocks : 0;
     const int b_end = SPLIT ? min(nblk, b_begin + (int) p.split_blocks) : nblk;
-    auto locate = [&](int blk) { return pf_locate(p, h, nblk_a, blk); };
+    auto locate = [&](int blk) { return pf_locate<HILO>(p, h, nblk_a, blk); };
     // Copies of block blk into a stage: full blocks by pf_dma_full, a
     // source's partial last block by pf_dma, which clamps its rows.  Both
     // issue kPfDmaPerBlock copies.
     auto dma = [&](int blk, uint16_t * stage) {
         blk = min(blk, b_end - 1);
         const PfBlk bl = locate(blk);
-        if (bl.k0 + kPfKeys <= bl.nk) pf_dma_full(bl, stage, wave, lane);
-        else pf_dma(bl, stage, wave, lane);
+        if (bl.k0 + kPfKeys <= bl.nk) pf_dma_full<HILO>(bl, stage, wave, lane);
+        else pf_dma<HILO>(bl, stage, wave, lane);
     };
 
     // Q^T fragments (B operand of S^T = K Q^T): lane holds query l32 of the
     // wave, dims 16s + 8hl .. +8 for k-step s.
-    bf16x8_t qf[8];
+    bf16x8_t qf[8], ql[HILO ? 8 : 1];
     {
         const int64_t qi = min(q0 + 32 * wave + l32, p.tq - 1);
         const uint16_t * qrow = p.q + (h * p.tq + qi) * kDh + 8 * hl;
 #pragma unroll
         for (int s = 0; s < 8; ++s) qf[s] = *(const bf16x8_t *) (qrow + 16 * s);
+        if constexpr (HILO) {
+            const uint16_t * qlrow = p.q_lo + (h * p.tq + qi) * kDh + 8 * hl;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) ql[s] = *(const bf16x8_t *) (qlrow + 16 * s);
+        }
     }
     // This lane's operand positions in a stage (elements): the K fragment of
     // k-step s is row l32 of key tile t (t adds 32 rows), chunk 2s + hl; the
@@ -681,18 +723,52 @@ __global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnPara
 #pragma unroll
                 for (int t = 0; t < 2; ++t) kb[j][t] = *(const bf16x8_t *) (stage + 32 * t * kDh + kro[2 * b + j]);
         };
-        kread(0, kf[0]);
-        kread(1, kf[1]);
-        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (HILO) {
+            // Half-batch x = 2b + lo: k-steps 2b, 2b+1 of the K tile (lo = 0:
+            // K Q^T and K Q_lo^T) or of the K remainder tile (lo = 1: K_lo
+            // Q^T), through the same two fragment buffers.
+            auto kread_x = [&](int x, bf16x8_t (&kb)[2][2]) __attribute__((always_inline)) {
+                const uint16_t * base = (x & 1) ? stage + kPfStageElems : stage;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-                    sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[b & 1][j][t], qf[2 * b + j], sacc[t], 0, 0, 0);
+                    for (int t = 0; t < 2; ++t)
+                        kb[j][t] = *(const bf16x8_t *) (base + 32 * t * kDh + kro[2 * (x >> 1) + j]);
+            };
+            kread_x(0, kf[0]);
+            kread_x(1, kf[1]);
             __builtin_amdgcn_sched_barrier(0);
-            if (b + 2 < 4) kread(b + 2, kf[b & 1]);
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+                const int b = x >> 1;
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[x & 1][j][t], qf[2 * b + j], sacc[t], 0,
+                                                                          0, 0);
+                        if (!(x & 1))
+                            sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[x & 1][j][t], ql[2 * b + j], sacc[t],
+                                                                              0, 0, 0);
+                    }
+                __builtin_amdgcn_sched_barrier(0);
+                if (x + 2 < 8) kread_x(x + 2, kf[x & 1]);
+            }
+        } else {
+            kread(0, kf[0]);
+            kread(1, kf[1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+                        sacc[t] =
+                            __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[b & 1][j][t], qf[2 * b + j], sacc[t], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (b + 2 < 4) kread(b + 2, kf[b & 1]);
+            }
         }
         // V^T operands of PV k-step g = 2t + hh (dim tile i), one k-step read
         // ahead.
@@ -1199,6 +1275,19 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     };
     const bool flash = flash_ok(0) && flash_ok(1) && p.seg_len[0] > 0 && ((uintptr_t) p.q & 15) == 0 &&
                        ((uintptr_t) p.out & 15) == 0;
+    // f32-accurate scores from hi/lo planes (one source, the prefix's
+    // visual cross-attention): the flash kernel's HILO form, plain grid.
+    if (a.q_lo || a.k_lo) {
+        if (!a.q_lo || !a.k_lo || p.seg_len[1] != 0 || !flash || ((uintptr_t) a.q_lo & 15) ||
+            ((uintptr_t) a.k_lo & 15) || p.heads != p.hb)
+            return hipErrorInvalidValue;
+        p.q_lo = (const uint16_t *) a.q_lo;
+        p.k_lo = (const uint16_t *) a.k_lo;
+        const int64_t qblocks = (a.tq + kPfQueries - 1) / kPfQueries;
+        hipLaunchKernelGGL((attn_prefill_kernel<false, true>), dim3((unsigned) a.heads, (unsigned) qblocks),
+                           dim3(kPfWaves * 64), 0, s, p);
+        return hipGetLastError();
+    }
     if (flash && a.tq > 64 && p.seg_len[1] == 0) {
         const int64_t qblocks = (a.tq + kPfQueries - 1) / kPfQueries;
         // The (head, query block) units fill rounds of two workgroups per CU.

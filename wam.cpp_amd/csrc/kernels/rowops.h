@@ -103,10 +103,10 @@ __device__ __forceinline__ RopeTok rope_tok(int mode, const int32_t * pos0, cons
 // RMSNorm-scaled chunk (x * inv_rms * w, f32) rotated in (even, odd) pairs:
 // theta = pos * base^(-2i/n) for pair i of its rope section, f32 sincos.
 // e0 is the chunk's first element within the head (head_dim % 8 == 0).
-__device__ __forceinline__ uint4 qk_chunk(const float (&v)[8], float inv_rms, const uint4 & wv, int dd0,
-                                          const RopeTok & r) {
+// The f32 values, before the bf16 cast.
+__device__ __forceinline__ void qk_chunk_f32(const float (&v)[8], float inv_rms, const uint4 & wv, int dd0,
+                                             const RopeTok & r, float (&o)[8]) {
     const uint32_t wu[4] = {wv.x, wv.y, wv.z, wv.w};
-    uint32_t packed[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         float a = v[2 * j] * inv_rms * __uint_as_float(wu[j] << 16);
@@ -125,9 +125,30 @@ __device__ __forceinline__ uint4 qk_chunk(const float (&v)[8], float inv_rms, co
             a = ra;
             b = rb;
         }
-        packed[j] = pack_bf16x2(a, b);
+        o[2 * j] = a;
+        o[2 * j + 1] = b;
     }
-    return make_uint4(packed[0], packed[1], packed[2], packed[3]);
+}
+__device__ __forceinline__ uint4 qk_chunk(const float (&v)[8], float inv_rms, const uint4 & wv, int dd0,
+                                          const RopeTok & r) {
+    float o[8];
+    qk_chunk_f32(v, inv_rms, wv, dd0, r, o);
+    return pack8(o);
+}
+// The same chunk as two bf16 planes: hi = bf16(o) and lo = bf16(o - hi), so
+// hi + lo carries the f32 value to about 2^-17 relative (o - hi is exact in
+// f32).  Products of hi and lo parts are exact in fp32, which lets bf16 MFMA
+// form f32-accurate dot products as hi*hi + hi*lo + lo*hi.
+__device__ __forceinline__ void qk_chunk_hilo(const float (&v)[8], float inv_rms, const uint4 & wv, int dd0,
+                                              const RopeTok & r, uint4 & hi, uint4 & lo) {
+    float o[8], l[8];
+    qk_chunk_f32(v, inv_rms, wv, dd0, r, o);
+    hi = pack8(o);
+    float h[8];
+    unpack8(hi, h);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) l[e] = o[e] - h[e];
+    lo = pack8(l);
 }
 
 }  // namespace wamx

@@ -120,6 +120,12 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_op_qk_norm_rope": (C.c_int, [vp, vp, i64, vp, vp, i64, i64, i64, i64, i64, C.c_int,
                                            vp, vp, vp, f32, f32]),
         "wamx_op_joint_attn": (C.c_int, [vp, vp, vp, vp, i64, vp, vp, i64, i64, vp, i64, i64, i64, f32]),
+        "wamx_op_qk_norm_rope_hilo": (C.c_int, [vp, vp, i64, vp, vp, vp, i64, i64, i64, i64, i64, C.c_int,
+                                                vp, vp, vp, f32, f32]),
+        "wamx_op_joint_attn_hilo": (C.c_int, [vp, vp, vp, vp, vp, vp, i64, i64, vp, i64, i64, i64, f32]),
+        "wamx_qk_norm_rope_hilo": (TensorP, [vp, TensorP, TensorP, TensorP, i64, C.c_int, TensorP, TensorP,
+                                             TensorP, f32, f32]),
+        "wamx_joint_attn_hilo": (TensorP, [vp, TensorP, TensorP, TensorP, f32]),
         "wamx_op_soft_max_f32": (C.c_int, [vp, vp, vp, i64, i64, f32]),
         "wamx_fill_normal": (C.c_int, [vp, vp, i32, i64, C.c_uint64, f32, f32]),
         "wamx_timer_new": (vp, [vp]),
