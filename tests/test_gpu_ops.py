@@ -402,6 +402,40 @@ def test_visual_cross_attention_f32_scores(wx, be, orc, wscale):
         assert rel_err(got_b, ref) > REL_TOL, "bf16 scores pass at large scores: the test does not discriminate"
 
 
+@pytest.mark.parametrize("H,tq,nk", [(2, 200, 72), (3, 64, 520), (1, 1, 8)])
+def test_joint_attention_hilo_shapes(wx, be, H, tq, nk):
+    """The hi/lo attention on the plain grid: ragged query blocks and a
+    partial last key block (its K and K-remainder rows clamped, scores
+    masked), against the f32-score reference at the per-op bar."""
+    print(f"joint_attn_hilo H={H} tq={tq} nk={nk}", flush=True)
+    rng = np.random.default_rng(H * tq + nk)
+    dh = 128
+    qf = rng.standard_normal((H, tq, dh)).astype(np.float32)
+    kf = rng.standard_normal((H, nk, dh)).astype(np.float32)
+    v = bf16(rng.standard_normal((H, dh, nk)))
+    ld = (nk + 7) // 8 * 8
+    vt = np.zeros((H, dh, ld), np.uint16)
+    vt[:, :, :nk] = v
+    hi_q, hi_k = bf16(qf), bf16(kf)
+    lo_q, lo_k = bf16(qf - f32(hi_q)), bf16(kf - f32(hi_k))
+    dq, dk = dev(be, np.stack([hi_q, lo_q])), dev(be, np.stack([hi_k, lo_k]))
+    dvt = dev(be, vt)
+    dout = be.empty(max(tq, 1) * H * dh * 2)
+    scale = 1.0 / np.sqrt(dh)
+    wx.check(be.lib.wamx_op_joint_attn_hilo(be.ptr, dq.ptr, dq.ptr + H * tq * dh * 2, dk.ptr, dk.ptr + H * nk * dh * 2,
+                                            dvt.ptr, nk, ld, dout.ptr, H, dh, tq, scale), "joint_attn_hilo")
+    got = f32(dout.download(np.uint16, (tq, H * dh)))
+    q64 = (f32(hi_q).astype(np.float64) + f32(lo_q)).astype(np.float64)
+    k64 = (f32(hi_k).astype(np.float64) + f32(lo_k)).astype(np.float64)
+    ref = np.empty((tq, H * dh), np.float32)
+    for h in range(H):
+        sc = q64[h] @ k64[h].T * scale
+        p = np.exp(sc - sc.max(axis=1, keepdims=True))
+        p = f32(bf16((p / p.sum(axis=1, keepdims=True)).astype(np.float32))).astype(np.float64)
+        ref[:, h * dh:(h + 1) * dh] = (p @ f32(v[h]).astype(np.float64).T).astype(np.float32)
+    assert_parity(got, f32(bf16(ref)), what="joint_attn_hilo")
+
+
 def test_empty_and_refused_sizes(wx, be):
     """Edge sizes through the C ABI: zero queries and zero rows are no-ops; an
     attention over no keys and a linear over no tokens are refused with an

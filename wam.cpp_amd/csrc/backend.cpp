@@ -1679,6 +1679,8 @@ wamx_status wamx_op_joint_attn_hilo(wamx_backend_t be, const void * q, const voi
     a.head_dim = head_dim;
     a.tq = tq;
     a.scale = scale;
+    a.ws = be->workspace;
+    a.ws_bytes = kWorkspaceBytes;
     WAMX_LAUNCH(launch_joint_attn(a, be->stream));
 }
 

@@ -572,8 +572,6 @@ __device__ __forceinline__ PfBlk pf_locate(const AttnParams & p, int64_t h, int 
 // kPfWaves waves: 8 global_load_lds_dwordx4 per thread.  DMA slots: K tile
 // 1024 chunks (key = s / 16), V^T tile 1024 chunks (row = s / 8).  Rows past
 // the source end are clamped to its last key (the consumer masks them).
-// HILO: the K remainder tile follows the V^T tile, same layout (4 more).
-template <bool HILO = false>
 __device__ __forceinline__ void pf_dma(const PfBlk & bl, uint16_t * stage, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -582,10 +580,6 @@ __device__ __forceinline__ void pf_dma(const PfBlk & bl, uint16_t * stage, int w
         const int64_t kr = min(bl.k0 + key, bl.nk - 1);
         __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.kb + kr * kDh + 8 * c),
                                          (lds_void_t *) (stage + (i * kPfWaves + wave) * 512), 16, 0, 0);
-        if constexpr (HILO)
-            __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.klb + kr * kDh + 8 * c),
-                                             (lds_void_t *) (stage + kPfStageElems + (i * kPfWaves + wave) * 512), 16,
-                                             0, 0);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -603,7 +597,6 @@ constexpr int kPfDmaPerBlock = 8;  // global_load_lds per thread per block
 // partial last block): 32-bit byte offsets of this thread's K and V^T chunks
 // from the block's first key row / first V^T column (V^T rows vld apart; the
 // launcher keeps 128 rows within 2^31 bytes) on 64-bit block base addresses.
-template <bool HILO = false>
 __device__ __forceinline__ void pf_dma_full(const PfBlk & bl, uint16_t * stage, int wave, int lane) {
     const char * kb = (const char *) (bl.kb + bl.k0 * kDh);
     const char * vb = (const char *) (bl.vb + bl.k0);
@@ -614,10 +607,6 @@ __device__ __forceinline__ void pf_dma_full(const PfBlk & bl, uint16_t * stage, 
         const uint32_t off = (key * kDh + 8 * (uint32_t) pf_kswz((int) key, (int) (slot & 15))) * 2;
         __builtin_amdgcn_global_load_lds((glb_void_t *) (kb + off),
                                          (lds_void_t *) (stage + (i * kPfWaves + wave) * 512), 16, 0, 0);
-        if constexpr (HILO)
-            __builtin_amdgcn_global_load_lds((glb_void_t *) ((const char *) (bl.klb + bl.k0 * kDh) + off),
-                                             (lds_void_t *) (stage + kPfStageElems + (i * kPfWaves + wave) * 512), 16,
-                                             0, 0);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -629,15 +618,29 @@ __device__ __forceinline__ void pf_dma_full(const PfBlk & bl, uint16_t * stage, 
     }
 }
 
+// The K remainder tile of a block (f32-accurate scores), as pf_dma's K tile
+// (clamped rows) into its own LDS tile.
+__device__ __forceinline__ void pf_dma_klo(const PfBlk & bl, uint16_t * tile, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int slot = (i * kPfWaves + wave) * 64 + lane;
+        const int key = slot >> 4, c = pf_kswz(key, slot & 15);
+        const int64_t kr = min(bl.k0 + key, bl.nk - 1);
+        __builtin_amdgcn_global_load_lds((glb_void_t *) (bl.klb + kr * kDh + 8 * c),
+                                         (lds_void_t *) (tile + (i * kPfWaves + wave) * 512), 16, 0, 0);
+    }
+}
+
 // HILO: f32-accurate scores from bf16 hi/lo planes of Q and K (q_lo, k_lo):
-// S^T = K Q^T + K Q_lo^T + K_lo Q^T with fp32 accumulation, the K remainder
-// tile staged after V^T (48 KB stages, one workgroup per CU).  One key
-// source; no key split.
+// S^T = K Q^T + K Q_lo^T + K_lo Q^T with fp32 accumulation.  The K remainder
+// has one LDS tile (16 KB; 80 KB per workgroup, two per CU): block b+1's is
+// copied in after a barrier that follows block b's score MFMAs, and lands
+// during its softmax and P.V.  One key source; no key split.
 template <bool SPLIT, bool HILO = false>
-__global__ __launch_bounds__(kPfWaves * 64, HILO ? 1 : 2) void attn_prefill_kernel(AttnParams p) {
-    constexpr int kStage = kPfStageElems + (HILO ? kPfKeys * kDh : 0);
-    __shared__ __align__(16) uint16_t st0[kStage];
-    __shared__ __align__(16) uint16_t st1[kStage];
+__global__ __launch_bounds__(kPfWaves * 64, 2) void attn_prefill_kernel(AttnParams p) {
+    __shared__ __align__(16) uint16_t st0[kPfStageElems];
+    __shared__ __align__(16) uint16_t st1[kPfStageElems];
+    __shared__ __align__(16) uint16_t klo[HILO ? kPfKeys * kDh : 8];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, hl = lane >> 5;
     // Work of this workgroup: head h, queries from q0 (and key range
@@ -656,9 +659,10 @@ __global__ __launch_bounds__(kPfWaves * 64, HILO ? 1 : 2) void attn_prefill_kern
     auto dma = [&](int blk, uint16_t * stage) {
         blk = min(blk, b_end - 1);
         const PfBlk bl = locate(blk);
-        if (bl.k0 + kPfKeys <= bl.nk) pf_dma_full<HILO>(bl, stage, wave, lane);
-        else pf_dma<HILO>(bl, stage, wave, lane);
+        if (bl.k0 + kPfKeys <= bl.nk) pf_dma_full(bl, stage, wave, lane);
+        else pf_dma(bl, stage, wave, lane);
     };
+    auto dma_lo = [&](int blk) { pf_dma_klo(locate(min(blk, b_end - 1)), klo, wave, lane); };
 
     // Q^T fragments (B operand of S^T = K Q^T): lane holds query l32 of the
     // wave, dims 16s + 8hl .. +8 for k-step s.
@@ -707,7 +711,7 @@ __global__ __launch_bounds__(kPfWaves * 64, HILO ? 1 : 2) void attn_prefill_kern
     // block body exists once); its V^T columns there are zeroed in the stage
     // before the block.
     constexpr float kPfSlack = 8.0f;
-    auto block = [&](int valid, const uint16_t * stage) __attribute__((always_inline)) {
+    auto block = [&](int valid, const uint16_t * stage, int next) __attribute__((always_inline)) {
         // S^T tiles: key tile t (32 keys) x the wave's 32 queries.  K
         // fragments in batches of two k-steps (both tiles), two batches in
         // flight ahead of the MFMAs.
@@ -728,7 +732,7 @@ __global__ __launch_bounds__(kPfWaves * 64, HILO ? 1 : 2) void attn_prefill_kern
             // K Q^T and K Q_lo^T) or of the K remainder tile (lo = 1: K_lo
             // Q^T), through the same two fragment buffers.
             auto kread_x = [&](int x, bf16x8_t (&kb)[2][2]) __attribute__((always_inline)) {
-                const uint16_t * base = (x & 1) ? stage + kPfStageElems : stage;
+                const uint16_t * base = (x & 1) ? klo : stage;
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -754,6 +758,10 @@ __global__ __launch_bounds__(kPfWaves * 64, HILO ? 1 : 2) void attn_prefill_kern
                 __builtin_amdgcn_sched_barrier(0);
                 if (x + 2 < 8) kread_x(x + 2, kf[x & 1]);
             }
+            // Every wave has read this block's K remainder: the tile takes the
+            // next block's.
+            cta_barrier();
+            if (next < b_end) dma_lo(next);
         } else {
             kread(0, kf[0]);
             kread(1, kf[1]);
@@ -861,10 +869,11 @@ __global__ __launch_bounds__(kPfWaves * 64, HILO ? 1 : 2) void attn_prefill_kern
             }
             __syncthreads();
         }
-        block((int) min((int64_t) kPfKeys, bl.nk - bl.k0), cur);
+        block((int) min((int64_t) kPfKeys, bl.nk - bl.k0), cur, blk + 1);
     };
 
     dma(b_begin, st0);
+    if constexpr (HILO) dma_lo(b_begin);
     for (int blk = b_begin; blk < b_end; blk += 2) {
         step(blk, st0, st1);
         if (blk + 1 < b_end) step(blk + 1, st1, st0);
@@ -1276,30 +1285,29 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
     const bool flash = flash_ok(0) && flash_ok(1) && p.seg_len[0] > 0 && ((uintptr_t) p.q & 15) == 0 &&
                        ((uintptr_t) p.out & 15) == 0;
     // f32-accurate scores from hi/lo planes (one source, the prefix's
-    // visual cross-attention): the flash kernel's HILO form, plain grid.
-    if (a.q_lo || a.k_lo) {
+    // visual cross-attention): the flash kernel's HILO form.
+    const bool hilo = a.q_lo || a.k_lo;
+    if (hilo) {
         if (!a.q_lo || !a.k_lo || p.seg_len[1] != 0 || !flash || ((uintptr_t) a.q_lo & 15) ||
             ((uintptr_t) a.k_lo & 15) || p.heads != p.hb)
             return hipErrorInvalidValue;
         p.q_lo = (const uint16_t *) a.q_lo;
         p.k_lo = (const uint16_t *) a.k_lo;
-        const int64_t qblocks = (a.tq + kPfQueries - 1) / kPfQueries;
-        hipLaunchKernelGGL((attn_prefill_kernel<false, true>), dim3((unsigned) a.heads, (unsigned) qblocks),
-                           dim3(kPfWaves * 64), 0, s, p);
-        return hipGetLastError();
     }
-    if (flash && a.tq > 64 && p.seg_len[1] == 0) {
+    if (flash && (a.tq > 64 || hilo) && p.seg_len[1] == 0) {
         const int64_t qblocks = (a.tq + kPfQueries - 1) / kPfQueries;
         // The (head, query block) units fill rounds of two workgroups per CU.
         // When the last round would run at most a quarter full (3072 queries
         // x 24 heads: 576 units on 512 slots), its units are split into key
         // ranges that fill it instead, with their partials merged after.
         // Sources of fewer than 16 blocks (the 512-key prompt) keep the plain
-        // grid: their ranges would be one or two blocks long.
+        // grid with bf16 scores (their ranges would be one or two blocks
+        // long); the hi/lo form, with three times the score MFMAs per block,
+        // splits them too (measured: 3072 x 512 x 24, 72 us plain).
         const int64_t units = a.heads * qblocks, slots = 2 * (int64_t) device_cus();
         const int64_t tail = slots > 0 ? units % slots : 0;
         const int64_t nblk = (p.seg_len[0] + kPfKeys - 1) / kPfKeys;
-        if (units > slots && tail > 0 && 4 * tail <= slots && nblk >= 16) {
+        if (units > slots && tail > 0 && 4 * tail <= slots && (nblk >= 16 || (hilo && nblk >= 2))) {
             int64_t nsplit = std::min<int64_t>({slots / tail, nblk / 2, (int64_t) kMaxSplits});
             p.split_blocks = (nblk + nsplit - 1) / nsplit;
             nsplit = (nblk + p.split_blocks - 1) / p.split_blocks;
@@ -1307,23 +1315,37 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
             if (nsplit >= 2 && a.ws && (size_t) nsplit * rows * (kDh + 2) * sizeof(float) <= a.ws_bytes) {
                 p.unit0 = 0;
                 p.units = units - tail;
-                hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3((unsigned) p.units), dim3(kPfWaves * 64), 0, s, p);
+                if (hilo)
+                    hipLaunchKernelGGL((attn_prefill_kernel<false, true>), dim3((unsigned) p.units),
+                                       dim3(kPfWaves * 64), 0, s, p);
+                else
+                    hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3((unsigned) p.units), dim3(kPfWaves * 64), 0,
+                                       s, p);
                 p.unit0 = units - tail;
                 p.units = tail;
                 p.part_o = (float *) a.ws;
                 p.part_m = p.part_o + (size_t) nsplit * rows * kDh;
                 p.part_l = p.part_m + (size_t) nsplit * rows;
-                hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3((unsigned) tail, 1, (unsigned) nsplit),
-                                   dim3(kPfWaves * 64), 0, s, p);
+                if (hilo)
+                    hipLaunchKernelGGL((attn_prefill_kernel<true, true>), dim3((unsigned) tail, 1, (unsigned) nsplit),
+                                       dim3(kPfWaves * 64), 0, s, p);
+                else
+                    hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3((unsigned) tail, 1, (unsigned) nsplit),
+                                       dim3(kPfWaves * 64), 0, s, p);
                 hipLaunchKernelGGL(joint_attn_merge, dim3((unsigned) ((rows + kMergeRows - 1) / kMergeRows)),
                                    dim3(32 * kMergeRows), 0, s, p, (int) nsplit, (int64_t) rows);
                 return hipGetLastError();
             }
         }
-        hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3((unsigned) a.heads, (unsigned) qblocks),
-                           dim3(kPfWaves * 64), 0, s, p);
+        if (hilo)
+            hipLaunchKernelGGL((attn_prefill_kernel<false, true>), dim3((unsigned) a.heads, (unsigned) qblocks),
+                               dim3(kPfWaves * 64), 0, s, p);
+        else
+            hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3((unsigned) a.heads, (unsigned) qblocks),
+                               dim3(kPfWaves * 64), 0, s, p);
         return hipGetLastError();
     }
+    if (hilo) return hipErrorInvalidValue;
     // At most 64 queries (the 48-token denoise step) over long key sources:
     // attn_decode, one workgroup per (head, key range) with about one
     // workgroup per CU in all, every key read once; the ranges' fp32 partials
