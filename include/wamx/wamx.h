@@ -99,6 +99,8 @@ typedef enum wamx_op {
     WAMX_OP_QK_NORM_ROPE,     /* RMS_NORM(bf16->f32) + ROPE + CAST(bf16) + PERMUTE/CONT */
     WAMX_OP_JOINT_ATTN,       /* CONCAT(K,V) + MUL_MAT(K,Q) + SOFT_MAX + MUL_MAT(V,P) + PERMUTE */
     WAMX_OP_MODULATION,       /* CAST(f32) + ADD of the adaLN modulation and table */
+    WAMX_OP_EULER_STEP,       /* CAST(f32) x2 + MUL(dt) + ADD + CAST(bf16): scheduler_step */
+    WAMX_OP_MLP_SMALL,        /* [GELU_ERF] + (MUL_MAT + ADD bias [+ GELU_ERF]) x2, widths <= 128 */
     WAMX_OP_COUNT
 } wamx_op;
 
@@ -277,6 +279,24 @@ WAMX_API wamx_tensor * wamx_rms_norm_bf16_f32(wamx_context * ctx, wamx_tensor * 
  *
  * wamx_modulation: f32 [ne={d, 6, L}] = f32(mod [ne={d,6}]) + f32(table_l) for the
  *   L per-layer tables packed in `tables` [ne={d, 6, L}] (mot.cpp:137-145, 380-393).
+ *   A mod of S columns ([ne={6d, S}], S timesteps) gives [ne={d, 6, L, S}]:
+ *   column s against every table.
+ *
+ * wamx_euler_step: bf16 [ne={A, N}] = bf16(f32(action) + f32(velocity) * dt),
+ *   the flow-matching update of scheduler_step (weights.cpp:885-902: two
+ *   casts to f32, MUL by the f32 dt [1], ADD, cast to bf16), with the
+ *   product and the sum rounded separately as those two ggml ops do.
+ *
+ * wamx_mlp_small: two linear layers of at most 128 features on at most 128
+ *   inputs, as the action/state encoder and the action decoder chain them
+ *   (mot.cpp:16-55): optionally GELU_ERF of x first (flag
+ *   WAMX_MLP_GELU_IN), then h = bf16(bf16(W1 x) + b1) (the bf16-output
+ *   MUL_MAT and bf16 bias ADD of linear_with_activation, weights.cpp:819-831)
+ *   with GELU_ERF after it (WAMX_MLP_GELU_MID), then y = bf16(bf16(W2 h) +
+ *   b2) with GELU_ERF after it (WAMX_MLP_GELU_OUT).  x bf16 [ne={K0, N}],
+ *   W1 bf16 [ne={K0, M1}], b1 bf16 [M1], W2 bf16 [ne={M1, M2}], b2 bf16 [M2];
+ *   y bf16 [ne={M2, N}].  Each GELU_ERF rounds to bf16.  fp32 accumulation
+ *   (in k order).
  */
 WAMX_API wamx_tensor * wamx_linear(wamx_context * ctx, wamx_tensor * w, wamx_tensor * x, wamx_tensor * bias,
                                    int32_t epilogue, wamx_tensor * residual, wamx_tensor * gate);
@@ -291,6 +311,11 @@ WAMX_API wamx_tensor * wamx_qk_norm_rope_hilo(wamx_context * ctx, wamx_tensor * 
                                               wamx_tensor * pos1, wamx_tensor * pos2, float eps, float freq_base);
 WAMX_API wamx_tensor * wamx_joint_attn_hilo(wamx_context * ctx, wamx_tensor * q, wamx_tensor * k, wamx_tensor * v,
                                             float scale);
+WAMX_API wamx_tensor * wamx_euler_step(wamx_context * ctx, wamx_tensor * action, wamx_tensor * velocity,
+                                       wamx_tensor * dt);
+enum { WAMX_MLP_GELU_IN = 1, WAMX_MLP_GELU_MID = 2, WAMX_MLP_GELU_OUT = 4 };
+WAMX_API wamx_tensor * wamx_mlp_small(wamx_context * ctx, wamx_tensor * x, wamx_tensor * w1, wamx_tensor * b1,
+                                      wamx_tensor * w2, wamx_tensor * b2, int32_t flags);
 
 /* Graphs. */
 WAMX_API wamx_cgraph * wamx_new_graph(wamx_context * ctx, size_t max_nodes);

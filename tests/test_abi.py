@@ -147,6 +147,34 @@ def test_hilo_constructors(wx, ctx):
     assert not lib.wamx_joint_attn_hilo(ctx, q, k12, lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 12, 128, 24), 0.088)
 
 
+def test_denoise_glue_constructors(wx, ctx):
+    """EULER_STEP, MLP_SMALL and the timestep-batched MODULATION."""
+    lib = wx.load()
+    a = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 32, 48)
+    dt = lib.wamx_new_tensor_1d(ctx, wx.TYPE_F32, 1)
+    e = lib.wamx_euler_step(ctx, a, a, dt)
+    assert e and e.contents.op == wx.OP["EULER_STEP"] and shape(e) == (32, 48, 1, 1)
+    assert lib.wamx_backend_supports_op(None, e)
+    assert not lib.wamx_euler_step(ctx, a, lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 32, 47), dt)
+    assert not lib.wamx_euler_step(ctx, a, a, lib.wamx_new_tensor_1d(ctx, wx.TYPE_F32, 2))
+    w1 = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 32, 128)
+    b1 = lib.wamx_new_tensor_1d(ctx, wx.TYPE_BF16, 128)
+    w2 = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 128, 96)
+    b2 = lib.wamx_new_tensor_1d(ctx, wx.TYPE_BF16, 96)
+    m = lib.wamx_mlp_small(ctx, a, w1, b1, w2, b2, 2 | 4)
+    assert m and m.contents.op == wx.OP["MLP_SMALL"] and shape(m) == (96, 48, 1, 1)
+    assert lib.wamx_backend_supports_op(None, m)
+    assert not lib.wamx_mlp_small(ctx, a, w1, b1, w2, b1, 0)  # b2 length must be M2
+    wide = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 128, 3072)
+    assert not lib.wamx_mlp_small(ctx, lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 128, 48), w2, b2, wide,
+                                  lib.wamx_new_tensor_1d(ctx, wx.TYPE_BF16, 3072), 0)  # 3072 wide
+    mod = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 6 * 64, 10)
+    tab = lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 64, 6, 30)
+    md = lib.wamx_modulation(ctx, mod, tab)
+    assert md and shape(md) == (64, 6, 30, 10) and lib.wamx_backend_supports_op(None, md)
+    assert not lib.wamx_modulation(ctx, lib.wamx_new_tensor_1d(ctx, wx.TYPE_F32, 6 * 64 + 1), tab)
+
+
 def test_graph_order_and_uid(wx, ctx):
     lib = wx.load()
     x = lib.wamx_new_tensor_2d(ctx, wx.TYPE_F32, 16, 4)

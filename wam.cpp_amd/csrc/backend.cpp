@@ -674,7 +674,14 @@ static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
             return run_joint_attn(be, node);
         case WAMX_OP_MODULATION:
             return launch_modulation(s0->data, s0->type, s1->data, s1->type, (float *) node->data,
-                                     wamx_nelements(s0), s1->ne[2] * s1->ne[3], s);
+                                     s1->ne[0] * s1->ne[1], s1->ne[2] * s1->ne[3], s, node->ne[3]);
+        case WAMX_OP_EULER_STEP:
+            return launch_euler_step(s0->data, s1->data, (const float *) node->src[2]->data, node->data,
+                                     wamx_nelements(node), s);
+        case WAMX_OP_MLP_SMALL:
+            return launch_mlp_small(s0->data, s1->data, node->src[2]->data, node->src[3]->data, node->src[4]->data,
+                                    node->data, s0->ne[1], s0->ne[0], s1->ne[1], node->src[3]->ne[1],
+                                    node->op_params[0], s);
         default:
             return hipErrorNotSupported;
     }
@@ -827,6 +834,10 @@ static bool supports(const wamx_tensor * t) {
             return check_joint_attn(t) == nullptr;
         case WAMX_OP_MODULATION:
             return check_modulation(t) == nullptr;
+        case WAMX_OP_EULER_STEP:
+            return check_euler_step(t) == nullptr;
+        case WAMX_OP_MLP_SMALL:
+            return check_mlp_small(t) == nullptr;
         default:
             return false;
     }

@@ -20,6 +20,7 @@
 #include <map>
 #include <memory>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "common.h"
@@ -181,7 +182,20 @@ struct Builder {
     }
 
     // action_encoder / action_decoder (mot.cpp:16-55): linear + GELU_ERF x2 + linear.
+    // The two layers that are at most 128 wide on both sides run as one
+    // MLP_SMALL node: in + mid of the encoder (action_dim -> hidden ->
+    // hidden), mid + out of the decoder (hidden -> hidden -> action_dim).
     wamx_tensor * mlp3(const Mlp3 & p, wamx_tensor * x) {
+        auto small = [](const wamx_tensor * w) { return w->ne[0] <= 128 && w->ne[1] <= 128; };
+        if (x->type == WAMX_TYPE_BF16 && small(p.in_w) && small(p.mid_w)) {
+            wamx_tensor * h = wamx_mlp_small(ctx, x, p.in_w, p.in_b, p.mid_w, p.mid_b,
+                                             WAMX_MLP_GELU_MID | WAMX_MLP_GELU_OUT);
+            return lin(p.out_w, p.out_b, h);
+        }
+        if (small(p.mid_w) && small(p.out_w)) {
+            wamx_tensor * h = lin(p.in_w, p.in_b, x);
+            return wamx_mlp_small(ctx, h, p.mid_w, p.mid_b, p.out_w, p.out_b, WAMX_MLP_GELU_IN | WAMX_MLP_GELU_MID);
+        }
         wamx_tensor * h = wamx_gelu_erf(ctx, lin(p.in_w, p.in_b, x));
         h = wamx_gelu_erf(ctx, lin(p.mid_w, p.mid_b, h));
         return lin(p.out_w, p.out_b, h);
@@ -206,9 +220,10 @@ struct Builder {
         return att->ne[2] == 1 ? att : wamx_reshape_2d(ctx, att, att->ne[0], att->ne[1] * att->ne[2]);
     }
 
-    // View (layer l, part i) of a modulation tensor [width, 6, L] (f32).
-    wamx_tensor * part(wamx_tensor * mods, int64_t width, int l, int i) {
-        return wamx_view_1d(ctx, mods, width, (size_t) ((int64_t) l * 6 + i) * width * sizeof(float));
+    // View (layer l, part i, step s) of a modulation tensor [width, 6, L, S] (f32).
+    wamx_tensor * part(wamx_tensor * mods, int64_t width, int l, int i, int s = 0) {
+        const int64_t L = mods->ne[2];
+        return wamx_view_1d(ctx, mods, width, (size_t) (((int64_t) s * L + l) * 6 + i) * width * sizeof(float));
     }
 
     // Column view [ne0 = cols, ne1 = rows] of a packed projection output.
@@ -596,16 +611,22 @@ static bool build_denoise_graph(wamx_gwp_model * m) {
     Builder b(m, ctx);
     wamx_cgraph * g = m->graph[gi] = wamx_new_graph(ctx, (size_t) (40 * c.n_layers + 64) * c.num_steps + 64);
     wamx_tensor * action = m->in_action;  // bf16 [A, B*T]
+    // The time branch of build_condition (mot.cpp:69-82), the per-layer
+    // modulation (mot.cpp:130-145) and the output modulation (mot.cpp:468-486)
+    // depend on the step's timestep only: they are computed for every step at
+    // once, each step's timestep embedding a column of in_freqs.
+    wamx_tensor *temb_all, *mod_all;
+    b.condition(m->acond, m->in_freqs, &temb_all, &mod_all);             // [da, S], [6 da, S]
+    wamx_tensor * mods = wamx_modulation(ctx, mod_all, m->a_tables);     // [da, 6, L, S] f32
+    wamx_tensor * tab = wamx_reshape_3d(ctx, m->action_sst, da, 1, 2);
+    wamx_tensor * om = wamx_modulation(ctx, temb_all, tab);              // [da, 1, 2, S]: shift, scale
     for (int s = 0; s < c.num_steps; ++s) {
-        wamx_tensor * freq = wamx_view_2d(ctx, m->in_freqs, 256, 1, m->in_freqs->nb[1], (size_t) s * 256 * 4);
         wamx_tensor * dt = wamx_view_1d(ctx, m->in_dts, 1, (size_t) s * 4);
         wamx_tensor * h = b.mlp3(m->action_enc, action);  // [da, T]
-        wamx_tensor *temb, *mod;
-        b.condition(m->acond, freq, &temb, &mod);
-        wamx_tensor * mods = wamx_modulation(ctx, mod, m->a_tables);  // [da, 6, L]
         for (int l = 0; l < c.n_layers; ++l) {
             const ExpertLayer & e = m->act[l];
-            wamx_tensor * n = wamx_norm_modulation_bf16(ctx, h, b.part(mods, da, l, 1), b.part(mods, da, l, 0), c.eps);
+            wamx_tensor * n = wamx_norm_modulation_bf16(ctx, h, b.part(mods, da, l, 1, s), b.part(mods, da, l, 0, s),
+                                                        c.eps);
             wamx_tensor * qkv = b.lin(e.qkv_w, e.qkv_b, n);
             wamx_tensor * Q = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, dh, T, H, B);
             Q = wamx_qk_norm_rope(ctx, b.cols(qkv, d, 0), e.norm_q, Q, 0, 0, m->in_apos, nullptr, nullptr, c.eps,
@@ -617,23 +638,19 @@ static bool build_denoise_graph(wamx_gwp_model * m) {
             wamx_tensor * Va = b.store_v(qkv, 2 * d, b.vt_view(vraw, 0, T));
             // Keys [state, action, reference]: prefix cache split after the state token.
             wamx_tensor * att = b.rows(wamx_joint_attn(ctx, Q, m->pk[l], m->pv[l], Ka, Va, 1, b.scale));
-            h = b.lin(e.o_w, e.o_b, att, WAMX_EPI_BIAS_GATED, h, b.part(mods, da, l, 2));
-            h = b.cross_ffn_cached(e, h, m->lk[l], m->lv[l], b.part(mods, da, l, 3), b.part(mods, da, l, 4),
-                                   b.part(mods, da, l, 5));
+            h = b.lin(e.o_w, e.o_b, att, WAMX_EPI_BIAS_GATED, h, b.part(mods, da, l, 2, s));
+            h = b.cross_ffn_cached(e, h, m->lk[l], m->lv[l], b.part(mods, da, l, 3, s), b.part(mods, da, l, 4, s),
+                                   b.part(mods, da, l, 5, s));
         }
         // Output modulation: f32(action_scale_shift_table) + f32(temb) (mot.cpp:468-486).
-        wamx_tensor * tab = wamx_reshape_3d(ctx, m->action_sst, da, 1, 2);
-        wamx_tensor * om = wamx_modulation(ctx, temb, tab);  // [da, 1, 2]: row 0 shift, row 1 scale
-        wamx_tensor * oshift = wamx_view_1d(ctx, om, da, 0);
-        wamx_tensor * oscale = wamx_view_1d(ctx, om, da, (size_t) da * 4);
+        wamx_tensor * oshift = wamx_view_1d(ctx, om, da, (size_t) (2 * s) * da * 4);
+        wamx_tensor * oscale = wamx_view_1d(ctx, om, da, (size_t) (2 * s + 1) * da * 4);
         wamx_tensor * n = wamx_norm_modulation_bf16(ctx, h, oscale, oshift, c.eps);
         wamx_tensor * pred = b.mlp3(m->action_dec, n);  // bf16 [A, T]
         wamx_set_output(pred);
         m->velocity.push_back(pred);
         // scheduler_step (weights.cpp:885-902): bf16(f32(a) + f32(v) * dt).
-        wamx_tensor * a32 = wamx_cast(ctx, action, WAMX_TYPE_F32);
-        wamx_tensor * v32 = wamx_cast(ctx, pred, WAMX_TYPE_F32);
-        action = wamx_cast(ctx, wamx_add(ctx, a32, wamx_mul(ctx, v32, dt)), WAMX_TYPE_BF16);
+        action = wamx_euler_step(ctx, action, pred, dt);
     }
     m->action_out = action;
     wamx_set_output(action);
@@ -641,6 +658,35 @@ static bool build_denoise_graph(wamx_gwp_model * m) {
     wamx_graph_assign_uid(g);
     m->galloc[gi] = wamx_gallocr_new(m->be);
     return m->galloc[gi] && wamx_gallocr_alloc_graph(m->galloc[gi], g);
+}
+
+// Index of the first Inf or NaN of v[0, n) (n when there is none).  An
+// all-ones exponent is tested on the bit patterns a block at a time so the
+// scan vectorises (AVX2 where the CPU has it); a block that has one is
+// scanned again for the first such element.
+template <int kUnused = 0>
+static inline size_t first_non_finite_impl(const float * v, size_t n) {
+    constexpr size_t kBlock = 4096;
+    for (size_t b = 0; b < n; b += kBlock) {
+        const size_t e = std::min(n, b + kBlock);
+        uint32_t bad = 0;
+        for (size_t i = b; i < e; ++i) {
+            uint32_t u;
+            memcpy(&u, v + i, sizeof u);
+            bad |= (uint32_t) ((u & 0x7f800000u) == 0x7f800000u);
+        }
+        if (bad)
+            for (size_t i = b; i < e; ++i)
+                if (!isfinite(v[i])) return i;
+    }
+    return n;
+}
+__attribute__((target("avx2"))) static size_t first_non_finite_avx2(const float * v, size_t n) {
+    return first_non_finite_impl<1>(v, n);
+}
+static size_t first_non_finite(const float * v, size_t n) {
+    static const bool avx2 = __builtin_cpu_supports("avx2");
+    return avx2 ? first_non_finite_avx2(v, n) : first_non_finite_impl<0>(v, n);
 }
 
 // ---------------------------------------------------------------------------
@@ -785,8 +831,26 @@ wamx_status wamx_gwp_init_synthetic(wamx_gwp_t m, uint64_t seed, float wstd) {
 
 wamx_status wamx_check_finite_f32(const float * values, size_t n, const char * field) {
     WAMX_REQUIRE(values || n == 0, "%s: null array", field ? field : "tensor");
-    for (size_t i = 0; i < n; ++i)
-        WAMX_REQUIRE(isfinite(values[i]), "%s contains NaN or Inf (element %zu)", field ? field : "tensor", i);
+    // Large arrays (the 2.1M-value prompt, the latent) are scanned by several
+    // threads: one core's memory bandwidth makes a 10 MB scan ~1 ms.
+    size_t nthreads = 1;
+    if (n >= (size_t) 1 << 20) nthreads = std::min<size_t>(8, std::max(1u, std::thread::hardware_concurrency()));
+    std::vector<size_t> first(nthreads, n);
+    auto scan = [&](size_t t) {
+        const size_t b = n * t / nthreads, e = n * (t + 1) / nthreads;
+        first[t] = first_non_finite(values + b, e - b) + b;
+    };
+    if (nthreads == 1) {
+        scan(0);
+    } else {
+        std::vector<std::thread> pool;
+        for (size_t t = 1; t < nthreads; ++t) pool.emplace_back(scan, t);
+        scan(0);
+        for (auto & th : pool) th.join();
+    }
+    for (size_t t = 0; t < nthreads; ++t)
+        WAMX_REQUIRE(first[t] >= n * (t + 1) / nthreads, "%s contains NaN or Inf (element %zu)",
+                     field ? field : "tensor", first[t]);
     return WAMX_STATUS_SUCCESS;
 }
 

@@ -16,6 +16,8 @@ const char * check_linear(const wamx_tensor * t);
 const char * check_qk_norm_rope(const wamx_tensor * t);
 const char * check_joint_attn(const wamx_tensor * t);
 const char * check_modulation(const wamx_tensor * t);
+const char * check_euler_step(const wamx_tensor * t);
+const char * check_mlp_small(const wamx_tensor * t);
 const char * check_im2col(const wamx_tensor * t);
 const char * check_conv_2d(const wamx_tensor * t);
 
@@ -161,7 +163,13 @@ hipError_t launch_im2col(const TensorRef & src, const TensorRef & dst, int KW, i
 hipError_t launch_conv2d(const TensorRef & kernel, const TensorRef & input, const TensorRef & dst, const int32_t * pp,
                          void * ws, size_t ws_bytes, hipStream_t s);
 hipError_t launch_modulation(const void * mod, int32_t mod_type, const void * tables, int32_t tab_type, float * out,
-                             int64_t per_layer, int64_t layers, hipStream_t s);
+                             int64_t per_layer, int64_t layers, hipStream_t s, int64_t steps = 1);
+// bf16 out[i] = bf16(f32(a[i]) + f32(v[i]) * dt[0]), product and sum rounded apart.
+hipError_t launch_euler_step(const void * a, const void * v, const float * dt, void * out, int64_t n, hipStream_t s);
+// Two small linear layers (wamx_mlp_small): x bf16 [N][K0], w1 [M1][K0],
+// w2 [M2][M1], biases bf16, y bf16 [N][M2]; flags WAMX_MLP_GELU_*.
+hipError_t launch_mlp_small(const void * x, const void * w1, const void * b1, const void * w2, const void * b2, void * y,
+                            int64_t N, int64_t K0, int64_t M1, int64_t M2, int32_t flags, hipStream_t s);
 
 // ---------------------------------------------------------------------------
 // Fused attention-side kernels.

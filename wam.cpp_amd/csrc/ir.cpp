@@ -208,8 +208,35 @@ const char * check_modulation(const wamx_tensor * t) {
     if ((mod->type != WAMX_TYPE_BF16 && mod->type != WAMX_TYPE_F32) ||
         (tables->type != WAMX_TYPE_BF16 && tables->type != WAMX_TYPE_F32))
         return "types";
-    if (wamx_nelements(mod) != tables->ne[0] * tables->ne[1]) return "sizes";
-    if (!is_f32(t) || !contig(t) || wamx_nelements(t) != wamx_nelements(tables)) return "output";
+    // mod holds S columns of ne0 * ne1 values (S timesteps): one output
+    // [ne0, ne1, L] per column.
+    const int64_t per = tables->ne[0] * tables->ne[1];
+    if (per <= 0 || wamx_nelements(mod) % per != 0) return "sizes";
+    const int64_t S = wamx_nelements(mod) / per;
+    if (!is_f32(t) || !contig(t) || wamx_nelements(t) != wamx_nelements(tables) * S || t->ne[3] != S) return "output";
+    return nullptr;
+}
+
+const char * check_euler_step(const wamx_tensor * t) {
+    const wamx_tensor *a = t->src[0], *v = t->src[1], *dt = t->src[2];
+    if (!is_bf16(a) || !is_bf16(v) || !is_f32(dt) || !is_bf16(t)) return "types (bf16 action and velocity, f32 dt)";
+    if (!wamx_are_same_shape(a, v) || !wamx_are_same_shape(a, t) || !contig(a) || !contig(v) || !contig(t))
+        return "action, velocity and output: one contiguous shape";
+    if (wamx_nelements(dt) != 1) return "dt is one value";
+    return nullptr;
+}
+
+const char * check_mlp_small(const wamx_tensor * t) {
+    const wamx_tensor *x = t->src[0], *w1 = t->src[1], *b1 = t->src[2], *w2 = t->src[3], *b2 = t->src[4];
+    if (!is_bf16(x) || !is_bf16(w1) || !is_bf16(b1) || !is_bf16(w2) || !is_bf16(b2) || !is_bf16(t)) return "types";
+    const int64_t K0 = x->ne[0], N = x->ne[1], M1 = w1->ne[1], M2 = w2->ne[1];
+    if (w1->ne[0] != K0 || w2->ne[0] != M1 || b1->ne[0] != M1 || b2->ne[0] != M2) return "shapes";
+    if (K0 < 1 || M1 < 1 || M2 < 1 || K0 > 128 || M1 > 128 || M2 > 128) return "widths must be 1..128";
+    if (x->ne[2] != 1 || x->ne[3] != 1 || w1->ne[2] != 1 || w2->ne[2] != 1 || !contig(x) || !contig(w1) ||
+        !contig(w2) || !contig(b1) || !contig(b2))
+        return "contiguous 2-D operands";
+    if (t->ne[0] != M2 || t->ne[1] != N || t->ne[2] != 1 || t->ne[3] != 1 || !contig(t)) return "output";
+    if (t->op_params[0] & ~7) return "flags";
     return nullptr;
 }
 
@@ -306,6 +333,7 @@ const char * wamx_op_name(int32_t op) {
         "NONE", "DUP", "ADD", "MUL", "SCALE", "CPY", "CONT", "RESHAPE", "VIEW", "PERMUTE",
         "TRANSPOSE", "CONCAT", "REPEAT", "NORM", "RMS_NORM", "MUL_MAT", "SOFT_MAX", "ROPE",
         "UNARY", "GET_ROWS", "IM2COL", "CONV_2D", "LINEAR", "QK_NORM_ROPE", "JOINT_ATTN", "MODULATION",
+        "EULER_STEP", "MLP_SMALL",
     };
     return (op >= 0 && op < WAMX_OP_COUNT) ? names[op] : "?";
 }
@@ -839,12 +867,41 @@ wamx_tensor * wamx_joint_attn(wamx_context * ctx, wamx_tensor * q, wamx_tensor *
 
 wamx_tensor * wamx_modulation(wamx_context * ctx, wamx_tensor * mod, wamx_tensor * tables) {
     if (!mod || !tables) return fail("wamx_modulation");
-    wamx_tensor * t = wamx_new_tensor_3d(ctx, WAMX_TYPE_F32, tables->ne[0], tables->ne[1], tables->ne[2] * tables->ne[3]);
+    const int64_t per = tables->ne[0] * tables->ne[1];
+    if (per <= 0 || wamx_nelements(mod) % per != 0) return fail("wamx_modulation (sizes)");
+    wamx_tensor * t = wamx_new_tensor_4d(ctx, WAMX_TYPE_F32, tables->ne[0], tables->ne[1], tables->ne[2] * tables->ne[3],
+                                         wamx_nelements(mod) / per);
     if (!t) return nullptr;
     t->op = WAMX_OP_MODULATION;
     t->src[0] = mod;
     t->src[1] = tables;
     return checked(t, check_modulation, "wamx_modulation");
+}
+
+wamx_tensor * wamx_euler_step(wamx_context * ctx, wamx_tensor * action, wamx_tensor * velocity, wamx_tensor * dt) {
+    if (!action || !velocity || !dt) return fail("wamx_euler_step");
+    wamx_tensor * t = new_tensor_impl(ctx, WAMX_TYPE_BF16, 4, action->ne);
+    if (!t) return nullptr;
+    t->op = WAMX_OP_EULER_STEP;
+    t->src[0] = action;
+    t->src[1] = velocity;
+    t->src[2] = dt;
+    return checked(t, check_euler_step, "wamx_euler_step");
+}
+
+wamx_tensor * wamx_mlp_small(wamx_context * ctx, wamx_tensor * x, wamx_tensor * w1, wamx_tensor * b1, wamx_tensor * w2,
+                             wamx_tensor * b2, int32_t flags) {
+    if (!x || !w1 || !b1 || !w2 || !b2) return fail("wamx_mlp_small");
+    wamx_tensor * t = wamx_new_tensor_2d(ctx, WAMX_TYPE_BF16, w2->ne[1], x->ne[1]);
+    if (!t) return nullptr;
+    t->op = WAMX_OP_MLP_SMALL;
+    t->op_params[0] = flags;
+    t->src[0] = x;
+    t->src[1] = w1;
+    t->src[2] = b1;
+    t->src[3] = w2;
+    t->src[4] = b2;
+    return checked(t, check_mlp_small, "wamx_mlp_small");
 }
 
 // ---------------------------------------------------------------------------

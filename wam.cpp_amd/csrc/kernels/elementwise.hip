@@ -283,12 +283,89 @@ __global__ void im2col_kernel(Ref4 src, Ref4 dst, int KW, int KH, int s0, int s1
 }
 
 // out[l][j] = f32(mod[j]) + f32(tables[l][j])  (modulation_add, mot.cpp:137-145).
+// out[s][r] = f32(mod[s][r % per_layer]) + f32(tables[r]) for the S columns
+// (timesteps) of mod, r over the per_step = per_layer * layers table values.
 __global__ void modulation_kernel(const void * mod, int32_t mod_type, const void * tables, int32_t tab_type, float * out,
-                                  int64_t per_layer, int64_t n) {
+                                  int64_t per_layer, int64_t per_step, int64_t n) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const int64_t j = i % per_layer;
-    out[i] = load_as_f32(mod, mod_type, j) + load_as_f32(tables, tab_type, i);
+    const int64_t st = i / per_step, r = i - st * per_step, j = r % per_layer;
+    out[i] = load_as_f32(mod, mod_type, st * per_layer + j) + load_as_f32(tables, tab_type, r);
+}
+
+// scheduler_step (weights.cpp:885-902): bf16(f32(a) + f32(v) * dt), the
+// product and the sum rounded separately as the MUL and ADD nodes do.
+#pragma clang fp contract(off)
+__global__ void euler_step_kernel(const uint16_t * __restrict__ a, const uint16_t * __restrict__ v,
+                                  const float * __restrict__ dt, uint16_t * __restrict__ out, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float t = bf16_to_f32(v[i]) * dt[0];
+    out[i] = f32_to_bf16(bf16_to_f32(a[i]) + t);
+}
+#pragma clang fp contract(on)
+
+// Two small linear layers (widths <= kMlpMax) for 16 tokens per workgroup:
+// the tokens' inputs transposed into LDS as f32 [k][16], one layer's weight
+// staged as bf16 [m][k] (rows padded by one element); thread t owns feature
+// t % 128 for tokens 8 (t / 128) .. +8 and accumulates in k order in f32.
+// Each layer: bf16(bf16(acc) + bias), then GELU_ERF rounded to bf16 where
+// its flag is set; layer 1's output is layer 2's input in LDS.
+constexpr int kMlpMax = 128, kMlpTok = 16;
+__global__ __launch_bounds__(256) void mlp_small_kernel(const uint16_t * __restrict__ x, const uint16_t * __restrict__ w1,
+                                                        const uint16_t * __restrict__ b1,
+                                                        const uint16_t * __restrict__ w2,
+                                                        const uint16_t * __restrict__ b2, uint16_t * __restrict__ y,
+                                                        int64_t N, int K0, int M1, int M2, int flags) {
+    __shared__ __align__(16) float xt[kMlpMax][kMlpTok];
+    __shared__ __align__(16) float ht[kMlpMax][kMlpTok];
+    __shared__ uint16_t ws[kMlpMax * (kMlpMax + 1)];
+    const int tid = threadIdx.x;
+    const int64_t n0 = (int64_t) blockIdx.x * kMlpTok;
+    for (int e = tid; e < kMlpTok * K0; e += 256) {
+        const int n = e / K0, k = e % K0;
+        float v = n0 + n < N ? bf16_to_f32(x[(n0 + n) * K0 + k]) : 0.0f;
+        if (flags & WAMX_MLP_GELU_IN) v = round_bf16(gelu_erf(v));
+        xt[k][n] = v;
+    }
+    const int m = tid % kMlpMax, g = tid / kMlpMax;  // feature, token group of 8
+    auto layer = [&](const uint16_t * __restrict__ w, const uint16_t * __restrict__ b, int K, int M, bool gelu,
+                     float (*in)[kMlpTok], float (*out)[kMlpTok], bool last) {
+        const int pitch = K + 1;
+        __syncthreads();  // the previous layer is done with the weight tile and has written `in`
+        for (int e = tid; e < M * K; e += 256) ws[(e / K) * pitch + e % K] = w[e];
+        __syncthreads();
+        if (m >= M) return;
+        float acc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            const float wv = bf16_to_f32(ws[m * pitch + k]);
+            const float4 xa = *(const float4 *) &in[k][8 * g], xb = *(const float4 *) &in[k][8 * g + 4];
+            acc[0] = fmaf(wv, xa.x, acc[0]);
+            acc[1] = fmaf(wv, xa.y, acc[1]);
+            acc[2] = fmaf(wv, xa.z, acc[2]);
+            acc[3] = fmaf(wv, xa.w, acc[3]);
+            acc[4] = fmaf(wv, xb.x, acc[4]);
+            acc[5] = fmaf(wv, xb.y, acc[5]);
+            acc[6] = fmaf(wv, xb.z, acc[6]);
+            acc[7] = fmaf(wv, xb.w, acc[7]);
+        }
+        const float bias = bf16_to_f32(b[m]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float v = round_bf16(round_bf16(acc[j]) + bias);
+            if (gelu) v = round_bf16(gelu_erf(v));
+            const int64_t n = n0 + 8 * g + j;
+            if (last) {
+                if (n < N) y[n * M + m] = f32_to_bf16(v);
+            } else {
+                out[m][8 * g + j] = v;
+            }
+        }
+    };
+    layer(w1, b1, K0, M1, flags & WAMX_MLP_GELU_MID, xt, ht, false);
+    layer(w2, b2, M1, M2, flags & WAMX_MLP_GELU_OUT, ht, nullptr, true);
 }
 
 // splitmix64 (Steele, Lea, Flood: "Fast splittable pseudorandom number
@@ -408,10 +485,28 @@ hipError_t launch_im2col(const TensorRef & src, const TensorRef & dst, int KW, i
 }
 
 hipError_t launch_modulation(const void * mod, int32_t mod_type, const void * tables, int32_t tab_type, float * out,
-                             int64_t per_layer, int64_t layers, hipStream_t s) {
-    const int64_t n = per_layer * layers;
+                             int64_t per_layer, int64_t layers, hipStream_t s, int64_t steps) {
+    const int64_t per_step = per_layer * layers, n = per_step * steps;
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(modulation_kernel, grid1d(n), dim3(256), 0, s, mod, mod_type, tables, tab_type, out, per_layer, n);
+    hipLaunchKernelGGL(modulation_kernel, grid1d(n), dim3(256), 0, s, mod, mod_type, tables, tab_type, out, per_layer,
+                       per_step, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_euler_step(const void * a, const void * v, const float * dt, void * out, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(euler_step_kernel, grid1d(n), dim3(256), 0, s, (const uint16_t *) a, (const uint16_t *) v, dt,
+                       (uint16_t *) out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_mlp_small(const void * x, const void * w1, const void * b1, const void * w2, const void * b2, void * y,
+                            int64_t N, int64_t K0, int64_t M1, int64_t M2, int32_t flags, hipStream_t s) {
+    if (N <= 0) return hipSuccess;
+    if (K0 < 1 || M1 < 1 || M2 < 1 || K0 > kMlpMax || M1 > kMlpMax || M2 > kMlpMax) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mlp_small_kernel, dim3((unsigned) ((N + kMlpTok - 1) / kMlpTok)), dim3(256), 0, s,
+                       (const uint16_t *) x, (const uint16_t *) w1, (const uint16_t *) b1, (const uint16_t *) w2,
+                       (const uint16_t *) b2, (uint16_t *) y, N, (int) K0, (int) M1, (int) M2, (int) flags);
     return hipGetLastError();
 }
 

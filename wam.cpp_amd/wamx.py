@@ -26,7 +26,8 @@ UNARY_GELU, UNARY_SILU, UNARY_GELU_ERF = 8, 10, 14
 
 OP_NAMES = ["NONE", "DUP", "ADD", "MUL", "SCALE", "CPY", "CONT", "RESHAPE", "VIEW", "PERMUTE",
             "TRANSPOSE", "CONCAT", "REPEAT", "NORM", "RMS_NORM", "MUL_MAT", "SOFT_MAX", "ROPE",
-            "UNARY", "GET_ROWS", "IM2COL", "CONV_2D", "LINEAR", "QK_NORM_ROPE", "JOINT_ATTN", "MODULATION"]
+            "UNARY", "GET_ROWS", "IM2COL", "CONV_2D", "LINEAR", "QK_NORM_ROPE", "JOINT_ATTN", "MODULATION",
+            "EULER_STEP", "MLP_SMALL"]
 OP = {name: i for i, name in enumerate(OP_NAMES)}
 
 
@@ -126,6 +127,8 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_qk_norm_rope_hilo": (TensorP, [vp, TensorP, TensorP, TensorP, i64, C.c_int, TensorP, TensorP,
                                              TensorP, f32, f32]),
         "wamx_joint_attn_hilo": (TensorP, [vp, TensorP, TensorP, TensorP, f32]),
+        "wamx_euler_step": (TensorP, [vp, TensorP, TensorP, TensorP]),
+        "wamx_mlp_small": (TensorP, [vp, TensorP, TensorP, TensorP, TensorP, TensorP, i32]),
         "wamx_op_soft_max_f32": (C.c_int, [vp, vp, vp, i64, i64, f32]),
         "wamx_fill_normal": (C.c_int, [vp, vp, i32, i64, C.c_uint64, f32, f32]),
         "wamx_timer_new": (vp, [vp]),
