@@ -112,6 +112,11 @@ struct wamx_gwp_model {
     std::vector<float> prompt_sig;
     bool prompt_stale = true;
     uint64_t prompt_hits = 0, prompt_misses = 0;
+    // Device staging of the f32 latent and prompt of set_inputs: uploaded
+    // there, scanned for Inf / NaN on the GPU (first bad index of each in
+    // `flags`), and copied into the input tensors only when both are finite.
+    void * stage = nullptr;
+    uint32_t * flags = nullptr;
 
     int n_graphs() const { return (int) (2 * B + 1); }
     int prompt_graph(int64_t b) const { return (int) b; }
@@ -119,6 +124,7 @@ struct wamx_gwp_model {
     int denoise_graph() const { return (int) (2 * B); }
 
     ~wamx_gwp_model() {
+        if (stage) wamx_device_free(be, stage);
         for (size_t i = 0; i < graph.size(); ++i) {
             wamx_gallocr_free(galloc[i]);
             wamx_free(gctx[i]);
@@ -857,38 +863,50 @@ wamx_status wamx_check_finite_f32(const float * values, size_t n, const char * f
 wamx_status wamx_gwp_set_inputs(wamx_gwp_t m, const float * state, const float * latent, const float * prompt,
                                 const float * noise) {
     WAMX_REQUIRE(m && state && latent && prompt && noise, "wamx_gwp_set_inputs: null argument");
-    // Non-finite inputs are refused before anything is uploaded, as the
-    // reference refuses them before its graphs run (engine.cpp:238-247 state,
-    // :274 reference latent, :320 prompt, :350-357 noise).
-    const struct {
-        const float * p;
-        wamx_tensor * t;
-        const char * name;
-    } checks[] = {{state, m->in_state, "wamx_gwp_set_inputs: state"},
-                  {latent, m->in_latent, "wamx_gwp_set_inputs: latent"},
-                  {prompt, m->in_prompt, "wamx_gwp_set_inputs: prompt"},
-                  {noise, m->in_action, "wamx_gwp_set_inputs: noise"}};
-    for (const auto & ck : checks) {
-        const wamx_status fs = wamx_check_finite_f32(ck.p, (size_t) wamx_nelements(ck.t), ck.name);
-        if (fs != WAMX_STATUS_SUCCESS) return fs;
-    }
-    wamx_status st = wamx_backend_tensor_set(m->in_state, state, 0, wamx_nbytes(m->in_state));
-    if (st == WAMX_STATUS_SUCCESS) st = wamx_backend_tensor_set(m->in_latent, latent, 0, wamx_nbytes(m->in_latent));
-    const size_t np = (size_t) wamx_nelements(m->in_prompt);
+    // Non-finite inputs are refused and the model's inputs left as they were,
+    // as the reference refuses them before its graphs run (engine.cpp:238-247
+    // state, :274 reference latent, :320 prompt, :350-357 noise).  The small
+    // state and noise are checked on the host; the latent and the prompt
+    // (10.6 MB of f32 at batch 1) are uploaded to a staging area, scanned
+    // there, and copied into the inputs only when finite.
+    const size_t ns = (size_t) wamx_nelements(m->in_state), na = (size_t) wamx_nelements(m->in_action);
+    const size_t nl = (size_t) wamx_nelements(m->in_latent), np = (size_t) wamx_nelements(m->in_prompt);
+    wamx_status st = wamx_check_finite_f32(state, ns, "wamx_gwp_set_inputs: state");
+    if (st == WAMX_STATUS_SUCCESS) st = wamx_check_finite_f32(noise, na, "wamx_gwp_set_inputs: noise");
+    if (st != WAMX_STATUS_SUCCESS) return st;
     const bool hit = m->prompt_cache_capacity > 0 && !m->prompt_stale && m->prompt_sig.size() == np &&
                      memcmp(m->prompt_sig.data(), prompt, np * sizeof(float)) == 0;
-    if (m->prompt_cache_capacity > 0) ++(hit ? m->prompt_hits : m->prompt_misses);
-    if (st == WAMX_STATUS_SUCCESS && !hit) {
-        m->prompt_stale = true;
-        st = wamx_backend_tensor_set(m->in_prompt, prompt, 0, wamx_nbytes(m->in_prompt));
-        if (st == WAMX_STATUS_SUCCESS && m->prompt_cache_capacity > 0) m->prompt_sig.assign(prompt, prompt + np);
+    hipStream_t s = (hipStream_t) wamx_backend_stream(m->be);
+    if (!m->stage) {
+        m->stage = wamx_device_malloc(m->be, (nl + np) * sizeof(float) + 256);
+        WAMX_REQUIRE(m->stage, "wamx_gwp_set_inputs: staging allocation failed");
+        m->flags = (uint32_t *) ((char *) m->stage + (nl + np) * sizeof(float));
     }
+    float * sl = (float *) m->stage;
+    float * sp = sl + nl;
+    WAMX_HIP_TRY(hipMemcpy(sl, latent, nl * sizeof(float), hipMemcpyHostToDevice));
+    if (!hit) WAMX_HIP_TRY(hipMemcpy(sp, prompt, np * sizeof(float), hipMemcpyHostToDevice));
+    uint32_t first[2] = {UINT32_MAX, UINT32_MAX};
+    WAMX_HIP_TRY(hipMemcpyAsync(m->flags, first, sizeof first, hipMemcpyHostToDevice, s));
+    WAMX_HIP_TRY(launch_nonfinite_scan(sl, (int64_t) nl, m->flags, s));
+    if (!hit) WAMX_HIP_TRY(launch_nonfinite_scan(sp, (int64_t) np, m->flags + 1, s));
+    WAMX_HIP_TRY(hipMemcpyAsync(first, m->flags, sizeof first, hipMemcpyDeviceToHost, s));
+    WAMX_HIP_TRY(hipStreamSynchronize(s));
+    WAMX_REQUIRE(first[0] == UINT32_MAX, "wamx_gwp_set_inputs: latent contains NaN or Inf (element %u)", first[0]);
+    WAMX_REQUIRE(first[1] == UINT32_MAX, "wamx_gwp_set_inputs: prompt contains NaN or Inf (element %u)", first[1]);
+    if (m->prompt_cache_capacity > 0) ++(hit ? m->prompt_hits : m->prompt_misses);
+    WAMX_HIP_TRY(hipMemcpyAsync(m->in_latent->data, sl, nl * sizeof(float), hipMemcpyDeviceToDevice, s));
+    if (!hit) {
+        m->prompt_stale = true;
+        WAMX_HIP_TRY(hipMemcpyAsync(m->in_prompt->data, sp, np * sizeof(float), hipMemcpyDeviceToDevice, s));
+        if (m->prompt_cache_capacity > 0) m->prompt_sig.assign(prompt, prompt + np);
+    }
+    st = wamx_backend_tensor_set(m->in_state, state, 0, ns * sizeof(float));
     if (st != WAMX_STATUS_SUCCESS) return st;
     // The action state is bf16 in the native profile (mot.cpp:523-525, set_f32_tensor).
-    const int64_t n = wamx_nelements(m->in_action);
-    std::vector<uint16_t> a(n);
-    for (int64_t i = 0; i < n; ++i) a[i] = f32_to_bf16_host(noise[i]);
-    return wamx_backend_tensor_set(m->in_action, a.data(), 0, n * 2);
+    std::vector<uint16_t> a(na);
+    for (size_t i = 0; i < na; ++i) a[i] = f32_to_bf16_host(noise[i]);
+    return wamx_backend_tensor_set(m->in_action, a.data(), 0, na * 2);
 }
 
 static wamx_status run_graph(wamx_gwp_t m, int which) {

@@ -164,6 +164,8 @@ hipError_t launch_conv2d(const TensorRef & kernel, const TensorRef & input, cons
                          void * ws, size_t ws_bytes, hipStream_t s);
 hipError_t launch_modulation(const void * mod, int32_t mod_type, const void * tables, int32_t tab_type, float * out,
                              int64_t per_layer, int64_t layers, hipStream_t s, int64_t steps = 1);
+// atomicMin of the index of every Inf / NaN of p[0, n) into *first (n < 2^32).
+hipError_t launch_nonfinite_scan(const float * p, int64_t n, uint32_t * first, hipStream_t s);
 // bf16 out[i] = bf16(f32(a[i]) + f32(v[i]) * dt[0]), product and sum rounded apart.
 hipError_t launch_euler_step(const void * a, const void * v, const float * dt, void * out, int64_t n, hipStream_t s);
 // Two small linear layers (wamx_mlp_small): x bf16 [N][K0], w1 [M1][K0],

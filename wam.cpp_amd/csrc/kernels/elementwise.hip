@@ -9,6 +9,8 @@
 #include "../internal.h"
 #include "device.h"
 
+#include <algorithm>
+
 namespace wamx {
 
 struct Ref4 {
@@ -490,6 +492,24 @@ hipError_t launch_modulation(const void * mod, int32_t mod_type, const void * ta
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(modulation_kernel, grid1d(n), dim3(256), 0, s, mod, mod_type, tables, tab_type, out, per_layer,
                        per_step, n);
+    return hipGetLastError();
+}
+
+// Smallest index of an Inf or NaN of p[0, n) into *first (left as is when
+// there is none; the caller starts it at UINT32_MAX).
+__global__ void nonfinite_scan_kernel(const float * __restrict__ p, int64_t n, uint32_t * first) {
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t) gridDim.x * blockDim.x) {
+        uint32_t u;
+        memcpy(&u, p + i, sizeof u);
+        if ((u & 0x7f800000u) == 0x7f800000u) atomicMin(first, (uint32_t) i);
+    }
+}
+
+hipError_t launch_nonfinite_scan(const float * p, int64_t n, uint32_t * first, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (n >= (int64_t) UINT32_MAX) return hipErrorInvalidValue;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 2048);
+    hipLaunchKernelGGL(nonfinite_scan_kernel, dim3((unsigned) blocks), dim3(256), 0, s, p, n, first);
     return hipGetLastError();
 }
 
