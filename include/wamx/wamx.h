@@ -254,7 +254,13 @@ WAMX_API wamx_tensor * wamx_rms_norm_bf16_f32(wamx_context * ctx, wamx_tensor * 
  *   starting at token offset tok0 (the head-major layout mot.cpp:395-396 builds
  *   with permute+cont).  rope_mode 0: 1-D rope over head_dim with pos0[T];
  *   rope_mode 1: 3-section {44,42,42} rope with pos0/pos1/pos2 (mot.cpp:182-202);
- *   rope_mode 2: no rope (cross-attention queries, mot.cpp:301-306).
+ *   rope_mode 2: no rope (cross-attention queries, mot.cpp:301-306);
+ *   rope_mode 3: the rotation of mode 0 or 1 from a precomputed table: pos0
+ *   is an f32 tensor [ne={head_dim, T}] holding (cos, sin) of every pair of
+ *   each token (wamx_op_rope_table; computed with the same angle and sincos
+ *   as modes 0 and 1, so the result is the same bit for bit).  For fixed
+ *   positions (the visual grid) it is built once and saves the
+ *   transcendental work of every layer.
  *   Writes into an existing tensor (dst), returned as a node that depends on it.
  *
  * wamx_joint_attn: softmax(scale * Q K^T) V per head over the key set
@@ -543,6 +549,15 @@ WAMX_API wamx_status wamx_op_qk_norm_rope_hilo(wamx_backend_t be, const void * x
 WAMX_API wamx_status wamx_op_joint_attn_hilo(wamx_backend_t be, const void * q, const void * q_lo, const void * k,
                                              const void * k_lo, const void * vt, int64_t nk, int64_t vt_ld,
                                              void * out, int64_t heads, int64_t head_dim, int64_t tq, float scale);
+/* The rope table of rope mode 3 for positions of mode 0 or 1: out f32
+ * [tokens][head_dim], (cos, sin) of pair i at 2i, 2i+1. */
+WAMX_API wamx_status wamx_op_rope_table(wamx_backend_t be, int rope_mode, const int32_t * pos0,
+                                        const int32_t * pos1, const int32_t * pos2, int64_t tokens,
+                                        int64_t head_dim, float freq_base, float * out);
+/* wamx_op_qk_norm_rope with rope mode 3 (rotation from `table`). */
+WAMX_API wamx_status wamx_op_qk_norm_rope_table(wamx_backend_t be, const void * x, int64_t ldx, const void * w,
+                                                void * dst, int64_t heads, int64_t head_dim, int64_t tokens,
+                                                int64_t dst_tokens, int64_t tok0, const float * table, float eps);
 /* SOFT_MAX_EXT without mask: y[r][:] = softmax(scale * x[r][:]) over ne0=cols, f32. */
 WAMX_API wamx_status wamx_op_soft_max_f32(wamx_backend_t be, const float * x, float * y,
                                           int64_t rows, int64_t cols, float scale);

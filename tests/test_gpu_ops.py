@@ -313,6 +313,49 @@ def test_qk_norm_rope_video_grid(wx, be, orc):
         assert np.mean(got != ref) < 0.01
 
 
+def test_qk_norm_rope_table_equals_positions(wx, be):
+    """Rope mode 3 (rotation from a precomputed (cos, sin) table) gives the
+    bits of the positions it was built from: the 3-D rope of the 3 x 1024
+    visual grid (t = 0, h in 0..31, w in 0..95) and the 1-D rope of the 48
+    action positions, plain and into hi/lo planes."""
+    print("qk_norm_rope table vs positions", flush=True)
+    rng = np.random.default_rng(0x5EED0303)
+    H, dh = 24, 128
+    for T, mode in ((3072, 1), (48, 0)):
+        x = bf16(rng.standard_normal((T, 3 * H * dh)))
+        w = bf16(1 + rng.standard_normal(H * dh) * 0.02)
+        idx = np.arange(T)
+        pos = [(idx // 96).astype(np.int32) * 0, (idx // 96).astype(np.int32), (idx % 96).astype(np.int32)] \
+            if mode == 1 else [(idx + 1).astype(np.int32)]
+        dpos = [dev(be, p) for p in pos]
+        ptrs = [p.ptr for p in dpos] + [None] * (3 - len(dpos))
+        dx, dw = dev(be, x), dev(be, w)
+        tab = be.empty(T * dh * 4)
+        wx.check(be.lib.wamx_op_rope_table(be.ptr, mode, *ptrs, T, dh, 10000.0, tab.ptr), "rope_table")
+        for tok0 in (0, 1):
+            n = T + tok0
+            a, b = be.empty(H * n * dh * 2), be.empty(H * n * dh * 2)
+            wx.check(be.lib.wamx_op_qk_norm_rope(be.ptr, dx.ptr, 3 * H * dh, dw.ptr, a.ptr, H, dh, T, n, tok0, mode,
+                                                 *ptrs, 1e-6, 10000.0))
+            wx.check(be.lib.wamx_op_qk_norm_rope_table(be.ptr, dx.ptr, 3 * H * dh, dw.ptr, b.ptr, H, dh, T, n, tok0,
+                                                       tab.ptr, 1e-6))
+            ga, gb = a.download(np.uint16, (H, n, dh)), b.download(np.uint16, (H, n, dh))
+            assert np.array_equal(ga[:, tok0:], gb[:, tok0:]), f"T={T} mode {mode} tok0 {tok0}"
+        # the table is (cos, sin) of pos * base^(-2i/n) per section
+        t = tab.download(np.float32, (T, dh // 2, 2))
+        i = np.arange(dh // 2)
+        if mode == 0:
+            theta = pos[0][:, None] * 10000.0 ** (-2.0 * i[None, :] / dh)
+        else:
+            sec = np.where(i < 22, 0, np.where(i < 43, 1, 2))
+            loc = np.where(i < 22, i, np.where(i < 43, i - 22, i - 43))
+            n_dims = np.where(i < 22, 44, 42)
+            p = np.stack(pos)[sec].T
+            theta = p * 10000.0 ** (-2.0 * loc[None, :] / n_dims[None, :])
+        assert np.max(np.abs(t[..., 0] - np.cos(theta))) < 1e-4
+        assert np.max(np.abs(t[..., 1] - np.sin(theta))) < 1e-4
+
+
 def test_joint_attention_dit_block(wx, be, orc):
     """Full bidirectional attention of one DiT block: 2096 queries over the
     same 2096 keys (2048 video + 48 action tokens), 24 heads x 128."""

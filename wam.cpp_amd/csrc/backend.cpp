@@ -387,7 +387,9 @@ static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post, bool la
         int64_t width, head_dim;
         if (t->op == WAMX_OP_QK_NORM_ROPE) {
             const wamx_tensor * x = t->src[0];
-            if (!column_view(x, lin, seg.col) || !t->src[1] || t->type != WAMX_TYPE_BF16 || t->op_params[4]) break;
+            if (!column_view(x, lin, seg.col) || !t->src[1] || t->type != WAMX_TYPE_BF16 || t->op_params[4] ||
+                t->op_params[1] == 3)
+                break;
             head_dim = t->ne[0];
             width = x->ne[0];
             if (width != head_dim * t->ne[2] || x->ne[1] % t->ne[3] != 0) break;
@@ -661,14 +663,16 @@ static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
         case WAMX_OP_QK_NORM_ROPE: {
             const wamx_tensor * x = node->src[0];
             const bool hilo = node->op_params[4] != 0;  // plane 1 takes the lo parts
+            const bool table = node->op_params[1] == 3;  // src[3]: the (cos, sin) table
             return launch_qk_norm_rope(x->data, (int64_t) x->nb[1] / 2, node->src[1]->data, node->data, node->ne[2],
                                        node->ne[0], x->ne[1], node->ne[1], node->op_params[0], node->op_params[1],
-                                       node->src[3] ? (const int32_t *) node->src[3]->data : nullptr,
+                                       node->src[3] && !table ? (const int32_t *) node->src[3]->data : nullptr,
                                        node->src[4] ? (const int32_t *) node->src[4]->data : nullptr,
                                        node->src[5] ? (const int32_t *) node->src[5]->data : nullptr,
                                        param_f32(node, 2), param_f32(node, 3), s,
                                        hilo ? x->ne[1] : x->ne[1] / node->ne[3], hilo ? 0 : (int64_t) node->nb[3] / 2,
-                                       hilo ? (int64_t) node->nb[3] / 2 : 0);
+                                       hilo ? (int64_t) node->nb[3] / 2 : 0,
+                                       table ? (const float *) node->src[3]->data : nullptr);
         }
         case WAMX_OP_JOINT_ATTN:
             return run_joint_attn(be, node);
@@ -1653,6 +1657,21 @@ wamx_status wamx_op_qk_norm_rope(wamx_backend_t be, const void * x, int64_t ldx,
     WAMX_REQUIRE(tok0 >= 0 && tok0 + tokens <= dst_tokens, "wamx_op_qk_norm_rope: token range");
     WAMX_LAUNCH(launch_qk_norm_rope(x, ldx, w, dst, heads, head_dim, tokens, dst_tokens, tok0, rope_mode, pos0, pos1,
                                     pos2, eps, freq_base, be->stream));
+}
+
+wamx_status wamx_op_rope_table(wamx_backend_t be, int rope_mode, const int32_t * pos0, const int32_t * pos1,
+                               const int32_t * pos2, int64_t tokens, int64_t head_dim, float freq_base, float * out) {
+    WAMX_REQUIRE(be && out, "wamx_op_rope_table: null argument");
+    WAMX_LAUNCH(launch_rope_table(rope_mode, pos0, pos1, pos2, tokens, head_dim, freq_base, out, be->stream));
+}
+
+wamx_status wamx_op_qk_norm_rope_table(wamx_backend_t be, const void * x, int64_t ldx, const void * w, void * dst,
+                                       int64_t heads, int64_t head_dim, int64_t tokens, int64_t dst_tokens,
+                                       int64_t tok0, const float * table, float eps) {
+    WAMX_REQUIRE(be && x && w && dst && table, "wamx_op_qk_norm_rope_table: null argument");
+    WAMX_REQUIRE(tok0 >= 0 && tok0 + tokens <= dst_tokens, "wamx_op_qk_norm_rope_table: token range");
+    WAMX_LAUNCH(launch_qk_norm_rope(x, ldx, w, dst, heads, head_dim, tokens, dst_tokens, tok0, 3, nullptr, nullptr,
+                                    nullptr, eps, 10000.0f, be->stream, 0, 0, 0, table));
 }
 
 wamx_status wamx_op_qk_norm_rope_hilo(wamx_backend_t be, const void * x, int64_t ldx, const void * w, void * dst_hi,

@@ -92,6 +92,10 @@ struct wamx_gwp_model {
     wamx_tensor *in_state = nullptr, *in_latent = nullptr, *in_prompt = nullptr, *in_action = nullptr;
     wamx_tensor *in_apos = nullptr, *in_spos = nullptr, *in_vt = nullptr, *in_vh = nullptr, *in_vw = nullptr;
     wamx_tensor *in_freq0 = nullptr, *in_freqs = nullptr, *in_dts = nullptr;
+    // (cos, sin) of the 3-D rope of every visual token [dh, nimg] (rope mode
+    // 3): the positions are the grid's, fixed, so the prefix's Q and K of
+    // every layer rotate from this table.
+    wamx_tensor * vis_rope = nullptr;
 
     // Graphs: a prompt and a prefix graph per chunk, then the denoise graph
     // of all chunks (graphs[2B]).
@@ -424,6 +428,7 @@ static bool create_storage(wamx_gwp_model * m) {
     m->in_freq0 = wamx_new_tensor_2d(s, WAMX_TYPE_F32, 256, 1);
     m->in_freqs = wamx_new_tensor_2d(s, WAMX_TYPE_F32, 256, c.num_steps);
     m->in_dts = wamx_new_tensor_1d(s, WAMX_TYPE_F32, c.num_steps);
+    m->vis_rope = wamx_new_tensor_2d(s, WAMX_TYPE_F32, dh, m->nimg);
     m->sbuf = wamx_backend_alloc_ctx_tensors(s, m->be);
     if (!m->sbuf) return false;
     // Views of the padded V^T storage covering the real key columns.
@@ -451,6 +456,16 @@ static bool create_storage(wamx_gwp_model * m) {
     wamx_backend_tensor_set(m->in_vt, vt.data(), 0, vt.size() * 4);
     wamx_backend_tensor_set(m->in_vh, vh.data(), 0, vh.size() * 4);
     wamx_backend_tensor_set(m->in_vw, vw.data(), 0, vw.size() * 4);
+    {
+        hipStream_t st = (hipStream_t) wamx_backend_stream(m->be);
+        if (launch_rope_table(1, (const int32_t *) m->in_vt->data, (const int32_t *) m->in_vh->data,
+                              (const int32_t *) m->in_vw->data, m->nimg, dh, 10000.0f, (float *) m->vis_rope->data,
+                              st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
+            set_error("wamx_gwp_create: rope table failed");
+            return false;
+        }
+    }
     auto embed = [](float t, float * out) {
         for (int i = 0; i < 128; ++i) {
             const float f = expf(-logf(10000.0f) * (float) i / 128.0f);
@@ -575,9 +590,9 @@ static bool build_prefix_graph(wamx_gwp_model * m, int64_t cb) {
         wamx_tensor * vn = wamx_norm_modulation_bf16(ctx, vh, b.part(vmods, d, l, 1), b.part(vmods, d, l, 0), c.eps);
         wamx_tensor * vqkv = b.lin(ev.qkv_w, ev.qkv_b, vn);
         wamx_tensor * Qv = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, dh, nimg, H);
-        Qv = wamx_qk_norm_rope(ctx, b.cols(vqkv, d, 0), ev.norm_q, Qv, 0, 1, m->in_vt, m->in_vh, m->in_vw, c.eps,
+        Qv = wamx_qk_norm_rope(ctx, b.cols(vqkv, d, 0), ev.norm_q, Qv, 0, 3, m->vis_rope, nullptr, nullptr, c.eps,
                                10000.0f);
-        K = wamx_qk_norm_rope(ctx, b.cols(vqkv, d, d), ev.norm_k, K, 1, 1, m->in_vt, m->in_vh, m->in_vw, c.eps,
+        K = wamx_qk_norm_rope(ctx, b.cols(vqkv, d, d), ev.norm_k, K, 1, 3, m->vis_rope, nullptr, nullptr, c.eps,
                               10000.0f);
         wamx_tensor * v1 = b.store_v(vqkv, 2 * d, after(b.vt_view(pv_raw, 1, nimg), v0));
         wamx_tensor * V = after(b.vt_view(pv_raw, 0, P), v1);

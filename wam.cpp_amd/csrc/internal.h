@@ -181,7 +181,12 @@ hipError_t launch_mlp_small(const void * x, const void * w1, const void * b1, co
 hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void * dst, int64_t heads, int64_t head_dim,
                                int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode, const int32_t * pos0,
                                const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s,
-                               int64_t chunk_tokens = 0, int64_t chunk_stride = 0, int64_t lo_off = 0);
+                               int64_t chunk_tokens = 0, int64_t chunk_stride = 0, int64_t lo_off = 0,
+                               const float * tab = nullptr);
+// (cos, sin) of every rope pair of `tokens` tokens (rope mode 0 or 1
+// positions) into out [tokens][head_dim]: the table of rope mode 3.
+hipError_t launch_rope_table(int rope_mode, const int32_t * pos0, const int32_t * pos1, const int32_t * pos2,
+                             int64_t tokens, int64_t head_dim, float freq_base, float * out, hipStream_t s);
 
 struct AttnArgs {
     const void * q = nullptr;      // bf16 [batch][H][Tq][dh]

@@ -145,8 +145,12 @@ const char * check_qk_norm_rope(const wamx_tensor * t) {
     const int64_t tok0 = t->op_params[0];
     const int rope_mode = t->op_params[1];
     if (tok0 < 0 || tok0 + T > dst->ne[1]) return "token range";
-    if (rope_mode < 0 || rope_mode > 2) return "rope mode";
+    if (rope_mode < 0 || rope_mode > 3) return "rope mode";
     auto pos_ok = [T](const wamx_tensor * p) { return p && p->type == WAMX_TYPE_I32 && p->ne[0] == T && p->nb[0] == 4; };
+    // Rope mode 3: a table of (cos, sin) per pair, f32 [head_dim, T].
+    if (rope_mode == 3 && (!t->src[3] || !is_f32(t->src[3]) || t->src[3]->ne[0] != dh || t->src[3]->ne[1] != T ||
+                           !contig(t->src[3]) || dh % 8 != 0))
+        return "rope table";
     if (rope_mode == 0 && !pos_ok(t->src[3])) return "positions";
     if (rope_mode == 1 && (dh != 128 || !pos_ok(t->src[3]) || !pos_ok(t->src[4]) || !pos_ok(t->src[5])))
         return "3-D rope needs head_dim 128 and three position streams";
@@ -803,7 +807,7 @@ wamx_tensor * wamx_qk_norm_rope(wamx_context * ctx, wamx_tensor * x, wamx_tensor
     t->src[0] = x;
     t->src[1] = weight;
     t->src[2] = dst;
-    t->src[3] = rope_mode <= 1 ? pos0 : nullptr;
+    t->src[3] = rope_mode <= 1 || rope_mode == 3 ? pos0 : nullptr;
     t->src[4] = rope_mode == 1 ? pos1 : nullptr;
     t->src[5] = rope_mode == 1 ? pos2 : nullptr;
     if (tok0 != (int64_t) t->op_params[0]) return fail("wamx_qk_norm_rope (token offset)");
@@ -826,7 +830,7 @@ wamx_tensor * wamx_qk_norm_rope_hilo(wamx_context * ctx, wamx_tensor * x, wamx_t
     t->src[0] = x;
     t->src[1] = weight;
     t->src[2] = dst;
-    t->src[3] = rope_mode <= 1 ? pos0 : nullptr;
+    t->src[3] = rope_mode <= 1 || rope_mode == 3 ? pos0 : nullptr;
     t->src[4] = rope_mode == 1 ? pos1 : nullptr;
     t->src[5] = rope_mode == 1 ? pos2 : nullptr;
     if (tok0 != (int64_t) t->op_params[0]) return fail("wamx_qk_norm_rope_hilo (token offset)");

@@ -108,7 +108,8 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
                                                           const int32_t * __restrict__ pos1,
                                                           const int32_t * __restrict__ pos2, float eps, float l2ts128,
                                                           float l2ts44, float l2ts42, int64_t chunk_tokens,
-                                                          int64_t chunk_stride, int64_t lo_off) {
+                                                          int64_t chunk_stride, int64_t lo_off,
+                                                          const float * __restrict__ tab) {
     __shared__ float red[16];
     const int64_t t = blockIdx.x;
     const int64_t b = t / chunk_tokens, tl = t - b * chunk_tokens;
@@ -121,7 +122,9 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
         xv[i] = *(const uint4 *) (x + t * ldx + 8 * c);
         wv[i] = *(const uint4 *) (w + 8 * c);
     }
-    const RopeTok rt = rope_tok(rope_mode, pos0, pos1, pos2, tl, l2ts128, l2ts44, l2ts42);
+    // Rope mode 3: the (cos, sin) of every pair from the table row of the token.
+    const RopeTok rt = rope_tok(tab ? 2 : rope_mode, pos0, pos1, pos2, tl, l2ts128, l2ts44, l2ts42);
+    const float * cs = tab ? tab + tl * head_dim : nullptr;
     float v[CPT][8];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -139,11 +142,11 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
         uint16_t * o = dst + b * chunk_stride + ((int64_t) h * dst_tokens + tok0 + tl) * head_dim + dd0;
         if (lo_off) {
             uint4 hi, lo;
-            qk_chunk_hilo(v[i], inv_rms, wv[i], dd0, rt, hi, lo);
+            qk_chunk_hilo(v[i], inv_rms, wv[i], dd0, rt, hi, lo, cs);
             *(uint4 *) o = hi;
             *(uint4 *) (o + lo_off) = lo;
         } else {
-            *(uint4 *) o = qk_chunk(v[i], inv_rms, wv[i], dd0, rt);
+            *(uint4 *) o = qk_chunk(v[i], inv_rms, wv[i], dd0, rt, cs);
         }
     }
 }
@@ -151,8 +154,11 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
 hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void * dst, int64_t heads, int64_t head_dim,
                                int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode, const int32_t * pos0,
                                const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s,
-                               int64_t chunk_tokens, int64_t chunk_stride, int64_t lo_off) {
+                               int64_t chunk_tokens, int64_t chunk_stride, int64_t lo_off, const float * tab) {
     if (tokens <= 0) return hipSuccess;
+    // Rope mode 3: the rotation comes from tab [tokens][head_dim] (cos, sin
+    // per pair), 16-byte aligned; only the vectorised kernel reads it.
+    if ((rope_mode == 3) != (tab != nullptr) || (tab && (((uintptr_t) tab & 15) || (head_dim % 8)))) return hipErrorInvalidValue;
     if (lo_off && ((lo_off & 7) || (chunk_tokens != tokens && chunk_tokens > 0))) return hipErrorInvalidValue;
     if (chunk_tokens <= 0) chunk_tokens = tokens;
     if (tokens % chunk_tokens != 0) return hipErrorInvalidValue;
@@ -169,14 +175,14 @@ hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void
     hipLaunchKernelGGL(qk_norm_rope_vec<CPT>, dim3((unsigned) tokens), dim3((unsigned) threads), 0, s,            \
                        (const uint16_t *) x, ldx, (const uint16_t *) w, (uint16_t *) dst, (int) heads, (int) head_dim, \
                        dst_tokens, tok0, rope_mode, pos0, pos1, pos2, eps, l2ts128, l2ts44, l2ts42, chunk_tokens,    \
-                       chunk_stride, lo_off)
+                       chunk_stride, lo_off, tab)
         if (cpt == 1) WAMX_QK_VEC(1);
         else if (cpt == 2) WAMX_QK_VEC(2);
         else WAMX_QK_VEC(4);
 #undef WAMX_QK_VEC
         return hipGetLastError();
     }
-    if ((heads * head_dim) / 2 > (int64_t) kQkThreads * kQkMaxPairs || (head_dim & 1) || (ldx & 1))
+    if ((heads * head_dim) / 2 > (int64_t) kQkThreads * kQkMaxPairs || (head_dim & 1) || (ldx & 1) || tab)
         return hipErrorInvalidValue;
     // theta_i = pos * theta_scale^i with theta_scale = base^(-2/n_dims) per rope section.
     const float ts128 = powf(freq_base, -2.0f / (float) head_dim);
@@ -185,6 +191,40 @@ hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void
     hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned) tokens), dim3(kQkThreads), 0, s, (const uint16_t *) x, ldx,
                        (const uint16_t *) w, (uint16_t *) dst, (int) heads, (int) head_dim, dst_tokens, tok0, rope_mode,
                        pos0, pos1, pos2, eps, ts128, ts44, ts42, chunk_tokens, chunk_stride, lo_off);
+    return hipGetLastError();
+}
+
+// The rope table of rope mode 3: out[t][dd] = cos, out[t][dd + 1] = sin of
+// rope_theta for token t's positions, every even dd < head_dim, with the
+// section scales launch_qk_norm_rope uses, so a table-driven rotation equals
+// the computed one bit for bit.
+__global__ void rope_table_kernel(int mode, const int32_t * __restrict__ pos0, const int32_t * __restrict__ pos1,
+                                  const int32_t * __restrict__ pos2, int64_t tokens, int head_dim, float l2ts128,
+                                  float l2ts44, float l2ts42, float * __restrict__ out) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int half = head_dim / 2;
+    if (i >= tokens * half) return;
+    const int64_t t = i / half;
+    const int dd = 2 * (int) (i - t * half);
+    const RopeTok r = rope_tok(mode, pos0, pos1, pos2, t, l2ts128, l2ts44, l2ts42);
+    float sn, cs;
+    sincosf(rope_theta(r, dd), &sn, &cs);
+    out[t * head_dim + dd] = cs;
+    out[t * head_dim + dd + 1] = sn;
+}
+
+hipError_t launch_rope_table(int rope_mode, const int32_t * pos0, const int32_t * pos1, const int32_t * pos2,
+                             int64_t tokens, int64_t head_dim, float freq_base, float * out, hipStream_t s) {
+    if (tokens <= 0) return hipSuccess;
+    if ((rope_mode != 0 && rope_mode != 1) || !pos0 || (rope_mode == 1 && (!pos1 || !pos2 || head_dim != 128)) ||
+        (head_dim & 1))
+        return hipErrorInvalidValue;
+    const float l2ts128 = -2.0f / (float) head_dim * log2f(freq_base);
+    const float l2ts44 = -2.0f / 44.0f * log2f(freq_base);
+    const float l2ts42 = -2.0f / 42.0f * log2f(freq_base);
+    const int64_t n = tokens * (head_dim / 2);
+    hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, s, rope_mode, pos0, pos1,
+                       pos2, tokens, (int) head_dim, l2ts128, l2ts44, l2ts42, out);
     return hipGetLastError();
 }
 

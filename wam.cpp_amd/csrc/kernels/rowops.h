@@ -100,26 +100,43 @@ __device__ __forceinline__ RopeTok rope_tok(int mode, const int32_t * pos0, cons
     return r;
 }
 
-// RMSNorm-scaled chunk (x * inv_rms * w, f32) rotated in (even, odd) pairs:
-// theta = pos * base^(-2i/n) for pair i of its rope section, f32 sincos.
-// e0 is the chunk's first element within the head (head_dim % 8 == 0).
-// The f32 values, before the bf16 cast.
+// Rotation angle of the pair at element dd of a head: theta = pos *
+// base^(-2i/n) for pair i of its rope section (mode 0: 1-D over head_dim;
+// mode 1: the {44, 42, 42} sections on positions p0, p1, p2).
+__device__ __forceinline__ float rope_theta(const RopeTok & r, int dd) {
+    if (r.mode == 0) return r.p0 * exp2f((float) (dd >> 1) * r.l2ts128);
+    if (dd < 44) return r.p0 * exp2f((float) (dd >> 1) * r.l2ts44);
+    if (dd < 86) return r.p1 * exp2f((float) ((dd - 44) >> 1) * r.l2ts42);
+    return r.p2 * exp2f((float) ((dd - 86) >> 1) * r.l2ts42);
+}
+
+// RMSNorm-scaled chunk (x * inv_rms * w, f32) rotated in (even, odd) pairs by
+// rope_theta, f32 sincos; or (cs_tab non-null) by the (cos, sin) pairs of a
+// precomputed table row, cs_tab[dd] = cos, cs_tab[dd + 1] = sin (built by the
+// same rope_theta and sincosf, so the bits are the same).  e0 is the chunk's
+// first element within the head (head_dim % 8 == 0).  The f32 values, before
+// the bf16 cast.
 __device__ __forceinline__ void qk_chunk_f32(const float (&v)[8], float inv_rms, const uint4 & wv, int dd0,
-                                             const RopeTok & r, float (&o)[8]) {
+                                             const RopeTok & r, float (&o)[8], const float * cs_tab = nullptr) {
     const uint32_t wu[4] = {wv.x, wv.y, wv.z, wv.w};
+    float4 ct[2];
+    if (cs_tab) {
+        ct[0] = *(const float4 *) (cs_tab + dd0);
+        ct[1] = *(const float4 *) (cs_tab + dd0 + 4);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         float a = v[2 * j] * inv_rms * __uint_as_float(wu[j] << 16);
         float b = v[2 * j + 1] * inv_rms * __uint_as_float(wu[j] & 0xFFFF0000u);
-        if (r.mode != 2) {
-            const int dd = dd0 + 2 * j;
-            float theta;
-            if (r.mode == 0) theta = r.p0 * exp2f((float) (dd >> 1) * r.l2ts128);
-            else if (dd < 44) theta = r.p0 * exp2f((float) (dd >> 1) * r.l2ts44);
-            else if (dd < 86) theta = r.p1 * exp2f((float) ((dd - 44) >> 1) * r.l2ts42);
-            else theta = r.p2 * exp2f((float) ((dd - 86) >> 1) * r.l2ts42);
+        if (cs_tab || r.mode != 2) {
             float sn, cs;
-            sincosf(theta, &sn, &cs);
+            if (cs_tab) {
+                const float4 & c = ct[j >> 1];
+                cs = (j & 1) ? c.z : c.x;
+                sn = (j & 1) ? c.w : c.y;
+            } else {
+                sincosf(rope_theta(r, dd0 + 2 * j), &sn, &cs);
+            }
             const float ra = a * cs - b * sn;
             const float rb = a * sn + b * cs;
             a = ra;
@@ -130,9 +147,9 @@ __device__ __forceinline__ void qk_chunk_f32(const float (&v)[8], float inv_rms,
     }
 }
 __device__ __forceinline__ uint4 qk_chunk(const float (&v)[8], float inv_rms, const uint4 & wv, int dd0,
-                                          const RopeTok & r) {
+                                          const RopeTok & r, const float * cs_tab = nullptr) {
     float o[8];
-    qk_chunk_f32(v, inv_rms, wv, dd0, r, o);
+    qk_chunk_f32(v, inv_rms, wv, dd0, r, o, cs_tab);
     return pack8(o);
 }
 // The same chunk as two bf16 planes: hi = bf16(o) and lo = bf16(o - hi), so
@@ -140,9 +157,9 @@ __device__ __forceinline__ uint4 qk_chunk(const float (&v)[8], float inv_rms, co
 // f32).  Products of hi and lo parts are exact in fp32, which lets bf16 MFMA
 // form f32-accurate dot products as hi*hi + hi*lo + lo*hi.
 __device__ __forceinline__ void qk_chunk_hilo(const float (&v)[8], float inv_rms, const uint4 & wv, int dd0,
-                                              const RopeTok & r, uint4 & hi, uint4 & lo) {
+                                              const RopeTok & r, uint4 & hi, uint4 & lo, const float * cs_tab = nullptr) {
     float o[8], l[8];
-    qk_chunk_f32(v, inv_rms, wv, dd0, r, o);
+    qk_chunk_f32(v, inv_rms, wv, dd0, r, o, cs_tab);
     hi = pack8(o);
     float h[8];
     unpack8(hi, h);

@@ -128,6 +128,8 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
                                              TensorP, f32, f32]),
         "wamx_joint_attn_hilo": (TensorP, [vp, TensorP, TensorP, TensorP, f32]),
         "wamx_euler_step": (TensorP, [vp, TensorP, TensorP, TensorP]),
+        "wamx_op_rope_table": (C.c_int, [vp, C.c_int, vp, vp, vp, i64, i64, f32, vp]),
+        "wamx_op_qk_norm_rope_table": (C.c_int, [vp, vp, i64, vp, vp, i64, i64, i64, i64, i64, vp, f32]),
         "wamx_mlp_small": (TensorP, [vp, TensorP, TensorP, TensorP, TensorP, TensorP, i32]),
         "wamx_op_soft_max_f32": (C.c_int, [vp, vp, vp, i64, i64, f32]),
         "wamx_fill_normal": (C.c_int, [vp, vp, i32, i64, C.c_uint64, f32, f32]),
