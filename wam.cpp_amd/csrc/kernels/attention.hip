@@ -81,10 +81,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(const uint16_t
             }
             float sn, cs;
             sincosf(theta, &sn, &cs);
-            const float ra = a * cs - b * sn;
-            const float rb = a * sn + b * cs;
-            a = ra;
-            b = rb;
+            rotate_pair(a, b, cs, sn);
         }
         uint32_t * out = (uint32_t *) (dst + cb * chunk_stride + ((int64_t) h * dst_tokens + tok0 + tl) * head_dim + dd);
         const uint32_t hi = pack_bf16x2(a, b);

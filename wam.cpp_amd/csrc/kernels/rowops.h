@@ -110,6 +110,17 @@ __device__ __forceinline__ float rope_theta(const RopeTok & r, int dd) {
     return r.p2 * exp2f((float) ((dd - 86) >> 1) * r.l2ts42);
 }
 
+// (a, b) rotated by the angle with cosine cs and sine sn, in one fixed
+// rounding sequence (each output one fma over a rounded product), so every
+// kernel that rotates gives the same bits whatever the compiler would
+// contract in `a * cs - b * sn`.
+__device__ __forceinline__ void rotate_pair(float & a, float & b, float cs, float sn) {
+    const float ra = fmaf(a, cs, -(b * sn));
+    const float rb = fmaf(a, sn, b * cs);
+    a = ra;
+    b = rb;
+}
+
 // RMSNorm-scaled chunk (x * inv_rms * w, f32) rotated in (even, odd) pairs by
 // rope_theta, f32 sincos; or (cs_tab non-null) by the (cos, sin) pairs of a
 // precomputed table row, cs_tab[dd] = cos, cs_tab[dd + 1] = sin (built by the
@@ -137,10 +148,7 @@ __device__ __forceinline__ void qk_chunk_f32(const float (&v)[8], float inv_rms,
             } else {
                 sincosf(rope_theta(r, dd0 + 2 * j), &sn, &cs);
             }
-            const float ra = a * cs - b * sn;
-            const float rb = a * sn + b * cs;
-            a = ra;
-            b = rb;
+            rotate_pair(a, b, cs, sn);
         }
         o[2 * j] = a;
         o[2 * j + 1] = b;
