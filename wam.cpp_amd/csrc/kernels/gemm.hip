@@ -662,8 +662,8 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_dma(GemmParams p, int 
 }
 
 // ---------------------------------------------------------------------------
-// gemm_dma_pipe: gemm_dma's LDS-DMA ring (BK = 32, S >= 3 stages) with a
-// software-pipelined step.  The compiler's wait insertion cannot tell the
+// gemm_dma_pipe: gemm_dma's LDS-DMA ring (BK = 32 or 64, S >= 3 stages) with
+// a software-pipelined step.  The compiler's wait insertion cannot tell the
 // ring's LDS stages apart and drains every in-flight copy before the first
 // fragment read after a barrier; here the fragment reads are explicit
 // ds_read_b128 instructions with explicit lgkmcnt waits, so only the wait
@@ -672,7 +672,8 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_dma(GemmParams p, int 
 //   reads; MFMAs of k-step 0; wait for tile kt+1's copies and barrier (every
 //   wave is past tile kt-1); refill tile kt-1's stage with tile kt+S-1; wait
 //   for k-step 1's reads; issue k-step 0's reads of tile kt+1; MFMAs of
-//   k-step 1.
+//   k-step 1.  With BK 64 the stage holds four k-steps: k-steps 1-3 are read
+//   one ahead of their MFMAs, and the barrier comes before k-step 3's.
 // Scheduling barriers keep the MFMA groups on their side of the waits.  Same
 // tiles, swizzle, accumulation order and epilogue as gemm_dma: same bits.
 //
@@ -713,15 +714,15 @@ __device__ __forceinline__ void lgkm_wait(bf16x8_t (&a)[FR], bf16x8_t (&b)[FC]) 
     for (int j = 0; j < FC; ++j) asm volatile("" : "+v"(b[j]));
 }
 
-template <int BM, int BN, int WM, int WN, int S, int SCHED = kSchedSingle>
+template <int BM, int BN, int WM, int WN, int S, int SCHED = kSchedSingle, int BK = 32>
 __global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1) void gemm_dma_pipe(
     GemmParams p, int nt_m, int nt_n) {
-    constexpr int BK = 32;
+    constexpr int KS = BK / 16;  // 16-deep MFMA k-steps per stage
     using C = DmaCfg<BM, BN, WM, WN, BK, S>;
     constexpr int FR = C::FR, FC = C::FC, P = C::P, E = C::kStageElems, CH = C::kChunks;
     constexpr bool PP = SCHED == kSchedPingPong, kProd = SCHED == kSchedProducer;
     static_assert(S >= 3, "the mid-step barrier needs three or more stages");
-    static_assert(!PP || WM * WN == 8, "ping-pong pairs two waves per SIMD");
+    static_assert(!PP || (WM * WN == 8 && BK == 32), "ping-pong pairs two waves per SIMD, BK 32");
     static_assert(!kProd || WM * WN == 4, "producers take the second wave of each SIMD");
     static_assert(FR <= 4 && FC <= 4, "fragment count");
     __shared__ __align__(16) uint16_t st0[E];
@@ -741,25 +742,27 @@ __global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1
     const int64_t n0 = (int64_t) tn * BM, m0 = (int64_t) tm * BN;
     const int64_t N = p.N, M = p.M;
     const int nk = (int) (p.K / BK);
-    const char * src[P];
+    // Copy sources as 32-bit byte offsets from the activation or weight base
+    // (the launcher keeps both operands under 4 GB).  Copy instruction i of a
+    // lane covers stage rows RPI i .. RPI (i + 1), all activation rows or all
+    // weight rows.
+    constexpr int RPI = C::kWaves * 64 / CH;
+    static_assert(BM % RPI == 0, "a copy instruction covers activation rows or weight rows only");
+    uint32_t soff[P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
         const int slot = (i * C::kWaves + cw) * 64 + lane;
         const int r = slot / CH, c = (slot % CH) ^ dma_swz<BK>(slot / CH);
-        if (r < BM) {
-            const int64_t n = min(n0 + r, N - 1);
-            src[i] = (const char *) ((const uint16_t *) p.x + n * p.ldx + 8 * c);
-        } else {
-            const int64_t m = min(m0 + (r - BM), M - 1);
-            src[i] = (const char *) (p.w + m * p.ldw + 8 * c);
-        }
+        if (i * RPI < BM) soff[i] = (uint32_t) ((min(n0 + r, N - 1) * p.ldx + 8 * c) * 2);
+        else soff[i] = (uint32_t) ((min(m0 + (r - BM), M - 1) * p.ldw + 8 * c) * 2);
     }
+    const char * const xb = (const char *) p.x, * const wb = (const char *) p.w;
     uint16_t * const stp[5] = {st0, st1, st2, S > 3 ? st3 : st0, S > 4 ? st4 : st0};
     auto dma = [&](int kt, int stage) {
-        const int64_t koff = (int64_t) min(kt, nk - 1) * BK * 2;
+        const uint32_t koff = (uint32_t) min(kt, nk - 1) * BK * 2;
 #pragma unroll
         for (int i = 0; i < P; ++i)
-            __builtin_amdgcn_global_load_lds((glb_void_t *) (src[i] + koff),
+            __builtin_amdgcn_global_load_lds((glb_void_t *) ((i * RPI < BM ? xb : wb) + (soff[i] + koff)),
                                              (lds_void_t *) (stp[stage] + (i * C::kWaves + cw) * 64 * 8), 16, 0, 0);
     };
 
@@ -799,23 +802,22 @@ __global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    // Byte offsets of this lane's fragments in a stage, per 16-wide k-step.
+    // Byte offsets of this lane's A fragments in a stage, per 16-wide k-step;
+    // its B fragments sit a wave-uniform distance further (the row swizzle
+    // repeats every 16 rows, and the wave tiles start at multiples of 16).
+    static_assert(C::kWaveM % 16 == 0 && C::kWaveN % 16 == 0 && BM % 16 == 0, "swizzle period");
     const int arow = wr * C::kWaveM + (lane & 31);
-    const int brow = BM + wc * C::kWaveN + (lane & 31);
     const int sw = dma_swz<BK>(lane & 31);
-    uint32_t aoff[2], boff[2];
+    const uint32_t bdelta = (uint32_t) ((BM + wc * C::kWaveN - wr * C::kWaveM) * BK * 2);
+    uint32_t aoff[KS];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int ko = ((2 * ks + (lane >> 5)) ^ sw) * 8;
-        aoff[ks] = (uint32_t) (arow * BK + ko) * 2;
-        boff[ks] = (uint32_t) (brow * BK + ko) * 2;
-    }
+    for (int ks = 0; ks < KS; ++ks) aoff[ks] = (uint32_t) (arow * BK + ((2 * ks + (lane >> 5)) ^ sw) * 8) * 2;
     const uint32_t sbase[5] = {lds_addr(st0), lds_addr(st1), lds_addr(st2), lds_addr(stp[3]), lds_addr(stp[4])};
 
     constexpr int RS = 32 * BK * 2;  // bytes between fragment rows 32 apart
     bf16x8_t a0[FR], b0[FC], a1[FR], b1[FC];
     auto read = [&](bf16x8_t (&a)[FR], bf16x8_t (&b)[FC], int stage, int ks) {
-        const uint32_t ab = sbase[stage] + aoff[ks], bb = sbase[stage] + boff[ks];
+        const uint32_t ab = sbase[stage] + aoff[ks], bb = ab + bdelta;
         a[0] = ds_read128<0>(ab);
         if constexpr (FR > 1) a[1] = ds_read128<RS>(ab);
         if constexpr (FR > 2) a[2] = ds_read128<2 * RS>(ab);
@@ -832,12 +834,26 @@ __global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1
             for (int j = 0; j < FC; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     };
+    // Step kt: the stage's k-steps alternate between the two fragment sets
+    // (the reads of k-step i + 1 in flight while k-step i multiplies); the
+    // barrier comes before the last k-step, and the first k-step of tile
+    // kt+1 is read behind it.
     auto step = [&](int kt, int cur) {
         const int nxt = cur + 1 == S ? 0 : cur + 1, prv = cur == 0 ? S - 1 : cur - 1;
         read(a1, b1, cur, 1);
         lgkm_wait<FR + FC>(a0, b0);
         mma(a0, b0);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (KS == 4) {
+            read(a0, b0, cur, 2);
+            lgkm_wait<FR + FC>(a1, b1);
+            mma(a1, b1);
+            __builtin_amdgcn_sched_barrier(0);
+            read(a1, b1, cur, 3);
+            lgkm_wait<FR + FC>(a0, b0);
+            mma(a0, b0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         if constexpr (!kProd) __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 3) * P));  // tile kt+1 landed
         cta_barrier();
         if constexpr (!kProd) dma(kt + S - 1, prv);
@@ -1694,14 +1710,16 @@ static hipError_t run_dma(const GemmParams & p, hipStream_t s) {
                        p, nt_m, nt_n);
     return hipGetLastError();
 }
-// The pipelined form (BK 32) for vector-stored bf16 outputs, else gemm_dma.
-template <int BM, int BN, int WM, int WN, int S, int BKF, int SF, int SCHED = kSchedSingle>
+// The pipelined form (K steps of BKP) for vector-stored bf16 outputs, else gemm_dma.
+template <int BM, int BN, int WM, int WN, int S, int BKF, int SF, int SCHED = kSchedSingle, int BKP = 32>
 static hipError_t run_dma_pipe(const GemmParams & p, hipStream_t s) {
-    if (!p.vec_out) return run_dma<BM, BN, WM, WN, BKF, SF>(p, s);
+    // The pipelined kernel addresses its copies by 32-bit offsets.
+    const bool small = (uint64_t) p.N * p.ldx * 2 < (1ull << 32) && (uint64_t) p.M * p.ldw * 2 < (1ull << 32);
+    if (!p.vec_out || !small) return run_dma<BM, BN, WM, WN, BKF, SF>(p, s);
     const int nt_m = (int) ((p.M + BN - 1) / BN), nt_n = (int) ((p.N + BM - 1) / BM);
     const int threads = 64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1);
-    hipLaunchKernelGGL((gemm_dma_pipe<BM, BN, WM, WN, S, SCHED>), dim3((unsigned) (nt_m * nt_n)), dim3(threads), 0, s,
-                       p, nt_m, nt_n);
+    hipLaunchKernelGGL((gemm_dma_pipe<BM, BN, WM, WN, S, SCHED, BKP>), dim3((unsigned) (nt_m * nt_n)), dim3(threads), 0,
+                       s, p, nt_m, nt_n);
     return hipGetLastError();
 }
 
@@ -1784,9 +1802,9 @@ static hipError_t run_dma_splitk(const GemmParams & p, int splits, void * ws, hi
 //    3072, FFN-up 14336 x 3072), ping-pong with BK 32 and 4 stages (6-9%
 //    faster than the single-group schedule on both);
 //  * 192 x 192, 4 waves: 3072 x 3072 products, which it cuts into exactly 256
-//    tiles (256 x 256 leaves 112 CUs idle), pipelined with BK 32 and 4 stages
-//    (5 for K >= 8192), copies issued by 4 producer waves (2-4% faster on O
-//    and FFN-down);
+//    tiles (256 x 256 leaves 112 CUs idle), pipelined with BK 64 and 3
+//    stages, copies issued by 4 producer waves (2-4% faster on O and
+//    FFN-down than without them);
 //  (f32 or unaligned outputs take gemm_dma with BK 32 / 64 and 3 stages);
 //  * 128 x 128, BK 64, 2 stages, 4 waves, two workgroups per CU: small grids
 //    (512-token prompt projections).
@@ -1799,11 +1817,10 @@ static bool dispatch_dma(const GemmParams & p, void * ws, size_t ws_bytes, hipSt
     }
     if (p.K % 64 != 0) return false;
     if (tiles_of(p, 192, 192) >= 192) {
-        // Long K (FFN-down, 14336): a 5-stage ring, 268-271 against 279-283 us
-        // on one box, 278 against 280 (within noise) on another; same bits.
-        // On 3072-deep products 4 stages stay (64.1 against 64.6).
-        if (p.K >= 8192) err = run_dma_pipe<192, 192, 2, 2, 5, 64, 3, kSchedProducer>(p, s);
-        else err = run_dma_pipe<192, 192, 2, 2, 4, 64, 3, kSchedProducer>(p, s);
+        // K steps of 64 in a 3-stage ring (144 KB): half the barriers and
+        // waits per K of the 4-stage BK 32 ring, same bits.  3072^2 55.6
+        // against 64.0 us, FFN-down (K 14336) 234 against 280.
+        err = run_dma_pipe<192, 192, 2, 2, 3, 64, 3, kSchedProducer, 64>(p, s);
         return true;
     }
     const int splits = ws && ((uintptr_t) ws & 15) == 0 ? dma_splitk_plan(p, ws_bytes) : 1;
