@@ -810,6 +810,34 @@ WAMX_API wamx_t5_t    wamx_t5_create_from_gguf(wamx_backend_t be, wamx_gguf_t g)
  * written. */
 WAMX_API wamx_status  wamx_t5_encode(wamx_t5_t t, const int32_t * tokens, const int32_t * mask, int32_t n,
                                      float * out);
+/* Prompt-embedding cache of wamx_t5_encode, the reference engine's LRU
+ * (src/models/gwp05/engine/weights.cpp:305-317, :394-451; engine.cpp:306-331):
+ * a request whose tokens and mask (all ones when null) equal a cached
+ * entry's gets that embedding without encoding and moves it to the front; a
+ * miss that encodes to a finite embedding is added at the front and the
+ * oldest entry dropped past the capacity.  Misses are counted only with the
+ * cache on.  The initial capacity is WAM_GWP05_PROMPT_CACHE_SIZE as the
+ * reference reads it (unset or empty: 4; any '-', a non-number or trailing
+ * characters: 0, off).  Setting the capacity drops the oldest entries past
+ * it (0 empties and disables).  wamx_t5_weight and wamx_t5_load_gguf empty
+ * the cache, since its embeddings were made with the weights they change. */
+WAMX_API wamx_status  wamx_t5_set_prompt_cache(wamx_t5_t t, size_t capacity);
+typedef struct wamx_prompt_cache_stats {
+    int32_t  enabled;   /* capacity != 0 (stats.prompt_cache_enabled) */
+    int32_t  last_hit;  /* the last encode was served by the cache or the fixed prompt */
+    uint64_t capacity;
+    uint64_t hits;      /* stats.prompt_cache_hits */
+    uint64_t misses;    /* stats.prompt_cache_misses */
+    uint64_t entries;   /* stats.prompt_cache_entries */
+    uint64_t bytes;     /* f32 embedding bytes held (stats.prompt_cache_bytes) */
+} wamx_prompt_cache_stats;
+WAMX_API wamx_status  wamx_t5_prompt_cache_stats(wamx_t5_t t, wamx_prompt_cache_stats * out);
+/* The `fixed` language policy (engine.cpp:180-199, :290-300): encode this one
+ * prompt now, release the encoder weights (unload_component), and from then
+ * on answer wamx_t5_encode only for exactly these tokens and mask, with the
+ * stored embedding; any other prompt is refused ("does not match the fixed
+ * prompt").  wamx_t5_weight then returns NULL. */
+WAMX_API wamx_status  wamx_t5_fix_prompt(wamx_t5_t t, const int32_t * tokens, const int32_t * mask, int32_t n);
 /* T5's bidirectional relative-position bucket of key - query
  * (text_encoder.cpp:13-24); -1 for invalid bucket parameters. */
 WAMX_API int32_t      wamx_t5_relative_bucket(int32_t relative, int32_t buckets, int32_t max_distance);

@@ -8,7 +8,8 @@
 * the t5.* tensors of a GGUF artifact (compact names) give the same
   embedding as the weights set by name;
 * refused inputs: a mask with a hole, a token outside the vocabulary, no
-  valid token, too many tokens.
+  valid token, too many tokens;
+* the prompt-embedding cache and the fixed-prompt policy.
 """
 from __future__ import annotations
 
@@ -124,3 +125,93 @@ def test_encoder_from_gguf_and_refusals(wx, be, orc, tmp_path):
     finally:
         lib.wamx_t5_free(t1)
         lib.wamx_t5_free(t2)
+
+
+def stats(wx, be, t):
+    s = wx.PromptCacheStats()
+    wx.check(be.lib.wamx_t5_prompt_cache_stats(t, C.byref(s)), "prompt_cache_stats")
+    return s
+
+
+def test_prompt_cache_lru_and_fixed_policy(wx, be, orc, monkeypatch):
+    """The prompt-embedding LRU of the reference's engine (weights.cpp:305-317,
+    :419-451; engine.cpp:306-331) and its `fixed` policy (engine.cpp:180-199,
+    :290-300): hits return the encoded embedding bit for bit, the least
+    recently used entry goes first, a different mask is a different prompt,
+    misses count only with the cache on, weight handles empty the cache, and
+    a fixed prompt refuses every other prompt."""
+    print("t5 prompt cache", flush=True)
+    cfg = SMALL
+    lib = be.lib
+    w = synth(orc, cfg, 0x5EED0B02)
+    rng = np.random.default_rng(11)
+    A, B, Cc = (rng.integers(0, cfg["vocab"], 64) for _ in range(3))
+    half = np.array([1] * 40 + [0] * 24)
+    # initial capacity from WAM_GWP05_PROMPT_CACHE_SIZE, read at creation
+    for value, cap in ((None, 4), ("", 4), ("7", 7), ("0", 0), ("-1", 0), ("abc", 0), ("3x", 0)):
+        if value is None:
+            monkeypatch.delenv("WAM_GWP05_PROMPT_CACHE_SIZE", raising=False)
+        else:
+            monkeypatch.setenv("WAM_GWP05_PROMPT_CACHE_SIZE", value)
+        t = make(wx, be, cfg)
+        s = stats(wx, be, t)
+        lib.wamx_t5_free(t)
+        assert (s.capacity, s.enabled) == (cap, int(cap != 0)), value
+    monkeypatch.delenv("WAM_GWP05_PROMPT_CACHE_SIZE", raising=False)
+
+    t = make(wx, be, cfg)
+    try:
+        upload(wx, be, t, w)
+        wx.check(lib.wamx_t5_set_prompt_cache(t, 2), "capacity 2")
+
+        def enc(tokens, mask=None):
+            st, out = encode(wx, be, t, cfg, tokens, mask)
+            wx.check(st, "t5_encode")
+            return out, stats(wx, be, t)
+
+        a0, s = enc(A)
+        assert (s.hits, s.misses, s.entries, s.last_hit) == (0, 1, 1, 0)
+        ref = orc.t5_encode(cfg, w, A, None)
+        assert_parity(a0, ref.astype(np.float32), what="t5 through the cache")
+        b0, s = enc(B)
+        a1, s = enc(A)                          # hit; order now A, B
+        assert (s.hits, s.misses, s.entries, s.last_hit) == (1, 2, 2, 1)
+        assert np.array_equal(a1, a0)
+        assert s.bytes == 2 * cfg["max_tokens"] * cfg["hidden"] * 4
+        _, s = enc(Cc)                          # miss; B, the oldest, goes
+        assert (s.hits, s.misses, s.entries) == (1, 3, 2)
+        _, s = enc(A)                           # still cached
+        assert (s.hits, s.misses) == (2, 3)
+        b1, s = enc(B)                          # evicted: encoded again
+        assert (s.hits, s.misses, s.last_hit) == (2, 4, 0)
+        assert np.array_equal(b1, b0)
+        _, s = enc(A, np.ones(64, np.int32))    # the all-ones mask is the null mask
+        assert (s.hits, s.misses) == (3, 4)
+        h0, s = enc(A, half)                    # same tokens, another mask
+        assert (s.hits, s.misses) == (3, 5) and not h0[40:].any()
+        # a weight handle empties the cache
+        assert lib.wamx_t5_weight(t, b"t5.shared.weight")
+        assert stats(wx, be, t).entries == 0
+        _, s = enc(A)
+        assert (s.hits, s.misses, s.entries) == (3, 6, 1)
+        # capacity 0: off, emptied, no counting
+        wx.check(lib.wamx_t5_set_prompt_cache(t, 0), "capacity 0")
+        _, s = enc(A)
+        assert (s.enabled, s.entries, s.hits, s.misses, s.last_hit) == (0, 0, 3, 6, 0)
+        # a refused request leaves the counters alone
+        st, _ = encode(wx, be, t, cfg, A, np.array([1, 0, 1] + [0] * 61))
+        assert st != 0 and "contiguous" in wx.last_error()
+
+        # the fixed policy
+        mk = np.ascontiguousarray(half, np.int32)
+        tk = np.ascontiguousarray(A, np.int32)
+        wx.check(lib.wamx_t5_fix_prompt(t, tk.ctypes.data, mk.ctypes.data, 64), "fix_prompt")
+        assert not lib.wamx_t5_weight(t, b"t5.shared.weight")
+        f, s = enc(A, half)
+        assert s.last_hit == 1 and np.array_equal(f, h0)
+        for toks, mask in ((A, None), (B, half)):
+            st, _ = encode(wx, be, t, cfg, toks, mask)
+            assert st != 0 and "does not match the fixed prompt" in wx.last_error()
+        assert lib.wamx_t5_fix_prompt(t, tk.ctypes.data, mk.ctypes.data, 64) != 0
+    finally:
+        lib.wamx_t5_free(t)

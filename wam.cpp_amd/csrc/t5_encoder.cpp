@@ -13,8 +13,11 @@
 // the gated-GELU FFN GELU(wi_0 x) * (wi_1 x) -> wo, residual ADD; a final
 // RMSNorm.  Only the valid (mask) prefix of the tokens is encoded; the rows
 // past it are zero, as the reference returns them.
+#include <cerrno>
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
+#include <list>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -39,6 +42,29 @@ int bucket_of(int relative, int buckets, int max_distance) {
     return base + std::min(half - 1, exact + (int) (r * (float) (half - exact)));
 }
 
+// Initial capacity of the prompt-embedding cache, read as the reference
+// reads WAM_GWP05_PROMPT_CACHE_SIZE (weights.cpp:305-317): unset or empty 4;
+// any '-', a non-number, trailing characters or overflow 0 (off).
+size_t prompt_cache_capacity_env() {
+    const char * v = std::getenv("WAM_GWP05_PROMPT_CACHE_SIZE");
+    if (!v || !*v) return 4;
+    if (std::strchr(v, '-')) return 0;
+    errno = 0;
+    char * end = nullptr;
+    const unsigned long long n = std::strtoull(v, &end, 10);
+    if (errno == ERANGE || end == v || !end || *end) return 0;
+    return (size_t) n;
+}
+
+// A cached prompt: the request's tokens and mask (all ones when the request
+// has none, as prompt_mask does, weights.cpp:412-417) and its embedding
+// ([max_tokens][hidden], rows past the valid prefix zero).
+struct PromptEntry {
+    std::vector<int32_t> tokens, mask;
+    std::vector<float> emb;
+    bool same(const std::vector<int32_t> & t, const std::vector<int32_t> & m) const { return tokens == t && mask == m; }
+};
+
 }  // namespace
 
 struct wamx_t5 {
@@ -49,6 +75,15 @@ struct wamx_t5 {
     std::vector<std::pair<std::string, wamx_tensor *>> weights;
     std::unordered_map<std::string, wamx_tensor *> by_name;
     wamx_gallocr_t galloc = nullptr;
+    // Prompt-embedding LRU (weights.cpp:394-451): most recent first.
+    std::list<PromptEntry> cache;
+    size_t cache_limit = prompt_cache_capacity_env();
+    uint64_t hits = 0, misses = 0;
+    bool last_hit = false;
+    // The `fixed` language policy: one prompt, encoded up front; the weights
+    // are released after it (engine.cpp:180-199).
+    bool fixed = false;
+    PromptEntry fixed_prompt;
 
     wamx_tensor * add(const std::string & name, int64_t ne0, int64_t ne1 = 1) {
         wamx_tensor * t = wamx_new_tensor_2d(wctx, WAMX_TYPE_BF16, ne0, ne1);
@@ -137,10 +172,19 @@ int wamx_t5_n_weights(wamx_t5_t t) { return t ? (int) t->weights.size() : 0; }
 const char * wamx_t5_weight_name(wamx_t5_t t, int i) {
     return t && i >= 0 && i < (int) t->weights.size() ? t->weights[(size_t) i].first.c_str() : nullptr;
 }
-wamx_tensor * wamx_t5_weight(wamx_t5_t t, const char * name) { return t && name ? t->w(name) : nullptr; }
+// A weight handle may be written through, so handing one out empties the
+// prompt cache (its embeddings were made with the old weights).  None after
+// wamx_t5_fix_prompt released the weights.
+wamx_tensor * wamx_t5_weight(wamx_t5_t t, const char * name) {
+    if (!t || !name || t->fixed) return nullptr;
+    t->cache.clear();
+    return t->w(name);
+}
 
 wamx_status wamx_t5_load_gguf(wamx_t5_t t, wamx_gguf_t g) {
     WAMX_REQUIRE(t && g, "wamx_t5_load_gguf: null argument");
+    WAMX_REQUIRE(!t->fixed, "wamx_t5_load_gguf: the encoder serves a fixed prompt; its weights were released");
+    t->cache.clear();
     std::vector<uint16_t> buf;
     char cname[128];
     for (auto & kv : t->weights) {
@@ -197,31 +241,14 @@ wamx_t5_t wamx_t5_create_from_gguf(wamx_backend_t be, wamx_gguf_t g) {
     return t;
 }
 
-wamx_status wamx_t5_encode(wamx_t5_t t5, const int32_t * tokens, const int32_t * mask, int32_t n, float * out) {
-    WAMX_REQUIRE(t5 && tokens && out, "wamx_t5_encode: null argument");
-    const wamx_t5_config & c = t5->cfg;
-    WAMX_REQUIRE(n >= 1 && n <= c.max_tokens, "wamx_t5_encode: token count %d outside [1,%d]", n, c.max_tokens);
-    // validate_prompt_mask (text_encoder.cpp:75-110): 0/1 values, the valid
-    // tokens a contiguous prefix, at least one.
-    int valid = n;
-    if (mask) {
-        valid = 0;
-        bool pad = false;
-        for (int i = 0; i < n; ++i) {
-            WAMX_REQUIRE(mask[i] == 0 || mask[i] == 1, "wamx_t5_encode: mask values must be zero or one");
-            if (mask[i] == 1) {
-                WAMX_REQUIRE(!pad, "wamx_t5_encode: mask must be a contiguous valid prefix");
-                ++valid;
-            } else {
-                pad = true;
-            }
-        }
-    }
-    WAMX_REQUIRE(valid >= 1, "wamx_t5_encode: mask contains no valid tokens");
-    for (int i = 0; i < valid; ++i)
-        WAMX_REQUIRE(tokens[i] >= 0 && tokens[i] < c.vocab, "wamx_t5_encode: token %d is outside the vocabulary",
-                     tokens[i]);
+}  // extern "C"
 
+namespace {
+
+// run_t5 on the valid prefix of a validated request (tokens in the
+// vocabulary); out [max_tokens][hidden] with the rows past it zero.
+wamx_status encode_graph(wamx_t5_t t5, const int32_t * tokens, int valid, float * out) {
+    const wamx_t5_config & c = t5->cfg;
     const int64_t V = valid, d = c.hidden, H = c.heads, dh = c.head_dim, inner = H * dh;
     wamx_context * ctx = wamx_init(64 * c.layers + 64);
     WAMX_REQUIRE(ctx, "wamx_t5_encode: context allocation failed");
@@ -281,6 +308,140 @@ wamx_status wamx_t5_encode(wamx_t5_t t5, const int32_t * tokens, const int32_t *
     if (gs != WAMX_STATUS_SUCCESS) return gs;
     // The engine refuses a non-finite T5 embedding (engine.cpp:314-320).
     return wamx_check_finite_f32(out, (size_t) V * (size_t) d, "wamx_t5_encode: embedding");
+}
+
+// validate_prompt_mask (text_encoder.cpp:75-110) and the vocabulary check:
+// 0/1 mask values, the valid tokens a contiguous prefix, at least one.  The
+// number of valid tokens, or -1 with the error set.
+int validate_request(const wamx_t5_config & c, const int32_t * tokens, const int32_t * mask, int32_t n) {
+    wamx::clear_error();
+    if (n < 1 || n > c.max_tokens) {
+        wamx::set_errorf("wamx_t5_encode: token count %d outside [1,%d]", n, c.max_tokens);
+        return -1;
+    }
+    int valid = n;
+    if (mask) {
+        valid = 0;
+        bool pad = false;
+        for (int i = 0; i < n; ++i) {
+            if (mask[i] != 0 && mask[i] != 1) {
+                wamx::set_error("wamx_t5_encode: mask values must be zero or one");
+                return -1;
+            }
+            if (mask[i] == 1) {
+                if (pad) {
+                    wamx::set_error("wamx_t5_encode: mask must be a contiguous valid prefix");
+                    return -1;
+                }
+                ++valid;
+            } else {
+                pad = true;
+            }
+        }
+    }
+    if (valid < 1) {
+        wamx::set_error("wamx_t5_encode: mask contains no valid tokens");
+        return -1;
+    }
+    for (int i = 0; i < valid; ++i)
+        if (tokens[i] < 0 || tokens[i] >= c.vocab) {
+            wamx::set_errorf("wamx_t5_encode: token %d is outside the vocabulary", tokens[i]);
+            return -1;
+        }
+    return valid;
+}
+
+std::vector<int32_t> request_mask(const int32_t * mask, int32_t n) {
+    return mask ? std::vector<int32_t>(mask, mask + n) : std::vector<int32_t>((size_t) n, 1);
+}
+
+}  // namespace
+
+extern "C" {
+
+// The engine's prompt step for token requests (engine.cpp:290-323): the fixed
+// prompt, else the cache (get_cached_prompt, weights.cpp:419-434: a hit moves
+// the entry to the front; misses are counted only with the cache on), else
+// run_t5 and, for a finite embedding, a new front entry with the oldest
+// dropped past the capacity (put_cached_prompt, :436-444).
+wamx_status wamx_t5_encode(wamx_t5_t t5, const int32_t * tokens, const int32_t * mask, int32_t n, float * out) {
+    WAMX_REQUIRE(t5 && tokens && out, "wamx_t5_encode: null argument");
+    const wamx_t5_config & c = t5->cfg;
+    const size_t emb = (size_t) c.max_tokens * (size_t) c.hidden;
+    t5->last_hit = false;
+    const int valid = validate_request(c, tokens, mask, n);
+    if (valid < 0) return WAMX_STATUS_FAILED;
+    const std::vector<int32_t> tok(tokens, tokens + n), m = request_mask(mask, n);
+    if (t5->fixed) {
+        WAMX_REQUIRE(t5->fixed_prompt.same(tok, m), "wamx_t5_encode: token input does not match the fixed prompt");
+        memcpy(out, t5->fixed_prompt.emb.data(), emb * sizeof(float));
+        t5->last_hit = true;
+        return WAMX_STATUS_SUCCESS;
+    }
+    if (t5->cache_limit) {
+        for (auto it = t5->cache.begin(); it != t5->cache.end(); ++it) {
+            if (!it->same(tok, m)) continue;
+            memcpy(out, it->emb.data(), emb * sizeof(float));
+            t5->cache.splice(t5->cache.begin(), t5->cache, it);
+            ++t5->hits;
+            t5->last_hit = true;
+            return WAMX_STATUS_SUCCESS;
+        }
+        ++t5->misses;
+    }
+    const wamx_status st = encode_graph(t5, tokens, valid, out);
+    if (st != WAMX_STATUS_SUCCESS || !t5->cache_limit) return st;
+    PromptEntry e;
+    e.tokens = tok;
+    e.mask = m;
+    e.emb.assign(out, out + emb);
+    t5->cache.push_front(std::move(e));
+    while (t5->cache.size() > t5->cache_limit) t5->cache.pop_back();
+    return WAMX_STATUS_SUCCESS;
+}
+
+wamx_status wamx_t5_set_prompt_cache(wamx_t5_t t, size_t capacity) {
+    WAMX_REQUIRE(t, "wamx_t5_set_prompt_cache: null argument");
+    t->cache_limit = capacity;
+    while (t->cache.size() > capacity) t->cache.pop_back();
+    return WAMX_STATUS_SUCCESS;
+}
+
+wamx_status wamx_t5_prompt_cache_stats(wamx_t5_t t, wamx_prompt_cache_stats * out) {
+    WAMX_REQUIRE(t && out, "wamx_t5_prompt_cache_stats: null argument");
+    out->enabled = t->cache_limit != 0;
+    out->last_hit = t->last_hit;
+    out->capacity = t->cache_limit;
+    out->hits = t->hits;
+    out->misses = t->misses;
+    out->entries = t->cache.size();
+    uint64_t bytes = 0;
+    for (const PromptEntry & e : t->cache) bytes += e.emb.size() * sizeof(float);
+    out->bytes = bytes;
+    return WAMX_STATUS_SUCCESS;
+}
+
+wamx_status wamx_t5_fix_prompt(wamx_t5_t t, const int32_t * tokens, const int32_t * mask, int32_t n) {
+    WAMX_REQUIRE(t && tokens, "wamx_t5_fix_prompt: null argument");
+    WAMX_REQUIRE(!t->fixed, "wamx_t5_fix_prompt: the encoder already serves a fixed prompt");
+    const int valid = validate_request(t->cfg, tokens, mask, n);
+    if (valid < 0) return WAMX_STATUS_FAILED;
+    PromptEntry e;
+    e.tokens.assign(tokens, tokens + n);
+    e.mask = request_mask(mask, n);
+    e.emb.resize((size_t) t->cfg.max_tokens * (size_t) t->cfg.hidden);
+    const wamx_status st = encode_graph(t, tokens, valid, e.emb.data());
+    if (st != WAMX_STATUS_SUCCESS) return st;
+    t->fixed_prompt = std::move(e);
+    t->fixed = true;
+    t->cache.clear();
+    // unload_component(t5) (engine.cpp:199): the encoder weights and the
+    // graph allocator go; the object keeps only the embedding.
+    wamx_gallocr_free(t->galloc);
+    t->galloc = nullptr;
+    wamx_buffer_free(t->wbuf);
+    t->wbuf = nullptr;
+    return WAMX_STATUS_SUCCESS;
 }
 
 }  // extern "C"

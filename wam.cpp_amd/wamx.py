@@ -70,6 +70,11 @@ class T5Config(C.Structure):
                [("eps", C.c_float)]
 
 
+class PromptCacheStats(C.Structure):
+    _fields_ = [("enabled", C.c_int32), ("last_hit", C.c_int32)] + \
+               [(k, C.c_uint64) for k in ("capacity", "hits", "misses", "entries", "bytes")]
+
+
 class GwpTiming(C.Structure):
     _fields_ = [("prompt_ms", C.c_float), ("prefix_ms", C.c_float), ("denoise_ms", C.c_float),
                 ("total_ms", C.c_float)]
@@ -274,6 +279,9 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "wamx_t5_load_gguf": (C.c_int, [vp, vp]),
         "wamx_t5_create_from_gguf": (vp, [vp, vp]),
         "wamx_t5_encode": (C.c_int, [vp, vp, vp, i32, vp]),
+        "wamx_t5_set_prompt_cache": (C.c_int, [vp, C.c_size_t]),
+        "wamx_t5_prompt_cache_stats": (C.c_int, [vp, vp]),
+        "wamx_t5_fix_prompt": (C.c_int, [vp, vp, vp, i32]),
         "wamx_t5_relative_bucket": (i32, [i32, i32, i32]),
     }
     for name, (res, args) in sig.items():
