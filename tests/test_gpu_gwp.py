@@ -231,7 +231,8 @@ def test_projected_prompt_cache(wx, be):
     nonzero capacity a request whose prompt has the same bytes as the last
     projected one skips the prompt graphs, and its action equals, bit for bit,
     that of a model that projects every prompt; a changed prompt, new weights
-    and a zero capacity all project again."""
+    (also written through a weight handle) and a zero capacity all project
+    again."""
     print("gwp projected-prompt cache", flush=True)
     lib = be.lib
     ref = make_model(wx, be, SMALL, seed=21)
@@ -256,11 +257,23 @@ def test_projected_prompt_cache(wx, be):
             wx.check(lib.wamx_gwp_init_synthetic(x, 0x77, 0.02), "init_synthetic")
         assert np.array_equal(run_gpu(wx, be, m, b), run_gpu(wx, be, ref, b))
         assert stats() == (2, 3)
+        # A weight handle may be written through: the same prompt is
+        # projected again, with the weights as they now are.
+        for x in (m, ref):
+            t = lib.wamx_gwp_weight(x, b"gwp.blocks.0.action_expert.attn2.to_k.weight")
+            assert t, wx.last_error()
+            n = lib.wamx_nelements(t)
+            w = np.empty(n, np.uint16)
+            wx.check(lib.wamx_backend_tensor_get(t, w.ctypes.data, 0, n * 2), "read")
+            w = wamx.f32_to_bf16(wamx.bf16_to_f32(w) * 1.5)
+            wx.check(lib.wamx_backend_tensor_set(t, w.ctypes.data, 0, n * 2), "write")
+        assert np.array_equal(run_gpu(wx, be, m, b), run_gpu(wx, be, ref, b))
+        assert stats() == (2, 4)
         # Capacity 0: every prompt is projected again and nothing is counted.
         wx.check(lib.wamx_gwp_set_prompt_cache(m, 0), "set_prompt_cache")
         assert np.array_equal(run_gpu(wx, be, m, a), run_gpu(wx, be, ref, a))
         assert np.array_equal(run_gpu(wx, be, m, a_other), run_gpu(wx, be, ref, a_other))
-        assert stats() == (2, 3)
+        assert stats() == (2, 4)
     finally:
         lib.wamx_gwp_free(m)
         lib.wamx_gwp_free(ref)

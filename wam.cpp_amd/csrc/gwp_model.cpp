@@ -793,10 +793,15 @@ int wamx_gwp_n_weights(wamx_gwp_t m) { return m ? (int) m->weights.size() : 0; }
 const char * wamx_gwp_weight_name(wamx_gwp_t m, int i) {
     return (m && i >= 0 && i < (int) m->weights.size()) ? m->weights[i].first.c_str() : nullptr;
 }
+// A weight handle may be written through (the GGUF loader does), so handing
+// one out marks the projected prompt stale: the next request projects it
+// again with the new weights.
 wamx_tensor * wamx_gwp_weight(wamx_gwp_t m, const char * name) {
     if (!m || !name) return nullptr;
     auto it = m->by_name.find(name);
-    return it == m->by_name.end() ? nullptr : it->second;
+    if (it == m->by_name.end()) return nullptr;
+    m->prompt_stale = true;
+    return it->second;
 }
 uint64_t wamx_gwp_param_count(wamx_gwp_t m) {
     uint64_t n = 0;
