@@ -482,12 +482,15 @@ WAMX_API wamx_status wamx_op_linear_tiled(wamx_backend_t be, const void * w, con
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, hosts that forbid hipMalloc).  stream is a
  * hipStream_t (NULL: the null stream); the caller owns w, x, bias, residual,
- * gate and y.  The split-K partials of products on <= 64 tokens live in a
- * library-owned device array of 32 MiB per GPU, held until the process ends;
- * a product whose partials would not fit is refused (status FAILED, reason in
- * wamx_last_error) before anything runs.  Every call on one GPU shares that
- * array: calls that overlap on one GPU race and must be serialised by the
- * caller.  Same kernels, same bits as wamx_op_linear. */
+ * gate and y.  The split-K partials of every product that takes a K split
+ * (products on <= 64 tokens, and products on more tokens whose grid is too
+ * small for the large tiles, e.g. 384 x 3072 x 3072) live in a library-owned
+ * device array of 32 MiB per GPU, held until the process ends.  The split is
+ * planned as wamx_op_linear plans it; a product whose partials would not fit
+ * the array is refused (status FAILED, reason in wamx_last_error) before
+ * anything runs.  Every call on one GPU shares that array: calls that overlap
+ * on one GPU race and must be serialised by the caller.  Same kernels, same
+ * K slices, same bits as wamx_op_linear. */
 WAMX_API wamx_status wamx_op_linear_noalloc(void * stream, const void * w, const void * x, int32_t x_type,
                                             const void * bias, int32_t epilogue, const void * residual,
                                             const float * gate, void * y, int64_t M, int64_t N, int64_t K);

@@ -21,7 +21,7 @@
 using namespace wamx;
 
 static constexpr size_t kAlign = 256;
-static constexpr size_t kWorkspaceBytes = 64ull << 20;  // K-split GEMM and key-split attention partials
+static constexpr size_t kWorkspaceBytes = kBackendWorkspaceBytes;
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 

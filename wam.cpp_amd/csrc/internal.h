@@ -59,6 +59,12 @@ bool tensor_is_tiled(const wamx_tensor * t);
 hipError_t tensor_set_from_device(wamx_tensor * t, const void * src, hipStream_t s);
 // Workspace the skinny path needs for an M x N x K product (0 when unsplit).
 size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K);
+// Workspace of a backend: K-split GEMM and key-split attention partials.
+constexpr size_t kBackendWorkspaceBytes = 64ull << 20;
+// Bytes of fp32 K-split partials that launch_gemm writes to its workspace
+// for a plain bf16-weight product (row-major, contiguous, one batch) of N
+// tokens, given ws_bytes of workspace; 0 when the product takes no K split.
+size_t linear_split_bytes(int64_t M, int64_t N, int64_t K, int32_t x_type, size_t ws_bytes);
 
 // Row ops that consume a skinny GEMM's output, applied by its split-K reduce
 // in the same launch (one workgroup per token row).  The GEMM output itself

@@ -1521,6 +1521,26 @@ size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     return splits > 1 ? (size_t) splits * N * M * sizeof(float) : 0;
 }
 
+static int64_t tiles_of(const GemmParams & p, int bm, int bn);
+static int dma_splitk_plan(const GemmParams & p, size_t ws_bytes);
+
+// The K split launch_gemm takes for a plain product with row-major weights:
+// the skinny plan up to 64 tokens, else the K-sliced 128 x 128 GEMM that
+// dispatch_dma runs for bf16 activations on grids too small for the 256 /
+// 192 tiles (whose slice count depends on the workspace size).
+size_t linear_split_bytes(int64_t M, int64_t N, int64_t K, int32_t x_type, size_t ws_bytes) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    if (N <= 64) return skinny_workspace_bytes(M, N, K);
+    GemmParams p{};
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    if (x_type != WAMX_TYPE_BF16 || K % 64 != 0 || tiles_of(p, 256, 256) >= 256 || tiles_of(p, 192, 192) >= 192)
+        return 0;
+    const int splits = dma_splitk_plan(p, ws_bytes);
+    return splits > 1 ? (size_t) splits * N * M * sizeof(float) : 0;
+}
+
 // gemm_skinny_part over `splits` K slices of ks columns; part == nullptr
 // (single slice only) applies the epilogue in the part kernel.
 // Workgroup shape of the tiled kernel: G waves (16 G features) by a K slice

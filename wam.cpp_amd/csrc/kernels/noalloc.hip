@@ -1,10 +1,14 @@
 // wamx_op_linear_noalloc: wamx_op_linear for callers that cannot allocate
 // device memory (code under HIP graph capture, tight serving loops, hosts
-// that forbid hipMalloc).  The split-K partials of the few-token path live in
-// `scratch`, a file-scope device array of kScratchBytes that every GPU the
-// library runs on holds until the process ends.  Nothing here allocates: no
-// backend is created, no workspace is malloc'd; the caller passes its stream,
-// inputs and output.
+// that forbid hipMalloc).  The split-K partials of any product that takes a
+// K split (few-token products on the skinny path, and 65..~500-token
+// products on small grids, K-sliced 128 x 128 tiles) live in `scratch`, a
+// file-scope device array of kScratchBytes that every GPU the library runs on
+// holds until the process ends.  Nothing here allocates: no backend is
+// created, no workspace is malloc'd; the caller passes its stream, inputs and
+// output.  The split is planned as wamx_op_linear plans it with a backend's
+// workspace; a product whose partials would then not fit the array is
+// refused, so both entry points always take the same slices (same bits).
 //
 // Every call on a GPU shares that GPU's array and it keeps the last call's
 // contents.  The partials are written whole by the part kernel before the
@@ -57,7 +61,7 @@ extern "C" wamx_status wamx_op_linear_noalloc(void * stream, const void * w, con
     WAMX_REQUIRE((epilogue != WAMX_EPI_BIAS_GATED && epilogue != WAMX_EPI_BIAS_RESIDUAL) || residual,
                  "wamx_op_linear_noalloc: residual required");
     WAMX_REQUIRE(epilogue != WAMX_EPI_BIAS_GATED || gate, "wamx_op_linear_noalloc: gate required");
-    const size_t need = N <= 64 ? skinny_workspace_bytes(M, N, K) : 0;
+    const size_t need = linear_split_bytes(M, N, K, x_type, kBackendWorkspaceBytes);
     WAMX_REQUIRE(need <= kScratchBytes,
                  "wamx_op_linear_noalloc: a %lld x %lld x %lld product needs %zu bytes of split-K scratch, more than "
                  "the %zu this entry point holds; use wamx_op_linear",
