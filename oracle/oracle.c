@@ -113,10 +113,34 @@ static void gemm_f64(const uint16_t * w, int64_t ldw, const void * x, int x_type
     free(xf);
 }
 
+/* The CPU-port switch (cpu_port.c): products and attention accumulate in
+ * fp32 in blocked order, for timing only. */
+static int g_port = 0;
+void orc_set_port(int on) { g_port = on != 0; }
+int orc_get_port(void) { return g_port; }
+
+/* acc[n][m] for either mode: the exact double sums or the fp32 port. */
+static void gemm_acc(const uint16_t * w, int64_t ldw, const void * x, int x_type, int64_t ldx, double * acc,
+                     int64_t M, int64_t N, int64_t K) {
+    if (!g_port) {
+        gemm_f64(w, ldw, x, x_type, ldx, acc, M, N, K);
+        return;
+    }
+    float * xf = (float *) malloc(sizeof(float) * (size_t) N * (size_t) K);
+    float * yf = (float *) malloc(sizeof(float) * (size_t) N * (size_t) M);
+#pragma omp parallel for
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t k = 0; k < K; ++k) xf[n * K + k] = x_as_bf16(x, x_type, n * ldx + k);
+    orc_port_gemm(w, ldw, xf, N, K, yf, M);
+    for (int64_t i = 0; i < N * M; ++i) acc[i] = yf[i];
+    free(xf);
+    free(yf);
+}
+
 void orc_mul_mat(const uint16_t * w, int64_t ldw, const void * x, int x_type, int64_t ldx, void * y, int y_type,
                  int64_t ldy, int64_t M, int64_t N, int64_t K) {
     double * acc = (double *) malloc(sizeof(double) * (size_t) M * (size_t) N);
-    gemm_f64(w, ldw, x, x_type, ldx, acc, M, N, K);
+    gemm_acc(w, ldw, x, x_type, ldx, acc, M, N, K);
     for (int64_t n = 0; n < N; ++n)
         for (int64_t m = 0; m < M; ++m) {
             const float v = (float) acc[n * M + m];
@@ -133,7 +157,7 @@ void orc_mul_mat(const uint16_t * w, int64_t ldw, const void * x, int x_type, in
 void orc_linear(const uint16_t * w, const void * x, int x_type, const uint16_t * bias, int epi,
                 const uint16_t * residual, const float * gate, uint16_t * y, int64_t M, int64_t N, int64_t K) {
     double * acc = (double *) malloc(sizeof(double) * (size_t) M * (size_t) N);
-    gemm_f64(w, K, x, x_type, K, acc, M, N, K);
+    gemm_acc(w, K, x, x_type, K, acc, M, N, K);
     for (int64_t n = 0; n < N; ++n)
         for (int64_t m = 0; m < M; ++m) {
             const float g = rb((float) acc[n * M + m]);
@@ -351,6 +375,10 @@ void orc_softmax_f32(const float * x, float * y, int64_t rows, int64_t cols, flo
 void orc_attention(const uint16_t * q, const uint16_t * k_a, const uint16_t * vt_a, int64_t na, int64_t vt_ld_a,
                    const uint16_t * k_b, const uint16_t * vt_b, int64_t nb, int64_t vt_ld_b, int64_t na_split,
                    uint16_t * out, int64_t heads, int64_t head_dim, int64_t tq, float scale) {
+    if (g_port) {
+        orc_port_attention(q, k_a, vt_a, na, vt_ld_a, k_b, vt_b, nb, vt_ld_b, na_split, out, heads, head_dim, tq, scale);
+        return;
+    }
     const int64_t nbk = k_b ? nb : 0;
     const int64_t nk = na + nbk;
 #pragma omp parallel for collapse(2)

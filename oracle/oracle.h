@@ -108,6 +108,19 @@ void orc_timestep_embedding(float timestep, int64_t dim, float * out);
  * Box-Muller over two 24-bit uniforms.  type ORC_F32 or ORC_BF16. */
 void orc_fill_normal(void * dst, int type, int64_t n, uint64_t seed, float mean, float std);
 
+/* CPU port (cpu_port.c): the same algorithm with fp32 accumulation in a
+ * blocked, vectorised order, for bench.py's cpu_baseline timing only.
+ * orc_set_port(1) routes orc_mul_mat, orc_linear, orc_attention and the MoT
+ * path's attentions through it; parity tests leave it off. */
+void orc_set_port(int on);
+int  orc_get_port(void);
+void orc_port_gemm(const uint16_t * w, int64_t ldw, const float * xf, int64_t N, int64_t K, float * y, int64_t M);
+void orc_port_attention(const uint16_t * q, const uint16_t * k_a, const uint16_t * vt_a, int64_t na, int64_t vt_ld_a,
+                        const uint16_t * k_b, const uint16_t * vt_b, int64_t nb, int64_t vt_ld_b, int64_t na_split,
+                        uint16_t * out, int64_t heads, int64_t head_dim, int64_t tq, float scale);
+void orc_port_attention_f32qk(const float * q, int64_t T, const float * k, int64_t NL, const uint16_t * vt,
+                              int64_t H, int64_t dh, float scale, uint16_t * out);
+
 #ifdef __cplusplus
 }
 #endif

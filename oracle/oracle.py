@@ -51,6 +51,8 @@ def load() -> C.CDLL:
         "orc_flow_schedule": (None, [C.c_int, f32, vp, vp]),
         "orc_timestep_embedding": (None, [f32, i64, vp]),
         "orc_fill_normal": (None, [vp, C.c_int, i64, C.c_uint64, f32, f32]),
+        "orc_set_port": (None, [C.c_int]),
+        "orc_get_port": (C.c_int, []),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -70,6 +72,12 @@ def _c(a, dtype):
 
 def num_threads() -> int:
     return int(load().orc_num_threads())
+
+
+def set_port(on: bool) -> None:
+    """Route the products and attentions through the fp32 CPU port
+    (cpu_port.c), for timing; off for parity."""
+    load().orc_set_port(1 if on else 0)
 
 
 def f32_to_bf16(x) -> np.ndarray:

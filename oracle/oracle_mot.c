@@ -159,6 +159,10 @@ static void store_vt(const uint16_t * rows, int64_t N, int64_t ld, int64_t off, 
  * output bf16 [T][d] (the O projection's input cast). */
 static void attention_f32qk(const float * q, int64_t T, const float * k, int64_t NL, const uint16_t * vt,
                             int64_t H, int64_t dh, float scale, uint16_t * out) {
+    if (orc_get_port()) {
+        orc_port_attention_f32qk(q, T, k, NL, vt, H, dh, scale, out);
+        return;
+    }
     const int64_t d = H * dh;
 #pragma omp parallel for collapse(2)
     for (int64_t h = 0; h < H; ++h)

@@ -372,3 +372,48 @@ def test_fill_normal_golden_and_moments(orc):
     assert abs(big.mean()) < 5e-3 and abs(big.std() - 1) < 5e-3
     assert abs(((big - big.mean()) ** 3).mean()) < 2e-2  # symmetric
     assert not np.array_equal(orc.fill_normal(16, 1), orc.fill_normal(16, 2))
+
+
+# --- the CPU port (cpu_port.c): the baseline bench.py times -------------------
+def test_cpu_port_matches_the_exact_oracle(orc, rng):
+    """The fp32 CPU port computes what the exact oracle computes, to fp32
+    accumulation error: products (ragged M, N and K, f32 and bf16
+    activations), two-source attention with a split, and the small MoT
+    chunk under the reference's action gates.  Its outputs are timed by
+    bench.py's cpu_baseline, so a port that computed something else would
+    make that baseline meaningless."""
+    import oracle as o
+    try:
+        for M, N, K, xt in ((37, 5, 300, o.F32), (64, 48, 3072, o.BF16), (130, 13, 513, o.BF16)):
+            w = bf16(rng.standard_normal(M * K) * 0.05).reshape(M, K)
+            x = rng.standard_normal((N, K)).astype(np.float32)
+            if xt == o.BF16:
+                x = bf16(x)
+            o.set_port(False)
+            ref = orc.mul_mat(w, x)
+            o.set_port(True)
+            got = orc.mul_mat(w, x)
+            assert rel_err(got, ref) < 1e-5, (M, N, K)
+        H, dh, tq, na, nb = 3, 64, 37, 150, 21
+        q = bf16(rng.standard_normal((H, tq, dh)))
+        ka, kb = bf16(rng.standard_normal((H, na, dh))), bf16(rng.standard_normal((H, nb, dh)))
+        va, vb = bf16(rng.standard_normal((H, dh, na + 3))), bf16(rng.standard_normal((H, dh, nb)))
+        o.set_port(False)
+        ref = orc.attention(q, ka, va, kb, vb, na_split=1)
+        o.set_port(True)
+        got = orc.attention(q, ka, va, kb, vb, na_split=1)
+        assert rel_err(f32(got), f32(ref)) < 1e-2 and cosine(f32(got), f32(ref)) > 0.9999
+        # the small MoT chunk, exact against port
+        import test_oracle_mot as tm
+        w = orc.gwp_synthetic_weights(tm.CFG, tm.SEED, 0.05)
+        ins = tm.inputs(orc)
+        chunks = []
+        for port in (False, True):
+            o.set_port(port)
+            g = tm.run(orc, w, ins)
+            chunks.append(g.denoise(ins[3]))
+            g.close()
+        d = np.abs(chunks[1].astype(np.float64) - chunks[0])
+        assert d.mean() <= 1e-3 and d.max() <= 1e-2 * max(1.0, float(np.abs(chunks[0]).max()))
+    finally:
+        o.set_port(False)
