@@ -359,3 +359,195 @@ def test_unfused_prefix_entry_matches_oracle(wx, be, orc):
     ref_k = orc.qk_norm_rope(x, norm_w, H, dh, 1, pos0=tpos, pos1=hpos, pos2=wpos, eps=EPS)   # [H][T][dh]
     got_k = r.fetch(kk, np.uint16, (nimg, H, dh)).transpose(1, 0, 2)
     assert_parity(bf(wx, got_k), bf(wx, ref_k), what="visual rope t>0")
+
+
+# --- the F32 reference profile ------------------------------------------------
+def action_layer_graph_f32(W, h, mod, table, apos, pk, pv, lk, lv, d, H, T, P, NL):
+    """The same layer in the F32 reference profile (Precision::f32_reference,
+    engine.cpp:45-51; `source-f32-v1` artifacts: F32 weights, hidden states
+    and caches), op for op:
+    * modulation_add of two F32 tensors (mot.cpp:137-145);
+    * modulated_norm's F32 form (mot.cpp:154-158): NORM, MUL, ADD, ADD, the
+      chain the backend matches into norm_modulation_f32;
+    * expert_qkv with separate q/k/v projections (no packed QKV outside the
+      qkv policy, mot.cpp:225-236): linear_with_activation -> linear
+      (weights.cpp:786-793, :819-829), MUL_MAT f32 x f32 + bias ADD;
+    * rms_norm (weights.cpp:904-917): RMS_NORM, a CPY of the weight to f32,
+      MUL; 1-D RoPE on f32 (mot.cpp:175-180); no bf16 casts;
+    * the unfused f32 attention (mot.cpp:432-445);
+    * gated_residual's F32 form (mot.cpp:164-166): MUL, ADD, matched into
+      gated_residual_f32;
+    * layer_norm (weights.cpp:919-930): NORM, MUL(CPY w), ADD(CPY b); the
+      cross-attention over cached f32 prompt K/V; linear_gelu_with_activation's
+      F32 form (weights.cpp:831-849): GELU of the linear."""
+    dh = d // H
+    scale = 1.0 / np.sqrt(dh)
+
+    def linear(wn, x):
+        return gm.add(gm.mul_mat(W[wn + ".weight"], x), W[wn + ".bias"])
+
+    def rms(x, wn):
+        return gm.mul(gm.rms_norm(x, EPS), gm.cast(W[wn], "f32"))
+
+    def modulated_norm(x, scl, sft):
+        n = gm.norm(x, EPS)
+        return gm.add(gm.add(n, gm.mul(n, scl)), sft)
+
+    def layer_norm(x, wn, bn):
+        return gm.add(gm.mul(gm.norm(x, EPS), gm.cast(W[wn], "f32")), gm.cast(W[bn], "f32"))
+
+    comb = gm.add(mod, table)
+    shift, scl, gate, cshift, cscale, cgate = [gm.view_2d(comb, d, 1, comb.nb[2], i * comb.nb[1]) for i in range(6)]
+    n = modulated_norm(h, scl, shift)
+    q = gm.reshape(rms(linear("attn1.to_q", n), "attn1.norm_q.weight"), dh, H, T)
+    k = gm.reshape(rms(linear("attn1.to_k", n), "attn1.norm_k.weight"), dh, H, T)
+    v = gm.reshape(linear("attn1.to_v", n), dh, H, T)
+    rope = dict(n_dims=dh, mode=gm.GGML_ROPE_TYPE_NORMAL, n_ctx_orig=0, freq_base=10000.0, freq_scale=1.0,
+                ext_factor=0.0, attn_factor=1.0, beta_fast=32.0, beta_slow=1.0)
+    q = gm.rope_ext(q, apos, **rope)
+    k = gm.rope_ext(k, apos, **rope)
+    Q = gm.cont(gm.permute(q, 0, 2, 1, 3))
+    ak = gm.cont(gm.permute(k, 0, 2, 1, 3))
+    av = gm.cont(gm.permute(v, 1, 2, 0, 3))
+    nimg = P - 1
+    state_k = gm.view_3d(pk, dh, 1, H, pk.nb[1], pk.nb[2], 0)
+    ref_k = gm.view_3d(pk, dh, nimg, H, pk.nb[1], pk.nb[2], pk.nb[1])
+    state_v = gm.view_3d(pv, 1, dh, H, pv.nb[1], pv.nb[2], 0)
+    ref_v = gm.view_3d(pv, nimg, dh, H, pv.nb[1], pv.nb[2], pv.nb[0])
+    jk = gm.concat(gm.concat(state_k, ak, 1), ref_k, 1)
+    jv = gm.concat(gm.concat(state_v, av, 0), ref_v, 0)
+    scores = gm.mul_mat(jk, Q)
+    gm.mul_mat_set_prec(scores, gm.GGML_PREC_F32)
+    probs = gm.soft_max_ext(scores, None, scale, 0.0)
+    att = gm.reshape(gm.cont(gm.permute(gm.mul_mat(jv, probs), 0, 2, 1, 3)), d, T)
+    att = linear("attn1.to_out.0", att)
+    h = gm.add(h, gm.mul(att, gate))
+    n2 = layer_norm(h, "norm2.weight", "norm2.bias")
+    cq = gm.reshape(rms(linear("attn2.to_q", n2), "attn2.norm_q.weight"), dh, H, T)
+    CQ = gm.cont(gm.permute(cq, 0, 2, 1, 3))
+    cs = gm.mul_mat(lk, CQ)
+    gm.mul_mat_set_prec(cs, gm.GGML_PREC_F32)
+    cp = gm.soft_max_ext(cs, None, scale, 0.0)
+    catt = gm.reshape(gm.cont(gm.permute(gm.mul_mat(lv, cp), 0, 2, 1, 3)), d, T)
+    h = gm.add(h, linear("attn2.to_out.0", catt))
+    n3 = modulated_norm(h, cscale, cshift)
+    u = gm.gelu(linear("ffn.net.0.proj", n3))
+    return gm.add(h, gm.mul(linear("ffn.net.2", u), cgate))
+
+
+def f64_action_layer(W, h, mod, table, apos, pk, pvt, lk, lvt, d, H, T):
+    """The F32-profile layer in float64 numpy from textbook operations:
+    LayerNorm (biased variance), RMSNorm, the GELU tanh form, 1-D RoPE on
+    (even, odd) pairs with theta = pos * 10000^(-2i/dh), softmax attention."""
+    dh = d // H
+    f = {k: v.astype(np.float64) for k, v in W.items()}
+    h = h.astype(np.float64)
+
+    def ln(x):
+        mu = x.mean(axis=1, keepdims=True)
+        return (x - mu) / np.sqrt(((x - mu) ** 2).mean(axis=1, keepdims=True) + EPS)
+
+    def rms(x, w):
+        return x / np.sqrt((x ** 2).mean(axis=1, keepdims=True) + EPS) * w
+
+    def lin(n, x):
+        return x @ f[n + ".weight"].T + f[n + ".bias"]
+
+    def rope(x):  # [T, H, dh]
+        i = np.arange(dh // 2)
+        th = apos[:, None].astype(np.float64) * 10000.0 ** (-2.0 * i / dh)
+        c, s = np.cos(th)[:, None, :], np.sin(th)[:, None, :]
+        a, b = x[..., 0::2], x[..., 1::2]
+        out = np.empty_like(x)
+        out[..., 0::2], out[..., 1::2] = a * c - b * s, a * s + b * c
+        return out
+
+    def attend(Q, K, Vt):  # Q [H,T,dh], K [H,n,dh], Vt [H,dh,n]
+        sc = np.einsum("htd,hnd->htn", Q, K) / np.sqrt(dh)
+        p = np.exp(sc - sc.max(axis=2, keepdims=True))
+        p /= p.sum(axis=2, keepdims=True)
+        return np.einsum("htn,hdn->thd", p, Vt).reshape(T, d)
+
+    m = (mod.astype(np.float64) + table.astype(np.float64)).reshape(6, d)
+    n = ln(h) * (1 + m[1]) + m[0]
+    q = rope(rms(lin("attn1.to_q", n), f["attn1.norm_q.weight"]).reshape(T, H, dh)).transpose(1, 0, 2)
+    k = rope(rms(lin("attn1.to_k", n), f["attn1.norm_k.weight"]).reshape(T, H, dh)).transpose(1, 0, 2)
+    v = lin("attn1.to_v", n).reshape(T, H, dh).transpose(1, 2, 0)
+    pk64, pv64 = pk.astype(np.float64), pvt.astype(np.float64)
+    K = np.concatenate([pk64[:, :1], k, pk64[:, 1:]], axis=1)
+    Vt = np.concatenate([pv64[:, :, :1], v, pv64[:, :, 1:]], axis=2)
+    h = h + lin("attn1.to_out.0", attend(q, K, Vt)) * m[2]
+    n2 = ln(h) * f["norm2.weight"] + f["norm2.bias"]
+    cq = rms(lin("attn2.to_q", n2), f["attn2.norm_q.weight"]).reshape(T, H, dh).transpose(1, 0, 2)
+    h = h + lin("attn2.to_out.0", attend(cq, lk.astype(np.float64), lvt.astype(np.float64)))
+    n3 = ln(h) * (1 + m[4]) + m[3]
+    u = lin("ffn.net.0.proj", n3)
+    u = 0.5 * u * (1 + np.tanh(np.sqrt(2 / np.pi) * (u + 0.044715 * u ** 3)))
+    return h + lin("ffn.net.2", u) * m[5]
+
+
+@pytest.mark.parametrize("d,H,F,P,NL", [(256, 2, 384, 129, 16), (3072, 24, 14336, 3073, 512)],
+                         ids=["small", "config5-layer"])
+def test_f32_profile_action_layer(wx, be, orc, d, H, F, P, NL, monkeypatch):
+    """The reference's action layer as its F32 reference profile builds it
+    (F32 weights, hidden states and caches), through the ggml import, against
+    a float64 restatement: max-rel <= 1e-4, cosine >= 0.999999.  At the small
+    size the same graph also runs on a backend with the F32 chain fusions off
+    (the reference's own switches): both results pass the bar and differ in
+    their last bits, so the matched norm_modulation_f32 and gated_residual_f32
+    kernels are what ran."""
+    print(f"drop-in F32-profile action layer d={d} H={H} F={F} P={P} NL={NL}", flush=True)
+    T, dh = 48, d // H
+    shapes = {"attn1.to_q.weight": (d, d), "attn1.to_q.bias": (d,), "attn1.to_k.weight": (d, d),
+              "attn1.to_k.bias": (d,), "attn1.to_v.weight": (d, d), "attn1.to_v.bias": (d,),
+              "attn1.norm_q.weight": (d,), "attn1.norm_k.weight": (d,),
+              "attn1.to_out.0.weight": (d, d), "attn1.to_out.0.bias": (d,),
+              "norm2.weight": (d,), "norm2.bias": (d,),
+              "attn2.to_q.weight": (d, d), "attn2.to_q.bias": (d,), "attn2.norm_q.weight": (d,),
+              "attn2.to_out.0.weight": (d, d), "attn2.to_out.0.bias": (d,),
+              "ffn.net.0.proj.weight": (F, d), "ffn.net.0.proj.bias": (F,),
+              "ffn.net.2.weight": (d, F), "ffn.net.2.bias": (d,)}
+    Wh = {}
+    for i, (name, shape) in enumerate(shapes.items()):
+        n = int(np.prod(shape))
+        mean, std = (1.0, 0.02) if "norm" in name else (0.0, 0.02)
+        Wh[name] = orc.fill_normal(n, 0x5EED0700 + i, mean, std, orc.F32).reshape(shape)
+    h = orc.fill_normal(T * d, 11, 0.0, 1.0, orc.F32).reshape(T, d)
+    mod = orc.fill_normal(6 * d, 12, 0.0, 0.5, orc.F32).reshape(6, d)
+    table = orc.fill_normal(6 * d, 13, 0.0, 0.1, orc.F32).reshape(6, d)
+    apos = np.arange(1, T + 1, dtype=np.int32)
+    pk = orc.fill_normal(H * P * dh, 14, 0.0, 1.0, orc.F32).reshape(H, P, dh)
+    pvt = orc.fill_normal(H * dh * P, 15, 0.0, 1.0, orc.F32).reshape(H, dh, P)
+    lk = orc.fill_normal(H * NL * dh, 16, 0.0, 1.0, orc.F32).reshape(H, NL, dh)
+    lvt = orc.fill_normal(H * dh * NL, 17, 0.0, 1.0, orc.F32).reshape(H, dh, NL)
+    ref = f64_action_layer(Wh, h, mod, table, apos, pk, pvt, lk, lvt, d, H, T)
+
+    def run(backend):
+        r = Runner(wx, backend, 2 << 30 if d > 1024 else 64 << 20)
+        W = {name: r.leaf("f32", tuple(reversed(a.shape)), a, name) for name, a in Wh.items()}
+        out = action_layer_graph_f32(W, r.leaf("f32", (d, T), h, "hidden"), r.leaf("f32", (d, 6, 1), mod, "time_proj"),
+                                     r.leaf("f32", (d, 6), table, "scale_shift_table"),
+                                     r.leaf("i32", (T,), apos, "positions"),
+                                     r.leaf("f32", (dh, P, H), pk, "prefix_keys"),
+                                     r.leaf("f32", (P, dh, H), pvt, "prefix_values"),
+                                     r.leaf("f32", (dh, NL, H), lk, "prompt_keys"),
+                                     r.leaf("f32", (NL, dh, H), lvt, "prompt_values"), d, H, T, P, NL)
+        graph = r.run([out])
+        assert {"MUL_MAT", "SOFT_MAX", "CONCAT", "CONT", "ROPE", "NORM", "RMS_NORM", "UNARY", "ADD", "MUL",
+                "CPY"} <= {t.op for t in graph.nodes}
+        got = r.fetch(out, np.float32, (T, d))
+        r.arena.free()
+        return got
+
+    got = run(be)
+    assert_parity(got, ref, rel=1e-4, cos=0.999999, what=f"F32-profile action layer d={d}")
+    if d <= 1024:
+        monkeypatch.setenv("WAMX_DISABLE_NORM_MODULATION_FUSION", "1")
+        monkeypatch.setenv("WAMX_DISABLE_GATED_RESIDUAL_FUSION", "1")
+        be2 = wx.Backend(0)
+        try:
+            unfused = run(be2)
+        finally:
+            be2.close()
+        assert_parity(unfused, ref, rel=1e-4, cos=0.999999, what="F32-profile action layer, fusions off")
+        assert not np.array_equal(got, unfused), "the F32 chains were not matched"
