@@ -261,6 +261,13 @@ WAMX_API wamx_tensor * wamx_rms_norm_bf16_f32(wamx_context * ctx, wamx_tensor * 
  *   as modes 0 and 1, so the result is the same bit for bit).  For fixed
  *   positions (the visual grid) it is built once and saves the
  *   transcendental work of every layer.
+ *   Chunks: dst [ne={head_dim, T_total, H, C}] takes C chunks (the batch of
+ *   chunks of a request, or the layers of a cache), each a contiguous block
+ *   at its own nb[3].  x is then [ne={d, C*T}] (the chunks' rows one after
+ *   another, positions restarting per chunk) or [ne={d, T, C}] with chunk c's
+ *   rows at x + c * nb[2] (for example layer c's column range of a packed
+ *   projection of every layer), and weight is [d] or one norm weight per
+ *   chunk [ne={d, C}] (the layers' own norm weights).
  *   Writes into an existing tensor (dst), returned as a node that depends on it.
  *
  * wamx_joint_attn: softmax(scale * Q K^T) V per head over the key set
@@ -276,7 +283,9 @@ WAMX_API wamx_tensor * wamx_rms_norm_bf16_f32(wamx_context * ctx, wamx_tensor * 
  *   Q and K in f32 (rms_norm_bf16_f32) and the scores are an f32 x f32
  *   MUL_MAT at GGML_PREC_F32.  wamx_qk_norm_rope_hilo writes dst
  *   [ne={head_dim, T_total, H, 2}]: plane 0 the bf16 rounding of the f32
- *   result, plane 1 its remainder bf16(v - plane0).  wamx_joint_attn_hilo
+ *   result, plane 1 its remainder bf16(v - plane0); with C chunks (x and
+ *   weight as for wamx_qk_norm_rope) dst is [ne={head_dim, T_total, H, 2C}],
+ *   planes 2c and 2c + 1 for chunk c, contiguous.  wamx_joint_attn_hilo
  *   takes q [ne={dh, Tq, H, 2}] and k [ne={dh, n, H, 2}] in that form, V^T
  *   bf16 [ne={n, dh, H}] (rows a multiple of 8 keys, n >= 8), and forms
  *   every score as K.Q + K.Q_lo + K_lo.Q with fp32 accumulation (the

@@ -147,6 +147,36 @@ def test_hilo_constructors(wx, ctx):
     assert not lib.wamx_joint_attn_hilo(ctx, q, k12, lib.wamx_new_tensor_3d(ctx, wx.TYPE_BF16, 12, 128, 24), 0.088)
 
 
+def test_qk_norm_rope_layer_chunks_constructor(wx, ctx):
+    """The Q/K norm over the layers of a packed projection: x [d, T, C] with
+    its own chunk stride, per-chunk norm weights [d, C], chunk-strided
+    destinations (plain) or 2C contiguous planes (hi/lo); mismatched chunk
+    counts, weights and plane counts are refused."""
+    lib = wx.load()
+    d, T, C, L = 3072, 512, 30, 30
+    kv = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, 2 * L * d, T)
+    x = lib.wamx_view_3d(ctx, kv, d, T, C, kv.contents.nb[1], 2 * d * 2, 0)
+    w = lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, d, C)
+    store = lib.wamx_new_tensor_4d(ctx, wx.TYPE_BF16, 128, T, 24, 2 * C)
+    nb = store.contents.nb
+    dst = lib.wamx_view_4d(ctx, store, 128, T, 24, C, nb[1], nb[2], 2 * nb[3], nb[3])
+    k = lib.wamx_qk_norm_rope(ctx, x, w, dst, 0, 2, None, None, None, 1e-6, 10000.0)
+    assert k and lib.wamx_backend_supports_op(None, k), wx.last_error()
+    kh = lib.wamx_qk_norm_rope_hilo(ctx, x, w, store, 0, 2, None, None, None, 1e-6, 10000.0)
+    assert kh and lib.wamx_backend_supports_op(None, kh), wx.last_error()
+    w1 = lib.wamx_new_tensor_1d(ctx, wx.TYPE_BF16, d)
+    assert lib.wamx_qk_norm_rope(ctx, x, w1, dst, 0, 2, None, None, None, 1e-6, 10000.0)  # one shared weight
+    bad = (
+        (lib.wamx_view_3d(ctx, kv, d, T, C - 1, kv.contents.nb[1], 2 * d * 2, 0), w, dst, False),  # chunk count
+        (x, lib.wamx_new_tensor_2d(ctx, wx.TYPE_BF16, d, C - 1), dst, False),                     # weights
+        (x, w, lib.wamx_new_tensor_4d(ctx, wx.TYPE_BF16, 128, T, 24, 2 * C - 1), True),            # odd planes
+        (x, w, dst, True),                                                                        # strided planes
+    )
+    for xx, ww, dd, hl in bad:
+        fn = lib.wamx_qk_norm_rope_hilo if hl else lib.wamx_qk_norm_rope
+        assert not fn(ctx, xx, ww, dd, 0, 2, None, None, None, 1e-6, 10000.0)
+
+
 def test_denoise_glue_constructors(wx, ctx):
     """EULER_STEP, MLP_SMALL and the timestep-batched MODULATION."""
     lib = wx.load()

@@ -332,3 +332,58 @@ def test_f32_profile_fusions(wx, be, orc, rng):
     for got in (f_y, u_y):
         assert np.max(np.abs(got - ref_y)) <= 1e-4 * np.max(np.abs(ref_y))
     assert np.max(np.abs(u_out - ref_out)) <= 1e-6 * np.max(np.abs(ref_out))
+
+
+@pytest.mark.parametrize("hilo", [False, True])
+def test_qk_norm_rope_layer_chunks(wx, be, rng, hilo):
+    """The Q/K norm over every layer's column block of a packed projection
+    ([d, T, C] rows, layer c's at columns 2c·d), each layer with its own norm
+    weight ([d, C]) and its own destination chunk (strided among a batch of
+    two, or hi/lo planes 2c and 2c + 1), in one launch, equals C launches on
+    the layer's columns with the layer's weight, bit for bit.  This is how
+    the prompt graph fills every layer's prompt-key cache."""
+    print(f"qk norm layer chunks hilo={hilo}", flush=True)
+    lib = be.lib
+    d, H, DH, T, C, B, cb = 512, 4, 128, 24, 3, 2, 1
+    g = Graph(wx, be)
+    try:
+        kv = g.t(wx.TYPE_BF16, 2 * C * d, T)
+        wts = g.t(wx.TYPE_BF16, d, C)
+        x = lib.wamx_view_3d(g.ctx, kv, d, T, C, kv.contents.nb[1], 2 * d * 2, 0)
+        if hilo:
+            store = g.t(wx.TYPE_BF16, DH, T, H, 2 * C)
+            node = lib.wamx_qk_norm_rope_hilo(g.ctx, x, wts, store, 0, 2, None, None, None, 1e-6, 10000.0)
+        else:
+            store = g.t(wx.TYPE_BF16, DH, T, H, C * B)
+            nb = store.contents.nb
+            dst = lib.wamx_view_4d(g.ctx, store, DH, T, H, C, nb[1], nb[2], nb[3] * B, nb[3] * cb)
+            node = lib.wamx_qk_norm_rope(g.ctx, x, wts, dst, 0, 2, None, None, None, 1e-6, 10000.0)
+        assert node, wx.last_error()
+        g.alloc()
+        g.set(kv, wx.f32_to_bf16(rng.standard_normal((T, 2 * C * d)).astype(np.float32)))
+        g.set(wts, wx.f32_to_bf16((1.0 + 0.1 * rng.standard_normal((C, d))).astype(np.float32)))
+        if not hilo:
+            g.set(store, np.full(DH * T * H * C * B, 0x7FC0, np.uint16))  # NaN: untouched chunks stay NaN
+        g.compute(node)
+        plane = DH * T * H
+        got = g.get(store, np.uint16, (plane * (2 * C if hilo else C * B),))
+        for c in range(C):
+            x_ptr, w_ptr = data(kv) + 2 * c * d * 2, data(wts) + c * d * 2
+            if hilo:
+                ref = be.empty(2 * plane * 2)
+                wx.check(lib.wamx_op_qk_norm_rope_hilo(be.ptr, x_ptr, 2 * C * d, w_ptr, ref.ptr, ref.ptr + plane * 2, H,
+                                                       DH, T, T, 0, 2, None, None, None, 1e-6, 10000.0))
+                be.sync()
+                assert np.array_equal(got[2 * c * plane:(2 * c + 2) * plane], ref.download(np.uint16, (2 * plane,))), c
+            else:
+                ref = be.empty(plane * 2)
+                wx.check(lib.wamx_op_qk_norm_rope(be.ptr, x_ptr, 2 * C * d, w_ptr, ref.ptr, H, DH, T, T, 0, 2, None,
+                                                  None, None, 1e-6, 10000.0))
+                be.sync()
+                k = c * B + cb
+                assert np.array_equal(got[k * plane:(k + 1) * plane], ref.download(np.uint16, (plane,))), c
+                other = c * B + (1 - cb)
+                assert np.all(got[other * plane:(other + 1) * plane] == 0x7FC0), "wrote outside its chunk"
+            ref.free()
+    finally:
+        g.close()

@@ -388,7 +388,7 @@ static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post, bool la
         if (t->op == WAMX_OP_QK_NORM_ROPE) {
             const wamx_tensor * x = t->src[0];
             if (!column_view(x, lin, seg.col) || !t->src[1] || t->type != WAMX_TYPE_BF16 || t->op_params[4] ||
-                t->op_params[1] == 3)
+                t->op_params[1] == 3 || x->ne[2] > 1 || t->src[1]->ne[1] > 1)
                 break;
             head_dim = t->ne[0];
             width = x->ne[0];
@@ -662,17 +662,21 @@ static hipError_t compute_node(wamx_backend * be, wamx_tensor * node) {
             return run_linear(be, node);
         case WAMX_OP_QK_NORM_ROPE: {
             const wamx_tensor * x = node->src[0];
-            const bool hilo = node->op_params[4] != 0;  // plane 1 takes the lo parts
+            const wamx_tensor * w = node->src[1];
+            const bool hilo = node->op_params[4] != 0;  // plane 2c + 1 takes chunk c's lo parts
             const bool table = node->op_params[1] == 3;  // src[3]: the (cos, sin) table
-            return launch_qk_norm_rope(x->data, (int64_t) x->nb[1] / 2, node->src[1]->data, node->data, node->ne[2],
-                                       node->ne[0], x->ne[1], node->ne[1], node->op_params[0], node->op_params[1],
+            const int64_t C = hilo ? node->ne[3] / 2 : node->ne[3];
+            const bool layered = x->ne[2] > 1;           // chunk c's rows at x + c * nb[2]
+            const int64_t T = layered ? x->ne[1] : x->ne[1] / C;
+            const int64_t plane = (int64_t) node->nb[3] / 2;
+            return launch_qk_norm_rope(x->data, (int64_t) x->nb[1] / 2, w->data, node->data, node->ne[2],
+                                       node->ne[0], T * C, node->ne[1], node->op_params[0], node->op_params[1],
                                        node->src[3] && !table ? (const int32_t *) node->src[3]->data : nullptr,
                                        node->src[4] ? (const int32_t *) node->src[4]->data : nullptr,
                                        node->src[5] ? (const int32_t *) node->src[5]->data : nullptr,
-                                       param_f32(node, 2), param_f32(node, 3), s,
-                                       hilo ? x->ne[1] : x->ne[1] / node->ne[3], hilo ? 0 : (int64_t) node->nb[3] / 2,
-                                       hilo ? (int64_t) node->nb[3] / 2 : 0,
-                                       table ? (const float *) node->src[3]->data : nullptr);
+                                       param_f32(node, 2), param_f32(node, 3), s, T, hilo ? 2 * plane : plane,
+                                       hilo ? plane : 0, table ? (const float *) node->src[3]->data : nullptr,
+                                       layered ? (int64_t) x->nb[2] / 2 : -1, w->ne[1] > 1 ? (int64_t) w->nb[1] / 2 : 0);
         }
         case WAMX_OP_JOINT_ATTN:
             return run_joint_attn(be, node);

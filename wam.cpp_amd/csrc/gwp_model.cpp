@@ -78,6 +78,10 @@ struct wamx_gwp_model {
     // 1 visual): weight [w, 2·L·d] and bias [2·L·d]; layer l's to_k rows start
     // at 2l·d and its to_v rows at (2l+1)·d.  The per-layer weights are views.
     wamx_tensor *kv_w[2] = {nullptr, nullptr}, *kv_b[2] = {nullptr, nullptr};
+    // Each expert's attn2.norm_k weights of every layer, packed [d, L] (the
+    // per-layer weights are views with their reference names), so the prompt
+    // keys of every layer are normalised by one launch.
+    wamx_tensor * cnk_all[2] = {nullptr, nullptr};
     Mlp3 state_enc{}, action_enc{}, action_dec{};
     Cond acond{}, vcond{};
     std::vector<ExpertLayer> act, vis;
@@ -89,6 +93,10 @@ struct wamx_gwp_model {
     wamx_tensor * action_prompt = nullptr;        // [da, NL, B]
     std::vector<wamx_tensor *> pk, pv_raw, pv;    // prefix K [dh,P,H,B]; V^T [Ppad,dh,H,B] and its [P,dh,H,B] view
     std::vector<wamx_tensor *> lk, lv_raw, lv;    // prompt K [dh,NL,H,B]; V^T
+    // The layers' prompt caches in one allocation each, layer-major
+    // ([dh, NL, H, L*B] and [NLpad, dh, H, L*B]); lk[l] and lv_raw[l] are
+    // views of them, so the prompt graph fills every layer in one launch.
+    wamx_tensor *lk_all = nullptr, *lv_raw_all = nullptr;
     wamx_tensor *in_state = nullptr, *in_latent = nullptr, *in_prompt = nullptr, *in_action = nullptr;
     wamx_tensor *in_apos = nullptr, *in_spos = nullptr, *in_vt = nullptr, *in_vh = nullptr, *in_vw = nullptr;
     wamx_tensor *in_freq0 = nullptr, *in_freqs = nullptr, *in_dts = nullptr;
@@ -160,6 +168,14 @@ struct wamx_gwp_model {
     }
     // A linear layer whose weight rows [row0, row0+out) and bias entries live
     // inside the packed tensors `pw` [in, R] and `pb` [R].
+    // A 1-D weight of n elements at element offset off of the packed tensor `pk`.
+    wamx_tensor * add_weight_view(const std::string & name, wamx_tensor * pk, int64_t off, int64_t n) {
+        wamx_tensor * t = wamx_view_1d(wctx, pk, n, (size_t) off * pk->nb[0]);
+        if (t) wamx_set_name(t, name.c_str());
+        weights.push_back({name, t});
+        by_name[name] = t;
+        return t;
+    }
     void add_linear_view(const std::string & prefix, wamx_tensor * pw, wamx_tensor * pb, int64_t row0, int64_t out,
                          wamx_tensor ** w, wamx_tensor ** b) {
         *w = wamx_view_2d(wctx, pw, pw->ne[0], out, pw->nb[1], (size_t) row0 * pw->nb[1]);
@@ -255,6 +271,23 @@ struct Builder {
         return wamx_cpy(ctx, vp, dst_view);
     }
 
+    // Layer l's K (half 0) or V (half 1) columns of a packed projection of
+    // every layer [2·L·d, T], as [d, T, L]: layer l's at columns (2l + half)·d.
+    // (The first `layers` layers.)
+    wamx_tensor * layer_cols(wamx_tensor * kv, int half, int64_t layers) {
+        const int64_t d = (int64_t) c.n_heads * c.head_dim;
+        return wamx_view_3d(ctx, kv, d, kv->ne[1], layers, kv->nb[1], (size_t) (2 * d) * kv->nb[0],
+                            (size_t) (half * d) * kv->nb[0]);
+    }
+    // The first dst->ne[3] layers' V^T [T, dh, H, layers] from a packed
+    // projection of every layer [2·L·d, T] into `dst` (one transposing copy).
+    wamx_tensor * store_v_layers(wamx_tensor * kv, wamx_tensor * dst) {
+        const int64_t dh = c.head_dim, H = c.n_heads, d = dh * H, T = kv->ne[1];
+        wamx_tensor * v = wamx_view_4d(ctx, kv, dh, H, T, dst->ne[3], (size_t) dh * kv->nb[0], kv->nb[1],
+                                       (size_t) (2 * d) * kv->nb[0], (size_t) d * kv->nb[0]);
+        return wamx_cpy(ctx, wamx_permute(ctx, v, 1, 2, 0, 3), dst);
+    }
+
     // V^T view of `raw` [ld, dh, H(, B)] covering key columns [k0, k0+n).
     wamx_tensor * vt_view(wamx_tensor * raw, int64_t k0, int64_t n) {
         if (raw->ne[3] == 1)
@@ -282,23 +315,18 @@ struct Builder {
     }
 
     // expert_cross_ffn against uncached text (build_attention, text_encoder.cpp:26-73).
-    // `kv` is the packed K/V projection of the text for every layer
-    // [2·L·d, NL]; layer l's K columns start at 2l·d, its V columns at (2l+1)·d.
     // RMSNorm keeps Q and K in f32 there and the scores are f32 x f32
     // (rms_norm_bf16_f32, then MUL_MAT at GGML_PREC_F32): Q and K are held as
-    // bf16 hi/lo planes and the scores formed f32-accurate from them.
-    wamx_tensor * cross_ffn_uncached(const ExpertLayer & e, wamx_tensor * h, wamx_tensor * kv, int64_t l,
+    // bf16 hi/lo planes and the scores formed f32-accurate from them.  K (the
+    // layer's text keys, hi/lo [dh, NL, H, 2]) and V (their V^T [NL, dh, H])
+    // come from text_kv, which makes them for every layer at once.
+    wamx_tensor * cross_ffn_uncached(const ExpertLayer & e, wamx_tensor * h, wamx_tensor * K, wamx_tensor * V,
                                      wamx_tensor * cshift, wamx_tensor * cscale, wamx_tensor * cgate) {
-        const int64_t T = h->ne[1], NL = kv->ne[1], d = (int64_t) c.n_heads * c.head_dim;
+        const int64_t T = h->ne[1];
         wamx_tensor * n = wamx_layer_norm_bf16(ctx, h, e.n2_w, e.n2_b, c.eps);
         wamx_tensor * q = lin(e.cq_w, e.cq_b, n);
-        wamx_tensor * k = cols(kv, d, 2 * l * d);
         wamx_tensor * Q = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, c.head_dim, T, c.n_heads, 2);
         Q = wamx_qk_norm_rope_hilo(ctx, q, e.cnq, Q, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
-        wamx_tensor * K = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, c.head_dim, NL, c.n_heads, 2);
-        K = wamx_qk_norm_rope_hilo(ctx, k, e.cnk, K, 0, 2, nullptr, nullptr, nullptr, c.eps, 10000.0f);
-        wamx_tensor * vraw = wamx_new_tensor_3d(ctx, WAMX_TYPE_BF16, round_up(NL, 8), c.head_dim, c.n_heads);
-        wamx_tensor * V = store_v(kv, (2 * l + 1) * d, vt_view(vraw, 0, NL));
         wamx_tensor * att = wamx_joint_attn_hilo(ctx, Q, K, V, scale);
         h = lin(e.co_w, e.co_b, att, WAMX_EPI_BIAS_RESIDUAL, h);
         return ffn(e, h, cshift, cscale, cgate);
@@ -366,7 +394,8 @@ static bool create_weights(wamx_gwp_model * m) {
     for (int x = 0; x < 2; ++x) {
         m->kv_w[x] = wamx_new_tensor_2d(m->wctx, WAMX_TYPE_BF16, x == 0 ? da : d, 2 * L * d);
         m->kv_b[x] = wamx_new_tensor_1d(m->wctx, WAMX_TYPE_BF16, 2 * L * d);
-        if (!m->kv_w[x] || !m->kv_b[x]) return false;
+        m->cnk_all[x] = wamx_new_tensor_2d(m->wctx, WAMX_TYPE_BF16, d, L);
+        if (!m->kv_w[x] || !m->kv_b[x] || !m->cnk_all[x]) return false;
     }
     // x: 0 action expert, 1 visual expert (the packed K/V weight); t: tiled.
     auto expert = [&](const std::string & p, int64_t w, int64_t ffn, ExpertLayer & e, int x, bool t, int64_t l) {
@@ -380,7 +409,7 @@ static bool create_weights(wamx_gwp_model * m) {
         m->add_linear_view(p + ".attn2.to_k", m->kv_w[x], m->kv_b[x], 2 * l * d, d, &e.ck_w, &e.ck_b);
         m->add_linear_view(p + ".attn2.to_v", m->kv_w[x], m->kv_b[x], (2 * l + 1) * d, d, &e.cv_w, &e.cv_b);
         e.cnq = m->add_weight(p + ".attn2.norm_q.weight", d);
-        e.cnk = m->add_weight(p + ".attn2.norm_k.weight", d);
+        e.cnk = m->add_weight_view(p + ".attn2.norm_k.weight", m->cnk_all[x], l * d, d);
         m->add_linear(p + ".attn2.to_out.0", d, w, &e.co_w, &e.co_b, t);
         m->add_linear(p + ".ffn.net.0.proj", w, ffn, &e.up_w, &e.up_b, t);
         m->add_linear(p + ".ffn.net.2", ffn, w, &e.dn_w, &e.dn_b, t);
@@ -413,9 +442,10 @@ static bool create_storage(wamx_gwp_model * m) {
     for (int64_t l = 0; l < L; ++l) {
         m->pk.push_back(wamx_new_tensor_4d(s, WAMX_TYPE_BF16, dh, m->P, H, B));
         m->pv_raw.push_back(wamx_new_tensor_4d(s, WAMX_TYPE_BF16, m->Ppad, dh, H, B));
-        m->lk.push_back(wamx_new_tensor_4d(s, WAMX_TYPE_BF16, dh, c.n_lang, H, B));
-        m->lv_raw.push_back(wamx_new_tensor_4d(s, WAMX_TYPE_BF16, m->NLpad, dh, H, B));
     }
+    m->lk_all = wamx_new_tensor_4d(s, WAMX_TYPE_BF16, dh, c.n_lang, H, L * B);
+    m->lv_raw_all = wamx_new_tensor_4d(s, WAMX_TYPE_BF16, m->NLpad, dh, H, L * B);
+    if (!m->lk_all || !m->lv_raw_all) return false;
     m->in_state = wamx_new_tensor_2d(s, WAMX_TYPE_F32, c.action_dim, B);
     m->in_latent = wamx_new_tensor_4d(s, WAMX_TYPE_F32, 2 * c.grid_w, 2 * c.grid_h, c.z_dim, B);
     m->in_prompt = wamx_new_tensor_3d(s, WAMX_TYPE_F32, c.t5_hidden, c.n_lang, B);
@@ -431,6 +461,12 @@ static bool create_storage(wamx_gwp_model * m) {
     m->vis_rope = wamx_new_tensor_2d(s, WAMX_TYPE_F32, dh, m->nimg);
     m->sbuf = wamx_backend_alloc_ctx_tensors(s, m->be);
     if (!m->sbuf) return false;
+    // Layer l's prompt caches: chunks l*B .. l*B + B-1 of the joint ones.
+    for (int64_t l = 0; l < L; ++l)
+        for (wamx_tensor * a : {m->lk_all, m->lv_raw_all})
+            (a == m->lk_all ? m->lk : m->lv_raw)
+                .push_back(wamx_view_4d(s, a, a->ne[0], a->ne[1], a->ne[2], B, a->nb[1], a->nb[2], a->nb[3],
+                                        a->nb[3] * (size_t) (l * B)));
     // Views of the padded V^T storage covering the real key columns.
     for (int64_t l = 0; l < L; ++l) {
         wamx_tensor * r = m->pv_raw[l];
@@ -440,7 +476,7 @@ static bool create_storage(wamx_gwp_model * m) {
     }
     // Zero the storage once so padded V^T columns hold finite values.
     for (auto * t : m->pv_raw) wamx_backend_tensor_memset(t, 0, 0, wamx_nbytes(t));
-    for (auto * t : m->lv_raw) wamx_backend_tensor_memset(t, 0, 0, wamx_nbytes(t));
+    wamx_backend_tensor_memset(m->lv_raw_all, 0, 0, wamx_nbytes(m->lv_raw_all));
     // Constant inputs: positions (semantics.cpp:210-257), schedule and
     // timestep embeddings (scheduler.cpp:26-55, text_encoder.cpp:1-12).
     std::vector<int32_t> apos(c.action_chunk), vt(m->nimg, 0), vh(m->nimg), vw(m->nimg);
@@ -512,16 +548,18 @@ static bool build_prompt_graph(wamx_gwp_model * m, int64_t cb) {
     wamx_tensor * ap = wamx_view_2d(ctx, m->action_prompt, c.action_hidden, c.n_lang, m->action_prompt->nb[1],
                                     m->action_prompt->nb[2] * (size_t) cb);
     wamx_build_forward_expand(g, wamx_cpy(ctx, txt, ap));
-    const int64_t d = (int64_t) c.n_heads * c.head_dim;
     wamx_tensor * kv = b.lin(m->kv_w[0], m->kv_b[0], txt);  // every layer's prompt K/V [2·L·d, NL]
-    for (int l = 0; l < c.n_layers; ++l) {
-        const ExpertLayer & e = m->act[l];
-        wamx_tensor * k = b.cols(kv, d, 2 * (int64_t) l * d);
-        wamx_build_forward_expand(g, wamx_qk_norm_rope(ctx, k, e.cnk, b.chunk(m->lk[l], cb), 0, 2, nullptr, nullptr,
-                                                       nullptr, c.eps, 10000.0f));
-        wamx_build_forward_expand(
-            g, b.store_v(kv, (2 * (int64_t) l + 1) * d, b.vt_view(b.chunk(m->lv_raw[l], cb), 0, c.n_lang)));
-    }
+    // Every layer's K (RMSNorm by the layer's own norm_k, no rope) and V^T
+    // cache of this chunk, one launch each: the layers are the chunks of the
+    // joint caches, chunk l*B + cb.
+    wamx_tensor * lk = wamx_view_4d(ctx, m->lk_all, c.head_dim, c.n_lang, c.n_heads, c.n_layers, m->lk_all->nb[1],
+                                    m->lk_all->nb[2], m->lk_all->nb[3] * (size_t) m->B, m->lk_all->nb[3] * (size_t) cb);
+    wamx_build_forward_expand(g, wamx_qk_norm_rope(ctx, b.layer_cols(kv, 0, c.n_layers), m->cnk_all[0], lk, 0, 2, nullptr,
+                                                   nullptr, nullptr, c.eps, 10000.0f));
+    wamx_tensor * lv = wamx_view_4d(ctx, m->lv_raw_all, c.n_lang, c.head_dim, c.n_heads, c.n_layers,
+                                    m->lv_raw_all->nb[1], m->lv_raw_all->nb[2], m->lv_raw_all->nb[3] * (size_t) m->B,
+                                    m->lv_raw_all->nb[3] * (size_t) cb);
+    wamx_build_forward_expand(g, b.store_v_layers(kv, lv));
     wamx_graph_assign_uid(g);
     m->galloc[gi] = wamx_gallocr_new(m->be);
     return m->galloc[gi] && wamx_gallocr_alloc_graph(m->galloc[gi], g);
@@ -566,6 +604,17 @@ static bool build_prefix_graph(wamx_gwp_model * m, int64_t cb) {
     b.condition(m->vcond, m->in_freq0, &vtemb, &vmod);
     wamx_tensor * vtext = b.text(m->vcond, prompt);
     wamx_tensor * vkv = b.lin(m->kv_w[1], m->kv_b[1], vtext);  // every layer's text K/V [2·L·d, NL]
+    // The text keys (RMSNorm by each layer's norm_k, as hi/lo planes) and
+    // their V^T for the visual cross-attention of layers 0 .. L-2, one launch
+    // each; layer l's are views at planes 2l, 2l + 1 and column block l.
+    const int64_t NL = c.n_lang, XL = std::max<int64_t>(1, c.n_layers - 1);
+    wamx_tensor * tk = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, dh, NL, H, 2 * XL);
+    wamx_tensor * tcnk = wamx_view_2d(ctx, m->cnk_all[1], d, XL, m->cnk_all[1]->nb[1], 0);
+    tk = wamx_qk_norm_rope_hilo(ctx, b.layer_cols(vkv, 0, XL), tcnk, tk, 0, 2, nullptr, nullptr, nullptr, c.eps,
+                                10000.0f);
+    wamx_tensor * tv_raw = wamx_new_tensor_4d(ctx, WAMX_TYPE_BF16, round_up(NL, 8), dh, H, XL);
+    wamx_tensor * tv = b.store_v_layers(vkv, wamx_view_4d(ctx, tv_raw, NL, dh, H, XL, tv_raw->nb[1], tv_raw->nb[2],
+                                                          tv_raw->nb[3], 0));
     wamx_tensor * vmods = wamx_modulation(ctx, vmod, m->v_tables);  // [d, 6, L] f32
 
     for (int l = 0; l < c.n_layers; ++l) {
@@ -605,7 +654,10 @@ static bool build_prefix_graph(wamx_gwp_model * m, int64_t cb) {
         // output does not depend on the other queries.
         wamx_tensor * vatt = wamx_joint_attn(ctx, Qv, K, V, nullptr, nullptr, 0, b.scale);  // [d, nimg]
         vh = b.lin(ev.o_w, ev.o_b, vatt, WAMX_EPI_BIAS_GATED, vh, b.part(vmods, d, l, 2));
-        vh = b.cross_ffn_uncached(ev, vh, vkv, l, b.part(vmods, d, l, 3), b.part(vmods, d, l, 4),
+        wamx_tensor * tk_l = wamx_view_4d(ctx, tk, dh, NL, H, 2, tk->nb[1], tk->nb[2], tk->nb[3],
+                                          tk->nb[3] * (size_t) (2 * l));
+        wamx_tensor * tv_l = wamx_view_3d(ctx, tv, NL, dh, H, tv->nb[1], tv->nb[2], tv->nb[3] * (size_t) l);
+        vh = b.cross_ffn_uncached(ev, vh, tk_l, tv_l, b.part(vmods, d, l, 3), b.part(vmods, d, l, 4),
                                   b.part(vmods, d, l, 5));
         wamx_set_lane(ctx, 1);
         wamx_tensor * satt = wamx_joint_attn(ctx, Qs, K, V, nullptr, nullptr, 0, b.scale);  // [d, 1]

@@ -184,11 +184,13 @@ hipError_t launch_mlp_small(const void * x, const void * w1, const void * b1, co
 // ---------------------------------------------------------------------------
 // Rows of x are chunk_tokens-token chunks (0: one chunk): token tl of chunk b
 // takes position pos[tl] and goes to dst + b * chunk_stride (elements).
+// Chunk b's rows start at x + b * x_cs (-1: right after chunk b - 1's) and
+// use the norm weight w + b * w_cs (0: one weight for every chunk).
 hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void * dst, int64_t heads, int64_t head_dim,
                                int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode, const int32_t * pos0,
                                const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s,
                                int64_t chunk_tokens = 0, int64_t chunk_stride = 0, int64_t lo_off = 0,
-                               const float * tab = nullptr);
+                               const float * tab = nullptr, int64_t x_cs = -1, int64_t w_cs = 0);
 // (cos, sin) of every rope pair of `tokens` tokens (rope mode 0 or 1
 // positions) into out [tokens][head_dim]: the table of rope mode 3.
 hipError_t launch_rope_table(int rope_mode, const int32_t * pos0, const int32_t * pos1, const int32_t * pos2,

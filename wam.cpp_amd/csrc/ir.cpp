@@ -129,17 +129,32 @@ const char * check_linear(const wamx_tensor * t) {
 const char * check_qk_norm_rope(const wamx_tensor * t) {
     const wamx_tensor *x = t->src[0], *weight = t->src[1], *dst = t->src[2];
     if (!is_bf16(x) || !is_bf16(weight) || !is_bf16(dst) || !is_bf16(t)) return "types";
-    // dst [dh, tokens, H, B]: the rows of x are B chunks of T tokens each.
-    // Hi/lo form (op_params[4] = 1): dst [dh, tokens, H, 2] holds the bf16
-    // rounding of the f32 result in plane 0 and the rest in plane 1, one chunk.
+    // dst [dh, tokens, H, C]: C chunks of T tokens.  x is [d, C*T] (the
+    // chunks' rows one after another) or [d, T, C] (chunk c's rows x->nb[2]
+    // bytes apart, e.g. column ranges of a packed projection); weight is one
+    // norm weight [d] or one per chunk [d, C].  Hi/lo form (op_params[4] = 1):
+    // dst [dh, tokens, H, 2C] holds for chunk c the bf16 rounding of the f32
+    // result in plane 2c and the rest in plane 2c + 1.
     const bool hilo = t->op_params[4] != 0;
-    const int64_t dh = dst->ne[0], H = dst->ne[2], B = hilo ? 1 : dst->ne[3];
-    if (hilo && dst->ne[3] != 2) return "hi/lo destination needs two planes";
-    if (B < 1 || x->ne[1] % B != 0) return "rows must split into the destination's chunks";
-    const int64_t T = x->ne[1] / B;
-    if (x->ne[0] != dh * H || weight->ne[0] != x->ne[0] || x->nb[0] != 2 || weight->nb[0] != 2 || !contig(dst) ||
-        x->ne[2] != 1 || x->ne[3] != 1 || (dh & 1))
+    const int64_t dh = dst->ne[0], H = dst->ne[2];
+    if (hilo && (dst->ne[3] % 2 != 0 || dst->ne[3] < 2)) return "hi/lo destination needs two planes per chunk";
+    const int64_t C = hilo ? dst->ne[3] / 2 : dst->ne[3];
+    const bool layered = x->ne[2] > 1;
+    if (C < 1 || x->ne[3] != 1 || (layered ? x->ne[2] != C : x->ne[1] % C != 0))
+        return "rows must split into the destination's chunks";
+    const int64_t T = layered ? x->ne[1] : x->ne[1] / C;
+    if (x->ne[0] != dh * H || weight->ne[0] != x->ne[0] || x->nb[0] != 2 || weight->nb[0] != 2 || (dh & 1))
         return "shapes";
+    if (weight->ne[2] != 1 || weight->ne[3] != 1 || (weight->ne[1] != 1 && weight->ne[1] != C))
+        return "norm weight: one row, or one per chunk";
+    // Destination chunks are contiguous [dh, tokens, H] blocks, 16-byte
+    // aligned apart (any distance); hi/lo planes are contiguous throughout.
+    if (dst->nb[0] != 2 || dst->nb[1] != (size_t) dh * 2 || dst->nb[2] != dst->nb[1] * (size_t) dst->ne[1] ||
+        (C > 1 && (dst->nb[3] < dst->nb[2] * (size_t) H || dst->nb[3] % 16 != 0)) || (hilo && !contig(dst)))
+        return "destination layout";
+    if ((layered || weight->ne[1] > 1) &&
+        (x->nb[1] % 16 != 0 || x->nb[2] % 16 != 0 || (weight->ne[1] > 1 && weight->nb[1] % 16 != 0)))
+        return "per-chunk rows and weights need 16-byte strides";
     for (int i = 0; i < 4; ++i)
         if (t->ne[i] != dst->ne[i] || t->nb[i] != dst->nb[i]) return "result must be the destination";
     const int64_t tok0 = t->op_params[0];

@@ -106,18 +106,20 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
                                                           const int32_t * __restrict__ pos2, float eps, float l2ts128,
                                                           float l2ts44, float l2ts42, int64_t chunk_tokens,
                                                           int64_t chunk_stride, int64_t lo_off,
-                                                          const float * __restrict__ tab) {
+                                                          const float * __restrict__ tab, int64_t x_cs, int64_t w_cs) {
     __shared__ float red[16];
     const int64_t t = blockIdx.x;
     const int64_t b = t / chunk_tokens, tl = t - b * chunk_tokens;
     const int d = heads * head_dim;
     const int nchunk = d >> 3;
+    const uint16_t * xr = x + b * x_cs + tl * ldx;
+    const uint16_t * wr = w + b * w_cs;
     uint4 xv[CPT], wv[CPT];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
         const int c = min((int) threadIdx.x + i * (int) blockDim.x, nchunk - 1);
-        xv[i] = *(const uint4 *) (x + t * ldx + 8 * c);
-        wv[i] = *(const uint4 *) (w + 8 * c);
+        xv[i] = *(const uint4 *) (xr + 8 * c);
+        wv[i] = *(const uint4 *) (wr + 8 * c);
     }
     // Rope mode 3: the (cos, sin) of every pair from the table row of the token.
     const RopeTok rt = rope_tok(tab ? 2 : rope_mode, pos0, pos1, pos2, tl, l2ts128, l2ts44, l2ts42);
@@ -151,17 +153,22 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_vec(const uint16_t * __rest
 hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void * dst, int64_t heads, int64_t head_dim,
                                int64_t tokens, int64_t dst_tokens, int64_t tok0, int rope_mode, const int32_t * pos0,
                                const int32_t * pos1, const int32_t * pos2, float eps, float freq_base, hipStream_t s,
-                               int64_t chunk_tokens, int64_t chunk_stride, int64_t lo_off, const float * tab) {
+                               int64_t chunk_tokens, int64_t chunk_stride, int64_t lo_off, const float * tab,
+                               int64_t x_cs, int64_t w_cs) {
     if (tokens <= 0) return hipSuccess;
     // Rope mode 3: the rotation comes from tab [tokens][head_dim] (cos, sin
     // per pair), 16-byte aligned; only the vectorised kernel reads it.
     if ((rope_mode == 3) != (tab != nullptr) || (tab && (((uintptr_t) tab & 15) || (head_dim % 8)))) return hipErrorInvalidValue;
-    if (lo_off && ((lo_off & 7) || (chunk_tokens != tokens && chunk_tokens > 0))) return hipErrorInvalidValue;
+    if (lo_off & 7) return hipErrorInvalidValue;
     if (chunk_tokens <= 0) chunk_tokens = tokens;
     if (tokens % chunk_tokens != 0) return hipErrorInvalidValue;
+    // Chunk b's rows start b * x_cs elements into x and use norm weight row b
+    // (w + b * w_cs); by default the rows follow each other and share w.
+    if (x_cs < 0) x_cs = chunk_tokens * ldx;
+    const bool layered = x_cs != chunk_tokens * ldx || w_cs != 0;
     const int64_t d = heads * head_dim;
-    if (d % 8 == 0 && head_dim % 8 == 0 && d / 8 <= 4096 && ldx % 8 == 0 && ((uintptr_t) x & 15) == 0 &&
-        ((uintptr_t) w & 15) == 0 && ((uintptr_t) dst & 15) == 0) {
+    if (d % 8 == 0 && head_dim % 8 == 0 && d / 8 <= 4096 && ldx % 8 == 0 && x_cs % 8 == 0 && w_cs % 8 == 0 &&
+        ((uintptr_t) x & 15) == 0 && ((uintptr_t) w & 15) == 0 && ((uintptr_t) dst & 15) == 0) {
         const int64_t nchunk = d / 8;
         const int cpt = nchunk <= 1024 ? 1 : nchunk <= 2048 ? 2 : 4;
         const int threads = (int) std::min<int64_t>(1024, ((nchunk + cpt - 1) / cpt + 63) / 64 * 64);
@@ -172,14 +179,14 @@ hipError_t launch_qk_norm_rope(const void * x, int64_t ldx, const void * w, void
     hipLaunchKernelGGL(qk_norm_rope_vec<CPT>, dim3((unsigned) tokens), dim3((unsigned) threads), 0, s,            \
                        (const uint16_t *) x, ldx, (const uint16_t *) w, (uint16_t *) dst, (int) heads, (int) head_dim, \
                        dst_tokens, tok0, rope_mode, pos0, pos1, pos2, eps, l2ts128, l2ts44, l2ts42, chunk_tokens,    \
-                       chunk_stride, lo_off, tab)
+                       chunk_stride, lo_off, tab, x_cs, w_cs)
         if (cpt == 1) WAMX_QK_VEC(1);
         else if (cpt == 2) WAMX_QK_VEC(2);
         else WAMX_QK_VEC(4);
 #undef WAMX_QK_VEC
         return hipGetLastError();
     }
-    if ((heads * head_dim) / 2 > (int64_t) kQkThreads * kQkMaxPairs || (head_dim & 1) || (ldx & 1) || tab)
+    if ((heads * head_dim) / 2 > (int64_t) kQkThreads * kQkMaxPairs || (head_dim & 1) || (ldx & 1) || tab || layered)
         return hipErrorInvalidValue;
     // theta_i = pos * theta_scale^i with theta_scale = base^(-2/n_dims) per rope section.
     const float ts128 = powf(freq_base, -2.0f / (float) head_dim);
