@@ -45,13 +45,15 @@ def gpu_mul_mat(wx, be, w, x, y_type):
 # ragged edges: skinny (N <= 64), 128x128 / 192x192 / 256x256 LDS-DMA tiles
 # (bf16 activations, K % 32 == 0), the 128x128 tiles with K split into f32
 # partial planes (eight 48-token chunks: 384 tokens; 200 ragged tokens), the
-# 192x192 tiles with the 5-stage ring of long K (FFN-down depth, 14336), and
-# the register-staged tile for the rest.
+# 192x192 tiles with the 5-stage ring of long K (FFN-down depth, 14336), the
+# 256x224 tiles with 16x16 fragments (14336 or 9216 features, the latter with
+# a 32-feature last tile column, and 3000 ragged tokens), and the
+# register-staged tile for the rest.
 @pytest.mark.parametrize("M,N,K", [(64, 48, 256), (96, 1, 136), (200, 64, 3072), (3072, 48, 3072),
                                    (128, 65, 64), (300, 300, 520), (1000, 129, 72), (77, 33, 31),
                                    (3072, 3000, 128), (4096, 4100, 64), (256, 200, 96), (640, 520, 192),
                                    (3072, 384, 3072), (3072, 384, 14336), (9216, 384, 3072), (1000, 200, 2048),
-                                   (3072, 2304, 14336)])
+                                   (3072, 2304, 14336), (14336, 3072, 64), (9216, 3000, 96)])
 @pytest.mark.parametrize("xt", ["f32", "bf16"])
 def test_mul_mat_integer_kat_exact(wx, be, M, N, K, xt):
     print(f"mul_mat KAT M={M} N={N} K={K} x={xt}", flush=True)
@@ -96,6 +98,31 @@ def test_linear_epilogues(wx, be, orc, N):
         ref = orc.linear(w, x, b, epi, h, g)
         assert_parity(f32(got), f32(ref), what=f"linear epi={epi} N={N}")
         # at most one bf16 ulp apart almost everywhere (fp32 vs exact accumulation)
+        ulps = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+        assert np.mean(ulps > 1) < 1e-3, f"epi={epi}: {np.mean(ulps > 1)} of outputs differ by >1 ulp"
+
+
+@pytest.mark.parametrize("M,N", [(9216, 1800), (14336, 1100)])
+def test_linear_epilogues_tile224(wx, be, orc, M, N):
+    """Every epilogue on the 256x224 tiles (16x16 fragments, padded copy
+    stages): 9216 features end in a 32-feature tile column, 1800 tokens in a
+    partial token tile."""
+    print(f"linear epilogues 256x224 tiles M={M} N={N}", flush=True)
+    rng = np.random.default_rng(M + N)
+    K = 256
+    w = bf16(rng.standard_normal((M, K)) * 0.05)
+    x = bf16(rng.standard_normal((N, K)))
+    b = bf16(rng.standard_normal(M) * 0.02)
+    h = bf16(rng.standard_normal((N, M)))
+    g = (rng.standard_normal(M) * 0.1).astype(np.float32)
+    dw, dx, db, dh, dg = dev(be, w), dev(be, x), dev(be, b), dev(be, h), dev(be, g)
+    dy = be.empty(N * M * 2)
+    for epi in (wx.EPI_NONE, wx.EPI_BIAS, wx.EPI_BIAS_GELU, wx.EPI_BIAS_GATED, wx.EPI_BIAS_RESIDUAL):
+        wx.check(be.lib.wamx_op_linear(be.ptr, dw.ptr, dx.ptr, wx.TYPE_BF16, db.ptr, epi, dh.ptr, dg.ptr, dy.ptr,
+                                       M, N, K), "linear")
+        got = dy.download(np.uint16, (N, M))
+        ref = orc.linear(w, x, b, epi, h, g)
+        assert_parity(f32(got), f32(ref), what=f"linear 256x224 epi={epi} M={M} N={N}")
         ulps = np.abs(got.astype(np.int32) - ref.astype(np.int32))
         assert np.mean(ulps > 1) < 1e-3, f"epi={epi}: {np.mean(ulps > 1)} of outputs differ by >1 ulp"
 

@@ -410,16 +410,21 @@ __device__ __forceinline__ void wave_lds_fence() {
 // instruction fall in disjoint banks), then reads them back as 16-byte row
 // chunks and applies bias / GELU / gated residual on 8 features at a time with
 // 16-byte residual loads and stores.  Same rounding points as tile_store.
-template <int E, int FR, int FC>
+// MF 16 (16x16 fragments: lane holds feature lane & 15, register v token
+// 4*(lane/16) + v): two fragment rows make one 32-token pass.
+template <int E, int FR, int FC, int MF = 32, typename AccT = f32x16_t>
 __device__ __forceinline__ void tile_store_lds(const GemmParams & p, uint16_t * __restrict__ y,
-                                               const uint16_t * __restrict__ resb, f32x16_t (&acc)[FR][FC],
+                                               const uint16_t * __restrict__ resb, AccT (&acc)[FR][FC],
                                                int64_t nb, int64_t mb, int lane, uint16_t * __restrict__ region) {
     constexpr bool kBias = E >= kEpiBias, kRes = E >= kEpiBiasGated;
-    constexpr int WN = 32 * FC, SP = WN + 8, CPR = WN / 8;
-    constexpr int PER = 32 * CPR / 64;            // 16-byte chunks per lane per fragment row
+    constexpr int WN = MF * FC, SP = WN + 8, CPR = WN / 8;
+    constexpr int FPP = 32 / MF;                  // fragment rows per 32-token pass
+    constexpr int NV = MF * MF / 64;              // accumulator registers per fragment
+    constexpr int PER = 32 * CPR / 64;            // 16-byte chunks per lane per pass
     constexpr bool kFixedCol = 64 % CPR == 0;     // each lane keeps one chunk column
     constexpr int G = PER % 4 == 0 ? 4 : PER % 3 == 0 ? 3 : PER;
     static_assert(PER * 64 == 32 * CPR, "fragment row must split evenly over the wave");
+    static_assert(FR % FPP == 0, "whole 32-token passes");
     const uint16_t * __restrict__ bias = p.bias;
     const float * __restrict__ gate = p.gate;
 
@@ -438,14 +443,16 @@ __device__ __forceinline__ void tile_store_lds(const GemmParams & p, uint16_t * 
     }
 
 #pragma unroll
-    for (int i = 0; i < FR; ++i) {
+    for (int i = 0; i < FR; i += FPP) {
 #pragma unroll
-        for (int j = 0; j < FC; ++j)
+        for (int ii = 0; ii < FPP; ++ii)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int r = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                region[r * SP + 32 * j + (lane & 31)] = f32_to_bf16(acc[i][j][v]);
-            }
+            for (int j = 0; j < FC; ++j)
+#pragma unroll
+                for (int v = 0; v < NV; ++v) {
+                    const int r = MF == 32 ? 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3) : 16 * ii + 4 * (lane >> 4) + v;
+                    region[r * SP + MF * j + (lane & (MF - 1))] = f32_to_bf16(acc[i + ii][j][v]);
+                }
         wave_lds_fence();
 
         // G chunks at a time: their LDS and residual loads are issued together,
@@ -458,14 +465,14 @@ __device__ __forceinline__ void tile_store_lds(const GemmParams & p, uint16_t * 
                 const int c = lane + 64 * (t0 + u), r = c / CPR, cc = c % CPR;
                 sv[u] = *(const uint4 *) (region + r * SP + 8 * cc);
                 if constexpr (kRes) {
-                    const int64_t n = min(nb + 32 * i + r, p.N - 1), m = min(mb + 8 * cc, p.M - 8);
+                    const int64_t n = min(nb + MF * i + r, p.N - 1), m = min(mb + 8 * cc, p.M - 8);
                     hv[u] = *(const uint4 *) (resb + n * p.ldres + m);
                 }
             }
 #pragma unroll
             for (int u = 0; u < G; ++u) {
                 const int c = lane + 64 * (t0 + u), r = c / CPR, cc = c % CPR;
-                const int64_t n = nb + 32 * i + r, m = mb + 8 * cc;
+                const int64_t n = nb + MF * i + r, m = mb + 8 * cc;
                 if (n >= p.N || m >= p.M) continue;
                 uint4 out = sv[u];
                 if constexpr (kBias) {
@@ -500,18 +507,26 @@ __device__ __forceinline__ void tile_store_lds(const GemmParams & p, uint16_t * 
     }
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int S>
+// MF: MFMA fragment edge, 32 (32x32x16) or 16 (16x16x32).  A stage holds the
+// BM activation rows, the BN weight rows and, when BM + BN is not a multiple
+// of the rows one copy instruction covers (RPI), padding rows that the last
+// instruction fills with duplicates of the tile's last weight row, so every
+// lane issues the same P copies per stage.
+template <int BM, int BN, int WM, int WN, int BK, int S, int MF = 32>
 struct DmaCfg {
     static constexpr int kThreads = 64 * WM * WN, kWaves = WM * WN;
     static constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
-    static constexpr int FR = kWaveM / 32, FC = kWaveN / 32;
+    static constexpr int FR = kWaveM / MF, FC = kWaveN / MF;
     static constexpr int kRows = BM + BN, kChunks = BK / 8;
-    static constexpr int kStageElems = kRows * BK;
-    static constexpr int P = kRows * kChunks / kThreads;  // DMA instructions per thread per stage
+    static constexpr int RPI = kThreads / kChunks;  // stage rows per copy instruction
+    static constexpr int kRowsPad = (kRows + RPI - 1) / RPI * RPI;
+    static constexpr int kStageElems = kRowsPad * BK;
+    static constexpr int P = kRowsPad / RPI;  // DMA instructions per thread per stage
     static_assert(BK == 32 || BK == 64, "BK");
+    static_assert(MF == 32 || MF == 16, "MFMA fragment edge");
     static_assert(S >= 2 && S <= 5, "ring of 2 to 5 stages");
-    static_assert(FR * 32 * WM == BM && FC * 32 * WN == BN, "wave tile must be whole 32x32 fragments");
-    static_assert(P * kThreads == kRows * kChunks, "stage/thread mismatch");
+    static_assert(FR * MF * WM == BM && FC * MF * WN == BN, "wave tile must be whole fragments");
+    static_assert(P * RPI == kRowsPad && RPI * kChunks == kThreads, "stage/thread mismatch");
     static_assert((size_t) S * kStageElems * 2 <= 160 * 1024, "LDS budget");
 };
 
@@ -525,6 +540,7 @@ template <int BM, int BN, int WM, int WN, int BK, int S, int OCC = 1>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_dma(GemmParams p, int nt_m, int nt_n) {
     using C = DmaCfg<BM, BN, WM, WN, BK, S>;
     constexpr int FR = C::FR, FC = C::FC, P = C::P, E = C::kStageElems, CH = C::kChunks;
+    static_assert(C::kRowsPad == C::kRows, "gemm_dma stages hold no padding rows");
     __shared__ __align__(16) uint16_t st0[E];
     __shared__ __align__(16) uint16_t st1[E];
     __shared__ __align__(16) uint16_t st2[S > 2 ? E : 8];
@@ -714,17 +730,24 @@ __device__ __forceinline__ void lgkm_wait(bf16x8_t (&a)[FR], bf16x8_t (&b)[FC]) 
     for (int j = 0; j < FC; ++j) asm volatile("" : "+v"(b[j]));
 }
 
-template <int BM, int BN, int WM, int WN, int S, int SCHED = kSchedSingle, int BK = 32>
+// Fragment reads of one operand: N ds_read_b128 at RS-byte steps from `base`.
+template <int RS, int N, int... I>
+__device__ __forceinline__ void read_frags(bf16x8_t (&f)[N], uint32_t base, std::integer_sequence<int, I...>) {
+    ((f[I] = ds_read128<I * RS>(base)), ...);
+}
+
+template <int BM, int BN, int WM, int WN, int S, int SCHED = kSchedSingle, int BK = 32, int MF = 32>
 __global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1) void gemm_dma_pipe(
     GemmParams p, int nt_m, int nt_n) {
-    constexpr int KS = BK / 16;  // 16-deep MFMA k-steps per stage
-    using C = DmaCfg<BM, BN, WM, WN, BK, S>;
+    constexpr int KS = BK / (512 / MF);  // MFMA k-steps per stage (16 deep for MF 32, 32 deep for MF 16)
+    using C = DmaCfg<BM, BN, WM, WN, BK, S, MF>;
     constexpr int FR = C::FR, FC = C::FC, P = C::P, E = C::kStageElems, CH = C::kChunks;
     constexpr bool PP = SCHED == kSchedPingPong, kProd = SCHED == kSchedProducer;
     static_assert(S >= 3, "the mid-step barrier needs three or more stages");
     static_assert(!PP || (WM * WN == 8 && BK == 32), "ping-pong pairs two waves per SIMD, BK 32");
     static_assert(!kProd || WM * WN == 4, "producers take the second wave of each SIMD");
-    static_assert(FR <= 4 && FC <= 4, "fragment count");
+    static_assert(PP || KS >= 2, "the single and producer steps alternate two fragment sets within a stage");
+    static_assert(FR + FC <= 15 && FR <= 8 && FC <= 8, "fragment count (lgkmcnt holds 15)");
     __shared__ __align__(16) uint16_t st0[E];
     __shared__ __align__(16) uint16_t st1[E];
     __shared__ __align__(16) uint16_t st2[E];
@@ -746,15 +769,21 @@ __global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1
     // (the launcher keeps both operands under 4 GB).  Copy instruction i of a
     // lane covers stage rows RPI i .. RPI (i + 1), all activation rows or all
     // weight rows.
-    constexpr int RPI = C::kWaves * 64 / CH;
+    constexpr int RPI = C::RPI;
     static_assert(BM % RPI == 0, "a copy instruction covers activation rows or weight rows only");
+    // A wave whose rows of the last copy instruction are all padding (past
+    // BM + BN) skips that copy, and its waits count P - 1 copies per stage.
+    constexpr bool kPad = C::kRowsPad != C::kRows;
+    static_assert(!kPad || PP, "padded stages run the ping-pong step");
+    static_assert(C::kRows % (64 / CH) == 0, "a wave's rows of one copy instruction are all real or all padding");
+    const bool skip_last = kPad && ((P - 1) * C::kWaves + cw) * (64 / CH) >= C::kRows;
     uint32_t soff[P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
         const int slot = (i * C::kWaves + cw) * 64 + lane;
         const int r = slot / CH, c = (slot % CH) ^ dma_swz<BK>(slot / CH);
         if (i * RPI < BM) soff[i] = (uint32_t) ((min(n0 + r, N - 1) * p.ldx + 8 * c) * 2);
-        else soff[i] = (uint32_t) ((min(m0 + (r - BM), M - 1) * p.ldw + 8 * c) * 2);
+        else soff[i] = (uint32_t) ((min(m0 + min(r - BM, BN - 1), M - 1) * p.ldw + 8 * c) * 2);
     }
     const char * const xb = (const char *) p.x, * const wb = (const char *) p.w;
     uint16_t * const stp[5] = {st0, st1, st2, S > 3 ? st3 : st0, S > 4 ? st4 : st0};
@@ -762,9 +791,19 @@ __global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1
         const uint32_t koff = (uint32_t) min(kt, nk - 1) * BK * 2;
 #pragma unroll
         for (int i = 0; i < P; ++i)
-            __builtin_amdgcn_global_load_lds((glb_void_t *) ((i * RPI < BM ? xb : wb) + (soff[i] + koff)),
-                                             (lds_void_t *) (stp[stage] + (i * C::kWaves + cw) * 64 * 8), 16, 0, 0);
+            if (!kPad || i < P - 1 || !skip_last)
+                __builtin_amdgcn_global_load_lds((glb_void_t *) ((i * RPI < BM ? xb : wb) + (soff[i] + koff)),
+                                                 (lds_void_t *) (stp[stage] + (i * C::kWaves + cw) * 64 * 8), 16, 0,
+                                                 0);
     };
+    // At most T stages of this wave's copies outstanding.
+    auto vm_wait = [&](auto t_c) {
+        constexpr int T = decltype(t_c)::value;
+        if (kPad && skip_last) __builtin_amdgcn_s_waitcnt(vmcnt_imm(T * (P - 1)));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(T * P));
+    };
+    using W1 = std::integral_constant<int, S - 1>;
+    using W2 = std::integral_constant<int, S - 2>;
 
     if constexpr (kProd) {
         if (producer) {
@@ -794,45 +833,48 @@ __global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1
         }
     }
 
-    f32x16_t acc[FR][FC];
+    // MF 32: 32x32 fragments (16 registers); MF 16: 16x16 fragments (4).
+    using acc_t = std::conditional_t<MF == 32, f32x16_t, f32x4_t>;
+    constexpr int NV = MF * MF / 64;
+    acc_t acc[FR][FC];
 #pragma unroll
     for (int i = 0; i < FR; ++i)
 #pragma unroll
         for (int j = 0; j < FC; ++j)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+            for (int v = 0; v < NV; ++v) acc[i][j][v] = 0.0f;
 
-    // Byte offsets of this lane's A fragments in a stage, per 16-wide k-step;
-    // its B fragments sit a wave-uniform distance further (the row swizzle
-    // repeats every 16 rows, and the wave tiles start at multiples of 16).
+    // Byte offsets of this lane's A fragments in a stage, per MFMA k-step (lane
+    // reads row lane % MF, 16-byte chunk lane / MF of the k-step's 64 / MF
+    // chunks); its B fragments sit a wave-uniform distance further (the row
+    // swizzle repeats every 16 rows, and the wave tiles start at multiples of 16).
     static_assert(C::kWaveM % 16 == 0 && C::kWaveN % 16 == 0 && BM % 16 == 0, "swizzle period");
-    const int arow = wr * C::kWaveM + (lane & 31);
-    const int sw = dma_swz<BK>(lane & 31);
+    const int arow = wr * C::kWaveM + (lane & (MF - 1));
+    const int sw = dma_swz<BK>(lane & (MF - 1));
     const uint32_t bdelta = (uint32_t) ((BM + wc * C::kWaveN - wr * C::kWaveM) * BK * 2);
     uint32_t aoff[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) aoff[ks] = (uint32_t) (arow * BK + ((2 * ks + (lane >> 5)) ^ sw) * 8) * 2;
+    for (int ks = 0; ks < KS; ++ks)
+        aoff[ks] = (uint32_t) (arow * BK + (((64 / MF) * ks + lane / MF) ^ sw) * 8) * 2;
     const uint32_t sbase[5] = {lds_addr(st0), lds_addr(st1), lds_addr(st2), lds_addr(stp[3]), lds_addr(stp[4])};
 
-    constexpr int RS = 32 * BK * 2;  // bytes between fragment rows 32 apart
+    constexpr int RS = MF * BK * 2;  // bytes between fragment rows MF apart
     bf16x8_t a0[FR], b0[FC], a1[FR], b1[FC];
     auto read = [&](bf16x8_t (&a)[FR], bf16x8_t (&b)[FC], int stage, int ks) {
         const uint32_t ab = sbase[stage] + aoff[ks], bb = ab + bdelta;
-        a[0] = ds_read128<0>(ab);
-        if constexpr (FR > 1) a[1] = ds_read128<RS>(ab);
-        if constexpr (FR > 2) a[2] = ds_read128<2 * RS>(ab);
-        if constexpr (FR > 3) a[3] = ds_read128<3 * RS>(ab);
-        b[0] = ds_read128<0>(bb);
-        if constexpr (FC > 1) b[1] = ds_read128<RS>(bb);
-        if constexpr (FC > 2) b[2] = ds_read128<2 * RS>(bb);
-        if constexpr (FC > 3) b[3] = ds_read128<3 * RS>(bb);
+        read_frags<RS>(a, ab, std::make_integer_sequence<int, FR>{});
+        read_frags<RS>(b, bb, std::make_integer_sequence<int, FC>{});
     };
     auto mma = [&](bf16x8_t (&a)[FR], bf16x8_t (&b)[FC]) {
 #pragma unroll
         for (int i = 0; i < FR; ++i)
 #pragma unroll
-            for (int j = 0; j < FC; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FC; ++j) {
+                if constexpr (MF == 32)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+                else
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+            }
     };
     // Step kt: the stage's k-steps alternate between the two fragment sets
     // (the reads of k-step i + 1 in flight while k-step i multiplies); the
@@ -873,25 +915,25 @@ __global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1
     auto pp_step = [&](int kt, auto cur_c) {
         constexpr int cur = decltype(cur_c)::value, prv = cur == 0 ? S - 1 : cur - 1;
         read(a0, b0, cur, 0);
-        read(a1, b1, cur, 1);
+        if constexpr (KS > 1) read(a1, b1, cur, 1);
         dma(kt + S - 1, prv);
         lgkm_wait<0>(a0, b0);
-        lgkm_wait<0>(a1, b1);
+        if constexpr (KS > 1) lgkm_wait<0>(a1, b1);
         __builtin_amdgcn_sched_barrier(0);
-        if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 1) * P));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * P));
+        if (grp == 0) vm_wait(W1{});
+        else vm_wait(W2{});
         cta_barrier();
         mma(a0, b0);
-        mma(a1, b1);
+        if constexpr (KS > 1) mma(a1, b1);
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * P));
+        vm_wait(W2{});
         cta_barrier();
     };
 
     if constexpr (!kProd) {
 #pragma unroll
         for (int i = 0; i < S - 1; ++i) dma(i, i);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * P));
+        vm_wait(W2{});
     }
     cta_barrier();
     if constexpr (PP) {
@@ -940,11 +982,13 @@ __global__ __launch_bounds__(64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1), 1
     uint16_t * region = (sa == 0 ? st0 : sa == 1 ? st1 : sa == 2 ? st2 : sa == 3 ? stp[3] : stp[4]) + (wave % WPS) * REG;
     uint16_t * y = (uint16_t *) p.y;
     switch (epi_kind(p)) {
-        case kEpiBias: tile_store_lds<kEpiBias>(p, y, p.res, acc, nb, mb, lane, region); break;
-        case kEpiBiasGelu: tile_store_lds<kEpiBiasGelu>(p, y, p.res, acc, nb, mb, lane, region); break;
-        case kEpiBiasGated: tile_store_lds<kEpiBiasGated>(p, y, p.res, acc, nb, mb, lane, region); break;
-        case kEpiBiasResidual: tile_store_lds<kEpiBiasResidual>(p, y, p.res, acc, nb, mb, lane, region); break;
-        default: tile_store_lds<kEpiBf16>(p, y, p.res, acc, nb, mb, lane, region); break;
+        case kEpiBias: tile_store_lds<kEpiBias, FR, FC, MF>(p, y, p.res, acc, nb, mb, lane, region); break;
+        case kEpiBiasGelu: tile_store_lds<kEpiBiasGelu, FR, FC, MF>(p, y, p.res, acc, nb, mb, lane, region); break;
+        case kEpiBiasGated: tile_store_lds<kEpiBiasGated, FR, FC, MF>(p, y, p.res, acc, nb, mb, lane, region); break;
+        case kEpiBiasResidual:
+            tile_store_lds<kEpiBiasResidual, FR, FC, MF>(p, y, p.res, acc, nb, mb, lane, region);
+            break;
+        default: tile_store_lds<kEpiBf16, FR, FC, MF>(p, y, p.res, acc, nb, mb, lane, region); break;
     }
 }
 
@@ -1730,17 +1774,24 @@ static hipError_t run_dma(const GemmParams & p, hipStream_t s) {
                        p, nt_m, nt_n);
     return hipGetLastError();
 }
-// The pipelined form (K steps of BKP) for vector-stored bf16 outputs, else gemm_dma.
-template <int BM, int BN, int WM, int WN, int S, int BKF, int SF, int SCHED = kSchedSingle, int BKP = 32>
-static hipError_t run_dma_pipe(const GemmParams & p, hipStream_t s) {
-    // The pipelined kernel addresses its copies by 32-bit offsets.
-    const bool small = (uint64_t) p.N * p.ldx * 2 < (1ull << 32) && (uint64_t) p.M * p.ldw * 2 < (1ull << 32);
-    if (!p.vec_out || !small) return run_dma<BM, BN, WM, WN, BKF, SF>(p, s);
+// The pipelined kernel addresses its copies by 32-bit offsets and stores bf16
+// rows in 16-byte chunks.
+static bool pipe_ok(const GemmParams & p) {
+    return p.vec_out && (uint64_t) p.N * p.ldx * 2 < (1ull << 32) && (uint64_t) p.M * p.ldw * 2 < (1ull << 32);
+}
+template <int BM, int BN, int WM, int WN, int S, int SCHED, int BKP, int MF = 32>
+static hipError_t launch_dma_pipe(const GemmParams & p, hipStream_t s) {
     const int nt_m = (int) ((p.M + BN - 1) / BN), nt_n = (int) ((p.N + BM - 1) / BM);
     const int threads = 64 * WM * WN * (SCHED == kSchedProducer ? 2 : 1);
-    hipLaunchKernelGGL((gemm_dma_pipe<BM, BN, WM, WN, S, SCHED, BKP>), dim3((unsigned) (nt_m * nt_n)), dim3(threads), 0,
-                       s, p, nt_m, nt_n);
+    hipLaunchKernelGGL((gemm_dma_pipe<BM, BN, WM, WN, S, SCHED, BKP, MF>), dim3((unsigned) (nt_m * nt_n)),
+                       dim3(threads), 0, s, p, nt_m, nt_n);
     return hipGetLastError();
+}
+// The pipelined form (K steps of BKP) where pipe_ok, else gemm_dma.
+template <int BM, int BN, int WM, int WN, int S, int BKF, int SF, int SCHED = kSchedSingle, int BKP = 32>
+static hipError_t run_dma_pipe(const GemmParams & p, hipStream_t s) {
+    if (!pipe_ok(p)) return run_dma<BM, BN, WM, WN, BKF, SF>(p, s);
+    return launch_dma_pipe<BM, BN, WM, WN, S, SCHED, BKP>(p, s);
 }
 
 static int64_t tiles_of(const GemmParams & p, int bm, int bn) { return ((p.N + bm - 1) / bm) * ((p.M + bn - 1) / bn); }
@@ -1818,9 +1869,11 @@ static hipError_t run_dma_splitk(const GemmParams & p, int splits, void * ws, hi
 
 // Tile shape of the bf16 x bf16 DMA path, chosen so the grid fills the 256 CUs
 // (measured on the 3072-token products of the prefix pass):
-//  * 256 x 256, 8 waves: when it gives at least one tile per CU (QKV 9216 x
-//    3072, FFN-up 14336 x 3072), ping-pong with BK 32 and 4 stages (6-9%
-//    faster than the single-group schedule on both);
+//  * 256 x 256, 8 waves: when it gives at least one tile per CU, ping-pong
+//    with BK 32 and 4 stages (6-9% faster than the single-group schedule);
+//    256 x 224 with 16x16 fragments instead where its whole rounds finish
+//    sooner (prefer_tile224: FFN-up 14336 x 3072 in 768 tiles, 3 rounds,
+//    against 672; QKV 9216 x 3072 in 504 against 432), same bits;
 //  * 192 x 192, 4 waves: 3072 x 3072 products, which it cuts into exactly 256
 //    tiles (256 x 256 leaves 112 CUs idle), pipelined with BK 64 and 3
 //    stages, copies issued by 4 producer waves (2-4% faster on O and
@@ -1829,10 +1882,33 @@ static hipError_t run_dma_splitk(const GemmParams & p, int splits, void * ws, hi
 //  * 128 x 128, BK 64, 2 stages, 4 waves, two workgroups per CU: small grids
 //    (512-token prompt projections).
 // Returns false when the shape does not meet the path's preconditions.
+static bool tile224_enabled() {
+    static const bool on = [] {
+        const char * e = getenv("WAMX_DISABLE_TILE224");
+        return !(e && e[0] && e[0] != '0');
+    }();
+    return on;
+}
+
+// Whether 256 x 224 tiles (16x16 fragments) finish the grid sooner than 256 x
+// 256 ones: a 224-wide tile is 7/8 of the work, so it wins when its rounds of
+// one tile per CU, weighted by that, come to fewer than the 256-wide rounds.
+static bool prefer_tile224(const GemmParams & p) {
+    const int64_t cus = device_cus();
+    if (cus <= 0 || !tile224_enabled()) return false;
+    const int64_t r256 = (tiles_of(p, 256, 256) + cus - 1) / cus, r224 = (tiles_of(p, 256, 224) + cus - 1) / cus;
+    return 7 * r224 < 8 * r256;
+}
+
 static bool dispatch_dma(const GemmParams & p, void * ws, size_t ws_bytes, hipStream_t s, hipError_t & err) {
     if (p.K % 32 != 0) return false;
     if (tiles_of(p, 256, 256) >= 256) {
-        err = run_dma_pipe<256, 256, 4, 2, 4, 32, 3, kSchedPingPong>(p, s);
+        // 256 x 224: FFN-up (14336 features x 3072 tokens) takes 768 tiles,
+        // three whole rounds of 256 CUs, where 256 x 256 leaves 672 (2.6).
+        if (pipe_ok(p) && prefer_tile224(p))
+            err = launch_dma_pipe<256, 224, 4, 2, 4, kSchedPingPong, 32, 16>(p, s);
+        else
+            err = run_dma_pipe<256, 256, 4, 2, 4, 32, 3, kSchedPingPong>(p, s);
         return true;
     }
     if (p.K % 64 != 0) return false;
