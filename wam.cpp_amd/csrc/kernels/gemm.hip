@@ -508,10 +508,10 @@ __device__ __forceinline__ void tile_store_lds(const GemmParams & p, uint16_t * 
 }
 
 // MF: MFMA fragment edge, 32 (32x32x16) or 16 (16x16x32).  A stage holds the
-// BM activation rows, the BN weight rows and, when BM + BN is not a multiple
-// of the rows one copy instruction covers (RPI), padding rows that the last
-// instruction fills with duplicates of the tile's last weight row, so every
-// lane issues the same P copies per stage.
+// BM activation rows and the BN weight rows.  When BM + BN is not a multiple
+// of the rows one copy instruction covers (RPI), the last instruction's slots
+// past them (padding rows) are not copied: the waves they would fall to skip
+// it (gemm_dma_pipe), so the stage needs only the real rows.
 template <int BM, int BN, int WM, int WN, int BK, int S, int MF = 32>
 struct DmaCfg {
     static constexpr int kThreads = 64 * WM * WN, kWaves = WM * WN;
@@ -520,7 +520,7 @@ struct DmaCfg {
     static constexpr int kRows = BM + BN, kChunks = BK / 8;
     static constexpr int RPI = kThreads / kChunks;  // stage rows per copy instruction
     static constexpr int kRowsPad = (kRows + RPI - 1) / RPI * RPI;
-    static constexpr int kStageElems = kRowsPad * BK;
+    static constexpr int kStageElems = kRows * BK;
     static constexpr int P = kRowsPad / RPI;  // DMA instructions per thread per stage
     static_assert(BK == 32 || BK == 64, "BK");
     static_assert(MF == 32 || MF == 16, "MFMA fragment edge");
