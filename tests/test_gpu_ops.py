@@ -44,7 +44,8 @@ def gpu_mul_mat(wx, be, w, x, y_type):
 # Shapes cover every kernel and tile configuration of the dispatcher, with
 # ragged edges: skinny (N <= 64), 128x128 / 192x192 / 256x256 LDS-DMA tiles
 # (bf16 activations, K % 32 == 0), the 128x128 tiles with K split into f32
-# partial planes (eight 48-token chunks: 384 tokens; 200 ragged tokens), the
+# partial planes (eight 48-token chunks: 384 tokens; 200 ragged tokens; at
+# 14336 features the 384-token grid fills half the slots and is not split), the
 # 192x192 tiles with the 5-stage ring of long K (FFN-down depth, 14336), the
 # 256x224 tiles with 16x16 fragments (14336 or 9216 features, the latter with
 # a 32-feature last tile column, and 3000 ragged tokens), and the
@@ -53,7 +54,7 @@ def gpu_mul_mat(wx, be, w, x, y_type):
                                    (128, 65, 64), (300, 300, 520), (1000, 129, 72), (77, 33, 31),
                                    (3072, 3000, 128), (4096, 4100, 64), (256, 200, 96), (640, 520, 192),
                                    (3072, 384, 3072), (3072, 384, 14336), (9216, 384, 3072), (1000, 200, 2048),
-                                   (3072, 2304, 14336), (14336, 3072, 64), (9216, 3000, 96)])
+                                   (3072, 2304, 14336), (14336, 3072, 64), (9216, 3000, 96), (14336, 384, 3072)])
 @pytest.mark.parametrize("xt", ["f32", "bf16"])
 def test_mul_mat_integer_kat_exact(wx, be, M, N, K, xt):
     print(f"mul_mat KAT M={M} N={N} K={K} x={xt}", flush=True)
