@@ -912,9 +912,22 @@ static bool plan_lanes(wamx_cgraph * g, std::vector<int> & wait_for, std::vector
             if (r != w) use[r].read[a] = i;
         }
         use[w].write[a] = i;
-        if (dep >= 0) {
-            wait_for[i] = dep;
-            signal[dep] = 1;
+        if (dep >= 0) wait_for[i] = dep;
+    }
+    // A lane that has waited for node j of the other lane need not wait for
+    // an earlier node of it: that lane's stream completes its nodes in order,
+    // so j's event covers them (a fused launch goes out at its first member's
+    // place, before the later members' own places).  Each wait costs the
+    // stream several microseconds even when its event has long completed.
+    int waited[2] = {-1, -1};
+    for (int i = 0; i < n; ++i) {
+        if (wait_for[i] < 0) continue;
+        const int a = wamx_graph_node(g, i)->lane ? 1 : 0;
+        if (wait_for[i] <= waited[a]) {
+            wait_for[i] = -1;
+        } else {
+            waited[a] = wait_for[i];
+            signal[wait_for[i]] = 1;
         }
     }
     return true;
