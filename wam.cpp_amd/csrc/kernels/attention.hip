@@ -1343,7 +1343,10 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
         // The (head, query block) units fill rounds of two workgroups per CU.
         // When the last round would run at most a quarter full (3072 queries
         // x 24 heads: 576 units on 512 slots), its units are split into key
-        // ranges that fill it instead, with their partials merged after.
+        // ranges that fill it instead, with their partials merged after: as
+        // many ranges as give one workgroup per CU (the 64 units of the prefix
+        // self-attention in 4 ranges of 13 blocks; 7 ranges filling both
+        // slots of every CU made the chunk 0.2 ms slower).
         // Sources of fewer than 16 blocks (the 512-key prompt) keep the plain
         // grid with bf16 scores (their ranges would be one or two blocks
         // long); the hi/lo form, with three times the score MFMAs per block,
@@ -1352,7 +1355,7 @@ hipError_t launch_joint_attn(const AttnArgs & a, hipStream_t s) {
         const int64_t tail = slots > 0 ? units % slots : 0;
         const int64_t nblk = (p.seg_len[0] + kPfKeys - 1) / kPfKeys;
         if (units > slots && tail > 0 && 4 * tail <= slots && (nblk >= 16 || (hilo && nblk >= 2))) {
-            int64_t nsplit = std::min<int64_t>({slots / tail, nblk / 2, (int64_t) kMaxSplits});
+            int64_t nsplit = std::min<int64_t>({slots / (2 * tail), nblk / 2, (int64_t) kMaxSplits});
             p.split_blocks = (nblk + nsplit - 1) / nsplit;
             nsplit = (nblk + p.split_blocks - 1) / p.split_blocks;
             const size_t rows = (size_t) tail * kPfQueries;
