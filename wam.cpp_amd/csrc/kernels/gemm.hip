@@ -1601,7 +1601,13 @@ size_t linear_split_bytes(int64_t M, int64_t N, int64_t K, int32_t x_type, size_
 // grid (rounds) only when no G <= 12 fits.  Chosen: 3072 x 3072 G6/384,
 // QKV 9216 x 3072 G9/768, FFN-up 14336 x 3072 G11/1024, FFN-down
 // 3072 x 14336 G12/896 (each within 0.1-0.7 us of the sweep's best).
+// A one-token product (the state token) runs beside the visual tokens'
+// kernels on the second stream; its rounds are of 64 workgroups, so it
+// takes a quarter of the CUs and delays fewer of the other stream's
+// one-round kernels (whole action chunk 83.40 against 83.60 ms at rounds of
+// 256; 32 and 16 were slower than 64).
 static void skinny_tiled_plan(int64_t M, int64_t N, int64_t K, int & splits, int & ks, int & waves) {
+    const int64_t cap = N == 1 ? 64 : 256;
     const int64_t ngrp = M / 16;
     const int nt = (int) ((N + 15) / 16);
     const int64_t kwhole = (K + 127) / 128 * 128;  // one slice over all of K
@@ -1619,7 +1625,7 @@ static void skinny_tiled_plan(int64_t M, int64_t N, int64_t K, int & splits, int
             if (s == 1 ? c != kwhole : c < 384) continue;
             if ((size_t) 16 * nt * (c + 8) * sizeof(uint16_t) > kSkinnyLdsMax) continue;
             int G = (int) std::min<int64_t>(4, std::max<int64_t>(1, ngrp));
-            while (G <= 12 && (ngrp + G - 1) / G * s > 256 * rounds) ++G;
+            while (G <= 12 && (ngrp + G - 1) / G * s > cap * rounds) ++G;
             if (G > 12) continue;
             const double score = (double) c + 64.0 * (double) s * (double) M / 3072.0;
             if (score < best) {
