@@ -58,12 +58,14 @@ def gelu_erf_bf16(h):
 
 
 @pytest.mark.parametrize("N", [48, 17, 384])
-@pytest.mark.parametrize("which", ["encoder", "decoder"])
+@pytest.mark.parametrize("which", ["encoder", "decoder", "ragged"])
 def test_mlp_small_matches_oracle(wx, be, orc, rng, N, which):
     """Encoder form: x [32] -> 128 + GELU-erf -> 128 + GELU-erf; decoder form:
-    GELU-erf(x [128]) -> 128 + GELU-erf -> 32."""
+    GELU-erf(x [128]) -> 128 + GELU-erf -> 32 (both on the register-row
+    kernel); ragged widths 20 -> 72 -> 30, which take the LDS-staged kernel."""
     print(f"mlp_small {which} N={N}", flush=True)
-    K0, M1, M2, flags = (32, 128, 128, 2 | 4) if which == "encoder" else (128, 128, 32, 1 | 2)
+    K0, M1, M2, flags = {"encoder": (32, 128, 128, 2 | 4), "decoder": (128, 128, 32, 1 | 2),
+                         "ragged": (20, 72, 30, 1 | 2 | 4)}[which]
     xh = bf16(rng.standard_normal((N, K0)))
     w1h = bf16(rng.standard_normal((M1, K0)) * 0.08)
     b1h = bf16(rng.standard_normal(M1) * 0.02)

@@ -370,6 +370,83 @@ __global__ __launch_bounds__(256) void mlp_small_kernel(const uint16_t * __restr
     layer(w2, b2, M1, M2, flags & WAMX_MLP_GELU_OUT, ht, nullptr, true);
 }
 
+// mlp_small_kernel's arithmetic (each output an f32 FMA chain over k in
+// ascending order, then the same roundings, so the same bits) spread over
+// more CUs: kMlpRegTok tokens per workgroup, thread t owning feature t % 128
+// for tokens 2 (t / 128) .. +2.  The FMAs are VALU work (16 tokens x 128 x
+// 128 per layer is 8k cycles of one CU), so the 16-token workgroups of
+// mlp_small_kernel ran 19-21 us on 3 CUs.  Each thread's weight rows of both
+// layers are loaded into registers up front as 16-byte chunks and the k loop
+// is unrolled over them, so the only LDS traffic is the broadcast activation
+// reads.  K0, M1 and M2 multiples of 8, weights 16-byte aligned.
+constexpr int kMlpChunks = kMlpMax / 8, kMlpRegTok = 4, kMlpTpt = kMlpRegTok / 2;
+__device__ __forceinline__ void mlp_row_load(const uint16_t * __restrict__ w, int K, int m, int M, uint4 (&r)[kMlpChunks]) {
+#pragma unroll
+    for (int c = 0; c < kMlpChunks; ++c)
+        r[c] = (m < M && 8 * c < K) ? *(const uint4 *) (w + (int64_t) m * K + 8 * c) : make_uint4(0, 0, 0, 0);
+}
+__device__ __forceinline__ void mlp_row_dot(const uint4 (&r)[kMlpChunks], int K, const float (*in)[kMlpRegTok], int g,
+                                            float (&acc)[kMlpTpt]) {
+#pragma unroll
+    for (int c = 0; c < kMlpChunks; ++c) {
+        if (8 * c >= K) break;
+        const uint32_t wp[4] = {r[c].x, r[c].y, r[c].z, r[c].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float wv = __uint_as_float(e & 1 ? wp[e >> 1] & 0xffff0000u : wp[e >> 1] << 16);
+            const float2 xv = *(const float2 *) &in[8 * c + e][kMlpTpt * g];
+            acc[0] = fmaf(wv, xv.x, acc[0]);
+            acc[1] = fmaf(wv, xv.y, acc[1]);
+        }
+    }
+}
+__global__ __launch_bounds__(256) void mlp_small_reg_kernel(const uint16_t * __restrict__ x,
+                                                            const uint16_t * __restrict__ w1,
+                                                            const uint16_t * __restrict__ b1,
+                                                            const uint16_t * __restrict__ w2,
+                                                            const uint16_t * __restrict__ b2, uint16_t * __restrict__ y,
+                                                            int64_t N, int K0, int M1, int M2, int flags) {
+    static_assert(kMlpTpt == 2, "two tokens per thread");
+    __shared__ __align__(16) float xt[kMlpMax][kMlpRegTok];
+    __shared__ __align__(16) float ht[kMlpMax][kMlpRegTok];
+    const int tid = threadIdx.x;
+    const int m = tid % kMlpMax, g = tid / kMlpMax;  // feature, token pair
+    const int64_t n0 = (int64_t) blockIdx.x * kMlpRegTok;
+    uint4 r1[kMlpChunks], r2[kMlpChunks];
+    mlp_row_load(w1, K0, m, M1, r1);
+    mlp_row_load(w2, M1, m, M2, r2);
+    const float bias1 = m < M1 ? bf16_to_f32(b1[m]) : 0.0f, bias2 = m < M2 ? bf16_to_f32(b2[m]) : 0.0f;
+    for (int e = tid; e < kMlpRegTok * K0; e += 256) {
+        const int n = e / K0, k = e % K0;
+        float v = n0 + n < N ? bf16_to_f32(x[(n0 + n) * K0 + k]) : 0.0f;
+        if (flags & WAMX_MLP_GELU_IN) v = round_bf16(gelu_erf(v));
+        xt[k][n] = v;
+    }
+    __syncthreads();
+    float acc[kMlpTpt];
+    if (m < M1) {
+        acc[0] = acc[1] = 0.0f;
+        mlp_row_dot(r1, K0, xt, g, acc);
+#pragma unroll
+        for (int j = 0; j < kMlpTpt; ++j) {
+            float v = round_bf16(round_bf16(acc[j]) + bias1);
+            if (flags & WAMX_MLP_GELU_MID) v = round_bf16(gelu_erf(v));
+            ht[m][kMlpTpt * g + j] = v;
+        }
+    }
+    __syncthreads();
+    if (m >= M2) return;
+    acc[0] = acc[1] = 0.0f;
+    mlp_row_dot(r2, M1, ht, g, acc);
+#pragma unroll
+    for (int j = 0; j < kMlpTpt; ++j) {
+        float v = round_bf16(round_bf16(acc[j]) + bias2);
+        if (flags & WAMX_MLP_GELU_OUT) v = round_bf16(gelu_erf(v));
+        const int64_t n = n0 + kMlpTpt * g + j;
+        if (n < N) y[n * M2 + m] = f32_to_bf16(v);
+    }
+}
+
 // splitmix64 (Steele, Lea, Flood: "Fast splittable pseudorandom number
 // generators", OOPSLA 2014) on seed + (i+1)*golden gamma, then Box-Muller
 // with two 24-bit uniforms in (0, 1).
@@ -524,7 +601,9 @@ hipError_t launch_mlp_small(const void * x, const void * w1, const void * b1, co
                             int64_t N, int64_t K0, int64_t M1, int64_t M2, int32_t flags, hipStream_t s) {
     if (N <= 0) return hipSuccess;
     if (K0 < 1 || M1 < 1 || M2 < 1 || K0 > kMlpMax || M1 > kMlpMax || M2 > kMlpMax) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(mlp_small_kernel, dim3((unsigned) ((N + kMlpTok - 1) / kMlpTok)), dim3(256), 0, s,
+    const bool reg = K0 % 8 == 0 && M1 % 8 == 0 && M2 % 8 == 0 && (((uintptr_t) w1 | (uintptr_t) w2) & 15) == 0;
+    const int tok = reg ? kMlpRegTok : kMlpTok;
+    hipLaunchKernelGGL(reg ? mlp_small_reg_kernel : mlp_small_kernel, dim3((unsigned) ((N + tok - 1) / tok)), dim3(256), 0, s,
                        (const uint16_t *) x, (const uint16_t *) w1, (const uint16_t *) b1, (const uint16_t *) w2,
                        (const uint16_t *) b2, (uint16_t *) y, N, (int) K0, (int) M1, (int) M2, (int) flags);
     return hipGetLastError();
