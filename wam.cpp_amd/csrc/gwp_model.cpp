@@ -362,14 +362,17 @@ static bool create_weights(wamx_gwp_model * m) {
     if (!m->wctx || !m->tctx) return false;
     m->patch_w = m->add_weight("gwp.patch_embedding.weight", 2, 2, c.z_dim, d);
     m->patch_b = m->add_weight("gwp.patch_embedding.bias", d);
-    auto mlp = [&](const std::string & p, int64_t in, int64_t out, Mlp3 & r) {
-        m->add_linear(p + ".in_proj", in, E, &r.in_w, &r.in_b);
+    // The action encoder's out_proj (hidden -> da) and the decoder's in_proj
+    // (da -> hidden) run on the denoise tokens only: tiled when those are few.
+    const bool few = m->B * c.action_chunk <= 64;
+    auto mlp = [&](const std::string & p, int64_t in, int64_t out, Mlp3 & r, bool t_in, bool t_out) {
+        m->add_linear(p + ".in_proj", in, E, &r.in_w, &r.in_b, t_in && E % 16 == 0 && in % 32 == 0);
         m->add_linear(p + ".mid_proj", E, E, &r.mid_w, &r.mid_b);
-        m->add_linear(p + ".out_proj", E, out, &r.out_w, &r.out_b);
+        m->add_linear(p + ".out_proj", E, out, &r.out_w, &r.out_b, t_out && out % 16 == 0 && E % 32 == 0);
     };
-    mlp("gwp.state_encoder", A, da, m->state_enc);
-    mlp("gwp.action_encoder", A, da, m->action_enc);
-    mlp("gwp.action_decoder", da, A, m->action_dec);
+    mlp("gwp.state_encoder", A, da, m->state_enc, false, false);
+    mlp("gwp.action_encoder", A, da, m->action_enc, false, few);
+    mlp("gwp.action_decoder", da, A, m->action_dec, few, false);
     auto cond = [&](const std::string & p, int64_t w, Cond & r) {
         m->add_linear(p + ".time_embedder.linear_1", 256, w, &r.t1_w, &r.t1_b);
         m->add_linear(p + ".time_embedder.linear_2", w, w, &r.t2_w, &r.t2_b);
