@@ -1441,6 +1441,7 @@ __global__ __launch_bounds__(kWkWaves * 64) void gemm_skinny_wk(GemmParams p) {
 struct RowSegDev {
     int32_t kind, rope_mode;
     int64_t col, dst_tokens, tok0, vt_ld, vt_hs, chunk_tokens, chunk_stride;
+    int32_t vt_tok;  // V^T segment: tokens per workgroup (1, or kVtTok when its stores can be 16-byte runs)
     const uint16_t * w;
     uint16_t * dst;
     const int32_t *pos0, *pos1, *pos2;
@@ -1456,14 +1457,24 @@ struct RowPostDev {
     RowSegDev seg[3];
 };
 
+// A V^T segment with vt_tok == kVtTok runs kVtTok tokens x (width / kVtTok)
+// columns per workgroup instead of one token row: each thread reduces the
+// same (token, 8-column chunk) as in the one-row form, the values meet in
+// LDS, and each thread then stores one column's kVtTok consecutive tokens
+// as one 16-byte run of V^T, where the one-row form stores 8 scattered
+// 2-byte values per thread.
+constexpr int kVtTok = 8;
+
 template <int E, int POST>
 __global__ __launch_bounds__(512) void skinny_reduce_row(GemmParams p, const float * __restrict__ part, int splits,
                                                          RowPostDev rp) {
     __shared__ float red[16];
-    const int64_t n = blockIdx.x;
-    const int c = threadIdx.x;
-    const int64_t NM = p.N * p.M;
     const RowSegDev & sg = rp.seg[POST == kPostSegs ? blockIdx.y : 0];
+    const bool vt_block = POST == kPostSegs && sg.kind == kRowSegVt && sg.vt_tok == kVtTok;  // workgroup-uniform
+    const int cpb = (int) blockDim.x / kVtTok;  // chunks per column block of a V^T block
+    const int64_t n = vt_block ? (int64_t) (blockIdx.x / kVtTok) * kVtTok + threadIdx.x / cpb : (int64_t) blockIdx.x;
+    const int c = vt_block ? (int) (blockIdx.x % kVtTok) * cpb + (int) threadIdx.x % cpb : (int) threadIdx.x;
+    const int64_t NM = p.N * p.M;
     const int64_t m = (POST == kPostSegs ? sg.col : 0) + 8 * c;
     const float * src = part + n * p.M + m;
     // The row op's and the epilogue's inputs are requested first, then every
@@ -1521,6 +1532,22 @@ __global__ __launch_bounds__(512) void skinny_reduce_row(GemmParams p, const flo
             const float inv_rms = row_inv_rms<1>(v, rp.width, sg.eps, red);
             *(uint4 *) (sg.dst + cb * sg.chunk_stride + ((int64_t) h * sg.dst_tokens + sg.tok0 + tl) * hd + dd0) =
                 qk_chunk(v[0], inv_rms, wv, dd0, rt);
+        } else if (vt_block) {
+            // v holds bf16 values (the epilogue rounds), so the packing below
+            // stores the bits the one-row form stores.
+            __shared__ __align__(16) uint16_t vtile[kVtTok * 512];
+            const int row = (int) threadIdx.x / cpb, k = (int) threadIdx.x % cpb, bw = (int) blockDim.x;
+            *(uint4 *) (vtile + row * bw + 8 * k) = pack8(v[0]);
+            __syncthreads();
+            const int f = (int) (blockIdx.x % kVtTok) * bw + (int) threadIdx.x;  // column of the segment
+            const int64_t n0 = (int64_t) (blockIdx.x / kVtTok) * kVtTok;
+            const int64_t cb0 = n0 / sg.chunk_tokens, tl0 = n0 - cb0 * sg.chunk_tokens;
+            uint32_t w[kVtTok / 2];
+#pragma unroll
+            for (int j = 0; j < kVtTok / 2; ++j)
+                w[j] = (uint32_t) vtile[(2 * j) * bw + threadIdx.x] | ((uint32_t) vtile[(2 * j + 1) * bw + threadIdx.x] << 16);
+            *(uint4 *) (sg.dst + cb0 * sg.chunk_stride + (int64_t) (f / hd) * sg.vt_hs + (int64_t) (f % hd) * sg.vt_ld +
+                        sg.tok0 + tl0) = make_uint4(w[0], w[1], w[2], w[3]);
         } else {
             uint16_t * d = sg.dst + cb * sg.chunk_stride + (int64_t) h * sg.vt_hs + sg.tok0 + tl;
 #pragma unroll
@@ -2060,6 +2087,16 @@ hipError_t launch_gemm_rowpost(const GemmArgs & a, const RowPost & post, hipStre
             o.chunk_tokens = g.chunk_tokens > 0 ? g.chunk_tokens : p.N;
             o.chunk_stride = g.chunk_tokens > 0 ? g.chunk_stride : 0;
             if (p.N % o.chunk_tokens != 0) return hipErrorNotSupported;
+            // V^T in blocks of kVtTok tokens: more than 64 tokens (eight
+            // 48-token chunks: decode 111.0 -> 109.8 ms; at 48 tokens the
+            // blocks' LDS pass cost the chunk 0.25 ms), whole blocks per
+            // chunk, 16-byte aligned runs, and a row of chunks that splits
+            // into kVtTok column blocks (a row is a multiple of 64 chunks).
+            o.vt_tok = g.kind == kRowSegVt && p.N > 64 && o.chunk_tokens % kVtTok == 0 && g.tok0 % kVtTok == 0 &&
+                               g.vt_ld % 8 == 0 && g.vt_hs % 8 == 0 && o.chunk_stride % 8 == 0 && aligned16(g.dst) &&
+                               (post.width / 8) % kVtTok == 0 && post.width / 8 <= 512
+                           ? kVtTok
+                           : 1;
             rope_scales(post.head_dim, g.freq_base, o.l2ts128, o.l2ts44, o.l2ts42);
         }
     } else {
