@@ -170,12 +170,16 @@ def test_qkv_split_is_bit_exact(wx, be, rng, T):
         g.close()
 
 
-def test_qkv_split_chunked_is_bit_exact(wx, be, rng):
+@pytest.mark.parametrize("tpad", [52, 64])
+def test_qkv_split_chunked_is_bit_exact(wx, be, rng, tpad):
     """Eight chunks of 48 tokens: Q and K into [dh, 48, H, 8], V^T into
-    [pad, dh, H, 8], each chunk's RoPE positions 1..48."""
+    [pad, dh, H, 8], each chunk's RoPE positions 1..48.  With V^T rows of
+    64 keys (16-byte aligned) the reduce's V^T segment runs in blocks of 8
+    tokens stored as 16-byte runs; with 52 it stores one token row at a
+    time."""
     B, Tc = 8, 48
     T = B * Tc
-    print(f"fusion qkv chunked B={B} Tc={Tc}", flush=True)
+    print(f"fusion qkv chunked B={B} Tc={Tc} tpad={tpad}", flush=True)
     lib = be.lib
     g = Graph(wx, be)
     try:
@@ -184,7 +188,6 @@ def test_qkv_split_chunked_is_bit_exact(wx, be, rng):
         b = g.t(wx.TYPE_BF16, 3 * D)
         nq, nk = g.t(wx.TYPE_BF16, D), g.t(wx.TYPE_BF16, D)
         pos = g.t(wx.TYPE_I32, Tc)
-        tpad = 52
         vraw = g.t(wx.TYPE_BF16, tpad, DH, H, B)
         qkv = lib.wamx_linear(g.ctx, w, x, b, wx.EPI_BIAS, None, None)
         pitch = qkv.contents.nb[1]
