@@ -114,7 +114,7 @@ def test_linear_then_norm_is_bit_exact(wx, be, rng, T, kind):
         g.close()
 
 
-@pytest.mark.parametrize("T", [48, 5])
+@pytest.mark.parametrize("T", [48, 5, 1])
 def test_qkv_split_is_bit_exact(wx, be, rng, T):
     print(f"fusion qkv T={T}", flush=True)
     lib = be.lib
