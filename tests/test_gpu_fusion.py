@@ -170,6 +170,69 @@ def test_qkv_split_is_bit_exact(wx, be, rng, T):
         g.close()
 
 
+def test_qkv_row_ops_apart_are_not_fused(wx, be, rng):
+    """A 48-token QKV product whose K norm and V^T store follow it but whose
+    Q norm comes after another launch: the fused reduce writes the product
+    only in its segments' columns, so the K and V segments alone (two thirds
+    of the columns) must not be fused, and the Q norm must read the product
+    as written.  The product's output holds a NaN pattern before the run; all
+    three results are compared bit for bit with the standalone ops."""
+    T = 48
+    print(f"fusion qkv row ops apart T={T}", flush=True)
+    lib = be.lib
+    g = Graph(wx, be)
+    try:
+        w = g.t(wx.TYPE_BF16, D, 3 * D)
+        x = g.t(wx.TYPE_BF16, D, T)
+        b = g.t(wx.TYPE_BF16, 3 * D)
+        nq, nk = g.t(wx.TYPE_BF16, D), g.t(wx.TYPE_BF16, D)
+        pos = g.t(wx.TYPE_I32, T)
+        vraw = g.t(wx.TYPE_BF16, 64, DH, H)
+        other_in = g.t(wx.TYPE_BF16, D, T)
+        qkv = lib.wamx_linear(g.ctx, w, x, b, wx.EPI_BIAS, None, None)
+        pitch = qkv.contents.nb[1]
+        k = lib.wamx_qk_norm_rope(g.ctx, lib.wamx_view_2d(g.ctx, qkv, D, T, pitch, 2 * D), nk,
+                                  g.t(wx.TYPE_BF16, DH, T, H), 0, 0, pos, None, None, 1e-6, 10000.0)
+        vsrc = lib.wamx_permute(g.ctx, lib.wamx_view_3d(g.ctx, qkv, DH, H, T, DH * 2, pitch, 4 * D), 1, 2, 0, 3)
+        vdst = lib.wamx_view_3d(g.ctx, vraw, T, DH, H, vraw.contents.nb[1], vraw.contents.nb[2], 0)
+        v = lib.wamx_cpy(g.ctx, vsrc, vdst)
+        other = lib.wamx_gelu(g.ctx, other_in)  # a launch between the V^T store and the Q norm
+        q = lib.wamx_qk_norm_rope(g.ctx, lib.wamx_view_2d(g.ctx, qkv, D, T, pitch, 0), nq,
+                                  g.t(wx.TYPE_BF16, DH, T, H), 0, 0, pos, None, None, 1e-6, 10000.0)
+        g.alloc()
+        hw = wx.f32_to_bf16(rng.standard_normal(3 * D * D).astype(np.float32) * 0.02)
+        hx = wx.f32_to_bf16(rng.standard_normal(D * T).astype(np.float32))
+        hb = wx.f32_to_bf16(rng.standard_normal(3 * D).astype(np.float32) * 0.02)
+        hnq = wx.f32_to_bf16(1.0 + rng.standard_normal(D).astype(np.float32) * 0.1)
+        hnk = wx.f32_to_bf16(1.0 + rng.standard_normal(D).astype(np.float32) * 0.1)
+        hpos = np.arange(1, T + 1, dtype=np.int32)
+        for t, a in ((w, hw), (x, hx), (b, hb), (nq, hnq), (nk, hnk), (pos, hpos), (other_in, hx),
+                     (vraw, np.zeros(64 * DH * H, np.uint16)), (qkv, np.full(T * 3 * D, 0x7FC1, np.uint16))):
+            g.set(t, a)
+        g.compute(k, v, other, q)
+        got_qkv = g.get(qkv, np.uint16, (T, 3 * D))
+        got_q = g.get(q, np.uint16, (H, T, DH))
+        got_k = g.get(k, np.uint16, (H, T, DH))
+        got_vt = g.get(vraw, np.uint16, (H, DH, 64))[:, :, :T]
+
+        ref_qkv, ref_q, ref_k = be.empty(T * 3 * D * 2), be.empty(T * D * 2), be.empty(T * D * 2)
+        wx.check(lib.wamx_op_linear(be.ptr, data(w), data(x), wx.TYPE_BF16, data(b), wx.EPI_BIAS, None, None,
+                                    ref_qkv.ptr, 3 * D, T, D))
+        pp = C.cast(data(pos), C.POINTER(C.c_int32))
+        wx.check(lib.wamx_op_qk_norm_rope(be.ptr, ref_qkv.ptr, 3 * D, data(nq), ref_q.ptr, H, DH, T, T, 0, 0, pp,
+                                          None, None, 1e-6, 10000.0))
+        wx.check(lib.wamx_op_qk_norm_rope(be.ptr, ref_qkv.ptr + 2 * D, 3 * D, data(nk), ref_k.ptr, H, DH, T, T, 0,
+                                          0, pp, None, None, 1e-6, 10000.0))
+        be.sync()
+        rq = ref_qkv.download(np.uint16, (T, 3 * D))
+        assert np.array_equal(got_qkv, rq), "the product's output"
+        assert np.array_equal(got_q, ref_q.download(np.uint16, (H, T, DH))), "Q norm after another launch"
+        assert np.array_equal(got_k, ref_k.download(np.uint16, (H, T, DH)))
+        assert np.array_equal(got_vt, rq[:, 2 * D:].reshape(T, H, DH).transpose(1, 2, 0))
+    finally:
+        g.close()
+
+
 @pytest.mark.parametrize("tpad", [52, 64])
 def test_qkv_split_chunked_is_bit_exact(wx, be, rng, tpad):
     """Eight chunks of 48 tokens: Q and K into [dh, 48, H, 8], V^T into

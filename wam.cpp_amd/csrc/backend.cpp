@@ -438,7 +438,18 @@ static int match_row_post(wamx_cgraph * g, int i, int n, RowPost & post, bool la
         last = j;
         j = next_compute(g, j, n, lanes);
     }
-    return post.nseg > 0 ? last : -1;
+    // The fused reduce writes the product's output only in its segments'
+    // columns, so the segments must tile every column: a row op of the
+    // product that does not follow here (another lane's node, or any node
+    // between them) reads its columns from that output.
+    if (post.nseg == 0 || post.nseg * post.width != lin->ne[0]) return -1;
+    bool covered[3] = {false, false, false};
+    for (int k = 0; k < post.nseg; ++k) {
+        const int64_t c = post.seg[k].col;
+        if (c % post.width != 0 || c / post.width >= post.nseg || covered[c / post.width]) return -1;
+        covered[c / post.width] = true;
+    }
+    return last;
 }
 
 // ---------------------------------------------------------------------------
