@@ -109,7 +109,10 @@ def test_layout_and_conversions(wx, be, rng):
         B.close()
 
 
+# One-token shapes (the state token's projections) run the K-split plans of
+# grids in rounds of 64 workgroups; the rest in rounds of 256.
 @pytest.mark.parametrize("M,K,N", [(3072, 3072, 48), (9216, 3072, 48), (3072, 14336, 48), (14336, 3072, 1),
+                                   (3072, 3072, 1), (9216, 3072, 1), (3072, 14336, 1),
                                    (3072, 3072, 17), (128, 96, 5)])
 def test_integer_products_exact(wx, be, M, K, N):
     print(f"tiled integer product M={M} K={K} N={N}", flush=True)
