@@ -136,6 +136,34 @@ def test_integer_products_exact(wx, be, M, K, N):
         B.close()
 
 
+@pytest.mark.parametrize("M,K,N", [(3072, 3072, 48), (3072, 3072, 1), (9216, 3072, 1), (3072, 14336, 1),
+                                   (3072, 3072, 17), (128, 96, 5)])
+def test_integer_products_f32_activations_exact(wx, be, M, K, N):
+    """Tiled weights times f32 activations (gemm_skinny_tiled's f32 form, which
+    rounds each activation to bf16 as it stages it). Small integers survive
+    that rounding, and their fp32 sums are exact, so the output must equal
+    x @ w.T exactly."""
+    print(f"tiled integer product, f32 activations, M={M} K={K} N={N}", flush=True)
+    lib = be.lib
+    rng = np.random.default_rng(M + 13 * K + 5 * N)
+    w = rng.integers(-4, 5, (M, K))
+    x = rng.integers(-4, 5, (N, K))
+    B = Bufs(wx, be)
+    try:
+        wt = B.tiled(K, M)
+        xt = B.plain(wx.TYPE_F32, K, N)
+        y = lib.wamx_mul_mat(B.pctx, wt, xt)
+        B.alloc()
+        B.set(wt, wx.f32_to_bf16(w.astype(np.float32)))
+        B.set(xt, x.astype(np.float32))
+        for rep in range(2):
+            B.compute(y)
+            got = B.get(y, np.float32, (N, M))
+            assert np.array_equal(got.astype(np.int64), x @ w.T), f"launch {rep}"
+    finally:
+        B.close()
+
+
 @pytest.mark.parametrize("M,K,N", [(14336, 3072, 48), (14336, 3072, 1), (12288, 4096, 17), (14336, 2048, 33),
                                    (14336, 3072, 64)])
 def test_integer_products_bf16_out_exact(wx, be, M, K, N):
